@@ -1,0 +1,254 @@
+"""CPU oracle for the quantized-linear path. TEST INFRASTRUCTURE ONLY.
+
+Imported by tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s
+cpu_baseline leg, always as the checker or the timed CPU baseline and never
+as the product path (venturi_amd never imports this package).
+
+Two layers:
+
+* ``liboracle.so`` (oracle.c, built by ``make -C oracle``): the reference's
+  device arithmetic restated in C, in the reference's association order.
+* numpy restatements of the codecs (pack/unpack/RTN) and of the MoE combine.
+
+Each function cites the reference file:line it restates (paths relative to
+/root/reference/src/venturi/). What pins each function is listed in
+tests/test_oracle_pins.py; functions that nothing pins are marked
+"parity unpinned" below.
+"""
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+LIBRARY = _HERE / "liboracle.so"
+
+_lib = None
+
+
+def lib():
+    """Loads liboracle.so (build it with ``make -C oracle``)."""
+    global _lib
+    if _lib is None:
+        if not LIBRARY.is_file():
+            raise FileNotFoundError(f"{LIBRARY} is not built; run make -C oracle")
+        handle = C.CDLL(str(LIBRARY))
+        P, I, F = C.c_void_p, C.c_int, C.c_float
+        handle.oracle_f32_to_f16.argtypes, handle.oracle_f32_to_f16.restype = [F], C.c_uint16
+        handle.oracle_f16_to_f32.argtypes, handle.oracle_f16_to_f32.restype = [C.c_uint16], F
+        handle.oracle_q8_linear.argtypes = [P, I, P, P, P] + [I] * 4
+        handle.oracle_a8_quantize.argtypes = [P, I, I, I, P, P]
+        handle.oracle_a8_linear.argtypes = [P] * 5 + [I] * 5
+        handle.oracle_a8_group_dots.argtypes = [P] * 3 + [I] * 4
+        handle.oracle_rms.argtypes = [P, I, P, P, I, I, F, P]
+        handle.oracle_rms_a8.argtypes = [P, P, I, I, F, I, P, P, P, P]
+        handle.oracle_q4_linear.argtypes = [P] * 4 + [I] * 4
+        handle.oracle_q4_decode.argtypes = [P] * 3 + [I] * 3
+        _lib = handle
+    return _lib
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _u16(a):
+    """View fp16/bf16 storage (numpy float16 or uint16) as contiguous uint16."""
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint16) if a.dtype == np.float16 else a.astype(np.uint16, copy=False)
+
+
+# ---------------------------------------------------------------- Q8 codec
+
+
+def q8_pack(source):
+    """Q8RowSplitWeight.from_dense (ops/weights.py:398-439) in numpy.
+
+    source: float32 (or float64) [n, k]. Returns (codes int8 [n, Kp], scales
+    float16 [n, Kp/32]). Raises ValueError for non-finite input or fp16 scale
+    overflow, as the reference does.
+    """
+    source = np.asarray(source)
+    work = np.float64 if source.dtype == np.float64 else np.float32
+    n, k = source.shape
+    padded = (k + 127) // 128 * 128
+    block = np.zeros((n, padded), dtype=work)
+    block[:, :k] = source
+    if not np.isfinite(block).all():
+        raise ValueError("Q8 source must be finite")
+    groups = block.reshape(n, -1, 32)
+    amax = np.abs(groups).max(-1)
+    with np.errstate(over="ignore"):
+        stored = (amax / work(127)).astype(np.float16)
+    if not np.isfinite(stored).all():
+        raise ValueError("Q8 group scale overflows FP16")
+    divisor = stored.astype(work)[:, :, None]
+    safe = np.where(divisor > 0, divisor, work(1))
+    q = np.where(divisor > 0, np.clip(np.rint(groups / safe), -127, 127), 0)
+    return q.astype(np.int8).reshape(n, padded), stored
+
+
+def q8_unpack(codes, scales, k):
+    """FP64 value code*scale (ops/weights.py:441-454), columns [0, k)."""
+    return (codes.astype(np.float64) * np.repeat(scales.astype(np.float64), 32, axis=1))[:, :k]
+
+
+# ---------------------------------------------------------------- Q4 codec
+
+
+def q4_pack_codes(codes, scales):
+    """Q4RowSplitWeight.from_codes (ops/weights.py:108-130): exact nibble packing."""
+    codes = np.asarray(codes)
+    n, k = codes.shape
+    if ((codes < -8) | (codes > 7)).any():
+        raise ValueError("Q4 codes must be in [-8, 7]")
+    padded = (k + 127) // 128 * 128
+    nib = np.zeros((n, padded), dtype=np.uint8)
+    nib[:, :k] = (codes.astype(np.int16) & 15).astype(np.uint8)
+    packed = nib[:, 0::2] | (nib[:, 1::2] << 4)
+    plane = np.zeros((n, padded // 64), dtype=np.float16)
+    plane[:, : scales.shape[1]] = scales
+    return packed, plane
+
+
+def q4_unpack_signed(packed, k):
+    """Signed codes [n, k] from packed nibbles (low nibble = even column)."""
+    lo = (packed & 15).astype(np.int16)
+    hi = (packed >> 4).astype(np.int16)
+    values = np.stack((lo, hi), -1).reshape(packed.shape[0], -1)[:, :k]
+    return np.where(values < 8, values, values - 16)
+
+
+def q4_rtn(weight):
+    """quantize_q4_rtn (models/flash_next/flash_next_q4.py:26-52) in numpy float32.
+
+    Returns (signed codes int8 [n, k], scales float16 [n, ceil(k/64)]).
+    """
+    value = np.asarray(weight, dtype=np.float32)
+    rows, cols = value.shape
+    padded = (cols + 127) // 128 * 128
+    blocks = np.zeros((rows, padded), dtype=np.float32)
+    blocks[:, :cols] = value
+    blocks = blocks.reshape(rows, padded // 64, 64)
+    scales = np.maximum(np.abs(blocks).max(-1) / np.float32(7), np.float32(2.0**-24)).astype(np.float16)
+    codes = np.clip(np.rint(blocks / scales.astype(np.float32)[:, :, None]), -7, 7).astype(np.int8)
+    return codes.reshape(rows, padded)[:, :cols], scales[:, : (cols + 63) // 64]
+
+
+def q4_decode_fp16(packed, scales, k):
+    """fp16(q * scale) (flash_next_q4.py:55-62; flash_next_q4.cu:7-14)."""
+    signed = q4_unpack_signed(packed, packed.shape[1] * 2).astype(np.float32)
+    values = signed.reshape(packed.shape[0], -1, 64) * scales.astype(np.float32)[:, :, None]
+    return values.reshape(packed.shape[0], -1)[:, :k].astype(np.float16)
+
+
+# -------------------------------------------------- device-order restatements
+
+
+def q8_linear(x, codes, scales, k, dtype=0):
+    """venturi_q8_head_run canonical bytes (ops/csrc/blocks.cu:306-321).
+
+    x: uint16 (fp16 dtype 0 / bf16 dtype 1) [tokens, k]; returns uint16 [tokens, n].
+    """
+    xs = _u16(x)
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    sc = _u16(scales)
+    tokens, n, padded = xs.shape[0], codes.shape[0], codes.shape[1]
+    out = np.zeros((tokens, n), dtype=np.uint16)
+    lib().oracle_q8_linear(_ptr(xs), dtype, _ptr(codes), _ptr(sc), _ptr(out), tokens, n, k, padded)
+    return out
+
+
+def a8_quantize(x, passes):
+    """vdq::quantize (ops/csrc/q8_dp4a.cuh:15-34): (codes int8 [P,T,G,32], scales f32 [P,T,G])."""
+    xs = _u16(x)
+    tokens, k = xs.shape
+    groups = (k + 31) // 32
+    codes = np.zeros((passes, tokens, groups, 32), dtype=np.int8)
+    scales = np.zeros((passes, tokens, groups), dtype=np.float32)
+    lib().oracle_a8_quantize(_ptr(xs), tokens, k, passes, _ptr(codes), _ptr(scales))
+    return codes, scales
+
+
+def a8_workspace(codes, scales):
+    """The reference workspace bytes: all codes, then all scales."""
+    return np.concatenate([codes.reshape(-1).view(np.uint8), scales.reshape(-1).view(np.uint8)])
+
+
+def a8_linear(acodes, ascales, codes, wscales, k):
+    """vdq::dot (ops/csrc/q8_dp4a.cuh:36-70): fp16 bits [tokens, n]."""
+    acodes = np.ascontiguousarray(acodes, dtype=np.int8)
+    ascales = np.ascontiguousarray(ascales, dtype=np.float32)
+    passes, tokens = acodes.shape[0], acodes.shape[1]
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    n, padded = codes.shape
+    out = np.zeros((tokens, n), dtype=np.uint16)
+    lib().oracle_a8_linear(
+        _ptr(acodes), _ptr(ascales), _ptr(codes), _ptr(_u16(wscales)), _ptr(out), tokens, n, k, padded, passes
+    )
+    return out
+
+
+def a8_group_dots(acodes, codes, k):
+    """Exact int32 per-group dots of pass 0: [tokens, n, groups]."""
+    acodes = np.ascontiguousarray(acodes[0], dtype=np.int8)
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    tokens, groups = acodes.shape[0], acodes.shape[1]
+    n, padded = codes.shape
+    dots = np.zeros((tokens, n, groups), dtype=np.int32)
+    lib().oracle_a8_group_dots(_ptr(acodes), _ptr(codes), _ptr(dots), tokens, n, k, padded)
+    return dots
+
+
+def rms(x, weight, epsilon, dtype=0):
+    """rms_norm (ops/csrc/blocks.cu:31-54) with 1/sqrt in place of rsqrtf.
+
+    dtype 0/1: x is uint16 fp16/bf16 bits; dtype 2: float32.
+    """
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    if dtype == 2:
+        xs = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros_like(xs)
+    else:
+        xs = _u16(x)
+        out = np.zeros_like(xs)
+    tokens, k = xs.shape
+    buffer = np.zeros(k, dtype=np.float32)
+    lib().oracle_rms(_ptr(xs), dtype, _ptr(w), _ptr(out), tokens, k, epsilon, _ptr(buffer))
+    return out
+
+
+def rms_a8(x, weight, epsilon, passes):
+    """RMSNorm -> fp16 -> A8 (ops/csrc/q8_rms_producer.cuh:8-53, any pass count).
+
+    Returns (codes [P,T,G,32], scales [P,T,G], fp16 bits of the normalised rows).
+    """
+    xs = _u16(x)
+    tokens, k = xs.shape
+    groups = (k + 31) // 32
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    codes = np.zeros((passes, tokens, groups, 32), dtype=np.int8)
+    scales = np.zeros((passes, tokens, groups), dtype=np.float32)
+    inter = np.zeros((tokens, k), dtype=np.uint16)
+    buffer = np.zeros(k, dtype=np.float32)
+    lib().oracle_rms_a8(_ptr(xs), _ptr(w), tokens, k, epsilon, passes, _ptr(codes), _ptr(scales), _ptr(inter),
+                        _ptr(buffer))
+    return codes, scales, inter
+
+
+def q4_linear(x, packed, scales, k):
+    """q4_linear (ops/csrc/flash_next_q4.cu:23-34): fp16 bits [tokens, rows]."""
+    xs = _u16(x)
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    tokens, rows, padded = xs.shape[0], packed.shape[0], packed.shape[1] * 2
+    out = np.zeros((tokens, rows), dtype=np.uint16)
+    lib().oracle_q4_linear(_ptr(xs), _ptr(packed), _ptr(_u16(scales)), _ptr(out), tokens, rows, k, padded)
+    return out
+
+
+def f32_to_f16_bits(values):
+    """Element-wise RNE fp32 -> fp16 through the oracle's own converter."""
+    f = lib().oracle_f32_to_f16
+    flat = np.asarray(values, dtype=np.float32).reshape(-1)
+    return np.array([f(float(v)) for v in flat], dtype=np.uint16).reshape(np.shape(values))

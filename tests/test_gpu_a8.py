@@ -1,0 +1,126 @@
+"""A8 path: quantizer bytes, W8A8 projection bytes, RMS and fused RMS+A8."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import bits, guarded_out, random_q8
+from venturi_amd import Q8RowSplitWeight, prepare_q8_dp4a, prepare_rms_q8
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(backend, device, n, k, tokens):
+    # Draws as the reference's A8 test (test_q8_dp4a.py:40-50).
+    padded = (k + 127) // 128 * 128
+    gen = torch.Generator().manual_seed(5821 + k + n + tokens)
+    codes = torch.randint(-127, 128, (n, padded), dtype=torch.int8, generator=gen)
+    scales = (torch.rand(n, padded // 32, generator=gen) * 0.01).half()
+    scales[:, 0] = 0
+    x = torch.randn(tokens, k, generator=gen).half()
+    resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, k), dtype=torch.float16, device=device)
+    return codes, scales, x, resident
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 8, 23, 32])
+@pytest.mark.parametrize("shape", [(7, 1), (33, 67), (17, 128), (9, 129), (257, 5120)])
+def test_quantizer_and_projection_bytes(backend, device, passes, tokens, shape):
+    n, k = shape
+    print(f"case a8 n={n} k={k} tokens={tokens} passes={passes}", flush=True)
+    codes, scales, x, resident = _setup(backend, device, n, k, tokens)
+    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=passes == 2)
+    workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    guard, out = guarded_out(tokens, n, torch.float16, device)
+    plan.run(x.to(device), out=out, workspace=workspace)
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    q, d = oracle.a8_quantize(bits(x), passes)
+    np.testing.assert_array_equal(workspace.cpu().numpy(), oracle.a8_workspace(q, d))
+    expected = oracle.a8_linear(q, d, codes.numpy(), scales.numpy(), k)
+    np.testing.assert_array_equal(bits(out), expected)
+    assert plan.precision_profile.endswith("-residual-a8") == (passes == 2)
+
+
+def test_nonfinite_and_zero_propagation(backend, device):
+    _, _, x, resident = _setup(backend, device, 16, 128, 1)
+    plan = prepare_q8_dp4a(resident, tokens=1, residual_compensation=True)
+    workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    x = x.to(device)
+    out = torch.empty(1, 16, dtype=torch.float16, device=device)
+    x.fill_(float("inf"))
+    plan.run(x, out=out, workspace=workspace)
+    assert not torch.isfinite(out).any()
+    x.zero_()
+    plan.run(x, out=out, workspace=workspace)
+    assert not out.any() and not workspace.any()
+
+
+def test_workspace_guards(backend, device):
+    _, _, x, resident = _setup(backend, device, 16, 128, 1)
+    plan = prepare_q8_dp4a(resident, tokens=1, residual_compensation=True)
+    workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    x = x.to(device)
+    out = torch.empty(1, 16, dtype=torch.float16, device=device)
+    with pytest.raises((ValueError, TypeError)):
+        plan.run(x, out=out, workspace=workspace[:-1])
+    with pytest.raises(ValueError, match="alias"):
+        plan.run(x, out=workspace[:32].view(torch.float16).view(1, 16), workspace=workspace)
+    unaligned = torch.empty(plan.workspace_bytes + 16, dtype=torch.uint8, device=device)
+    with pytest.raises(ValueError, match="16-byte alignment"):
+        plan.run(x, out=out, workspace=unaligned[4 : 4 + plan.workspace_bytes])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("k", [1, 31, 67, 1025, 5120])
+def test_rms_bytes_and_fp64(backend, device, dtype, k):
+    tokens = 5
+    g = torch.Generator().manual_seed(17 + k)
+    x = torch.randn(tokens, k, generator=g).to(dtype)
+    w = 1 + 0.03 * torch.randn(k, generator=g)
+    plan = backend.upload_rmsnorm(w, dtype=dtype, device=device, epsilon=1e-6).prepare(tokens=tokens)
+    out = torch.empty(tokens, k, dtype=dtype, device=device)
+    plan.run(x.to(device), out=out)
+    code = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}[dtype]
+    if dtype == torch.float32:
+        expected = oracle.rms(x.numpy(), w.numpy(), 1e-6, dtype=2)
+        np.testing.assert_array_equal(out.cpu().numpy(), expected)
+    else:
+        expected = oracle.rms(bits(x), w.numpy(), 1e-6, dtype=code)
+        np.testing.assert_array_equal(bits(out), expected)
+    xd = x.double()
+    ideal = (xd * torch.rsqrt(xd.square().mean(-1, keepdim=True) + 1e-6) * w.double()).to(dtype)
+    rtol = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2, torch.float32: 1e-5}[dtype]
+    torch.testing.assert_close(out.cpu(), ideal, rtol=rtol, atol=2e-6)
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+@pytest.mark.parametrize("tokens", [1, 8, 23])
+@pytest.mark.parametrize("k", [1, 31, 33, 67, 1025, 5120, 8704])
+def test_fused_rms_a8_bytes(backend, device, passes, tokens, k):
+    # Shapes of the reference's fused-producer test (test_rms_quant.py:163-176).
+    print(f"case rms-a8 k={k} tokens={tokens} passes={passes}", flush=True)
+    g = torch.Generator().manual_seed(17 + tokens + k)
+    x = torch.randn(tokens, k, generator=g).half()
+    w = 1 + 0.03 * torch.randn(k, generator=g)
+    norm = backend.upload_rmsnorm(w, dtype=torch.float16, device=device, epsilon=1e-6)
+    plan = prepare_rms_q8(norm, tokens=tokens, residual_compensation=passes == 2)
+    storage = torch.full((plan.workspace_bytes + 32,), 71, dtype=torch.uint8, device=device)
+    workspace = storage[16:-16]
+    inter = torch.empty(tokens, k, dtype=torch.float16, device=device)
+    plan.run(x.to(device), workspace=workspace, intermediate=inter)
+    s = storage.cpu()
+    assert bool((s[:16] == 71).all()) and bool((s[-16:] == 71).all())
+    q, d, y = oracle.rms_a8(bits(x), w.numpy(), 1e-6, passes)
+    np.testing.assert_array_equal(bits(inter), y)
+    np.testing.assert_array_equal(workspace.cpu().numpy(), oracle.a8_workspace(q, d))
+    # Fused == RMSNorm then the plain quantizer on the same device.
+    y_dev = torch.empty(tokens, k, dtype=torch.float16, device=device)
+    norm.prepare(tokens=tokens).run(x.to(device), out=y_dev)
+    assert torch.equal(y_dev, inter)
+    lib = backend._native
+    separate = torch.empty_like(workspace)
+    backend._check(lib.venturi_q8_dp4a_quantize(y_dev.data_ptr(), separate.data_ptr(), separate.numel(), tokens, k,
+                                                 passes, torch.cuda.current_stream().cuda_stream))
+    assert torch.equal(separate, workspace)

@@ -1,0 +1,100 @@
+"""Q8 A16 projection (exact route) against the oracle's canonical-order bytes."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import bits, guarded_out, random_q8
+from venturi_amd import Q8RowSplitWeight
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(1, 1), (7, 65), (33, 129), (7, 256), (33, 512), (257, 5120)])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 5, 7, 8, 9, 16, 26, 32])
+def test_exact_bytes_tails_and_guards(backend, device, dtype, shape, tokens):
+    # Shapes/tokens of the reference's byte-equality test (test_q8_tiling.py:222-248).
+    n, k = shape
+    print(f"case q8-exact n={n} k={k} tokens={tokens} dtype={dtype}", flush=True)
+    codes, scales = random_q8(n, k, 9367 + n + tokens)
+    weight = Q8RowSplitWeight(codes, scales, k)
+    gen = torch.Generator().manual_seed(11 + tokens)
+    x = torch.randn(tokens, k, generator=gen).to(dtype)
+    resident = backend.upload_linear(weight, dtype=dtype, device=device)
+    plan = resident.prepare(tokens=tokens, route="exact")
+    assert "q8" in plan.route
+    guard, out = guarded_out(tokens, n, dtype, device)
+    plan.run(x.to(device), out=out)
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    expected = oracle.q8_linear(bits(x), codes.numpy(), scales.numpy(), k, dtype=0 if dtype == torch.float16 else 1)
+    np.testing.assert_array_equal(bits(out), expected)
+
+
+def test_config1_decode_bitexact(backend, device):
+    # W ~ N(0, 0.02) [4096, 4096] seed 0, x ~ N(0, 1) [1, 4096].
+    w = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(0)) * 0.02
+    weight = Q8RowSplitWeight.from_dense(w.half())
+    x = torch.randn(1, 4096, generator=torch.Generator().manual_seed(1)).half()
+    resident = backend.upload_linear(weight, dtype=torch.float16, device=device)
+    out = torch.empty(1, 4096, dtype=torch.float16, device=device)
+    resident.prepare(tokens=1, route="exact").run(x.to(device), out=out)
+    expected = oracle.q8_linear(bits(x), weight.codes.numpy(), weight.scales.numpy(), 4096)
+    np.testing.assert_array_equal(bits(out), expected)
+    # FP64 closed form: the fp32 result rounds within one fp16 ulp of the exact value.
+    exact = x.double() @ weight.dequantize_reference().T
+    err = (out.cpu().double() - exact).abs()
+    ulp = torch.finfo(torch.float16).eps * exact.abs().clamp_min(2**-14)
+    assert bool((err <= ulp).all())
+
+
+@pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
+@pytest.mark.parametrize("tokens", [1, 4, 8, 16])
+def test_config2_shapes_sampled_rows(backend, device, n, k, tokens):
+    # Full-size launch; the oracle checks a seeded sample of 256 rows.
+    print(f"case q8-config2 n={n} k={k} tokens={tokens}", flush=True)
+    gen = torch.Generator(device=device).manual_seed(n + k)
+    w = torch.randn(n, k, generator=gen, device=device) * 0.02
+    codes, scales = oracle.q8_pack(w.cpu().numpy())
+    del w
+    weight = Q8RowSplitWeight(torch.from_numpy(codes), torch.from_numpy(scales), k)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens)).half()
+    resident = backend.upload_linear(weight, dtype=torch.float16, device=device)
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    resident.prepare(tokens=tokens, route="exact").run(x.to(device), out=out)
+    rows = np.sort(np.random.default_rng(n).choice(n, 256, replace=False))
+    expected = oracle.q8_linear(bits(x), codes[rows], scales[rows], k)
+    np.testing.assert_array_equal(bits(out)[:, rows], expected)
+
+
+def test_impulse_last_column_and_nonfinite(backend, device):
+    # Impulse at the last valid column (test_quantlinear_cuda.py:17-49 pattern).
+    for k in (255, 257, 511, 512):
+        n = 19
+        padded = (k + 127) // 128 * 128
+        codes = torch.zeros(n, padded, dtype=torch.int8)
+        codes[:, k - 1] = 1
+        scales = torch.ones(n, padded // 32, dtype=torch.float16)
+        resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, k), dtype=torch.float16, device=device)
+        x = torch.zeros(4, k, dtype=torch.float16, device=device)
+        x[:, -1] = 1
+        out = torch.full((4, n), float("nan"), dtype=torch.float16, device=device)
+        resident.prepare(tokens=4, route="exact").run(x, out=out)
+        assert torch.equal(out.cpu(), torch.ones(4, n, dtype=torch.float16))
+        x[0, 0] = float("inf")
+        resident.prepare(tokens=4, route="exact").run(x, out=out)
+        assert not torch.isfinite(out[0]).any() or bool(torch.isnan(out[0]).all())
+
+
+def test_embedding_matches_decode(backend, device):
+    codes, scales = random_q8(31, 65, 18)
+    weight = Q8RowSplitWeight(codes, scales, 65)
+    for dtype in (torch.float16, torch.bfloat16):
+        resident = backend.upload_linear(weight, dtype=dtype, device=device)
+        lookup = resident.prepare_embedding([1, 30, 0])
+        out = torch.empty(3, 65, dtype=dtype, device=device)
+        lookup.run(out=out)
+        expected = (codes.float() * scales.float().repeat_interleave(32, -1))[[1, 30, 0], :65].to(dtype)
+        assert torch.equal(out.cpu(), expected)

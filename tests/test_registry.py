@@ -1,0 +1,81 @@
+"""Codec registry geometry and byte accounting (quantization/layout.py, codecs.py)."""
+
+import pytest
+import torch
+
+from venturi_amd.quantization import (
+    CODECS,
+    EXECUTION_QUALIFIED,
+    GFX950,
+    ROW_FORMATS,
+    codec_for,
+    dequantize_planes,
+    row_geometry,
+    row_payload_bytes,
+    validate_reported_plan,
+)
+
+
+def test_formats_and_codecs():
+    assert ROW_FORMATS == {"q4_g64_fp16": (4, 64), "q5_g64_fp16": (5, 64), "q6_g64_fp16": (6, 64), "q8_g32_fp16": (8, 32)}
+    q8 = codec_for("q8_g32_fp16")
+    assert q8.quantized and q8.layout == "row_split_k128_v1" and q8.forbidden_codes == (-128,)
+    assert not codec_for("fp16").quantized and codec_for("fp16").dense
+    assert set(CODECS) == set(ROW_FORMATS) | {"fp16", "bf16", "fp32"}
+    assert EXECUTION_QUALIFIED[GFX950] == {"q8_g32_fp16", "q4_g64_fp16"}
+    with pytest.raises(ValueError, match="Unknown weight format"):
+        codec_for("q3")
+
+
+def test_byte_counts_at_baseline_shapes():
+    # Config 1: 16 777 216 B codes + 1 048 576 B scales.
+    assert row_geometry((4096, 4096), "q8_g32_fp16") == (8, 32, 128, 16777216, 16777216, 17825792)
+    assert codec_for("q8_g32_fp16").upload_bytes(4096, 4096) == 17825792
+    assert row_payload_bytes((4096, 4096), "q8_g32_fp16") == 17825792
+    # Config 2 layer: QKV, o, gate+up, down.
+    shapes = [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)]
+    assert sum(codec_for("q8_g32_fp16").upload_bytes(n, k) for n, k in shapes) == 356515840
+    # Config 4 expert pair (gate_up [1536, 2048] + down [2048, 768]).
+    q4 = codec_for("q4_g64_fp16")
+    assert q4.upload_bytes(1536, 2048) + q4.upload_bytes(2048, 768) == 2506752
+    # Padding: K=65 pads to 128.
+    assert codec_for("q8_g32_fp16").encoded_bytes(3, 65) == 3 * (128 + 8)
+
+
+@pytest.mark.parametrize("fmt,bits", [("q4_g64_fp16", 4), ("q5_g64_fp16", 5), ("q6_g64_fp16", 6)])
+def test_all_signed_codes_and_high_bit_positions(fmt, bits):
+    # Known-answer pattern of the reference (test_codec_loading.py:88-113).
+    values = [(i % (1 << bits)) - (1 << (bits - 1)) for i in range(128)]
+    codes = torch.zeros((1, 64), dtype=torch.uint8)
+    high = torch.zeros((1, 16 * (bits - 4)), dtype=torch.uint8) if bits > 4 else None
+    for group in range(2):
+        for lane in range(64):
+            unsigned = values[group * 64 + lane] % (1 << bits)
+            codes[0, group * 32 + lane // 2] |= (unsigned & 15) << (4 * (lane % 2))
+            if high is not None:
+                hb = bits - 4
+                high[0, group * 8 * hb + lane * hb // 8] |= (unsigned >> 4) << (lane * hb % 8)
+    scales = torch.tensor([[0.125, 0.25]], dtype=torch.float16)
+    actual = dequantize_planes(codes, scales, high, (1, 117), fmt)
+    expected = torch.tensor([[v * (0.125 if i < 64 else 0.25) for i, v in enumerate(values[:117])]], dtype=torch.float16)
+    assert torch.equal(actual, expected)
+
+
+def test_dequantize_rejects_invalid_planes():
+    codes = torch.zeros((1, 128), dtype=torch.int8)
+    codes[0, 5] = -128
+    with pytest.raises(ValueError, match="Forbidden"):
+        dequantize_planes(codes, torch.ones(1, 4, dtype=torch.float16), None, (1, 128), "q8_g32_fp16")
+    with pytest.raises(ValueError, match="scale"):
+        dequantize_planes(torch.zeros((1, 128), dtype=torch.int8), -torch.ones(1, 4, dtype=torch.float16), None,
+                          (1, 128), "q8_g32_fp16")
+
+
+def test_reported_plan_binding():
+    assert validate_reported_plan("q8_g32_fp16", "fp16", GFX950, [8, 32, 0, 0, 0, 0]) == "direct"
+    assert validate_reported_plan("q8_g32_fp16", "int8", GFX950, [8, 32, 1, 2, 0, 0]) == "activation-int8"
+    assert validate_reported_plan("q4_g64_fp16", "fp16", GFX950, [4, 64, 0, 1, 0, 0]) == "chunked-dense"
+    with pytest.raises(RuntimeError):
+        validate_reported_plan("q8_g32_fp16", "fp16", GFX950, [8, 32, 1, 0, 0, 0])
+    with pytest.raises(ValueError):
+        validate_reported_plan("q4_g64_fp16", "fp16", GFX950, [4, 64, 0, 0, 0, 0])

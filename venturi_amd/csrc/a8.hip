@@ -1,0 +1,388 @@
+// A8 activation path: per-32-group int8 activation quantization (one or two
+// residual passes), RMSNorm, RMSNorm fused with quantization, and the W8A8
+// decode projection in the reference's accumulation order.
+//
+// Workspace layout (q8_dp4a.cuh:7-13, 72-76): with G = ceil(k/32) groups and
+// count = tokens*G, int8 codes [pass][token][group][32] are followed directly
+// by fp32 scales [pass][token][group]; total count*36*passes bytes.
+#include "common.hpp"
+
+namespace vt {
+
+std::uint64_t a8_bytes(int tokens, int k, int passes) {
+    // Same admission as q8_dp4a.cuh:7-13.
+    require(tokens > 0 && tokens <= 262140 && k > 0 && k <= INT32_MAX - 1024 && (passes == 1 || passes == 2),
+            "invalid A8 geometry/profile");
+    const std::uint64_t groups = (static_cast<std::uint64_t>(k) + 31) / 32;
+    const std::uint64_t n = static_cast<std::uint64_t>(tokens) * groups;
+    require(n <= INT32_MAX / 32, "A8 activation workspace exceeds int32");
+    return n * 36 * passes;
+}
+
+namespace {
+
+// Quantization of one 32-value group (q8_dp4a.cuh:15-34). GL adjacent lanes
+// hold NV values each (NV*GL == 32). The group max is order independent; the
+// scale and inverse are IEEE f32 divisions, the code is the RNE f32 product
+// rounded half-to-even and clamped to +-127, and the residual update is one
+// fused multiply-add, exactly as the reference. A group with any non-finite
+// input stores zero codes and a NaN scale for every pass.
+template <int NV, int GL>
+__device__ __forceinline__ void quantize_group(float (&r)[NV], bool bad_local, int passes,
+                                               std::int8_t* codes_out, float* scale_out,
+                                               std::int64_t code_pass_stride,
+                                               std::int64_t scale_pass_stride, bool leader) {
+    static_assert(NV * GL == 32, "a group is 32 values");
+    int bad = bad_local ? 1 : 0;
+#pragma unroll
+    for (int m = 1; m < GL; m <<= 1) bad |= __shfl_xor(bad, m, 64);
+    const bool invalid = bad != 0;
+    for (int p = 0; p < passes; ++p) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) mx = fmaxf(mx, fabsf(r[v]));
+#pragma unroll
+        for (int m = 1; m < GL; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+        const float scale = __fdiv_rn(mx, 127.0f);
+        const float inverse = mx > 0.0f ? __fdiv_rn(127.0f, mx) : 0.0f;
+        std::uint32_t word[NV / 4];
+#pragma unroll
+        for (int i = 0; i < NV / 4; ++i) word[i] = 0u;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            int code = 0;
+            if (!invalid) {
+                const float scaled = rintf(__fmul_rn(r[v], inverse));
+                code = static_cast<int>(fminf(fmaxf(scaled, -127.0f), 127.0f));
+            }
+            word[v / 4] |= static_cast<std::uint32_t>(code & 0xff) << (8 * (v % 4));
+            r[v] = __fmaf_rn(-static_cast<float>(code), scale, r[v]);
+        }
+        std::int8_t* dst = codes_out + p * code_pass_stride;
+        if constexpr (NV == 4) {
+            *reinterpret_cast<std::uint32_t*>(dst) = word[0];
+        } else {
+            static_assert(NV == 8, "4 or 8 values per lane");
+            *reinterpret_cast<uint2*>(dst) = make_uint2(word[0], word[1]);
+        }
+        if (leader) scale_out[p * scale_pass_stride] = invalid ? __builtin_nanf("") : scale;
+    }
+}
+
+// Plain quantizer: 4 lanes per group, 8 consecutive values per lane.
+__global__ __launch_bounds__(256) void a8_quantize(const __half* __restrict__ x, std::int8_t* codes,
+                                                   float* scales, int tokens, int k, int groups,
+                                                   int passes, bool vec) {
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    const std::int64_t index = (static_cast<std::int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 2;
+    const int sub = threadIdx.x & 3;
+    if (index >= count) return;  // the 4 lanes of a group exit together
+    const int token = static_cast<int>(index / groups);
+    const int g = static_cast<int>(index % groups);
+    const int col = g * 32 + sub * 8;
+    const __half* src = x + static_cast<std::int64_t>(token) * k;
+    float r[8];
+    if (vec && col + 7 < k) {
+        const uint4 w = *reinterpret_cast<const uint4*>(src + col);
+        r[0] = half_lo(w.x); r[1] = half_hi(w.x); r[2] = half_lo(w.y); r[3] = half_hi(w.y);
+        r[4] = half_lo(w.z); r[5] = half_hi(w.z); r[6] = half_lo(w.w); r[7] = half_hi(w.w);
+    } else {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) r[v] = col + v < k ? __half2float(src[col + v]) : 0.0f;
+    }
+    bool bad = false;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) bad |= !isfinite(r[v]);
+    quantize_group<8, 4>(r, bad, passes, codes + index * 32 + sub * 8, scales + index, count * 32, count,
+                         sub == 0);
+}
+
+// RMS statistics of one row in the reference order (blocks.cu:31-54): 256
+// sequential fmaf(v, v, s) chains over columns j, j+256, ..., then the
+// two-level tree; inv = 1/sqrt(sum/k + eps) with IEEE division and square
+// root. (The reference uses rsqrtf, an approximation its tests pin only by
+// tolerance; this library fixes the correctly rounded form.)
+template <class T>
+__device__ __forceinline__ float row_inverse_rms(const T* src, int k, float epsilon, int lane) {
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int base = 0; base < k; base += 256) {
+        const int col = base + 4 * lane;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            if (col + v < k) {
+                const float x = to_f32(src[col + v]);
+                a[v] = fmaf(x, x, a[v]);
+            }
+    }
+    const float sum = __shfl(canonical_sum(a[0], a[1], a[2], a[3]), 0, 64);
+    return __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(sum, static_cast<float>(k)) + epsilon));
+}
+
+// One wave per row; the normalised value is ((x * inv) * gamma) rounded once.
+template <class T>
+__global__ __launch_bounds__(256) void rms_norm(const T* __restrict__ x, const float* __restrict__ w,
+                                                T* __restrict__ out, int tokens, int k, float epsilon) {
+    const int lane = threadIdx.x & 63;
+    const int token = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (token >= tokens) return;
+    const T* src = x + static_cast<std::int64_t>(token) * k;
+    T* dst = out + static_cast<std::int64_t>(token) * k;
+    const float inv = row_inverse_rms(src, k, epsilon, lane);
+    for (int col = lane; col < k; col += 64) dst[col] = from_f32<T>((to_f32(src[col]) * inv) * w[col]);
+}
+
+// RMSNorm fused with A8 quantization (q8_rms_producer.cuh:8-53 for two
+// passes): the quantizer sees exactly the fp16-rounded normalised values.
+// One wave per token; 8 lanes x 4 values form each group of 32.
+__global__ __launch_bounds__(256) void rms_a8(const __half* __restrict__ x, const float* __restrict__ w,
+                                              std::int8_t* codes, float* scales, __half* intermediate,
+                                              int tokens, int k, int groups, int passes, float epsilon) {
+    const int lane = threadIdx.x & 63;
+    const int token = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (token >= tokens) return;
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    const __half* src = x + static_cast<std::int64_t>(token) * k;
+    const float inv = row_inverse_rms(src, k, epsilon, lane);
+    for (int base = 0; base < groups * 32; base += 256) {
+        const int col = base + 4 * lane;
+        const int g = col >> 5;
+        float r[4];
+        bool bad = false;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            r[v] = 0.0f;
+            if (col + v < k) {
+                const __half y = from_f32<__half>((__half2float(src[col + v]) * inv) * w[col + v]);
+                if (intermediate) intermediate[static_cast<std::int64_t>(token) * k + col + v] = y;
+                r[v] = __half2float(y);
+            }
+            bad |= !isfinite(r[v]);
+        }
+        const std::int64_t index = static_cast<std::int64_t>(token) * groups + min(g, groups - 1);
+        // The 8 lanes of a group share g, so skipping whole groups keeps every
+        // cross-lane exchange inside active lanes.
+        if (g < groups)
+            quantize_group<4, 8>(r, bad, passes, codes + index * 32 + (col & 31), scales + index, count * 32,
+                                 count, (lane & 7) == 0);
+    }
+}
+
+// W8A8 projection in the reference order (q8_dp4a.cuh:36-70). One reference
+// warp = one half-wave: lane l owns groups l, l+32, ... (< ceil(k/32));
+// per group the int8 dot d is exact; sum = fmaf(f32(d), ws*as, sum) over
+// passes in order; a 32-lane shfl_down tree; RNE cast to fp16. Each half-wave
+// handles RR rows and TT tokens so activation words are reused RR times.
+template <int TT, int RR, int P>
+__global__ __launch_bounds__(256) void a8_gemv(const std::int8_t* __restrict__ acodes,
+                                               const float* __restrict__ ascales,
+                                               const std::int8_t* __restrict__ wcodes,
+                                               const __half* __restrict__ wscales, __half* __restrict__ out,
+                                               int tokens, int n, int k, int padded, int groups) {
+    const int lane = threadIdx.x & 31;
+    const int half = (threadIdx.x >> 5) & 1;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row0 = (wave * 2 + half) * RR;
+    const int t0 = blockIdx.y * TT;
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    float sum[TT][RR];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int r = 0; r < RR; ++r) sum[t][r] = 0.0f;
+    if (row0 < n) {
+        for (int g = lane; g < groups; g += 32) {
+            uint4 w0[RR], w1[RR];
+            float ws[RR];
+#pragma unroll
+            for (int r = 0; r < RR; ++r) {
+                const std::int64_t row = min(row0 + r, n - 1);
+                const uint4* wp = reinterpret_cast<const uint4*>(wcodes + row * padded + g * 32);
+                w0[r] = wp[0];
+                w1[r] = wp[1];
+                ws[r] = __half2float(wscales[row * (padded / 32) + g]);
+            }
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                if (t0 + t >= tokens) break;
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const std::int64_t gi = p * count + static_cast<std::int64_t>(t0 + t) * groups + g;
+                    const uint4* ap = reinterpret_cast<const uint4*>(acodes + gi * 32);
+                    const uint4 a0 = ap[0], a1 = ap[1];
+                    const float as = ascales[gi];
+#pragma unroll
+                    for (int r = 0; r < RR; ++r) {
+                        int d = __builtin_amdgcn_sdot4(static_cast<int>(w0[r].x), static_cast<int>(a0.x), 0, false);
+                        d = __builtin_amdgcn_sdot4(static_cast<int>(w0[r].y), static_cast<int>(a0.y), d, false);
+                        d = __builtin_amdgcn_sdot4(static_cast<int>(w0[r].z), static_cast<int>(a0.z), d, false);
+                        d = __builtin_amdgcn_sdot4(static_cast<int>(w0[r].w), static_cast<int>(a0.w), d, false);
+                        d = __builtin_amdgcn_sdot4(static_cast<int>(w1[r].x), static_cast<int>(a1.x), d, false);
+                        d = __builtin_amdgcn_sdot4(static_cast<int>(w1[r].y), static_cast<int>(a1.y), d, false);
+                        d = __builtin_amdgcn_sdot4(static_cast<int>(w1[r].z), static_cast<int>(a1.z), d, false);
+                        d = __builtin_amdgcn_sdot4(static_cast<int>(w1[r].w), static_cast<int>(a1.w), d, false);
+                        sum[t][r] = __fmaf_rn(static_cast<float>(d), __fmul_rn(ws[r], as), sum[t][r]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int r = 0; r < RR; ++r) {
+            const float y = warp32_sum(sum[t][r]);
+            if (lane == 0 && row0 + r < n && t0 + t < tokens)
+                out[static_cast<std::int64_t>(t0 + t) * n + row0 + r] = from_f32<__half>(y);
+        }
+}
+
+template <int TT, int RR, int P>
+void launch_a8_gemv(const std::int8_t* acodes, const float* ascales, const std::int8_t* codes,
+                    const __half* scales, __half* out, int tokens, int n, int k, int padded, int groups,
+                    hipStream_t stream) {
+    const dim3 grid((n + 8 * RR - 1) / (8 * RR), (tokens + TT - 1) / TT);
+    require(grid.y <= 65535, "token tiles exceed the launch grid");
+    a8_gemv<TT, RR, P><<<grid, 256, 0, stream>>>(acodes, ascales, codes, scales, out, tokens, n, k, padded, groups);
+}
+
+template <int P>
+void dispatch_a8_gemv(const std::int8_t* acodes, const float* ascales, const std::int8_t* codes,
+                      const __half* scales, __half* out, int tokens, int n, int k, int padded, int groups,
+                      hipStream_t stream) {
+    if (tokens == 1) launch_a8_gemv<1, 2, P>(acodes, ascales, codes, scales, out, tokens, n, k, padded, groups, stream);
+    else if (tokens == 2) launch_a8_gemv<2, 2, P>(acodes, ascales, codes, scales, out, tokens, n, k, padded, groups, stream);
+    else launch_a8_gemv<4, 2, P>(acodes, ascales, codes, scales, out, tokens, n, k, padded, groups, stream);
+}
+
+bool overlap(const void* a, std::uint64_t an, const void* b, std::uint64_t bn) {
+    const auto x = reinterpret_cast<std::uintptr_t>(a), y = reinterpret_cast<std::uintptr_t>(b);
+    return x < y + bn && y < x + an;
+}
+
+}  // namespace
+
+void a8_quantize_launch(const void* x, void* workspace, std::uint64_t available, int tokens, int k, int passes,
+                        hipStream_t stream) {
+    const std::uint64_t needed = a8_bytes(tokens, k, passes);
+    require(x && workspace && available >= needed && aligned(workspace, 16) && aligned(x, 2),
+            "invalid A8 workspace/input");
+    const int groups = (k + 31) / 32;
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    auto* codes = static_cast<std::int8_t*>(workspace);
+    auto* scales = reinterpret_cast<float*>(codes + count * 32 * passes);
+    const bool vec = (k % 8 == 0) && aligned(x, 16);
+    const std::int64_t blocks = (count * 4 + 255) / 256;
+    require(blocks <= INT32_MAX, "A8 grid too large");
+    a8_quantize<<<static_cast<unsigned>(blocks), 256, 0, stream>>>(static_cast<const __half*>(x), codes, scales,
+                                                                   tokens, k, groups, passes, vec);
+}
+
+void a8_gemv_launch(const void* workspace, std::uint64_t available, const std::int8_t* codes, const __half* scales,
+                    void* out, int tokens, int n, int k, int padded, int passes, hipStream_t stream) {
+    const std::uint64_t needed = a8_bytes(tokens, k, passes);
+    require(workspace && available >= needed && codes && scales && out && n > 0 && n <= INT32_MAX - 3 &&
+                padded == padded_k(k) && static_cast<std::uint64_t>(tokens) * n < INT32_MAX &&
+                aligned(workspace, 16) && aligned(codes, 16) && aligned(scales, 2) && aligned(out, 2),
+            "invalid A8 projection geometry/buffers");
+    const int groups = (k + 31) / 32;
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    const auto* acodes = static_cast<const std::int8_t*>(workspace);
+    const auto* ascales = reinterpret_cast<const float*>(acodes + count * 32 * passes);
+    auto* y = static_cast<__half*>(out);
+    if (passes == 1) dispatch_a8_gemv<1>(acodes, ascales, codes, scales, y, tokens, n, k, padded, groups, stream);
+    else dispatch_a8_gemv<2>(acodes, ascales, codes, scales, y, tokens, n, k, padded, groups, stream);
+}
+
+void rms_launch(const void* x, const float* w, void* out, int tokens, int k, int dtype, float epsilon,
+                hipStream_t stream) {
+    require(x && w && out && tokens > 0 && k > 0, "invalid RMSNorm operand");
+    require(epsilon > 0.0f && std::isfinite(epsilon), "invalid RMSNorm epsilon");
+    const dim3 grid((tokens + 3) / 4);
+    if (dtype == kF16)
+        rms_norm<<<grid, 256, 0, stream>>>(static_cast<const __half*>(x), w, static_cast<__half*>(out), tokens, k, epsilon);
+    else if (dtype == kBF16)
+        rms_norm<<<grid, 256, 0, stream>>>(static_cast<const __hip_bfloat16*>(x), w,
+                                           static_cast<__hip_bfloat16*>(out), tokens, k, epsilon);
+    else if (dtype == kF32)
+        rms_norm<<<grid, 256, 0, stream>>>(static_cast<const float*>(x), w, static_cast<float*>(out), tokens, k, epsilon);
+    else
+        throw Invalid("unsupported scalar type");
+}
+
+void rms_a8_launch(const void* x, const float* w, void* workspace, std::uint64_t available, int tokens, int k,
+                   float epsilon, int passes, void* intermediate, hipStream_t stream) {
+    const std::uint64_t needed = a8_bytes(tokens, k, passes);
+    const std::uint64_t xb = static_cast<std::uint64_t>(tokens) * k * 2, wb = static_cast<std::uint64_t>(k) * 4;
+    require(x && w && workspace && available >= needed && epsilon > 0.0f && std::isfinite(epsilon) &&
+                aligned(x, 2) && aligned(w, 4) && aligned(workspace, 16) && aligned(intermediate, 2) &&
+                !overlap(workspace, needed, x, xb) && !overlap(workspace, needed, w, wb) &&
+                (!intermediate || (!overlap(intermediate, xb, x, xb) && !overlap(intermediate, xb, w, wb) &&
+                                   !overlap(intermediate, xb, workspace, needed))),
+            "invalid RMS/A8 operands");
+    const int groups = (k + 31) / 32;
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    auto* codes = static_cast<std::int8_t*>(workspace);
+    auto* scales = reinterpret_cast<float*>(codes + count * 32 * passes);
+    rms_a8<<<(tokens + 3) / 4, 256, 0, stream>>>(static_cast<const __half*>(x), w, codes, scales,
+                                                 static_cast<__half*>(intermediate), tokens, k, groups, passes,
+                                                 epsilon);
+}
+
+}  // namespace vt
+
+#define VT_EXPORT extern "C" __attribute__((visibility("default")))
+
+// Reference: q8_dp4a.cuh:90-92. Returns 0 on invalid geometry.
+VT_EXPORT std::uint64_t venturi_q8_dp4a_bytes(int tokens, int k, int passes) {
+    std::uint64_t result = 0;
+    if (vt::guarded([&] { result = vt::a8_bytes(tokens, k, passes); }) != 0) return 0;
+    return result;
+}
+
+// Reference: q8_dp4a.cuh:93-101.
+VT_EXPORT int venturi_q8_dp4a_quantize(const void* x, void* workspace, std::uint64_t available, int tokens, int k,
+                                       int passes, void* stream) {
+    return vt::guarded([&] {
+        vt::a8_quantize_launch(x, workspace, available, tokens, k, passes, static_cast<hipStream_t>(stream));
+    });
+}
+
+// Reference: q8_dp4a.cuh:102-109.
+VT_EXPORT int venturi_q8_dp4a_run(const void* workspace, std::uint64_t available, const std::int8_t* codes,
+                                  const __half* scales, void* out, int tokens, int n, int k, int padded, int passes,
+                                  void* stream) {
+    return vt::guarded([&] {
+        vt::a8_gemv_launch(workspace, available, codes, scales, out, tokens, n, k, padded, passes,
+                           static_cast<hipStream_t>(stream));
+    });
+}
+
+// Reference: blocks.cu:727-740.
+VT_EXPORT int venturi_rms_run(const void* x, const float* w, void* out, int tokens, int features, int dtype,
+                              float epsilon, void* stream) {
+    return vt::guarded([&] {
+        vt::rms_launch(x, w, out, tokens, features, dtype, epsilon, static_cast<hipStream_t>(stream));
+    });
+}
+
+// Reference: q8_rms_producer.cuh:67-84 (two passes; `chunk` is validated
+// for ABI compatibility and does not change the bytes produced).
+VT_EXPORT int venturi_rms_q8_quantize(const void* x, const float* w, void* workspace, std::uint64_t available,
+                                      int tokens, int k, float epsilon, int chunk, void* intermediate,
+                                      void* stream) {
+    return vt::guarded([&] {
+        vt::require(chunk == 8 || chunk == 32 || chunk == 128, "invalid RMS/A8 chunk");
+        vt::rms_a8_launch(x, w, workspace, available, tokens, k, epsilon, 2, intermediate,
+                          static_cast<hipStream_t>(stream));
+    });
+}
+
+// Extension: the same fused producer with an explicit pass count (1 or 2).
+VT_EXPORT int venturi_rms_q8_quantize_passes(const void* x, const float* w, void* workspace,
+                                             std::uint64_t available, int tokens, int k, float epsilon, int passes,
+                                             void* intermediate, void* stream) {
+    return vt::guarded([&] {
+        vt::rms_a8_launch(x, w, workspace, available, tokens, k, epsilon, passes, intermediate,
+                          static_cast<hipStream_t>(stream));
+    });
+}

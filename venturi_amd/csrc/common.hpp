@@ -1,0 +1,137 @@
+// Shared host/device helpers for the gfx950 quantized-linear library.
+//
+// Every exported entry point follows one contract: validate geometry and
+// pointers on the host, launch on the caller's stream, return 0 on success or
+// -1 with a per-thread message readable through venturi_blocks_error().
+// Nothing here allocates device memory or synchronises.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace vt {
+
+// Per-thread error text (defined once in api.cpp).
+void set_error(const char* text);
+void clear_error();
+
+struct Invalid : std::invalid_argument {
+    using std::invalid_argument::invalid_argument;
+};
+
+inline void require(bool ok, const char* message) {
+    if (!ok) throw Invalid(message);
+}
+
+inline void check(hipError_t status) {
+    if (status != hipSuccess) throw std::runtime_error(hipGetErrorString(status));
+}
+
+inline bool aligned(const void* p, std::uintptr_t bytes) {
+    return (reinterpret_cast<std::uintptr_t>(p) % bytes) == 0;
+}
+
+inline std::int64_t padded_k(std::int64_t k) { return (k + 127) / 128 * 128; }
+
+// Runs `body`, mapping exceptions to the -1 / message convention.
+template <class F>
+int guarded(F&& body) {
+    try {
+        clear_error();
+        body();
+        check(hipGetLastError());
+        return 0;
+    } catch (const std::exception& e) {
+        set_error(e.what());
+        return -1;
+    }
+}
+
+// Activation scalar types selected by the reference's dtype codes
+// (0 = fp16, 1 = bf16, 2 = fp32).
+enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
+
+__device__ __forceinline__ float to_f32(__half v) { return __half2float(v); }
+__device__ __forceinline__ float to_f32(__hip_bfloat16 v) { return __bfloat162float(v); }
+__device__ __forceinline__ float to_f32(float v) { return v; }
+
+// The reference rounds every result to fp32 first and then to the 16-bit
+// output type (two roundings). Without a barrier LLVM folds fp16(a*b) or
+// fp16(a+b) into v_fma_mixlo_f16, which rounds once, straight to fp16, and
+// differs in rare double-rounding cases; the empty asm pins the fp32 value.
+__device__ __forceinline__ float f32_pin(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+template <class T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ __half from_f32<__half>(float v) { return __float2half_rn(f32_pin(v)); }
+template <> __device__ __forceinline__ __hip_bfloat16 from_f32<__hip_bfloat16>(float v) {
+    return __float2bfloat16(f32_pin(v));  // round-to-nearest-even
+}
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+
+// Bit-level fp16 decode of the low/high half of a 32-bit word.
+__device__ __forceinline__ float half_lo(std::uint32_t w) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(w & 0xffffu)));
+}
+__device__ __forceinline__ float half_hi(std::uint32_t w) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(w >> 16)));
+}
+__device__ __forceinline__ float bf16_lo(std::uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(std::uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Sign-extending byte extraction from a packed int8x4 word.
+__device__ __forceinline__ float sbyte(std::uint32_t w, int i) {
+    return static_cast<float>(static_cast<std::int8_t>(w >> (8 * i)));
+}
+
+// Correctly rounded square root. hipcc lowers __builtin_sqrtf for gfx950 to
+// v_sqrt_f32 followed by an exact neighbour correction (checked bit-for-bit
+// against IEEE sqrt on 16.8M random normal inputs); __fsqrt_rn does not
+// correct and is up to one ulp off, so it is not used.
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+
+// Cross-lane read of `v` from lane (lane + delta) within a 64-lane wave.
+__device__ __forceinline__ float lane_down(float v, int delta) {
+    return __shfl_down(v, delta, 64);
+}
+
+// The reference's 256-thread reduction (cuda_common.cuh:38-51, block_sum)
+// applied to 256 "virtual threads" held four per lane: lane L holds the
+// partials of threads 4L..4L+3 in a0..a3. Threads 32w..32w+31 (lanes
+// 8w..8w+7) are first summed by the shfl_down 16/8/4/2/1 tree over
+// t = 4*(lane%8) + v, i.e. lane offsets +4, +2, +1 and then register pairs
+// (+2, +1). The eight group sums are then reduced by the same tree run over
+// 32 lanes of which only 0..7 are nonzero: the +16 and +8 steps add exact
+// zeros, the +4/+2/+1 steps pair group sums (lane offsets 32, 16, 8 here).
+// The result is valid in lane 0.
+__device__ __forceinline__ float canonical_sum(float a0, float a1, float a2, float a3) {
+    a0 += lane_down(a0, 4); a1 += lane_down(a1, 4); a2 += lane_down(a2, 4); a3 += lane_down(a3, 4);
+    a0 += lane_down(a0, 2); a1 += lane_down(a1, 2); a2 += lane_down(a2, 2); a3 += lane_down(a3, 2);
+    a0 += lane_down(a0, 1); a1 += lane_down(a1, 1); a2 += lane_down(a2, 1); a3 += lane_down(a3, 1);
+    float p = (a0 + a2) + (a1 + a3);
+    p = (p + 0.0f) + 0.0f;
+    p += lane_down(p, 32);
+    p += lane_down(p, 16);
+    p += lane_down(p, 8);
+    return p;
+}
+
+// 32-lane shfl_down 16/8/4/2/1 tree (one reference warp per half-wave);
+// valid in lanes 0 and 32.
+__device__ __forceinline__ float warp32_sum(float v) {
+    v += __shfl_down(v, 16, 32);
+    v += __shfl_down(v, 8, 32);
+    v += __shfl_down(v, 4, 32);
+    v += __shfl_down(v, 2, 32);
+    v += __shfl_down(v, 1, 32);
+    return v;
+}
+
+}  // namespace vt

@@ -1,0 +1,80 @@
+"""ctypes binding of libventuri_ops.so, the gfx950 C-ABI library.
+
+The library is built in-tree (``venturi_amd/_lib``) by ``__graft_entry__.build``
+or ``make -C venturi_amd/csrc``. Loading fails loudly when it is missing: no
+operator in this package has a CPU or PyTorch substitute.
+"""
+
+import ctypes as C
+import os
+from pathlib import Path
+import threading
+
+ABI_VERSION = 18
+ARCH_TAG = 950
+
+DEFAULT_LIBRARY = Path(__file__).resolve().parent / "_lib" / "libventuri_ops.so"
+
+_P = C.c_void_p
+_I = C.c_int
+_U64 = C.c_uint64
+_F = C.c_float
+
+# name -> (argtypes, restype); signatures match include/venturi_ops.h.
+SIGNATURES = {
+    "venturi_blocks_abi": ([], _I),
+    "venturi_blocks_arch": ([], _I),
+    "venturi_blocks_error": ([], C.c_char_p),
+    "venturi_q8_head_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
+    "venturi_q8_embedding_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
+    "venturi_q8_dp4a_bytes": ([_I] * 3, _U64),
+    "venturi_q8_dp4a_quantize": ([_P, _P, _U64] + [_I] * 3 + [_P], _I),
+    "venturi_q8_dp4a_run": ([_P, _U64] + [_P] * 3 + [_I] * 5 + [_P], _I),
+    "venturi_rms_run": ([_P] * 3 + [_I] * 3 + [_F, _P], _I),
+    "venturi_rms_q8_quantize": ([_P] * 3 + [_U64, _I, _I, _F, _I, _P, _P], _I),
+    "venturi_rms_q8_quantize_passes": ([_P] * 3 + [_U64, _I, _I, _F, _I, _P, _P], _I),
+}
+
+_lock = threading.Lock()
+_loaded = {}
+
+
+class NativeLibrary:
+    """One loaded library with typed entry points and the error channel."""
+
+    def __init__(self, path):
+        self.path = Path(path).expanduser().resolve()
+        if not self.path.is_file():
+            raise FileNotFoundError(
+                f"{self.path} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `make -C venturi_amd/csrc` (there is no CPU fallback)"
+            )
+        self.handle = C.CDLL(str(self.path))
+        for name, (args, result) in SIGNATURES.items():
+            try:
+                function = getattr(self.handle, name)
+            except AttributeError as error:
+                raise RuntimeError(f"{self.path} lacks export {name}; rebuild the library") from error
+            function.argtypes, function.restype = args, result
+            setattr(self, name, function)
+        if self.venturi_blocks_abi() != ABI_VERSION:
+            raise RuntimeError("Venturi blocks ABI mismatch; rebuild explicitly")
+        if self.venturi_blocks_arch() != ARCH_TAG:
+            raise RuntimeError("Library is not built for gfx950")
+
+    def error(self):
+        return self.venturi_blocks_error().decode("utf-8", "replace")
+
+    def check(self, status):
+        if status < 0:
+            raise RuntimeError(self.error())
+        return status
+
+
+def load(path=None):
+    """Loads (once per path) the in-tree library or an explicit one."""
+    target = Path(path or os.environ.get("VENTURI_OPS_LIBRARY") or DEFAULT_LIBRARY).expanduser().resolve()
+    with _lock:
+        if target not in _loaded:
+            _loaded[target] = NativeLibrary(target)
+        return _loaded[target]

@@ -1,0 +1,102 @@
+"""W8A8 projection: int8 activations with fp32 group-32 scales, optional residual pass.
+
+Mirrors venturi.ops.q8_dp4a (reference q8_dp4a.py:43-114): the plan quantizes
+fp16 activations into a caller-owned workspace (``workspace_bytes`` bytes,
+16-byte aligned, layout int8 codes [pass][token][group][32] then fp32 scales
+[pass][token][group]) and projects them against the resident Q8 planes. Each
+32-column group's integer dot is exact; groups are combined in fp32 in the
+reference's order, so the fp16 outputs are byte-identical to the reference's.
+"""
+
+from dataclasses import dataclass
+
+import torch
+
+from .blocks import ResidentLinear, _no_overlap, _shape, _stream, _tensor
+from .vocabulary import ResidentQ8Vocabulary
+
+
+@dataclass(frozen=True)
+class PreparedQ8DP4A:
+    resident: ResidentQ8Vocabulary
+    tokens: int
+    passes: int
+    workspace_bytes: int
+    _native: object
+
+    @property
+    def precision_profile(self):
+        return "w8-a8-g32-f32scale" + ("-residual-a8" if self.passes == 2 else "")
+
+    @property
+    def route(self):
+        return "venturi-q8-a8"
+
+    def quantize(self, x, *, workspace):
+        """Only the activation quantization step (fills ``workspace``)."""
+        r = self.resident
+        _tensor(x, (self.tokens, r.hidden_size), torch.float16, r.device, "x")
+        _tensor(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
+        _no_overlap(workspace, (x,) + r.storage_tensors)
+        if workspace.data_ptr() % 16:
+            raise ValueError("A8 workspace requires 16-byte alignment")
+        with torch.cuda.device(r.device):
+            r.backend._check(
+                self._native.venturi_q8_dp4a_quantize(
+                    x.data_ptr(), workspace.data_ptr(), self.workspace_bytes, self.tokens, r.hidden_size,
+                    self.passes, _stream(r.device),
+                )
+            )
+        return workspace
+
+    def project(self, *, out, workspace):
+        """Only the int8 projection of an already filled workspace."""
+        r = self.resident
+        _tensor(out, (self.tokens, r.vocab_size), torch.float16, r.device, "out")
+        _tensor(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
+        _no_overlap(out, (workspace,) + r.storage_tensors)
+        if workspace.data_ptr() % 16:
+            raise ValueError("A8 workspace requires 16-byte alignment")
+        with torch.cuda.device(r.device):
+            r.backend._check(
+                self._native.venturi_q8_dp4a_run(
+                    workspace.data_ptr(), self.workspace_bytes, r._codes.data_ptr(), r._scales.data_ptr(),
+                    out.data_ptr(), self.tokens, r.vocab_size, r.hidden_size, r._codes.shape[1], self.passes,
+                    _stream(r.device),
+                )
+            )
+        return out
+
+    def run(self, x, *, out, workspace):
+        r = self.resident
+        _tensor(x, (self.tokens, r.hidden_size), torch.float16, r.device, "x")
+        _tensor(out, (self.tokens, r.vocab_size), torch.float16, r.device, "out")
+        _tensor(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
+        _no_overlap(out, (x, workspace) + r.storage_tensors)
+        _no_overlap(workspace, (x,) + r.storage_tensors)
+        if workspace.data_ptr() % 16:
+            raise ValueError("A8 workspace requires 16-byte alignment")
+        self.quantize(x, workspace=workspace)
+        return self.project(out=out, workspace=workspace)
+
+
+def prepare_q8_dp4a(resident, *, tokens, residual_compensation):
+    """Opt-in A8 plan; the caller owns the workspace (q8_dp4a.py:95-114)."""
+    if isinstance(resident, ResidentLinear):
+        resident = resident._payload
+    if not isinstance(resident, ResidentQ8Vocabulary):
+        raise ValueError("A8 requires resident native Q8 planes")
+    if type(residual_compensation) is not bool:
+        raise ValueError("Explicit boolean residual_compensation required")
+    _shape(tokens, resident.hidden_size)
+    if resident.dtype != torch.float16 or resident.device.type != "cuda":
+        raise ValueError("A8 profile requires GPU FP16 input/output")
+    resident.backend.validate_device(resident.dtype, resident.device)
+    if tokens * resident.vocab_size >= 2**31:
+        raise ValueError("A8 output geometry exceeds int32")
+    native = resident.backend._native
+    passes = 2 if residual_compensation else 1
+    size = native.venturi_q8_dp4a_bytes(tokens, resident.hidden_size, passes)
+    if not size:
+        resident.backend._check(-1)
+    return PreparedQ8DP4A(resident, tokens, passes, size, native)

@@ -1,0 +1,173 @@
+"""Resident Q8 row-split planes: projection (output head) and embedding lookup.
+
+Mirrors venturi.ops.vocabulary (reference vocabulary.py:23-173). A resident
+Q8 matrix keeps its int8 codes and fp16 group scales on the device and is
+never expanded to dense weights. ``prepare(tokens=...)`` selects the kernel
+family once:
+
+* ``exact``: the reference's canonical fp32 order (bytes identical to
+  ``venturi_q8_head_run`` on the reference's GPUs);
+* ``mfma``: fp16 matrix cores with per-group fp32 scaling, for larger token
+  counts (same values up to fp32 association, see ``Q8OutputHead.route``);
+* ``auto``: ``exact`` for up to 4 tokens, where it is bound by HBM anyway,
+  otherwise ``mfma`` when the library provides it.
+"""
+
+from dataclasses import dataclass
+
+import torch
+
+from .blocks import _DTYPES, Q8_ROUTES, _no_overlap, _shape, _stream, _tensor
+
+EXACT_MAX_AUTO_TOKENS = 4
+
+
+def _ids(ids, vocab):
+    if not isinstance(ids, (list, tuple)) or not ids:
+        raise ValueError("Vocabulary IDs must be a nonempty list/tuple")
+    if len(ids) >= 2**31 or any(type(i) is not int or not 0 <= i < vocab for i in ids):
+        raise ValueError("Vocabulary ID/count is out of range")
+
+
+@dataclass(frozen=True)
+class Q8VocabularyWeights:
+    codes: torch.Tensor
+    scales: torch.Tensor
+    hidden_size: int
+
+    def validate(self):
+        if type(self.hidden_size) is not int or self.hidden_size <= 0:
+            raise ValueError("Q8 hidden size must be positive")
+        if not isinstance(self.codes, torch.Tensor) or self.codes.ndim != 2:
+            raise ValueError("Q8 codes require [vocab,padded_hidden]")
+        n, padded = self.codes.shape
+        _shape(n, self.hidden_size)
+        if padded != (self.hidden_size + 127) // 128 * 128:
+            raise ValueError("Q8 hidden padding must be a multiple of 128")
+        device = self.codes.device
+        _tensor(self.codes, (n, padded), torch.int8, device, "codes")
+        _tensor(self.scales, (n, padded // 32), torch.float16, device, "scales")
+        if bool((self.codes == -128).any()):
+            raise ValueError("Q8 code -128 is outside the artifact contract")
+        if not bool(torch.isfinite(self.scales).all()) or bool((self.scales < 0).any()):
+            raise ValueError("Q8 scales must be finite and nonnegative")
+
+    def upload(self, backend, *, device="cuda:0", dtype=torch.bfloat16):
+        """Copies the planes to the device once (a same-device source is copied too)."""
+        self.validate()
+        if dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError("Q8 vocabulary supports FP16/BF16 activations")
+        target = backend.validate_device(dtype, device)
+        with torch.cuda.device(target):
+            codes, scales = (t.detach().to(target, copy=True) for t in (self.codes, self.scales))
+            torch.cuda.current_stream(target).synchronize()
+        return ResidentQ8Vocabulary(backend, codes, scales, self.hidden_size, dtype)
+
+
+@dataclass(frozen=True)
+class ResidentQ8Vocabulary:
+    backend: object
+    _codes: torch.Tensor
+    _scales: torch.Tensor
+    hidden_size: int
+    dtype: torch.dtype = torch.bfloat16
+
+    @property
+    def device(self):
+        return self._codes.device
+
+    @property
+    def vocab_size(self):
+        return self._codes.shape[0]
+
+    @property
+    def storage_tensors(self):
+        return (self._codes, self._scales)
+
+    @property
+    def storage_nbytes(self):
+        return sum(t.numel() * t.element_size() for t in self.storage_tensors)
+
+    def prepare_embedding(self, ids):
+        _ids(ids, self.vocab_size)
+        self.backend.validate_device(self.dtype, self.device)
+        indices = torch.tensor(ids, dtype=torch.int64, device=self.device)
+        torch.cuda.current_stream(self.device).synchronize()
+        return Q8Embedding(self, indices)
+
+    def prepare(self, *, tokens, route="auto"):
+        _shape(tokens, self.vocab_size)
+        if tokens * self.vocab_size >= 2**31:
+            raise ValueError("Q8 head row count must fit int32")
+        if route not in Q8_ROUTES:
+            raise ValueError(f"Q8 route must be one of {Q8_ROUTES}")
+        self.backend.validate_device(self.dtype, self.device)
+        if route == "auto":
+            mfma = hasattr(self.backend._native, "venturi_q8_gemm_run")
+            route = "exact" if tokens <= EXACT_MAX_AUTO_TOKENS or not mfma else "mfma"
+        if route == "mfma" and not hasattr(self.backend._native, "venturi_q8_gemm_run"):
+            raise RuntimeError("The loaded library has no Q8 MFMA export; rebuild it")
+        return Q8OutputHead(self, tokens, route)
+
+
+@dataclass(frozen=True)
+class Q8Embedding:
+    resident: ResidentQ8Vocabulary
+    _indices: torch.Tensor
+
+    def run(self, *, out):
+        r = self.resident
+        _tensor(out, (self._indices.numel(), r.hidden_size), r.dtype, r.device, "out")
+        _no_overlap(out, r.storage_tensors + (self._indices,))
+        with torch.cuda.device(r.device):
+            r.backend._check(
+                r.backend._native.venturi_q8_embedding_run(
+                    r._codes.data_ptr(),
+                    r._scales.data_ptr(),
+                    self._indices.data_ptr(),
+                    out.data_ptr(),
+                    self._indices.numel(),
+                    r.vocab_size,
+                    r.hidden_size,
+                    r._codes.shape[1],
+                    _DTYPES[r.dtype],
+                    _stream(r.device),
+                )
+            )
+        return out
+
+
+@dataclass(frozen=True)
+class Q8OutputHead:
+    resident: ResidentQ8Vocabulary
+    tokens: int
+    kernel: str = "exact"
+    workspace_bytes = 0
+
+    @property
+    def route(self):
+        return "venturi-q8-exact" if self.kernel == "exact" else "venturi-q8-mfma"
+
+    def run(self, x, *, out):
+        r = self.resident
+        _tensor(x, (self.tokens, r.hidden_size), r.dtype, r.device, "x")
+        _tensor(out, (self.tokens, r.vocab_size), r.dtype, r.device, "out")
+        _no_overlap(out, (x,) + r.storage_tensors)
+        lib = r.backend._native
+        entry = lib.venturi_q8_head_run if self.kernel == "exact" else lib.venturi_q8_gemm_run
+        with torch.cuda.device(r.device):
+            r.backend._check(
+                entry(
+                    x.data_ptr(),
+                    r._codes.data_ptr(),
+                    r._scales.data_ptr(),
+                    out.data_ptr(),
+                    self.tokens,
+                    r.vocab_size,
+                    r.hidden_size,
+                    r._codes.shape[1],
+                    _DTYPES[r.dtype],
+                    _stream(r.device),
+                )
+            )
+        return out
