@@ -98,3 +98,21 @@ def test_embedding_matches_decode(backend, device):
         lookup.run(out=out)
         expected = (codes.float() * scales.float().repeat_interleave(32, -1))[[1, 30, 0], :65].to(dtype)
         assert torch.equal(out.cpu(), expected)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(11, 1), (11, 31), (7, 65), (5, 129), (64, 4096)])
+def test_device_pack_matches_from_dense(backend, device, dtype, shape):
+    gen = torch.Generator().manual_seed(38 + shape[1])
+    src = (torch.randn(*shape, generator=gen) * 0.01).to(dtype)
+    src[0].zero_()
+    if shape[1] > 40:
+        src[1, 3] = 1e-30 if dtype != torch.float16 else 0  # underflowing group scale
+    got = backend.quantize_q8(src.to(device))
+    want = Q8RowSplitWeight.from_dense(src)
+    assert torch.equal(got.codes.cpu(), want.codes)
+    assert torch.equal(got.scales.cpu().view(torch.int16), want.scales.view(torch.int16))
+    with pytest.raises(ValueError):
+        bad = src.clone().to(device)
+        bad[0, 0] = float("nan")
+        backend.quantize_q8(bad)

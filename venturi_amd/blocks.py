@@ -218,6 +218,37 @@ class HipBackend(Backend):
             self, resident, resident.storage_tensors, dtype, target, weight.in_features, weight.out_features
         )
 
+    def quantize_q8(self, source):
+        """Device Q8 packing with the arithmetic of ``Q8RowSplitWeight.from_dense``.
+
+        ``source`` is a contiguous fp16/bf16/fp32 [N, K] tensor on this
+        backend's device; the result is a device-resident ``Q8RowSplitWeight``
+        whose bytes equal ``Q8RowSplitWeight.from_dense(source.cpu())``.
+        (Extension: the reference quantizes on the CPU only.)
+        """
+        if not isinstance(source, torch.Tensor) or source.ndim != 2 or not source.is_contiguous():
+            raise ValueError("Q8 packing requires a contiguous [N, K] tensor")
+        if source.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError("Device Q8 packing supports fp16/bf16/fp32 sources")
+        target = self.resolve_device(source.device)
+        n, k = source.shape
+        _shape(n, k)
+        padded = (k + 127) // 128 * 128
+        with torch.cuda.device(target):
+            if not bool(torch.isfinite(source).all()):
+                raise ValueError("Q8 source must be finite")
+            if float(source.abs().amax().float()) / 127 >= 65520:
+                raise ValueError("Q8 group scale overflows FP16")
+            codes = torch.empty(n, padded, dtype=torch.int8, device=target)
+            scales = torch.empty(n, padded // 32, dtype=torch.float16, device=target)
+            self._check(
+                self._native.venturi_q8_pack_run(
+                    source.data_ptr(), codes.data_ptr(), scales.data_ptr(), n, k, padded, _DTYPES[source.dtype],
+                    _stream(target),
+                )
+            )
+        return Q8RowSplitWeight(codes, scales, k)
+
     def bind_linear(self, resident, *, tokens, route="auto"):
         _shape(tokens, 1)
         if resident._backend is not self:

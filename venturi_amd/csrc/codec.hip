@@ -1,0 +1,72 @@
+// Row-codec packing on the device.
+//
+// Q8 (q8_g32_fp16): the arithmetic of Q8RowSplitWeight.from_dense
+// (ops/weights.py:398-439) for fp32-or-narrower sources: per 32-column group
+// of the zero-padded row, scale = fp16(f32(max|x|) / 127) (IEEE division, then
+// round-to-nearest-even); code = clamp(rint(x / f32(scale)), -127, 127), or 0
+// when the stored scale is 0. The host rejects non-finite sources and scale
+// overflow before launch, as the reference does.
+#include "common.hpp"
+
+namespace vt {
+namespace {
+
+template <class T>
+__global__ __launch_bounds__(256) void q8_pack(const T* __restrict__ src, std::int8_t* __restrict__ codes,
+                                               __half* __restrict__ scales, int n, int k, int padded) {
+    // 4 lanes per group, 8 consecutive columns per lane.
+    const int groups = padded >> 5;
+    const std::int64_t index = (static_cast<std::int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 2;
+    const int sub = threadIdx.x & 3;
+    if (index >= static_cast<std::int64_t>(n) * groups) return;  // a group's 4 lanes exit together
+    const std::int64_t row = index / groups;
+    const int col = static_cast<int>(index % groups) * 32 + sub * 8;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = col + i < k ? to_f32(src[row * k + col + i]) : 0.0f;
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    const __half stored = from_f32<__half>(__fdiv_rn(mx, 127.0f));
+    const float d = __half2float(stored);
+    std::uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        int q = 0;
+        if (d > 0.0f) q = static_cast<int>(fminf(fmaxf(rintf(__fdiv_rn(v[i], d)), -127.0f), 127.0f));
+        const std::uint32_t byte = static_cast<std::uint32_t>(q & 0xff) << (8 * (i & 3));
+        if (i < 4) lo |= byte; else hi |= byte;
+    }
+    *reinterpret_cast<uint2*>(codes + row * padded + col) = make_uint2(lo, hi);
+    if (sub == 0) scales[index] = stored;
+}
+
+}  // namespace
+}  // namespace vt
+
+// Extension (the reference packs on the CPU only): device Q8 packing of an
+// [n, k] fp16/bf16/fp32 matrix into codes [n][padded] and scales [n][padded/32].
+extern "C" __attribute__((visibility("default"))) int venturi_q8_pack_run(const void* src, std::int8_t* codes,
+                                                                         void* scales, int n, int k, int padded,
+                                                                         int dtype, void* stream) {
+    return vt::guarded([&] {
+        vt::require(src && codes && scales && n > 0 && k > 0 && padded == vt::padded_k(k), "invalid Q8 pack geometry");
+        vt::require(vt::aligned(codes, 8) && vt::aligned(scales, 2), "Q8 pack outputs must be aligned");
+        const std::int64_t lanes = static_cast<std::int64_t>(n) * (padded / 32) * 4;
+        const std::int64_t blocks = (lanes + 255) / 256;
+        vt::require(blocks <= INT32_MAX, "Q8 pack grid too large");
+        auto s = static_cast<hipStream_t>(stream);
+        auto* sc = static_cast<__half*>(scales);
+        if (dtype == vt::kF16)
+            vt::q8_pack<<<static_cast<unsigned>(blocks), 256, 0, s>>>(static_cast<const __half*>(src), codes, sc, n, k, padded);
+        else if (dtype == vt::kBF16)
+            vt::q8_pack<<<static_cast<unsigned>(blocks), 256, 0, s>>>(static_cast<const __hip_bfloat16*>(src), codes, sc,
+                                                                      n, k, padded);
+        else if (dtype == vt::kF32)
+            vt::q8_pack<<<static_cast<unsigned>(blocks), 256, 0, s>>>(static_cast<const float*>(src), codes, sc, n, k, padded);
+        else
+            throw vt::Invalid("unsupported source dtype");
+    });
+}

@@ -11,138 +11,240 @@
 // gfx950 mapping: one 64-lane wave owns all 256 virtual threads of a row;
 // lane L holds j = 4L..4L+3, so one chunk of 256 columns is a single dword
 // per lane (256 contiguous bytes per wave) and every virtual thread's FMA
-// chain stays in one lane in increasing column order. A wave processes RR
-// rows and TT tokens at once so the activation words are reused RR times and
-// the weight words TT times. The code*scale product is exact in fp32 (8-bit
-// by 11-bit significands), so its evaluation order is immaterial.
+// chain stays in one lane in increasing column order. The activations of
+// the workgroup's token tile are staged once in LDS (zero past k): streamed
+// weights would otherwise evict them from the vector L1 and every chunk
+// would re-read them from L2, which halves the achievable HBM rate. The
+// code*scale product is exact in fp32 (8-bit by 11-bit significands), so
+// its evaluation order is immaterial.
 #include "common.hpp"
+
+#include <algorithm>
+#include <type_traits>
 
 namespace vt {
 namespace {
 
-constexpr int kWaves = 4;  // waves per 256-thread workgroup
+constexpr int kWaves = 16;  // waves per 1024-thread workgroup
+constexpr int kThreads = kWaves * 64;
 
-template <class T>
-__device__ __forceinline__ void load_x4(const T* x, std::int64_t base, int col, int k,
-                                        bool vec, float (&xv)[4]);
-
-template <>
-__device__ __forceinline__ void load_x4<__half>(const __half* x, std::int64_t base, int col,
-                                                int k, bool vec, float (&xv)[4]) {
-    if (vec && col + 3 < k) {
-        const uint2 w = *reinterpret_cast<const uint2*>(x + base + col);
-        xv[0] = half_lo(w.x); xv[1] = half_hi(w.x);
-        xv[2] = half_lo(w.y); xv[3] = half_hi(w.y);
-    } else {
+// Accumulates one chunk of 256 columns (lane L: columns 4L..4L+3 of the
+// chunk) for TT tokens and RR rows. Activations come from LDS, where columns
+// at or beyond k hold +0: with finite weights they contribute
+// fma(+0, w, acc) == acc exactly (accumulators start at +0 and a
+// round-to-nearest sum is never -0), so they need no masking.
+template <class T, int TT, int RR>
+__device__ __forceinline__ void chunk_fma(const uint2* __restrict__ xs, int stride, const std::uint32_t (&cw)[RR],
+                                          const float (&s)[RR], float (&acc)[TT][RR][4]) {
+    float w[RR][4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) xv[v] = col + v < k ? to_f32(x[base + col + v]) : 0.0f;
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) w[r][v] = sbyte(cw[r], v) * s[r];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        const uint2 xw = xs[t * stride];
+        float xv[4];
+        if constexpr (std::is_same<T, __half>::value) {
+            xv[0] = half_lo(xw.x); xv[1] = half_hi(xw.x); xv[2] = half_lo(xw.y); xv[3] = half_hi(xw.y);
+        } else {
+            xv[0] = bf16_lo(xw.x); xv[1] = bf16_hi(xw.x); xv[2] = bf16_lo(xw.y); xv[3] = bf16_hi(xw.y);
+        }
+#pragma unroll
+        for (int r = 0; r < RR; ++r)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[t][r][v] = fmaf(xv[v], w[r][v], acc[t][r][v]);
     }
 }
 
-template <>
-__device__ __forceinline__ void load_x4<__hip_bfloat16>(const __hip_bfloat16* x, std::int64_t base,
-                                                        int col, int k, bool vec, float (&xv)[4]) {
-    if (vec && col + 3 < k) {
-        const uint2 w = *reinterpret_cast<const uint2*>(x + base + col);
-        xv[0] = bf16_lo(w.x); xv[1] = bf16_hi(w.x);
-        xv[2] = bf16_lo(w.y); xv[3] = bf16_hi(w.y);
-    } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) xv[v] = col + v < k ? to_f32(x[base + col + v]) : 0.0f;
-    }
-}
+// Persistent waves. Wave w owns row blocks w, w+W, w+2W, ... (RR rows each);
+// every row block is a sequence of tiles of U chunks, and a wave walks the
+// flat sequence of its (row block, tile) pairs with a two-deep ping-pong
+// prefetch: the code words and scales of tile i+1 are in flight while tile i
+// is accumulated. Each virtual thread's chain still advances one chunk at a
+// time in increasing column order, so the association is the canonical one.
+template <int RR, int U>
+struct Tile {
+    std::uint32_t cw[U][RR];
+    unsigned short sb[U][RR];
+};
 
-template <class T, int TT, int RR, bool VEC>
-__global__ __launch_bounds__(256) void q8_exact(const T* __restrict__ x,
+template <class T, int TT, int RR, int U, bool VEC>
+__global__ __launch_bounds__(kThreads) void q8_exact(const T* __restrict__ x,
                                                 const std::int8_t* __restrict__ codes,
                                                 const __half* __restrict__ scales,
                                                 T* __restrict__ out, int tokens, int n, int k,
                                                 int padded) {
+    extern __shared__ uint2 xs[];  // [TT][tiles*U*64] words of 4 activations
     const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * RR;
+    const int chunks = (k + 255) >> 8;
+    const int tiles = (chunks + U - 1) / U;
+    const int stride = tiles * U * 64;
     const int t0 = blockIdx.y * TT;
-    if (row0 >= n) return;
-    const int groups = padded >> 5;
 
-    float acc[TT][RR][4];
+    // Stage the token tile's activations; zero past k and past `tokens`.
+    for (int t = 0; t < TT; ++t) {
+        const bool live_token = t0 + t < tokens;
+        const T* src = x + static_cast<std::int64_t>(min(t0 + t, tokens - 1)) * k;
+        for (int i = threadIdx.x; i < stride; i += kThreads) {
+            const int col = 4 * i;
+            uint2 w = make_uint2(0u, 0u);
+            if (live_token && col < k) {
+                if (VEC) {
+                    w = *reinterpret_cast<const uint2*>(src + col);
+                } else {
+                    const unsigned short* p = reinterpret_cast<const unsigned short*>(src);
+                    unsigned short h[4];
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
-#pragma unroll
-        for (int r = 0; r < RR; ++r)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) acc[t][r][v] = 0.0f;
-
-    const std::uint32_t* wrow[RR];
-    const __half* srow[RR];
-#pragma unroll
-    for (int r = 0; r < RR; ++r) {
-        const int row = min(row0 + r, n - 1);  // clamped rows are computed, never stored
-        wrow[r] = reinterpret_cast<const std::uint32_t*>(codes + static_cast<std::int64_t>(row) * padded);
-        srow[r] = scales + static_cast<std::int64_t>(row) * groups;
+                    for (int v = 0; v < 4; ++v) h[v] = col + v < k ? p[col + v] : static_cast<unsigned short>(0);
+                    w.x = h[0] | (static_cast<std::uint32_t>(h[1]) << 16);
+                    w.y = h[2] | (static_cast<std::uint32_t>(h[3]) << 16);
+                }
+            }
+            xs[t * stride + i] = w;
+        }
     }
+    __syncthreads();
 
-    for (int base = 0; base < k; base += 256) {
-        const int col = base + 4 * lane;
-        const bool live = col < k;
-        std::uint32_t cw[RR];
-        float s[RR];
+    // Wave-uniform quantities live in scalar registers, so every branch on
+    // them below is a scalar branch and the prefetch is never predicated
+    // (a predicated prefetch would make the compiler wait for it at once).
+    const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + (threadIdx.x >> 6));
+    const int waves = gridDim.x * kWaves;
+    const int blocks = (n + RR - 1) / RR;
+    if (wave >= blocks) return;
+    const int total = ((blocks - 1 - wave) / waves + 1) * tiles;
+    const int groups = padded >> 5;
+    const int full = k >> 8;                  // chunks whose 256 columns are all valid
+    const int last_word = (padded >> 2) - 1;  // last code word of a row
+
+    // Interior tiles address every chunk from one per-tile base with constant
+    // offsets; the edge tile clamps its indices into the row. Weights read for
+    // columns at or past k meet zero activations; clamped rows are computed
+    // and never stored.
+    auto fetch = [&](int i, Tile<RR, U>& tile) {
+        const int block = wave + (i / tiles) * waves;
+        const int c0 = (i % tiles) * U;
+        const int row0 = block * RR;
 #pragma unroll
         for (int r = 0; r < RR; ++r) {
-            cw[r] = live ? wrow[r][col >> 2] : 0u;
-            s[r] = live ? __half2float(srow[r][col >> 5]) : 0.0f;
-        }
-        float w[RR][4];
+            const std::int64_t row = min(row0 + r, n - 1);
+            const std::uint32_t* wp = reinterpret_cast<const std::uint32_t*>(codes + row * padded);
+            const unsigned short* sp = reinterpret_cast<const unsigned short*>(scales + row * groups);
+            if (c0 + U <= full) {
+                const std::uint32_t* wt = wp + c0 * 64 + lane;
+                const unsigned short* st = sp + c0 * 8 + (lane >> 3);
 #pragma unroll
-        for (int r = 0; r < RR; ++r)
+                for (int u = 0; u < U; ++u) {
+                    tile.cw[u][r] = wt[u * 64];
+                    tile.sb[u][r] = st[u * 8];
+                }
+            } else {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) w[r][v] = sbyte(cw[r], v) * s[r];
-#pragma unroll
-        for (int t = 0; t < TT; ++t) {
-            if (t0 + t < tokens && live) {
-                float xv[4];
-                load_x4<T>(x, static_cast<std::int64_t>(t0 + t) * k, col, k, VEC, xv);
-#pragma unroll
-                for (int r = 0; r < RR; ++r)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v)
-                        if (col + v < k) acc[t][r][v] = fmaf(xv[v], w[r][v], acc[t][r][v]);
+                for (int u = 0; u < U; ++u) {
+                    tile.cw[u][r] = wp[min((c0 + u) * 64 + lane, last_word)];
+                    tile.sb[u][r] = sp[min((c0 + u) * 8 + (lane >> 3), groups - 1)];
+                }
             }
         }
-    }
+    };
 
+    float acc[TT][RR][4];
+    auto reset = [&] {
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
+        for (int t = 0; t < TT; ++t)
 #pragma unroll
-        for (int r = 0; r < RR; ++r) {
-            const float y = canonical_sum(acc[t][r][0], acc[t][r][1], acc[t][r][2], acc[t][r][3]);
-            if (lane == 0 && t0 + t < tokens && row0 + r < n)
-                out[static_cast<std::int64_t>(t0 + t) * n + row0 + r] = from_f32<T>(y);
+            for (int r = 0; r < RR; ++r)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[t][r][v] = 0.0f;
+    };
+
+    auto consume = [&](int i, const Tile<RR, U>& tile) {
+        const int c0 = (i % tiles) * U;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float s[RR];
+#pragma unroll
+            for (int r = 0; r < RR; ++r) s[r] = __half2float(__ushort_as_half(tile.sb[u][r]));
+            chunk_fma<T, TT, RR>(xs + (c0 + u) * 64 + lane, stride, tile.cw[u], s, acc);
         }
+        if (i % tiles == tiles - 1) {
+            const int row0 = (wave + (i / tiles) * waves) * RR;
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+#pragma unroll
+                for (int r = 0; r < RR; ++r) {
+                    const float y = canonical_sum(acc[t][r][0], acc[t][r][1], acc[t][r][2], acc[t][r][3]);
+                    if (lane == 0 && t0 + t < tokens && row0 + r < n)
+                        out[static_cast<std::int64_t>(t0 + t) * n + row0 + r] = from_f32<T>(y);
+                }
+            reset();
+        }
+    };
+
+    // Ping-pong over the wave's tiles; the prefetch past the last tile re-reads
+    // the last tile (unconditional, so the wait before each consume covers only
+    // the older tile).
+    reset();
+    Tile<RR, U> a, b;
+    fetch(0, a);
+    for (int i = 0; i < total; i += 2) {
+        fetch(min(i + 1, total - 1), b);
+        consume(i, a);
+        if (i + 1 >= total) break;
+        fetch(min(i + 2, total - 1), a);
+        consume(i + 1, b);
     }
 }
 
-template <class T, int TT, int RR>
+// LDS bytes for TT tokens at width k with tiles of U chunks.
+inline std::size_t exact_lds_bytes(int tt, int u, int k) {
+    const int chunks = (k + 255) >> 8;
+    return static_cast<std::size_t>(tt) * ((chunks + u - 1) / u) * u * 64 * sizeof(uint2);
+}
+
+constexpr std::size_t kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
+
+template <class T, int TT, int RR, int U>
 void launch_tile(const void* x, const std::int8_t* codes, const __half* scales, void* out,
                  int tokens, int n, int k, int padded, hipStream_t stream) {
-    const dim3 grid((n + kWaves * RR - 1) / (kWaves * RR), (tokens + TT - 1) / TT);
+    // At most two 16-wave workgroups per CU (256 CUs): each stages the
+    // activations once and streams many rows; grid.y walks token tiles (each
+    // re-streams the weights).
+    const int blocks = (n + RR - 1) / RR;
+    const int groups = std::min((blocks + kWaves - 1) / kWaves, 512);
+    const dim3 grid(groups, (tokens + TT - 1) / TT);
     require(grid.y <= 65535, "token tiles exceed the launch grid");
+    const std::size_t lds = exact_lds_bytes(TT, U, k);
+    require(lds <= kMaxLds, "activation tile exceeds LDS");
     const bool vec = (k % 4 == 0) && aligned(x, 8);
-    if (vec)
-        q8_exact<T, TT, RR, true><<<grid, 256, 0, stream>>>(
-            static_cast<const T*>(x), codes, scales, static_cast<T*>(out), tokens, n, k, padded);
-    else
-        q8_exact<T, TT, RR, false><<<grid, 256, 0, stream>>>(
-            static_cast<const T*>(x), codes, scales, static_cast<T*>(out), tokens, n, k, padded);
+    auto kernel = vec ? q8_exact<T, TT, RR, U, true> : q8_exact<T, TT, RR, U, false>;
+    if (lds > 64 * 1024) {
+        // Raise the dynamic-LDS limit of both variants once per process.
+        static const hipError_t raised = [] {
+            const hipError_t a = hipFuncSetAttribute(reinterpret_cast<const void*>(q8_exact<T, TT, RR, U, true>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     static_cast<int>(kMaxLds));
+            const hipError_t b = hipFuncSetAttribute(reinterpret_cast<const void*>(q8_exact<T, TT, RR, U, false>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     static_cast<int>(kMaxLds));
+            return a != hipSuccess ? a : b;
+        }();
+        check(raised);
+    }
+    kernel<<<grid, kThreads, lds, stream>>>(static_cast<const T*>(x), codes, scales, static_cast<T*>(out), tokens, n, k,
+                                       padded);
 }
 
 template <class T>
 void launch_exact(const void* x, const std::int8_t* codes, const __half* scales, void* out,
                   int tokens, int n, int k, int padded, hipStream_t stream) {
-    if (tokens == 1) launch_tile<T, 1, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else if (tokens == 2) launch_tile<T, 2, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else if (tokens <= 4) launch_tile<T, 4, 2>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else if (tokens <= 8) launch_tile<T, 8, 2>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else launch_tile<T, 16, 1>(x, codes, scales, out, tokens, n, k, padded, stream);
+    // Token tiles of up to 4 share one weight stream; wider tiles do not fit the
+    // activations in LDS at the widths of interest and are VALU bound anyway.
+    if (tokens == 1) launch_tile<T, 1, 1, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else if (tokens == 2 || exact_lds_bytes(4, 4, k) > kMaxLds)
+        launch_tile<T, 2, 1, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else launch_tile<T, 4, 2, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
 }
 
 __global__ void q8_embedding(const std::int8_t* codes, const __half* scales, const std::int64_t* ids,
