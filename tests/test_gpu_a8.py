@@ -124,3 +124,42 @@ def test_fused_rms_a8_bytes(backend, device, passes, tokens, k):
     backend._check(lib.venturi_q8_dp4a_quantize(y_dev.data_ptr(), separate.data_ptr(), separate.numel(), tokens, k,
                                                  passes, torch.cuda.current_stream().cuda_stream))
     assert torch.equal(separate, workspace)
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+@pytest.mark.parametrize("tokens", [64, 65, 100, 257])
+@pytest.mark.parametrize("shape", [(7, 1), (33, 67), (129, 1000), (64, 5120), (100, 6144)])
+def test_matrix_core_projection_bytes(backend, device, passes, tokens, shape):
+    # Token counts that take the int8 matrix-core GEMM: bytes must still be the reference's.
+    n, k = shape
+    print(f"case a8-gemm n={n} k={k} tokens={tokens} passes={passes}", flush=True)
+    codes, scales, x, resident = _setup(backend, device, n, k, tokens)
+    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=passes == 2)
+    workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    guard, out = guarded_out(tokens, n, torch.float16, device)
+    plan.run(x.to(device), out=out, workspace=workspace)
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    q, d = oracle.a8_quantize(bits(x), passes)
+    np.testing.assert_array_equal(bits(out), oracle.a8_linear(q, d, codes.numpy(), scales.numpy(), k))
+
+
+@pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
+def test_config3_prefill_sampled(backend, device, n, k):
+    # BASELINE config 3 shapes at 2048 tokens; the oracle checks a seeded sample
+    # of 64 tokens x 128 rows (every output's order is independent of the others).
+    tokens = 2048
+    gen = torch.Generator(device=device).manual_seed(n ^ k)
+    packed = backend.quantize_q8(torch.randn(n, k, generator=gen, device=device) * 0.02)
+    x = torch.randn(tokens, k, generator=gen, device=device).half()
+    resident = backend.upload_linear(packed, dtype=torch.float16, device=device)
+    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=False)
+    workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    plan.run(x, out=out, workspace=workspace)
+    rng = np.random.default_rng(n + k)
+    ts = np.sort(rng.choice(tokens, 64, replace=False))
+    rows = np.sort(rng.choice(n, 128, replace=False))
+    q, d = oracle.a8_quantize(bits(x[ts]), 1)
+    expected = oracle.a8_linear(q, d, packed.codes.cpu().numpy()[rows], packed.scales.cpu().numpy()[rows], k)
+    np.testing.assert_array_equal(bits(out)[ts][:, rows], expected)

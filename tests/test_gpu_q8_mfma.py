@@ -1,0 +1,84 @@
+"""Q8 A16 projection on matrix cores: agreement with the canonical order and FP64.
+
+The MFMA route sums each 32-column group on the matrix core and applies the
+group scale in fp32, so it differs from the canonical order only by fp32
+association. Tolerances (written here, not relaxed silently):
+  * vs FP64 exact: |y - exact| <= 0.5 ulp_fp16(exact) + 2^-19 * sum_k |x_k w_k|
+  * vs the canonical-order oracle: rel-L2 <= 1e-3, and every output within
+    max(2e-3, 1 fp16 ulp of the oracle value); the number of 1-ulp flips is
+    reported.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import bits, random_q8
+from venturi_amd import Q8RowSplitWeight
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp16(v):
+    v = np.abs(v)
+    e = np.floor(np.log2(np.maximum(v, 2.0**-14)))
+    return 2.0 ** (e - 10)
+
+
+def check(out, x, codes, scales, k):
+    got = out.cpu().float().numpy().astype(np.float64)
+    w = oracle.q8_unpack(codes, scales, k)
+    xd = x.float().numpy().astype(np.float64)
+    exact = xd @ w.T
+    bound = 0.5 * ulp16(exact) + 2.0**-19 * (np.abs(xd) @ np.abs(w).T)
+    assert (np.abs(got - exact) <= bound).all()
+    canon = oracle.q8_linear(bits(x), codes, scales, k).view(np.float16).astype(np.float64)
+    diff = np.abs(got - canon)
+    assert (diff <= np.maximum(2e-3, ulp16(canon))).all()
+    assert np.linalg.norm(got - canon) <= 1e-3 * max(np.linalg.norm(canon), 1e-12)
+    return int((diff > 0).sum())
+
+
+@pytest.mark.parametrize("shape", [(1, 64), (7, 72), (33, 136), (16, 256), (257, 5120), (100, 1000)])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 8, 13, 16])
+def test_mfma_tolerances_tails_and_guards(backend, device, shape, tokens):
+    n, k = shape
+    print(f"case q8-mfma n={n} k={k} tokens={tokens}", flush=True)
+    codes, scales = random_q8(n, k, 77 + n + tokens)
+    weight = Q8RowSplitWeight(codes, scales, k)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens)).half()
+    plan = backend.upload_linear(weight, dtype=torch.float16, device=device).prepare(tokens=tokens, route="mfma")
+    assert plan.route == "venturi-q8-mfma"
+    guard = torch.full((tokens * n + 2,), 47, dtype=torch.float16, device=device)
+    out = guard[1:-1].view(tokens, n)
+    plan.run(x.to(device), out=out)
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    flips = check(out, x, codes.numpy(), scales.numpy(), k)
+    print(f"flips={flips} of {tokens * n}", flush=True)
+
+
+@pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
+@pytest.mark.parametrize("tokens", [4, 16])
+def test_mfma_config2_sampled_rows(backend, device, n, k, tokens):
+    gen = torch.Generator(device=device).manual_seed(n + k)
+    w = torch.randn(n, k, generator=gen, device=device) * 0.02
+    packed = backend.quantize_q8(w)
+    del w
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens)).half()
+    plan = backend.upload_linear(packed, dtype=torch.float16, device=device).prepare(tokens=tokens, route="mfma")
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    plan.run(x.to(device), out=out)
+    rows = np.sort(np.random.default_rng(n).choice(n, 256, replace=False))
+    codes, scales = packed.codes.cpu().numpy()[rows], packed.scales.cpu().numpy()[rows]
+    flips = check(out[:, rows], x, codes, scales, k)
+    print(f"config2 n={n} k={k} tokens={tokens}: flips={flips} of {tokens * 256}", flush=True)
+
+
+def test_mfma_route_admission(backend, device):
+    codes, scales = random_q8(8, 65, 1)
+    resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, 65), dtype=torch.float16, device=device)
+    with pytest.raises(ValueError, match="MFMA"):
+        resident.prepare(tokens=1, route="mfma")  # k % 8 != 0
+    assert resident.prepare(tokens=8).route == "venturi-q8-exact"

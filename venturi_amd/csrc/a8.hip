@@ -9,6 +9,11 @@
 
 namespace vt {
 
+constexpr int kA8GemmMinTokens = 64;
+
+void a8_gemm_launch(const void* workspace, const std::int8_t* codes, const __half* scales, void* out, int tokens,
+                    int n, int k, int padded, int passes, hipStream_t stream);
+
 std::uint64_t a8_bytes(int tokens, int k, int passes) {
     // Same admission as q8_dp4a.cuh:7-13.
     require(tokens > 0 && tokens <= 262140 && k > 0 && k <= INT32_MAX - 1024 && (passes == 1 || passes == 2),
@@ -289,6 +294,12 @@ void a8_gemv_launch(const void* workspace, std::uint64_t available, const std::i
     const auto* acodes = static_cast<const std::int8_t*>(workspace);
     const auto* ascales = reinterpret_cast<const float*>(acodes + count * 32 * passes);
     auto* y = static_cast<__half*>(out);
+    // Both kernels produce the reference's bytes; the matrix-core GEMM takes
+    // over once a 64-token tile is filled.
+    if (tokens >= kA8GemmMinTokens && (groups + 31) / 32 <= 24) {
+        a8_gemm_launch(workspace, codes, scales, out, tokens, n, k, padded, passes, stream);
+        return;
+    }
     if (passes == 1) dispatch_a8_gemv<1>(acodes, ascales, codes, scales, y, tokens, n, k, padded, groups, stream);
     else dispatch_a8_gemv<2>(acodes, ascales, codes, scales, y, tokens, n, k, padded, groups, stream);
 }

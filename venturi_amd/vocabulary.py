@@ -20,6 +20,7 @@ import torch
 from .blocks import _DTYPES, Q8_ROUTES, _no_overlap, _shape, _stream, _tensor
 
 EXACT_MAX_AUTO_TOKENS = 4
+MFMA_MAX_TOKENS = 16
 
 
 def _ids(ids, vocab):
@@ -102,11 +103,13 @@ class ResidentQ8Vocabulary:
         if route not in Q8_ROUTES:
             raise ValueError(f"Q8 route must be one of {Q8_ROUTES}")
         self.backend.validate_device(self.dtype, self.device)
+        mfma_ok = self.dtype == torch.float16 and self.hidden_size % 8 == 0 and tokens <= MFMA_MAX_TOKENS
         if route == "auto":
-            mfma = hasattr(self.backend._native, "venturi_q8_gemm_run")
-            route = "exact" if tokens <= EXACT_MAX_AUTO_TOKENS or not mfma else "mfma"
-        if route == "mfma" and not hasattr(self.backend._native, "venturi_q8_gemm_run"):
-            raise RuntimeError("The loaded library has no Q8 MFMA export; rebuild it")
+            route = "mfma" if mfma_ok and tokens > EXACT_MAX_AUTO_TOKENS else "exact"
+        if route == "mfma" and not mfma_ok:
+            raise ValueError(
+                f"The Q8 MFMA route takes FP16 activations, K % 8 == 0 and at most {MFMA_MAX_TOKENS} tokens"
+            )
         return Q8OutputHead(self, tokens, route)
 
 
