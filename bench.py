@@ -47,6 +47,7 @@ def parse():
     p.add_argument("--copy-mb", type=float, default=600.0, help="minimum rotated weight bytes per projection")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-prefill", action="store_true", help="skip the config-3 A8 prefill section")
     return p.parse_args()
 
 
@@ -93,6 +94,74 @@ def cpu_baseline(copies, xs, seconds):
         "sample": f"{reps} repetitions of the full config-2 step (4 projections x M in {list(TOKENS)}), "
         f"torch {torch.__version__} CPU GEMM, FP32 weights materialised before timing, "
         f"{elapsed:.1f} s on {platform.processor() or platform.machine()}",
+    }
+
+
+INT8_PEAK_TOPS = 5000.0
+
+
+def prefill_a8(backend, device, steps, warmup):
+    """RMSNorm + 1-pass A8 at hidden 5120, int8 GEMMs at the config-2 shapes, M = 2048.
+
+    x fp16 [2048, 5120] ~ N(0, 1) with 51 seeded channels (1%) scaled by 20;
+    gamma ~ N(1, 0.1); eps 1e-6. QKV and gate+up consume the fused RMS+A8
+    workspace; o_proj (K 6144) and down (K 17408) quantize seeded N(0, 1)
+    activations with the plain A8 quantizer. Each stage runs `steps` times back
+    to back between one pair of events; TOPS = 2*M*N*K / average time.
+    """
+    from venturi_amd import prepare_q8_dp4a, prepare_rms_q8
+
+    m = 2048
+    gen = torch.Generator(device=device).manual_seed(3)
+    x = torch.randn(m, 5120, generator=gen, device=device)
+    outliers = torch.randperm(5120, generator=torch.Generator().manual_seed(3))[:51].to(device)
+    x[:, outliers] *= 20
+    x = x.half()
+    gamma = (1 + 0.1 * torch.randn(5120, generator=gen, device=device)).float()
+    norm = backend.upload_rmsnorm(gamma, dtype=torch.float16, device=device, epsilon=1e-6)
+    rms_plan = prepare_rms_q8(norm, tokens=m, residual_compensation=False)
+    stream = torch.cuda.current_stream(device)
+    results, total_ops, total_s = {}, 0, 0.0
+
+    def timed(fn, reps):
+        for _ in range(warmup):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        b.synchronize()
+        return a.elapsed_time(b) / 1e3 / reps
+
+    ws_5120 = torch.empty(rms_plan.workspace_bytes, dtype=torch.uint8, device=device)
+    results["rms_a8_k5120"] = {"us": round(timed(lambda: rms_plan.run(x, workspace=ws_5120), steps) * 1e6, 2)}
+    for i, (name, n, k) in enumerate(PROJECTIONS):
+        packed = backend.quantize_q8(torch.randn(n, k, generator=gen, device=device) * 0.02)
+        resident = backend.upload_linear(packed, dtype=torch.float16, device=device)
+        del packed
+        plan = prepare_q8_dp4a(resident, tokens=m, residual_compensation=False)
+        out = torch.empty(m, n, dtype=torch.float16, device=device)
+        if k == 5120:
+            ws = ws_5120
+        else:
+            ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+            xa = torch.randn(m, k, generator=gen, device=device).half()
+            results[f"a8_quantize_k{k}"] = {"us": round(timed(lambda: plan.quantize(xa, workspace=ws), steps) * 1e6, 2)}
+        t = timed(lambda: plan.project(out=out, workspace=ws), steps)
+        ops = 2 * m * n * k
+        total_ops += ops
+        total_s += t
+        results[name] = {"us": round(t * 1e6, 1), "TOPS": round(ops / t / 1e12, 1),
+                         "frac_int8_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4)}
+        del resident, plan, out
+    tops = total_ops / total_s / 1e12
+    return {
+        "workload": "config3: RMSNorm+A8 (1 pass) -> int8 GEMMs at the config-2 shapes, M=2048",
+        "gemm_TOPS": round(tops, 1),
+        "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                     "frac": round(tops / INT8_PEAK_TOPS, 4)},
+        "stages": results,
     }
 
 
@@ -181,6 +250,9 @@ def main():
         },
         "per_launch": detail,
     }
+    if not args.no_prefill:
+        del plans
+        result["prefill_a8"] = prefill_a8(backend, device, max(args.steps // 2, 3), 2)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(copies, xs, args.cpu_seconds)
     print(json.dumps(result), flush=True)

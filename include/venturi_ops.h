@@ -69,6 +69,77 @@ int venturi_rms_q8_quantize(const void* x, const float* w, void* workspace, uint
 int venturi_rms_q8_quantize_passes(const void* x, const float* w, void* workspace, uint64_t available, int tokens,
                                    int k, float epsilon, int passes, void* intermediate, void* stream);
 
+/* Extension (the reference packs Q8 on the CPU only, weights.py:398-439):
+ * device Q8 packing of a dense fp16/bf16/fp32 [n][k] source with the
+ * arithmetic of Q8RowSplitWeight.from_dense; codes/scales bytes identical. */
+int venturi_q8_pack_run(const void* source, int8_t* codes, void* scales, int n, int k, int padded, int dtype,
+                        void* stream);
+
+/* Extension: Q8 A16 projection on fp16 matrix cores (same arguments as
+ * venturi_q8_head_run; fp16 activations, k % 8 == 0, tokens <= 16). Per-group
+ * fp32 scaling of exact group dots; agrees with the canonical order to fp32
+ * association, not bit-for-bit. */
+int venturi_q8_gemm_run(const void* x, const int8_t* codes, const void* scales, void* out, int tokens, int n, int k,
+                        int padded, int dtype, void* stream);
+
+/* ---- Q4 (q4_g64_fp16): codes uint8 [n][padded/2] (column 2j in the low
+ * nibble of byte j, two's complement), scales fp16 [n][padded/64]. ---- */
+
+/* Expert operator ABI 1 (flash_next_q4.cu:36-54). These two return a HIP error
+ * code (0 = success, hipErrorInvalidValue on bad arguments), as the reference
+ * returns a CUDA error code; padded >= k with padded % 128 == 0. */
+int venturi_q4_abi(void); /* returns 1 */
+/* fp16 matrix fp16(q * scale) [rows][cols]. Replaces flash_next_q4.cu:37-46. */
+int venturi_q4_decode(const void* codes, const void* scales, void* out, int rows, int cols, int padded,
+                      void* stream);
+/* Expert GEMV, 1..64 fp16 tokens, fp16(q*scale) weights in the lane-strided
+ * fmaf order; bytes identical. Replaces flash_next_q4.cu:47-54. */
+int venturi_q4_linear(const void* x, const void* codes, const void* scales, void* out, int tokens, int rows,
+                      int cols, int padded, void* stream);
+
+/* Research fused Q4 GEMV (FP32 scaled integer products), fp16 only; bytes
+ * identical to q4_fused_run_kernel. Replaces ops_api.h:49 / blocks.cu:1067-1076. */
+int venturi_q4_fused_run(const void* x, const void* codes, const void* scales, void* out, int t, int rows, int k,
+                         int padded, int dtype, void* stream);
+
+/* Row-codec decode of rows [row, row+rows) into out [rows][k] fp16; bits must
+ * be 4 in this library (the q5/q6 high plane is not implemented, `high` is
+ * ignored). Replaces ops_api.h:98 / blocks.cu:1077-1086. */
+int venturi_row_dequant_rows(const void* codes, const void* high, const void* scales, void* out, int row, int rows,
+                             int k, int padded, int bits, void* stream);
+
+/* Plugin ABI 2 (q4_linear.cu:60-88): its own thread-local error text. */
+int venturi_ada_abi(void); /* returns 2 */
+const char* venturi_ada_error(void);
+/* Admission: returns route 0 (requested -1 auto or 0 generic) or -1. Device
+ * must be gfx950. Replaces q4_linear.cu:62-75. */
+int venturi_q4_prepare(int n, int k, int tokens, int dtype, int requested);
+/* FP32-weight SIMT order, fp16/bf16 (dtype 0/1), padded_k == ceil(k/128)*128;
+ * bytes identical. Replaces q4_linear.cu:76-88. */
+int venturi_q4_run(const void* x, const void* codes, const void* scales, void* out, int n, int k, int padded_k,
+                   int tokens, int dtype, int route, void* stream);
+
+/* Extension: the W4A16 contract GEMM (fp16(q*scale) weights, fp32 accumulation
+ * on fp16 matrix cores), fp16 activations, k % 8 == 0, x 16-byte aligned, any
+ * token count. Stands where the reference dequantizes to an fp16 shadow and
+ * calls cuBLAS (row_codec_dispatch.cuh:41-48, qwen_runtime.cuh:348-364). */
+int venturi_q4_gemm_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
+                        int padded, int dtype, void* stream);
+
+/* Extension: workspace bytes of venturi_moe_q4_run (0 on invalid geometry). */
+uint64_t venturi_moe_q4_bytes(int tokens, int top_k, int experts, int hidden, int inter);
+
+/* Extension: routed-expert Q4 W4A16 MoE, replacing the per-expert host loop of
+ * flash_next_moe.py:139-161 / flash_next_q4.py:204-224. x fp16 [tokens][hidden];
+ * ids int64 [tokens][top_k]; scores fp16 [tokens][top_k]; gate_up planes stacked
+ * [experts][2*inter][...] (gate rows first), down planes [experts][hidden][...];
+ * out fp16 [tokens][hidden]; workspace 256-byte aligned. Ids outside
+ * [0, experts) are skipped and counted in the workspace status word. */
+int venturi_moe_q4_run(const void* x, const int64_t* ids, const void* scores, const void* gate_up_codes,
+                       const void* gate_up_scales, const void* down_codes, const void* down_scales, void* out,
+                       void* workspace, uint64_t workspace_bytes, int tokens, int top_k, int experts, int hidden,
+                       int inter, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,8 @@ def lib():
         handle.oracle_rms_a8.argtypes = [P, P, I, I, F, I, P, P, P, P]
         handle.oracle_q4_linear.argtypes = [P] * 4 + [I] * 4
         handle.oracle_q4_decode.argtypes = [P] * 3 + [I] * 3
+        handle.oracle_q4_generic.argtypes = [P] * 4 + [I] * 5
+        handle.oracle_q4_fused.argtypes = [P] * 4 + [I] * 4
         _lib = handle
     return _lib
 
@@ -244,6 +246,35 @@ def q4_linear(x, packed, scales, k):
     tokens, rows, padded = xs.shape[0], packed.shape[0], packed.shape[1] * 2
     out = np.zeros((tokens, rows), dtype=np.uint16)
     lib().oracle_q4_linear(_ptr(xs), _ptr(packed), _ptr(_u16(scales)), _ptr(out), tokens, rows, k, padded)
+    return out
+
+
+def q4_generic(x, packed, scales, k, dtype=0):
+    """q4_generic (ops/csrc/q4_linear.cu:21-56): fp16/bf16 bits [tokens, n]."""
+    xs = _u16(x)
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    tokens, n, padded = xs.shape[0], packed.shape[0], packed.shape[1] * 2
+    out = np.zeros((tokens, n), dtype=np.uint16)
+    lib().oracle_q4_generic(_ptr(xs), _ptr(packed), _ptr(_u16(scales)), _ptr(out), n, k, padded, tokens, dtype)
+    return out
+
+
+def q4_fused(x, packed, scales, k):
+    """q4_fused_run_kernel (ops/csrc/q4_fused.cuh:10-89): fp16 bits [tokens, rows]."""
+    xs = _u16(x)
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    tokens, rows, padded = xs.shape[0], packed.shape[0], packed.shape[1] * 2
+    out = np.zeros((tokens, rows), dtype=np.uint16)
+    lib().oracle_q4_fused(_ptr(xs), _ptr(packed), _ptr(_u16(scales)), _ptr(out), tokens, rows, k, padded)
+    return out
+
+
+def q4_decode(packed, scales, k):
+    """q4_decode (ops/csrc/flash_next_q4.cu:16-21) through the C restatement: fp16 bits [rows, k]."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    rows, padded = packed.shape[0], packed.shape[1] * 2
+    out = np.zeros((rows, k), dtype=np.uint16)
+    lib().oracle_q4_decode(_ptr(packed), _ptr(_u16(scales)), _ptr(out), rows, k, padded)
     return out
 
 

@@ -308,3 +308,60 @@ EXPORT void oracle_q4_decode(const uint8_t* codes, const uint16_t* scales, uint1
         for (int c = 0; c < cols; ++c)
             out[(int64_t)row * cols + c] = f32_to_f16(q4_weight(codes, scales, row, c, padded));
 }
+
+/* ---- Q4 plugin GEMV q4_generic (q4_linear.cu:21-56) ----------------------
+ * Lane l owns byte l of each 32-byte group: columns 64g+2l (low nibble) and
+ * 64g+2l+1 (high); FP32 weights w = f32(q) * f32(scale) (exact); per token
+ * sum = fmaf(x0, w0, sum) then fmaf(x1, w1, sum) for columns < k, groups in
+ * order; 32-lane tree; RNE cast to the activation type. */
+EXPORT void oracle_q4_generic(const uint16_t* x, const uint8_t* codes, const uint16_t* scales, uint16_t* out, int n,
+                              int k, int padded, int tokens, int dtype) {
+    const int groups = (k + 63) / 64;
+    for (int t = 0; t < tokens; ++t)
+        for (int row = 0; row < n; ++row) {
+            float lanes[32];
+            for (int l = 0; l < 32; ++l) {
+                float sum = 0.0f;
+                for (int g = 0; g < groups; ++g) {
+                    const unsigned byte = codes[(int64_t)row * (padded / 2) + (int64_t)g * 32 + l];
+                    const float scale = f16_to_f32(scales[(int64_t)row * (padded / 64) + g]);
+                    const float w0 = (float)((int)((byte & 15) ^ 8) - 8) * scale;
+                    const float w1 = (float)((int)((byte >> 4) ^ 8) - 8) * scale;
+                    const int col = g * 64 + 2 * l;
+                    if (col < k) sum = fmaf(act(x, (int64_t)t * k + col, dtype), w0, sum);
+                    if (col + 1 < k) sum = fmaf(act(x, (int64_t)t * k + col + 1, dtype), w1, sum);
+                }
+                lanes[l] = sum;
+            }
+            out[(int64_t)t * n + row] = cast_out(warp_tree(lanes), dtype);
+        }
+}
+
+/* ---- research fused Q4 GEMV (q4_fused.cuh:10-89) -------------------------
+ * Lane l: for every padded group g, term = RNE(lo*x0 + hi*x1) (both products
+ * are exact in fp32, so the fma contraction of either is the same value),
+ * acc = fmaf(scale, term, acc); x past k reads 0; 32-lane tree; fp16. */
+EXPORT void oracle_q4_fused(const uint16_t* x, const uint8_t* codes, const uint16_t* scales, uint16_t* out,
+                            int tokens, int rows, int k, int padded) {
+    const int groups = padded / 64;
+    for (int t = 0; t < tokens; ++t)
+        for (int row = 0; row < rows; ++row) {
+            float lanes[32];
+            for (int l = 0; l < 32; ++l) {
+                float acc = 0.0f;
+                for (int g = 0; g < groups; ++g) {
+                    const unsigned byte = codes[(int64_t)row * (padded / 2) + (int64_t)g * 32 + l];
+                    int lo = byte & 15, hi = byte >> 4;
+                    lo = lo >= 8 ? lo - 16 : lo;
+                    hi = hi >= 8 ? hi - 16 : hi;
+                    const int col = g * 64 + 2 * l;
+                    const float x0 = col < k ? f16_to_f32(x[(int64_t)t * k + col]) : 0.0f;
+                    const float x1 = col + 1 < k ? f16_to_f32(x[(int64_t)t * k + col + 1]) : 0.0f;
+                    const float term = fmaf((float)hi, x1, (float)lo * x0);
+                    acc = fmaf(f16_to_f32(scales[(int64_t)row * groups + g]), term, acc);
+                }
+                lanes[l] = acc;
+            }
+            out[(int64_t)t * rows + row] = f32_to_f16(warp_tree(lanes));
+        }
+}

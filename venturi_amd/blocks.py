@@ -140,7 +140,7 @@ def _capabilities():
         OperatorSupport("rmsnorm", devices, frozenset((torch.float16, torch.bfloat16, torch.float32))),
         OperatorSupport("linear", devices, quant, "q8_g32_fp16", "row_split_k128_v1"),
         OperatorSupport("embedding", devices, quant, "q8_g32_fp16", "row_split_k128_v1"),
-        OperatorSupport("linear", devices, frozenset((torch.float16,)), "q4_g64_fp16", "row_split_k128_v1"),
+        OperatorSupport("linear", devices, quant, "q4_g64_fp16", "row_split_k128_v1"),
     ]
     return BackendCapabilities("venturi-ops-gfx950", tuple(operators), reference=False, cuda_graphs=True)
 

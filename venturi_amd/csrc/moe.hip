@@ -1,0 +1,523 @@
+// Q4 W4A16 on fp16 matrix cores: a grouped (routed-expert) GEMM and the
+// plain W4A16 GEMM, plus the device routing and per-token combine of the
+// routed-expert MoE.
+//
+// Weight contract (flash_next_q4.cu:7-14, quantization/linear.py:86-95):
+// w = fp16_RNE(q * scale). In registers: the nibble u = q + 8 becomes the
+// fp16 1024 + u by byte permutation with 0x64, a packed fp16 add of -1032
+// gives q exactly, and a packed fp16 multiply by the group scale rounds
+// q * scale once, which is the contract's value. Dot products accumulate in
+// fp32 on v_mfma_f32_16x16x32_f16 (association differs from the reference's
+// cuBLAS/F.linear, which it pins by tolerance only).
+//
+// MoE semantics (flash_next_moe.py:139-161, flash_next_q4.py:204-224):
+// for each expert e in ascending order, over its routed tokens:
+//   gate, up = (x @ Wgu_e^T).chunk(2)      fp16 outputs
+//   h = fp16(fp16(silu(gate)) * up)
+//   y = fp16(h @ Wd_e^T) ; v = fp16(y * score)
+//   out[token] = fp16(out[token] + v)       out starts at +0
+// Every (token, slot) product is independent of the other tokens in its
+// expert's segment, so the routing kernel may place a token anywhere inside
+// its segment; the combine adds each token's values in ascending expert order
+// (ties in position order), which is the reference's index_add_ order.
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace vt {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+constexpr int kRows = 128;        // weight rows per workgroup tile
+constexpr int kWaves = 8;         // 512 threads; wave w owns 16 rows
+constexpr int kChunk = 256;       // K columns staged per iteration (128 code bytes per row)
+constexpr int kPassTokens = 64;   // tokens per pass: four 16-token MFMA blocks
+constexpr int kWStride = 144;     // LDS bytes per weight row (128 + 16 pad)
+constexpr int kXStride = 264;     // LDS halves per token row (256 + 8 pad)
+constexpr int kMaxExperts = 1024;
+
+enum Epilogue { kPlain = 0, kSwiGLU = 1, kScore = 2 };
+
+struct Q4Gemm {
+    const __half* x;           // activation rows, row stride x_stride halves
+    const int* gather;         // slot -> x row (null: slot itself)
+    const std::uint8_t* codes; // expert 0 codes [n][padded/2]
+    const __half* scales;      // expert 0 scales [n][padded/64]
+    std::int64_t code_stride;  // bytes between experts
+    std::int64_t scale_stride; // halves between experts
+    const int* seg;            // [experts+1] slot offsets (null: one segment [0, tokens))
+    const __half* score;       // per-slot fp16 factor (kScore)
+    __half* out;               // out[slot][out_stride]
+    int tokens, n, k, padded, x_stride, out_stride, experts, row_tiles, half_rows;
+};
+
+// Eight signed nibbles (one code word: columns c..c+7, even columns in the
+// low nibbles) -> eight fp16 weights fp16(q * s), in the K order
+// c, c+2, c+4, c+6, c+1, c+3, c+5, c+7 (activations are staged in that order).
+__device__ __forceinline__ half8 dequant8(std::uint32_t word, half2v s2) {
+    const std::uint32_t u = word ^ 0x88888888u;     // nibble u = q + 8
+    const std::uint32_t lo = u & 0x0F0F0F0Fu;       // columns c, c+2, c+4, c+6
+    const std::uint32_t hi = (u >> 4) & 0x0F0F0F0Fu;  // columns c+1, c+3, c+5, c+7
+    const half2v bias = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    half2v p[4];
+    p[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u));
+    p[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u));
+    p[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u));
+    p[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u));
+    half8 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v q = p[i] + bias;  // exact: q in [-8, 7]
+        const half2v v = q * s2;       // one fp16 rounding of q * s
+        w[2 * i] = v[0];
+        w[2 * i + 1] = v[1];
+    }
+    return w;
+}
+
+// Eight consecutive activations x0..x7 -> x0, x2, x4, x6, x1, x3, x5, x7.
+__device__ __forceinline__ uint4 interleave8(uint4 v) {
+    uint4 r;
+    r.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
+    r.y = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
+    r.z = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
+    r.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
+    return r;
+}
+
+__device__ __forceinline__ float silu(float g) { return __fdiv_rn(g, 1.0f + expf(-g)); }
+
+// Register staging of one chunk: 2 x 16 code bytes, one scale pair, 4 x 8 activations.
+struct Stage {
+    uint4 w[2];
+    std::uint32_t s;
+    uint4 x[4];
+};
+
+template <int EPI>
+__global__ __launch_bounds__(512) void q4_mfma(Q4Gemm p) {
+    __shared__ __attribute__((aligned(16))) std::uint8_t wl[kRows * kWStride];
+    __shared__ std::uint32_t sl[kRows][2];
+    __shared__ __attribute__((aligned(16))) _Float16 xl[kPassTokens * kXStride];
+
+    // Workgroup -> (expert, row tile); with experts % 8 == 0 every expert's
+    // tiles run on one XCD (round-robin dispatch), so its routed activation
+    // rows are fetched into one L2.
+    const int linear = blockIdx.x;
+    int expert, tile;
+    if (p.experts % 8 == 0) {
+        const int xcd = linear % 8, idx = linear / 8;
+        expert = 8 * (idx / p.row_tiles) + xcd;
+        tile = idx % p.row_tiles;
+    } else {
+        expert = linear / p.row_tiles;
+        tile = linear % p.row_tiles;
+    }
+    const int seg_begin = p.seg ? p.seg[expert] : 0;
+    const int seg_end = p.seg ? p.seg[expert + 1] : p.tokens;
+    if (seg_begin >= seg_end) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4, m = lane & 15;
+    const std::uint8_t* codes = p.codes + expert * p.code_stride;
+    const __half* scales = p.scales + expert * p.scale_stride;
+    const int row_bytes = p.padded / 2, groups = p.padded / 64;
+    const int chunks = (p.padded + kChunk - 1) / kChunk;
+
+    // Tile row slot -> weight row (clamped; clamped rows are never stored).
+    auto weight_row = [&](int slot) {
+        if (EPI == kSwiGLU) {
+            const int r = tile * (kRows / 2) + (slot & 63);
+            return slot < 64 ? min(r, p.half_rows - 1) : min(p.half_rows + r, p.n - 1);
+        }
+        return min(tile * kRows + slot, p.n - 1);
+    };
+    // This lane's MFMA column (weight row slot): plain waves own 16 consecutive
+    // slots; SwiGLU waves own 8 gate slots and the 8 matching up slots.
+    const int my_slot = EPI == kSwiGLU ? (m < 8 ? 8 * wave + m : 64 + 8 * wave + (m - 8)) : 16 * wave + m;
+
+    // Staging assignment: code piece i covers row (tid + 512 i) / 8, bytes 16 * (tid % 8);
+    // scale pair: row tid / 2 (tid < 256), groups 2 * (tid % 2) .. +1;
+    // activation piece j: token (tid + 512 j) / 32, columns 8 * (tid % 32).
+    const std::uint8_t* wsrc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) wsrc[i] = codes + static_cast<std::int64_t>(weight_row((tid + 512 * i) >> 3)) * row_bytes + 16 * (tid & 7);
+    const __half* ssrc = scales + static_cast<std::int64_t>(weight_row((tid & 255) >> 1)) * groups + 2 * (tid & 1);
+
+    for (int pass = seg_begin; pass < seg_end; pass += kPassTokens) {
+        const int live = min(kPassTokens, seg_end - pass);
+        const int blocks = (live + 15) >> 4;
+        const __half* xsrc[4];
+        bool xlive[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = (tid + 512 * j) >> 5;
+            xlive[j] = t < live;
+            const int slot = pass + min(t, live - 1);
+            const int row = p.gather ? p.gather[slot] : slot;
+            xsrc[j] = p.x + static_cast<std::int64_t>(row) * p.x_stride + 8 * (tid & 31);
+        }
+
+        auto load = [&](int c, Stage& st) {
+            const int col0 = c * kChunk;
+            const bool second_half = col0 + 128 < p.padded;  // chunk tail past padded K is absent
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const bool ok = (tid & 7) < 4 || second_half;
+                st.w[i] = ok ? *reinterpret_cast<const uint4*>(wsrc[i] + col0 / 2) : make_uint4(0, 0, 0, 0);
+            }
+            {
+                const int g = col0 / 64 + 2 * (tid & 1);
+                st.s = (tid < 256 && g < groups) ? *reinterpret_cast<const std::uint32_t*>(ssrc + col0 / 64) : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = col0 + 8 * (tid & 31);
+                st.x[j] = (xlive[j] && col < p.k) ? *reinterpret_cast<const uint4*>(xsrc[j] + col0) : make_uint4(0, 0, 0, 0);
+            }
+        };
+        auto store = [&](const Stage& st) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int piece = tid + 512 * i;
+                *reinterpret_cast<uint4*>(wl + (piece >> 3) * kWStride + 16 * (piece & 7)) = st.w[i];
+            }
+            if (tid < 256) sl[tid >> 1][tid & 1] = st.s;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int piece = tid + 512 * j;
+                *reinterpret_cast<uint4*>(xl + (piece >> 5) * kXStride + 8 * (piece & 31)) = interleave8(st.x[j]);
+            }
+        };
+
+        float4v acc[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+        Stage st;
+        load(0, st);
+        for (int c = 0; c < chunks; ++c) {
+            __syncthreads();
+            store(st);
+            __syncthreads();
+            if (c + 1 < chunks) load(c + 1, st);
+
+            // Lane (m, q): weight slot my_slot, chunk columns [64q, 64q + 64) = group q.
+            const uint4* wrow = reinterpret_cast<const uint4*>(wl + my_slot * kWStride + 32 * q);
+            const uint4 w0 = wrow[0], w1 = wrow[1];
+            const std::uint32_t spair = sl[my_slot][q >> 1];
+            const std::uint32_t sbits = (q & 1) ? (spair >> 16) : (spair & 0xFFFFu);
+            const half2v s2 = __builtin_bit_cast(half2v, sbits | (sbits << 16));
+            const std::uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const half8 wf = dequant8(words[s], s2);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    if (b < blocks) {
+                        const half8 xf = *reinterpret_cast<const half8*>(xl + (16 * b + m) * kXStride + 64 * q + 8 * s);
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf, wf, acc[b], 0, 0, 0);
+                    }
+                }
+            }
+        }
+
+        // D layout: lane holds weight slot my_slot for tokens 16b + 4q + i.
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            if (b >= blocks) break;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * b + 4 * q + i;
+                const float v = acc[b][i];
+                if (EPI == kSwiGLU) {
+                    const float other = __shfl_xor(v, 8, 64);  // lane m^8 holds the paired up/gate row
+                    const int col = tile * (kRows / 2) + 8 * wave + (m & 7);
+                    if (m < 8 && t < live && col < p.half_rows) {
+                        const float g = __half2float(from_f32<__half>(v));
+                        const float u = __half2float(from_f32<__half>(other));
+                        const float a = __half2float(from_f32<__half>(silu(g)));
+                        p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + col] = from_f32<__half>(__fmul_rn(a, u));
+                    }
+                } else {
+                    const int row = tile * kRows + my_slot;
+                    if (t < live && row < p.n) {
+                        float y = __half2float(from_f32<__half>(v));
+                        if (EPI == kScore) y = __fmul_rn(y, __half2float(p.score[pass + t]));
+                        p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + row] = from_f32<__half>(y);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Routing: one workgroup. Pair i = token * top_k + position. Pass 1 counts
+// pairs per expert (LDS atomics give each pair a rank in its expert), a scan
+// gives segment offsets, pass 2 places every pair at offset + rank.
+__global__ __launch_bounds__(1024) void moe_route(const std::int64_t* __restrict__ ids,
+                                                  const __half* __restrict__ scores, int pairs, int top_k,
+                                                  int experts, int* __restrict__ seg, int* __restrict__ status,
+                                                  int* __restrict__ pair_slot, int* __restrict__ slot_token,
+                                                  __half* __restrict__ slot_score) {
+    __shared__ int count[kMaxExperts];
+    __shared__ int scan[kMaxExperts];
+    __shared__ int invalid;
+    const int tid = threadIdx.x;
+    for (int e = tid; e < experts; e += 1024) count[e] = 0;
+    if (tid == 0) invalid = 0;
+    __syncthreads();
+    for (int i = tid; i < pairs; i += 1024) {
+        const std::int64_t e = ids[i];
+        if (e < 0 || e >= experts) {
+            pair_slot[i] = -1;
+            atomicAdd(&invalid, 1);
+        } else {
+            pair_slot[i] = atomicAdd(&count[e], 1);
+        }
+    }
+    __syncthreads();
+    // Inclusive Hillis-Steele scan over the expert counts.
+    for (int e = tid; e < experts; e += 1024) scan[e] = count[e];
+    __syncthreads();
+    for (int d = 1; d < experts; d <<= 1) {
+        int add[1] = {0};
+        const int e = tid;
+        if (e < experts && e >= d) add[0] = scan[e - d];
+        __syncthreads();
+        if (e < experts) scan[e] += add[0];
+        __syncthreads();
+    }
+    for (int e = tid; e < experts; e += 1024) seg[e + 1] = scan[e];
+    if (tid == 0) {
+        seg[0] = 0;
+        *status = invalid;
+    }
+    for (int i = tid; i < pairs; i += 1024) {
+        const int rank = pair_slot[i];
+        if (rank < 0) continue;
+        const int e = static_cast<int>(ids[i]);
+        const int slot = scan[e] - count[e] + rank;
+        pair_slot[i] = slot;
+        slot_token[slot] = i / top_k;
+        slot_score[slot] = scores[i];
+    }
+}
+
+// Combine: one workgroup per token; each thread owns 8 consecutive columns.
+__global__ __launch_bounds__(256) void moe_combine(const std::int64_t* __restrict__ ids,
+                                                   const int* __restrict__ pair_slot, const __half* __restrict__ v,
+                                                   __half* __restrict__ out, int top_k, int hidden) {
+    const int token = blockIdx.x;
+    int order[16];
+    std::int64_t key[16];
+    int n = 0;
+    for (int pos = 0; pos < top_k; ++pos) {
+        const int slot = pair_slot[token * top_k + pos];
+        if (slot < 0) continue;
+        const std::int64_t e = ids[token * top_k + pos];
+        int at = n++;
+        while (at > 0 && key[at - 1] > e) {  // stable insertion: ascending expert, then position
+            key[at] = key[at - 1];
+            order[at] = order[at - 1];
+            --at;
+        }
+        key[at] = e;
+        order[at] = slot;
+    }
+    for (int col = 8 * threadIdx.x; col < hidden; col += 8 * 256) {
+        half2v acc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = half2v{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
+        for (int i = 0; i < n; ++i) {
+            const uint4 r = *reinterpret_cast<const uint4*>(v + static_cast<std::int64_t>(order[i]) * hidden + col);
+            acc[0] += __builtin_bit_cast(half2v, r.x);
+            acc[1] += __builtin_bit_cast(half2v, r.y);
+            acc[2] += __builtin_bit_cast(half2v, r.z);
+            acc[3] += __builtin_bit_cast(half2v, r.w);
+        }
+        uint4 o;
+        o.x = __builtin_bit_cast(std::uint32_t, acc[0]);
+        o.y = __builtin_bit_cast(std::uint32_t, acc[1]);
+        o.z = __builtin_bit_cast(std::uint32_t, acc[2]);
+        o.w = __builtin_bit_cast(std::uint32_t, acc[3]);
+        *reinterpret_cast<uint4*>(out + static_cast<std::int64_t>(token) * hidden + col) = o;
+    }
+}
+
+template <int EPI>
+void launch_q4_mfma(const Q4Gemm& p, hipStream_t stream) {
+    const dim3 grid(p.experts * p.row_tiles);
+    q4_mfma<EPI><<<grid, kWaves * 64, 0, stream>>>(p);
+}
+
+std::uint64_t align256(std::uint64_t v) { return (v + 255) / 256 * 256; }
+
+}  // namespace
+
+// Workspace of one MoE call (offsets in bytes, each section 256-byte aligned):
+// seg int32[experts+1], status int32, pair_slot int32[P], slot_token int32[P],
+// slot_score fp16[P], h fp16[P][inter], v fp16[P][hidden]; P = tokens * top_k.
+struct MoELayout {
+    std::uint64_t seg, status, pair_slot, slot_token, slot_score, h, v, total;
+};
+
+MoELayout moe_layout(std::int64_t tokens, std::int64_t top_k, std::int64_t experts, std::int64_t hidden,
+                     std::int64_t inter) {
+    const std::uint64_t pairs = static_cast<std::uint64_t>(tokens * top_k);
+    MoELayout l;
+    l.seg = 0;
+    l.status = align256(4 * (experts + 1));
+    l.pair_slot = l.status + 256;
+    l.slot_token = l.pair_slot + align256(4 * pairs);
+    l.slot_score = l.slot_token + align256(4 * pairs);
+    l.h = l.slot_score + align256(2 * pairs);
+    l.v = l.h + align256(2 * pairs * inter);
+    l.total = l.v + align256(2 * pairs * hidden);
+    return l;
+}
+
+void moe_validate(int tokens, int top_k, int experts, int hidden, int inter) {
+    require(tokens > 0 && top_k > 0 && top_k <= 16 && experts > 0 && experts <= kMaxExperts,
+            "MoE needs tokens > 0, 0 < top_k <= 16, 0 < experts <= 1024");
+    require(hidden > 0 && inter > 0 && hidden % 8 == 0 && inter % 8 == 0,
+            "MoE hidden and intermediate sizes must be positive multiples of 8");
+    require(static_cast<std::int64_t>(tokens) * top_k * std::max(hidden, 2 * inter) < INT32_MAX,
+            "MoE routed rows exceed int32 geometry");
+}
+
+void q4_gemm_launch(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
+                    int padded, int dtype, hipStream_t stream) {
+    require(x && codes && scales && out, "null Q4 operand");
+    require(tokens > 0 && n > 0 && k > 0 && padded == padded_k(k), "invalid Q4 geometry");
+    require(static_cast<std::int64_t>(tokens) * n < INT32_MAX, "Q4 output count exceeds int32");
+    require(dtype == kF16, "the Q4 matrix-core route takes FP16 activations");
+    require(k % 8 == 0 && aligned(x, 16), "the Q4 matrix-core route needs k % 8 == 0 and 16-byte aligned x");
+    require(aligned(codes, 16) && aligned(scales, 4) && aligned(out, 2), "misaligned Q4 operand");
+    Q4Gemm p{};
+    p.x = static_cast<const __half*>(x);
+    p.codes = static_cast<const std::uint8_t*>(codes);
+    p.scales = static_cast<const __half*>(scales);
+    p.out = static_cast<__half*>(out);
+    p.tokens = tokens;
+    p.n = n;
+    p.k = k;
+    p.padded = padded;
+    p.x_stride = k;
+    p.out_stride = n;
+    p.experts = 1;
+    p.row_tiles = (n + kRows - 1) / kRows;
+    launch_q4_mfma<kPlain>(p, stream);
+}
+
+void moe_q4_launch(const void* x, const std::int64_t* ids, const void* scores, const void* gu_codes,
+                   const void* gu_scales, const void* dn_codes, const void* dn_scales, void* out, void* workspace,
+                   std::uint64_t workspace_bytes, int tokens, int top_k, int experts, int hidden, int inter,
+                   hipStream_t stream) {
+    moe_validate(tokens, top_k, experts, hidden, inter);
+    require(x && ids && scores && gu_codes && gu_scales && dn_codes && dn_scales && out && workspace,
+            "null MoE operand");
+    const MoELayout l = moe_layout(tokens, top_k, experts, hidden, inter);
+    require(workspace_bytes >= l.total, "MoE workspace is too small");
+    require(aligned(x, 16) && aligned(out, 16) && aligned(workspace, 256) && aligned(ids, 8) && aligned(scores, 2),
+            "misaligned MoE operand");
+    require(aligned(gu_codes, 16) && aligned(dn_codes, 16) && aligned(gu_scales, 4) && aligned(dn_scales, 4),
+            "misaligned Q4 expert plane");
+    auto* ws = static_cast<std::uint8_t*>(workspace);
+    int* seg = reinterpret_cast<int*>(ws + l.seg);
+    int* status = reinterpret_cast<int*>(ws + l.status);
+    int* pair_slot = reinterpret_cast<int*>(ws + l.pair_slot);
+    int* slot_token = reinterpret_cast<int*>(ws + l.slot_token);
+    auto* slot_score = reinterpret_cast<__half*>(ws + l.slot_score);
+    auto* h = reinterpret_cast<__half*>(ws + l.h);
+    auto* v = reinterpret_cast<__half*>(ws + l.v);
+    const int pairs = tokens * top_k;
+
+    moe_route<<<1, 1024, 0, stream>>>(ids, static_cast<const __half*>(scores), pairs, top_k, experts, seg, status,
+                                      pair_slot, slot_token, slot_score);
+
+    const int gu_padded = static_cast<int>(padded_k(hidden));
+    const int dn_padded = static_cast<int>(padded_k(inter));
+    Q4Gemm gu{};
+    gu.x = static_cast<const __half*>(x);
+    gu.gather = slot_token;
+    gu.codes = static_cast<const std::uint8_t*>(gu_codes);
+    gu.scales = static_cast<const __half*>(gu_scales);
+    gu.code_stride = static_cast<std::int64_t>(2 * inter) * (gu_padded / 2);
+    gu.scale_stride = static_cast<std::int64_t>(2 * inter) * (gu_padded / 64);
+    gu.seg = seg;
+    gu.out = h;
+    gu.tokens = pairs;
+    gu.n = 2 * inter;
+    gu.k = hidden;
+    gu.padded = gu_padded;
+    gu.x_stride = hidden;
+    gu.out_stride = inter;
+    gu.experts = experts;
+    gu.half_rows = inter;
+    gu.row_tiles = (inter + kRows / 2 - 1) / (kRows / 2);
+    launch_q4_mfma<kSwiGLU>(gu, stream);
+
+    Q4Gemm dn{};
+    dn.x = h;
+    dn.codes = static_cast<const std::uint8_t*>(dn_codes);
+    dn.scales = static_cast<const __half*>(dn_scales);
+    dn.code_stride = static_cast<std::int64_t>(hidden) * (dn_padded / 2);
+    dn.scale_stride = static_cast<std::int64_t>(hidden) * (dn_padded / 64);
+    dn.seg = seg;
+    dn.score = slot_score;
+    dn.out = v;
+    dn.tokens = pairs;
+    dn.n = hidden;
+    dn.k = inter;
+    dn.padded = dn_padded;
+    dn.x_stride = inter;
+    dn.out_stride = hidden;
+    dn.experts = experts;
+    dn.row_tiles = (hidden + kRows - 1) / kRows;
+    launch_q4_mfma<kScore>(dn, stream);
+
+    moe_combine<<<tokens, 256, 0, stream>>>(ids, pair_slot, v, static_cast<__half*>(out), top_k, hidden);
+}
+
+}  // namespace vt
+
+#define VT_EXPORT extern "C" __attribute__((visibility("default")))
+
+// Extension: the W4A16 contract GEMM on matrix cores (fp16 activations).
+VT_EXPORT int venturi_q4_gemm_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n,
+                                  int k, int padded, int dtype, void* stream) {
+    return vt::guarded([&] {
+        vt::q4_gemm_launch(x, codes, scales, out, tokens, n, k, padded, dtype, static_cast<hipStream_t>(stream));
+    });
+}
+
+// Extension: workspace bytes of venturi_moe_q4_run (0 on invalid geometry).
+VT_EXPORT std::uint64_t venturi_moe_q4_bytes(int tokens, int top_k, int experts, int hidden, int inter) {
+    try {
+        vt::moe_validate(tokens, top_k, experts, hidden, inter);
+        return vt::moe_layout(tokens, top_k, experts, hidden, inter).total;
+    } catch (const std::exception& e) {
+        vt::set_error(e.what());
+        return 0;
+    }
+}
+
+// Extension: the routed-expert Q4 W4A16 MoE (flash_next_moe.py:139-161) in four
+// launches: routing, gate/up GEMM with SiLU*up, down GEMM with the score,
+// per-token combine. ids int64 [tokens][top_k], scores fp16 [tokens][top_k],
+// expert planes stacked [experts][rows][...].
+VT_EXPORT int venturi_moe_q4_run(const void* x, const std::int64_t* ids, const void* scores, const void* gu_codes,
+                                 const void* gu_scales, const void* dn_codes, const void* dn_scales, void* out,
+                                 void* workspace, std::uint64_t workspace_bytes, int tokens, int top_k, int experts,
+                                 int hidden, int inter, void* stream) {
+    return vt::guarded([&] {
+        vt::moe_q4_launch(x, ids, scores, gu_codes, gu_scales, dn_codes, dn_scales, out, workspace, workspace_bytes,
+                          tokens, top_k, experts, hidden, inter, static_cast<hipStream_t>(stream));
+    });
+}

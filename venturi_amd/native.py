@@ -35,6 +35,18 @@ SIGNATURES = {
     "venturi_rms_q8_quantize_passes": ([_P] * 3 + [_U64, _I, _I, _F, _I, _P, _P], _I),
     "venturi_q8_pack_run": ([_P] * 3 + [_I] * 4 + [_P], _I),
     "venturi_q8_gemm_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
+    "venturi_q4_abi": ([], _I),
+    "venturi_q4_decode": ([_P] * 3 + [_I] * 3 + [_P], _I),
+    "venturi_q4_linear": ([_P] * 4 + [_I] * 4 + [_P], _I),
+    "venturi_q4_fused_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
+    "venturi_row_dequant_rows": ([_P] * 4 + [_I] * 5 + [_P], _I),
+    "venturi_ada_abi": ([], _I),
+    "venturi_ada_error": ([], C.c_char_p),
+    "venturi_q4_prepare": ([_I] * 5, _I),
+    "venturi_q4_run": ([_P] * 4 + [_I] * 6 + [_P], _I),
+    "venturi_q4_gemm_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
+    "venturi_moe_q4_bytes": ([_I] * 5, _U64),
+    "venturi_moe_q4_run": ([_P] * 9 + [_U64] + [_I] * 5 + [_P], _I),
 }
 
 _lock = threading.Lock()

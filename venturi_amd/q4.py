@@ -6,10 +6,22 @@ floored at 2^-24, codes = clamp(round_half_even(w / scale), -7, 7), and the
 W4A16 weight value fp16(q * scale).
 """
 
+from dataclasses import dataclass
+from pathlib import Path
+
 import torch
 from torch.nn import functional as F
 
+from .blocks import _DTYPES, _no_overlap, _shape, _stream, _tensor
 from .weights import Q4RowSplitWeight
+
+# Plan routes of a resident Q4 linear:
+#   mfma    W4A16 contract (fp16(q*scale) weights) on fp16 matrix cores, any tokens;
+#   generic the plugin order of q4_linear.cu:21-56 (FP32 weights), fp16/bf16;
+#   exact   the expert order of flash_next_q4.cu:23-34 (fp16 weights), fp16, <= 64 tokens;
+#   fused   the research order of q4_fused.cuh:10-89 (FP32 weights), fp16.
+# auto: mfma for fp16 activations, generic for bf16.
+Q4_ROUTES = ("auto", "mfma", "generic", "exact", "fused")
 
 
 def quantize_q4_rtn(weight, *, max_elements=16 * 2**20):
@@ -49,5 +61,254 @@ def decode_q4_fp16(weight):
     return values.reshape(weight.out_features, -1)[:, : weight.in_features].half()
 
 
+def _q4_planes(weight):
+    if not isinstance(weight, Q4RowSplitWeight):
+        raise TypeError("Q4RowSplitWeight required")
+    weight.validate()
+    if not bool(torch.isfinite(weight.scales).all()):
+        raise ValueError("scales must be finite")
+
+
+@dataclass(frozen=True)
+class ResidentQ4Linear:
+    """Owned device Q4 planes shared by many token-shape plans."""
+
+    backend: object
+    weight: Q4RowSplitWeight
+    dtype: torch.dtype
+
+    @property
+    def device(self):
+        return self.weight.codes.device
+
+    @property
+    def storage_tensors(self):
+        return (self.weight.codes, self.weight.scales)
+
+    @property
+    def in_features(self):
+        return self.weight.in_features
+
+    @property
+    def out_features(self):
+        return self.weight.out_features
+
+    def prepare(self, *, tokens, route="auto"):
+        _shape(tokens, self.out_features)
+        if tokens * self.out_features >= 2**31:
+            raise ValueError("Q4 output count must fit int32")
+        if route not in Q4_ROUTES:
+            raise ValueError(f"Q4 route must be one of {Q4_ROUTES}")
+        if route == "auto":
+            route = "mfma" if self.dtype == torch.float16 and self.in_features % 8 == 0 else "generic"
+        fp16 = self.dtype == torch.float16
+        if route == "mfma" and not (fp16 and self.in_features % 8 == 0):
+            raise ValueError("The Q4 matrix-core route takes FP16 activations and K % 8 == 0")
+        if route == "exact" and not (fp16 and tokens <= 64):
+            raise ValueError("The exact expert Q4 route takes FP16 activations and at most 64 tokens")
+        if route == "fused" and not (fp16 and tokens <= 65535):
+            raise ValueError("The fused Q4 route takes FP16 activations")
+        if route == "generic" and tokens > 4 * 65535:
+            raise ValueError("The generic Q4 route takes at most 262140 tokens")
+        self.backend.validate_device(self.dtype, self.device)
+        return Q4LinearPlan(self, tokens, route)
+
+    def decode(self, *, out, row=0):
+        """fp16 rows fp16(q * scale) of [row, row + len(out)) into ``out`` (blocks.cu:1077-1086)."""
+        rows = out.shape[0] if isinstance(out, torch.Tensor) and out.ndim == 2 else -1
+        if type(row) is not int or row < 0 or rows <= 0 or row + rows > self.out_features:
+            raise ValueError("Q4 decode rows must lie inside the matrix")
+        _tensor(out, (rows, self.in_features), torch.float16, self.device, "out")
+        _no_overlap(out, self.storage_tensors)
+        w = self.weight
+        with torch.cuda.device(self.device):
+            self.backend._check(
+                self.backend._native.venturi_row_dequant_rows(
+                    w.codes.data_ptr(), None, w.scales.data_ptr(), out.data_ptr(), row, rows, w.in_features,
+                    w.padded_k, 4, _stream(self.device),
+                )
+            )
+        return out
+
+
+@dataclass(frozen=True)
+class Q4LinearPlan:
+    """out[T, N] = x[T, K] @ W[N, K]^T without bias; caller-owned buffers only."""
+
+    resident: ResidentQ4Linear
+    tokens: int
+    kernel: str
+    workspace_bytes = 0
+
+    @property
+    def route(self):
+        return "venturi-q4-" + self.kernel
+
+    @property
+    def dtype(self):
+        return self.resident.dtype
+
+    @property
+    def device(self):
+        return self.resident.device
+
+    @property
+    def in_features(self):
+        return self.resident.in_features
+
+    @property
+    def out_features(self):
+        return self.resident.out_features
+
+    @property
+    def storage_tensors(self):
+        return self.resident.storage_tensors
+
+    def run(self, x, *, out, workspace=None):
+        if workspace is not None:
+            raise ValueError("Q4 Linear uses no workspace")
+        r = self.resident
+        _tensor(x, (self.tokens, r.in_features), r.dtype, r.device, "x")
+        _tensor(out, (self.tokens, r.out_features), r.dtype, r.device, "out")
+        _no_overlap(out, (x,) + r.storage_tensors)
+        w, lib, stream = r.weight, r.backend._native, _stream(r.device)
+        args = (x.data_ptr(), w.codes.data_ptr(), w.scales.data_ptr(), out.data_ptr())
+        with torch.cuda.device(r.device):
+            if self.kernel == "mfma":
+                status = lib.venturi_q4_gemm_run(
+                    *args, self.tokens, w.out_features, w.in_features, w.padded_k, _DTYPES[r.dtype], stream
+                )
+            elif self.kernel == "generic":
+                status = lib.venturi_q4_run(
+                    *args, w.out_features, w.in_features, w.padded_k, self.tokens, _DTYPES[r.dtype], 0, stream
+                )
+                if status < 0:
+                    raise RuntimeError(lib.venturi_ada_error().decode("utf-8", "replace"))
+            elif self.kernel == "exact":
+                code = lib.venturi_q4_linear(*args, self.tokens, w.out_features, w.in_features, w.padded_k, stream)
+                if code:
+                    raise RuntimeError(f"Q4 GEMV HIP launch failed: {code}")
+                status = 0
+            else:
+                status = lib.venturi_q4_fused_run(
+                    *args, self.tokens, w.out_features, w.in_features, w.padded_k, 0, stream
+                )
+            r.backend._check(status)
+        return out
+
+
 def upload_q4(backend, weight, *, device, dtype):
-    raise NotImplementedError("Q4 linear kernels are not in this build yet")
+    """Copies the Q4 planes to the device once (reference ada.py:46-58)."""
+    _q4_planes(weight)
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("Q4 activations require float16 or bfloat16")
+    target = backend.validate_device(dtype, device)
+    with torch.cuda.device(target):
+        codes = weight.codes.detach().to(target, copy=True)
+        scales = weight.scales.detach().to(target, copy=True)
+        torch.cuda.current_stream(target).synchronize()
+    return ResidentQ4Linear(backend, Q4RowSplitWeight(codes, scales, weight.in_features), dtype)
+
+
+# ---------------------------------------------------------------------------
+# The reference's stand-alone Q4 operator objects, over the same library.
+
+
+@dataclass(frozen=True)
+class PreparedQ4:
+    weight: Q4RowSplitWeight
+    ready: object
+
+
+class NativeQ4:
+    """Expert Q4 operators of ABI 1 (reference ops/flash_next_q4.py:17-89).
+
+    ``linear`` is the expert GEMV order (fp16(q*scale) weights, lane-strided
+    fmaf, 32-lane tree) for 1..64 fp16 tokens; ``decode`` writes the fp16
+    matrix. Device qualification is gfx950 instead of SM70.
+    """
+
+    def __init__(self, library=None, *, max_output_bytes=64 * 2**20):
+        from . import native
+
+        if type(max_output_bytes) is not int or max_output_bytes <= 0:
+            raise ValueError("Positive explicit output budget required")
+        self.max_output_bytes = max_output_bytes
+        self.lib = native.load(library)
+        self.library = Path(self.lib.path)
+        if self.lib.venturi_q4_abi() != 1:
+            raise ValueError("Unsupported Q4 operator ABI")
+
+    def prepare(self, weight, *, device):
+        from .blocks import is_gfx950
+
+        if not isinstance(weight, Q4RowSplitWeight) or weight.codes.device.type != "cpu":
+            raise ValueError("Explicit CPU Q4 descriptor required for preparation")
+        weight.validate()
+        if (
+            not torch.isfinite(weight.scales).all()
+            or (weight.scales < 0).any()
+            or weight.out_features * weight.in_features * 2 > self.max_output_bytes
+        ):
+            raise ValueError("Finite nonnegative Q4 scales and bounded matrix required")
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise ValueError("Explicit GPU device required")
+        with torch.cuda.device(device):
+            if not is_gfx950(device):
+                raise ValueError("This operator is qualified only for gfx950")
+            result = Q4RowSplitWeight(weight.codes.to(device), weight.scales.to(device), weight.in_features)
+            ready = torch.cuda.Event()
+            ready.record(torch.cuda.current_stream(device))
+        return PreparedQ4(result, ready)
+
+    def _lease(self, prepared):
+        if not isinstance(prepared, PreparedQ4) or prepared.weight.codes.device.type != "cuda":
+            raise ValueError("Explicit prepared GPU Q4 weight required")
+        w = prepared.weight
+        w.validate()
+        stream = torch.cuda.current_stream(w.codes.device)
+        stream.wait_event(prepared.ready)
+        w.codes.record_stream(stream)
+        w.scales.record_stream(stream)
+        return w, stream
+
+    def decode(self, prepared):
+        with torch.cuda.device(prepared.weight.codes.device):
+            w, stream = self._lease(prepared)
+            if w.out_features * w.in_features * 2 > self.max_output_bytes:
+                raise ValueError("Q4 decode exceeds output budget")
+            out = torch.empty((w.out_features, w.in_features), device=w.codes.device, dtype=torch.float16)
+            status = self.lib.venturi_q4_decode(
+                w.codes.data_ptr(), w.scales.data_ptr(), out.data_ptr(), w.out_features, w.in_features, w.padded_k,
+                stream.cuda_stream,
+            )
+            if status:
+                raise RuntimeError(f"Q4 decode HIP launch failed: {status}")
+            return out
+
+    def linear(self, x, prepared):
+        if not isinstance(prepared, PreparedQ4):
+            raise ValueError("Explicit prepared GPU Q4 weight required")
+        w = prepared.weight
+        if (
+            x.ndim != 2
+            or not 1 <= len(x) <= 64
+            or x.shape[1] != w.in_features
+            or x.dtype != torch.float16
+            or x.device != w.codes.device
+            or not x.is_contiguous()
+        ):
+            raise ValueError("Bounded contiguous FP16 GPU input required")
+        if len(x) * w.out_features * 2 > self.max_output_bytes:
+            raise ValueError("Q4 linear exceeds output budget")
+        with torch.cuda.device(x.device):
+            w, stream = self._lease(prepared)
+            out = torch.empty((len(x), w.out_features), device=x.device, dtype=x.dtype)
+            status = self.lib.venturi_q4_linear(
+                x.data_ptr(), w.codes.data_ptr(), w.scales.data_ptr(), out.data_ptr(), len(x), w.out_features,
+                w.in_features, w.padded_k, stream.cuda_stream,
+            )
+            if status:
+                raise RuntimeError(f"Q4 GEMV HIP launch failed: {status}")
+            return out
