@@ -33,6 +33,11 @@ TOKENS = (1, 4, 8, 16)
 HBM_PEAK_GBS = 8000.0
 
 
+def log(message):
+    """Progress of the bench's own stages, on stderr (stdout carries only the JSON line)."""
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
 def launch_bytes(m, n, k):
     padded = (k + 127) // 128 * 128
     return n * padded + n * (padded // 32) * 2 + m * k * 2 + m * n * 2
@@ -48,6 +53,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-prefill", action="store_true", help="skip the config-3 A8 prefill section")
+    p.add_argument("--no-moe", action="store_true", help="skip the config-4 routed-expert MoE section")
     return p.parse_args()
 
 
@@ -165,6 +171,90 @@ def prefill_a8(backend, device, steps, warmup):
     }
 
 
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
+    """routed-expert Q4 W4A16 MoE, 128 experts, H 2048, I 768, 512 tokens top-8.
+
+    Expert weights N(0, 0.02) packed on the device with quantize_q4_rtn
+    arithmetic; x fp16 N(0, 1); per token 8 distinct ids from a seeded
+    randperm(128); scores = softmax of 8 seeded N(0, 1) logits (fp32 -> fp16).
+    Two independent banks (2 x 321 MB) alternate so that no step is served
+    from the 256 MB Infinity Cache. One step = routing + gate/up GEMM with
+    SiLU*up + down GEMM with the score + ordered combine (four launches).
+    Algorithmic bytes per step = expert planes + x + out + ids + scores;
+    FLOPs = 2 * pairs * (2I*H + H*I).
+    """
+    from venturi_amd.moe import MoEGeometry, Q4ExpertBank
+
+    g = MoEGeometry(2048, 128, 8, 768)
+    tokens = 512
+    banks = []
+    for copy in range(2):
+        experts = []
+        for e in range(g.num_experts):
+            gen = torch.Generator(device=device).manual_seed(100_000 * copy + e)
+            gu = backend.quantize_q4(torch.randn(2 * g.intermediate_size, g.hidden_size, generator=gen, device=device) * 0.02)
+            dn = backend.quantize_q4(torch.randn(g.hidden_size, g.intermediate_size, generator=gen, device=device) * 0.02)
+            experts.append((gu, dn))
+        banks.append(Q4ExpertBank.upload(backend, g, experts, device=device))
+        del experts
+    cpu_gen = torch.Generator().manual_seed(4)
+    ids = torch.stack([torch.randperm(g.num_experts, generator=cpu_gen)[: g.top_k] for _ in range(tokens)])
+    scores = torch.softmax(torch.randn(tokens, g.top_k, generator=cpu_gen), -1).half()
+    x = torch.randn(tokens, g.hidden_size, generator=cpu_gen).half()
+    xd, idsd, scoresd = x.to(device), ids.to(device), scores.to(device)
+    plans = [b.prepare(tokens=tokens) for b in banks]
+    workspace = torch.empty(plans[0].workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty(tokens, g.hidden_size, dtype=torch.float16, device=device)
+    stream = torch.cuda.current_stream(device)
+    for i in range(warmup):
+        plans[i % 2].run(xd, idsd, scoresd, out=out, workspace=workspace)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(device)
+    a.record(stream)
+    for i in range(steps):
+        plans[i % 2].run(xd, idsd, scoresd, out=out, workspace=workspace)
+    b.record(stream)
+    b.synchronize()
+    step_s = a.elapsed_time(b) / 1e3 / steps
+    pairs = tokens * g.top_k
+    nbytes = banks[0].storage_nbytes + 2 * tokens * g.hidden_size * 2 + pairs * (8 + 2)
+    flops = 2 * pairs * (2 * g.intermediate_size * g.hidden_size + g.hidden_size * g.intermediate_size)
+    gbs = nbytes / step_s / 1e9
+    result = {
+        "workload": "config4: Q4 W4A16 routed experts, 128 experts, H 2048, I 768, 512 tokens top-8",
+        "us_per_step": round(step_s * 1e6, 2),
+        "GB/s": round(gbs, 1),
+        "TFLOP/s": round(flops / step_s / 1e12, 2),
+        "tokens_per_s": round(tokens / step_s, 1),
+        "bytes_per_step": nbytes,
+        "flops_per_step": flops,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "fp16_mfma_frac": round(flops / step_s / 1e12 / FP16_PEAK_TFLOPS, 4)},
+    }
+    if cpu_seconds > 0:
+        from oracle.cpu_path import CpuRoutedExperts, cpu_threads, q4_fp32_weight, time_calls
+
+        threads = cpu_threads()
+        bank = banks[0]
+        sample = list(range(16))
+        gate_up = [q4_fp32_weight(bank.gate_up_codes[e].cpu(), bank.gate_up_scales[e].cpu(), g.hidden_size) for e in sample]
+        down = [q4_fp32_weight(bank.down_codes[e].cpu(), bank.down_scales[e].cpu(), g.intermediate_size) for e in sample]
+        runner = CpuRoutedExperts(gate_up, down)
+        reps, elapsed = time_calls([lambda: runner.run(x, ids, scores, sample)], cpu_seconds)
+        full_s = elapsed / reps * g.num_experts / len(sample)
+        result["cpu_baseline"] = {
+            "value": round(nbytes / full_s / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"experts 0-15 of 128 ({reps} repetitions, {elapsed:.1f} s), staged-fp32 cpu_expert path "
+            f"with pre-materialised fp32 weights, scaled x8 to the full step ({full_s * 1e3:.1f} ms per step)",
+        }
+    del banks, plans
+    return result
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -176,6 +266,7 @@ def main():
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     backend = create_backend("hip")
+    log("packing config-2 weight copies")
     copies = build_copies(backend, device, args.copy_mb)
     gen = torch.Generator(device=device).manual_seed(7)
     xs = {m: {k: torch.randn(m, k, generator=gen, device=device).half() for k in {p[2] for p in PROJECTIONS}}
@@ -197,6 +288,7 @@ def main():
         if events is not None:
             events[1].record(stream)
 
+    log("config-2 decode: warm-up and timed region")
     for mi, pi in launches:
         run(mi, pi, args.warmup)
     torch.cuda.synchronize(device)
@@ -252,8 +344,13 @@ def main():
     }
     if not args.no_prefill:
         del plans
+        log("config-3 A8 prefill")
         result["prefill_a8"] = prefill_a8(backend, device, max(args.steps // 2, 3), 2)
+    if not args.no_moe:
+        log("config-4 routed-expert MoE")
+        result["moe_w4a16"] = moe_w4a16(backend, device, max(args.steps, 10), 3, 0 if args.no_cpu else 4.0)
     if not args.no_cpu:
+        log("CPU baseline (reference CPU path)")
         result["cpu_baseline"] = cpu_baseline(copies, xs, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 

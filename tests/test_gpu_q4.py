@@ -189,3 +189,21 @@ def test_status_codes_and_plugin_errors(backend, device):
     assert lib.venturi_q4_run(None, None, None, None, 1, 1, 128, 1, 0, 1, None) == -1
     assert lib.venturi_q4_gemm_run(None, None, None, None, 1, 1, 1, 128, 0, None) == -1
     assert "null" in backend._native.error()
+
+
+@pytest.mark.parametrize("k", [1, 63, 64, 65, 129, 2048, 4097])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_device_q4_pack_equals_rtn(backend, device, k, dtype):
+    """venturi_q4_pack_run == quantize_q4_rtn (flash_next_q4.py:26-52) byte for byte."""
+    from venturi_amd import quantize_q4_rtn
+
+    print(f"case q4-pack k={k} {dtype}", flush=True)
+    gen = torch.Generator().manual_seed(k)
+    w = (torch.randn(37, k, generator=gen) * 0.02).to(dtype)
+    w[0] = 0  # all-zero row: scale floor 2^-24, codes 0
+    if k >= 6:
+        w[1, :6] = torch.tensor([7.0, 0.5, 1.5, 2.5, -0.5, -1.5]).to(dtype)  # ties
+    ref = quantize_q4_rtn(w)
+    got = backend.quantize_q4(w.to(device))
+    assert torch.equal(got.codes.cpu(), ref.codes)
+    assert torch.equal(got.scales.cpu().view(torch.int16), ref.scales.view(torch.int16))

@@ -249,6 +249,39 @@ class HipBackend(Backend):
             )
         return Q8RowSplitWeight(codes, scales, k)
 
+    def quantize_q4(self, source):
+        """Device Q4 packing with the arithmetic of ``quantize_q4_rtn``.
+
+        ``source`` is a contiguous fp16/bf16/fp32 [N, K] tensor on this
+        backend's device; the result is a device-resident ``Q4RowSplitWeight``
+        whose bytes equal ``quantize_q4_rtn(source.cpu())``
+        (models/flash_next/flash_next_q4.py:26-52). (Extension: the reference
+        quantizes on the CPU only.)
+        """
+        if not isinstance(source, torch.Tensor) or source.ndim != 2 or not source.is_contiguous():
+            raise ValueError("Q4 packing requires a contiguous [N, K] tensor")
+        if source.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError("Device Q4 packing supports fp16/bf16/fp32 sources")
+        target = self.resolve_device(source.device)
+        n, k = source.shape
+        _shape(n, k)
+        padded = (k + 127) // 128 * 128
+        with torch.cuda.device(target):
+            if not bool(torch.isfinite(source).all()):
+                raise ValueError("Finite source weights required")
+            top = torch.clamp_min(source.abs().amax().float() / 7, 2**-24).half()
+            if not bool(torch.isfinite(top)) or not bool(torch.isfinite((top.float() * 7).half())):
+                raise ValueError("Source scale overflows FP16")
+            codes = torch.empty(n, padded // 2, dtype=torch.uint8, device=target)
+            scales = torch.empty(n, padded // 64, dtype=torch.float16, device=target)
+            self._check(
+                self._native.venturi_q4_pack_run(
+                    source.data_ptr(), codes.data_ptr(), scales.data_ptr(), n, k, padded, _DTYPES[source.dtype],
+                    _stream(target),
+                )
+            )
+        return Q4RowSplitWeight(codes, scales, k)
+
     def bind_linear(self, resident, *, tokens, route="auto"):
         _shape(tokens, 1)
         if resident._backend is not self:

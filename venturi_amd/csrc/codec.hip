@@ -6,6 +6,13 @@
 // round-to-nearest-even); code = clamp(rint(x / f32(scale)), -127, 127), or 0
 // when the stored scale is 0. The host rejects non-finite sources and scale
 // overflow before launch, as the reference does.
+//
+// Q4 (q4_g64_fp16): the arithmetic of quantize_q4_rtn
+// (models/flash_next/flash_next_q4.py:26-52): per 64-column group of the
+// zero-padded row, scale = fp16(max(f32(max|x|) / 7, 2^-24)); code =
+// clamp(rint(x / f32(scale)), -7, 7); groups wholly past k keep scale 0
+// (from_codes zero-fills the plane past ceil(k/64)). Nibbles are packed two's
+// complement, column 2j low (weights.py:108-130).
 #include "common.hpp"
 
 namespace vt {
@@ -43,8 +50,68 @@ __global__ __launch_bounds__(256) void q8_pack(const T* __restrict__ src, std::i
     if (sub == 0) scales[index] = stored;
 }
 
+template <class T>
+__global__ __launch_bounds__(256) void q4_pack(const T* __restrict__ src, std::uint8_t* __restrict__ codes,
+                                               __half* __restrict__ scales, int n, int k, int padded) {
+    // 8 lanes per 64-column group, 8 consecutive columns (4 code bytes) per lane.
+    const int groups = padded >> 6;
+    const std::int64_t index = (static_cast<std::int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 3;
+    const int sub = threadIdx.x & 7;
+    if (index >= static_cast<std::int64_t>(n) * groups) return;  // a group's 8 lanes exit together
+    const std::int64_t row = index / groups;
+    const int group = static_cast<int>(index % groups);
+    const int col = group * 64 + sub * 8;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = col + i < k ? to_f32(src[row * k + col + i]) : 0.0f;
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+    const bool live = group * 64 < k;
+    const __half stored = live ? from_f32<__half>(fmaxf(__fdiv_rn(mx, 7.0f), 0x1p-24f)) : __float2half(0.0f);
+    const float d = __half2float(stored);
+    std::uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int q = live ? static_cast<int>(fminf(fmaxf(rintf(__fdiv_rn(v[i], d)), -7.0f), 7.0f)) : 0;
+        word |= static_cast<std::uint32_t>(q & 15) << (4 * i);
+    }
+    *reinterpret_cast<std::uint32_t*>(codes + row * (padded / 2) + col / 2) = word;
+    if (sub == 0) scales[index] = stored;
+}
+
 }  // namespace
 }  // namespace vt
+
+// Extension (the reference quantizes Q4 on the CPU only): device
+// quantize_q4_rtn of an [n, k] fp16/bf16/fp32 matrix into codes [n][padded/2]
+// and scales [n][padded/64].
+extern "C" __attribute__((visibility("default"))) int venturi_q4_pack_run(const void* src, void* codes, void* scales,
+                                                                         int n, int k, int padded, int dtype,
+                                                                         void* stream) {
+    return vt::guarded([&] {
+        vt::require(src && codes && scales && n > 0 && k > 0 && padded == vt::padded_k(k), "invalid Q4 pack geometry");
+        vt::require(vt::aligned(codes, 4) && vt::aligned(scales, 2), "Q4 pack outputs must be aligned");
+        const std::int64_t lanes = static_cast<std::int64_t>(n) * (padded / 64) * 8;
+        const std::int64_t blocks = (lanes + 255) / 256;
+        vt::require(blocks <= INT32_MAX, "Q4 pack grid too large");
+        auto s = static_cast<hipStream_t>(stream);
+        auto* c = static_cast<std::uint8_t*>(codes);
+        auto* sc = static_cast<__half*>(scales);
+        const unsigned grid = static_cast<unsigned>(blocks);
+        if (dtype == vt::kF16)
+            vt::q4_pack<<<grid, 256, 0, s>>>(static_cast<const __half*>(src), c, sc, n, k, padded);
+        else if (dtype == vt::kBF16)
+            vt::q4_pack<<<grid, 256, 0, s>>>(static_cast<const __hip_bfloat16*>(src), c, sc, n, k, padded);
+        else if (dtype == vt::kF32)
+            vt::q4_pack<<<grid, 256, 0, s>>>(static_cast<const float*>(src), c, sc, n, k, padded);
+        else
+            throw vt::Invalid("unsupported source dtype");
+    });
+}
 
 // Extension (the reference packs on the CPU only): device Q8 packing of an
 // [n, k] fp16/bf16/fp32 matrix into codes [n][padded] and scales [n][padded/32].

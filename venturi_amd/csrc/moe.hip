@@ -23,6 +23,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace vt {
 namespace {
@@ -90,15 +91,8 @@ __device__ __forceinline__ uint4 interleave8(uint4 v) {
 
 __device__ __forceinline__ float silu(float g) { return __fdiv_rn(g, 1.0f + expf(-g)); }
 
-// Register staging of one chunk: 2 x 16 code bytes, one scale pair, 4 x 8 activations.
-struct Stage {
-    uint4 w[2];
-    std::uint32_t s;
-    uint4 x[4];
-};
-
 template <int EPI>
-__global__ __launch_bounds__(512) void q4_mfma(Q4Gemm p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void q4_mfma(Q4Gemm p) {
     __shared__ __attribute__((aligned(16))) std::uint8_t wl[kRows * kWStride];
     __shared__ std::uint32_t sl[kRows][2];
     __shared__ __attribute__((aligned(16))) _Float16 xl[kPassTokens * kXStride];
@@ -146,120 +140,325 @@ __global__ __launch_bounds__(512) void q4_mfma(Q4Gemm p) {
     // activation piece j: token (tid + 512 j) / 32, columns 8 * (tid % 32).
     const std::uint8_t* wsrc[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) wsrc[i] = codes + static_cast<std::int64_t>(weight_row((tid + 512 * i) >> 3)) * row_bytes + 16 * (tid & 7);
+    for (int i = 0; i < 2; ++i)
+        wsrc[i] = codes + static_cast<std::int64_t>(weight_row((tid + 512 * i) >> 3)) * row_bytes + 16 * (tid & 7);
     const __half* ssrc = scales + static_cast<std::int64_t>(weight_row((tid & 255) >> 1)) * groups + 2 * (tid & 1);
 
     for (int pass = seg_begin; pass < seg_end; pass += kPassTokens) {
         const int live = min(kPassTokens, seg_end - pass);
-        const int blocks = (live + 15) >> 4;
-        const __half* xsrc[4];
-        bool xlive[4];
+        // Token blocks of 16 (activation load j feeds block j), fixed at compile
+        // time so that no load sits behind a branch.
+        auto run_pass = [&](auto nb_tag) {
+            constexpr int NB = decltype(nb_tag)::value;
+            const __half* xrow[NB];
+            bool xlive[NB];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = (tid + 512 * j) >> 5;
-            xlive[j] = t < live;
-            const int slot = pass + min(t, live - 1);
-            const int row = p.gather ? p.gather[slot] : slot;
-            xsrc[j] = p.x + static_cast<std::int64_t>(row) * p.x_stride + 8 * (tid & 31);
-        }
+            for (int j = 0; j < NB; ++j) {
+                const int t = (tid + 512 * j) >> 5;
+                xlive[j] = t < live;
+                const int slot = pass + min(t, live - 1);
+                const int row = p.gather ? p.gather[slot] : slot;
+                xrow[j] = p.x + static_cast<std::int64_t>(row) * p.x_stride;
+            }
 
-        auto load = [&](int c, Stage& st) {
-            const int col0 = c * kChunk;
-            const bool second_half = col0 + 128 < p.padded;  // chunk tail past padded K is absent
+            // Every load is unconditional from a valid (clamped) address; data past
+            // the matrix is replaced by zeros when the stage is stored to LDS (after
+            // the wait that store needs anyway), never by writing the load's
+            // destination registers early, which would force a wait per load.
+            struct Stage {
+                uint4 w[2];
+                std::uint32_t s;
+                uint4 x[NB];
+                bool wok, sok, xok[NB];
+            };
+            auto load = [&](int c, Stage& st) {
+                const int col0 = c * kChunk;
+                const bool second_half = col0 + 128 < p.padded;  // chunk tail past padded K is absent
+                st.wok = second_half || (tid & 7) < 4;
+                const int wofs = second_half ? col0 / 2 : col0 / 2 - 64 * ((tid & 7) >> 2);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const bool ok = (tid & 7) < 4 || second_half;
-                st.w[i] = ok ? *reinterpret_cast<const uint4*>(wsrc[i] + col0 / 2) : make_uint4(0, 0, 0, 0);
-            }
-            {
-                const int g = col0 / 64 + 2 * (tid & 1);
-                st.s = (tid < 256 && g < groups) ? *reinterpret_cast<const std::uint32_t*>(ssrc + col0 / 64) : 0u;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
+                for (int i = 0; i < 2; ++i) st.w[i] = *reinterpret_cast<const uint4*>(wsrc[i] + wofs);
+                st.sok = col0 / 64 + 2 * (tid & 1) < groups;
+                st.s = *reinterpret_cast<const std::uint32_t*>(ssrc + col0 / 64 - (st.sok ? 0 : 2 * (tid & 1)));
                 const int col = col0 + 8 * (tid & 31);
-                st.x[j] = (xlive[j] && col < p.k) ? *reinterpret_cast<const uint4*>(xsrc[j] + col0) : make_uint4(0, 0, 0, 0);
-            }
-        };
-        auto store = [&](const Stage& st) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int piece = tid + 512 * i;
-                *reinterpret_cast<uint4*>(wl + (piece >> 3) * kWStride + 16 * (piece & 7)) = st.w[i];
-            }
-            if (tid < 256) sl[tid >> 1][tid & 1] = st.s;
+                for (int j = 0; j < NB; ++j) {
+                    st.x[j] = *reinterpret_cast<const uint4*>(xrow[j] + min(col, p.k - 8));
+                    st.xok[j] = xlive[j] && col < p.k;
+                }
+            };
+            auto store = [&](const Stage& st) {
+                const uint4 zero = make_uint4(0, 0, 0, 0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int piece = tid + 512 * j;
-                *reinterpret_cast<uint4*>(xl + (piece >> 5) * kXStride + 8 * (piece & 31)) = interleave8(st.x[j]);
-            }
-        };
+                for (int i = 0; i < 2; ++i) {
+                    const int piece = tid + 512 * i;
+                    *reinterpret_cast<uint4*>(wl + (piece >> 3) * kWStride + 16 * (piece & 7)) = st.wok ? st.w[i] : zero;
+                }
+                if (tid < 256) sl[tid >> 1][tid & 1] = st.sok ? st.s : 0u;
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const int piece = tid + 512 * j;
+                    *reinterpret_cast<uint4*>(xl + (piece >> 5) * kXStride + 8 * (piece & 31)) =
+                        st.xok[j] ? interleave8(st.x[j]) : zero;
+                }
+            };
 
-        float4v acc[4];
+            float4v acc[NB];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int b = 0; b < NB; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-        Stage st;
-        load(0, st);
-        for (int c = 0; c < chunks; ++c) {
-            __syncthreads();
-            store(st);
-            __syncthreads();
-            if (c + 1 < chunks) load(c + 1, st);
+            Stage st;
+            load(0, st);
+            for (int c = 0; c < chunks; ++c) {
+                __syncthreads();
+                store(st);
+                __syncthreads();
+                if (c + 1 < chunks) load(c + 1, st);  // in flight while chunk c computes
 
-            // Lane (m, q): weight slot my_slot, chunk columns [64q, 64q + 64) = group q.
-            const uint4* wrow = reinterpret_cast<const uint4*>(wl + my_slot * kWStride + 32 * q);
-            const uint4 w0 = wrow[0], w1 = wrow[1];
-            const std::uint32_t spair = sl[my_slot][q >> 1];
-            const std::uint32_t sbits = (q & 1) ? (spair >> 16) : (spair & 0xFFFFu);
-            const half2v s2 = __builtin_bit_cast(half2v, sbits | (sbits << 16));
-            const std::uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                // Lane (m, q): weight slot my_slot, chunk columns [64q, 64q + 64) = group q.
+                const uint4* wrow = reinterpret_cast<const uint4*>(wl + my_slot * kWStride + 32 * q);
+                const uint4 w0 = wrow[0], w1 = wrow[1];
+                const std::uint32_t spair = sl[my_slot][q >> 1];
+                const std::uint32_t sbits = (q & 1) ? (spair >> 16) : (spair & 0xFFFFu);
+                const half2v s2 = __builtin_bit_cast(half2v, sbits | (sbits << 16));
+                const std::uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const half8 wf = dequant8(words[s], s2);
+                for (int s = 0; s < 8; ++s) {
+                    const half8 wf = dequant8(words[s], s2);
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    if (b < blocks) {
+                    for (int b = 0; b < NB; ++b) {
                         const half8 xf = *reinterpret_cast<const half8*>(xl + (16 * b + m) * kXStride + 64 * q + 8 * s);
                         acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf, wf, acc[b], 0, 0, 0);
                     }
                 }
             }
-        }
 
-        // D layout: lane holds weight slot my_slot for tokens 16b + 4q + i.
+            // D layout: lane holds weight slot my_slot for tokens 16b + 4q + i.
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            if (b >= blocks) break;
+            for (int b = 0; b < NB; ++b) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * b + 4 * q + i;
-                const float v = acc[b][i];
-                if (EPI == kSwiGLU) {
-                    const float other = __shfl_xor(v, 8, 64);  // lane m^8 holds the paired up/gate row
-                    const int col = tile * (kRows / 2) + 8 * wave + (m & 7);
-                    if (m < 8 && t < live && col < p.half_rows) {
-                        const float g = __half2float(from_f32<__half>(v));
-                        const float u = __half2float(from_f32<__half>(other));
-                        const float a = __half2float(from_f32<__half>(silu(g)));
-                        p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + col] = from_f32<__half>(__fmul_rn(a, u));
-                    }
-                } else {
-                    const int row = tile * kRows + my_slot;
-                    if (t < live && row < p.n) {
-                        float y = __half2float(from_f32<__half>(v));
-                        if (EPI == kScore) y = __fmul_rn(y, __half2float(p.score[pass + t]));
-                        p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + row] = from_f32<__half>(y);
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * b + 4 * q + i;
+                    const float v = acc[b][i];
+                    if (EPI == kSwiGLU) {
+                        const float other = __shfl_xor(v, 8, 64);  // lane m^8 holds the paired up/gate row
+                        const int col = tile * (kRows / 2) + 8 * wave + (m & 7);
+                        if (m < 8 && t < live && col < p.half_rows) {
+                            const float g = __half2float(from_f32<__half>(v));
+                            const float u = __half2float(from_f32<__half>(other));
+                            const float a = __half2float(from_f32<__half>(silu(g)));
+                            p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + col] =
+                                from_f32<__half>(__fmul_rn(a, u));
+                        }
+                    } else {
+                        const int row = tile * kRows + my_slot;
+                        if (t < live && row < p.n) {
+                            float y = __half2float(from_f32<__half>(v));
+                            if (EPI == kScore) y = __fmul_rn(y, __half2float(p.score[pass + t]));
+                            p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + row] = from_f32<__half>(y);
+                        }
                     }
                 }
             }
+        };
+        switch ((live + 15) >> 4) {
+            case 1: run_pass(std::integral_constant<int, 1>{}); break;
+            case 2: run_pass(std::integral_constant<int, 2>{}); break;
+            case 3: run_pass(std::integral_constant<int, 3>{}); break;
+            default: run_pass(std::integral_constant<int, 4>{}); break;
+        }
+        __syncthreads();  // the next pass restages LDS
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Tiled expert planes (built at upload): a matrix is cut into tiles of 128 rows
+// x 256 columns, stored tile after tile in [row tile][chunk] order, so one
+// workgroup's stage is 16 KB of contiguous codes. Inside a tile, row block w
+// (16 rows, one wave) is 2 KB laid out [half h][lane l][16 bytes] with
+// l = 16q + m: lane (m, q) gets the 32 code bytes of its row m for chunk
+// columns [64q, 64q + 64) (group q) as two 1 KB contiguous wave loads. Scales:
+// [row tile][chunk][w][l] fp16, one 128-byte wave load. For gate/up, row block
+// w holds gate rows 8w..8w+7 of the tile's 64 (m < 8) and the matching up rows
+// (m >= 8). Padding rows and columns hold zero codes and scales.
+struct Q4Tiled {
+    const __half* x;            // activation rows (x_stride halves apart)
+    const int* gather;          // slot -> x row (null: slot itself)
+    const uint4* codes;         // expert 0 tiled codes
+    const __half* scales;       // expert 0 tiled scales
+    std::int64_t code_stride;   // uint4 units between experts
+    std::int64_t scale_stride;  // halves between experts
+    const int* seg;             // [experts + 1] slot offsets
+    const __half* score;        // per-slot fp16 factor (kScore)
+    __half* out;                // out[slot][out_stride]
+    int n, k, chunks, x_stride, out_stride, experts, row_tiles, half_rows;
+};
+
+constexpr int kTileCodes = 8 * 128;  // uint4 per (tile, chunk): 8 row blocks x 2 KB
+
+template <int EPI>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void q4_tiled(Q4Tiled p) {
+    __shared__ __attribute__((aligned(16))) _Float16 xl[2][kPassTokens * kXStride];
+
+    const int linear = blockIdx.x;
+    int expert, tile;
+    if (p.experts % 8 == 0) {  // an expert's tiles share one XCD (round-robin dispatch) and its L2
+        const int xcd = linear % 8, idx = linear / 8;
+        expert = 8 * (idx / p.row_tiles) + xcd;
+        tile = idx % p.row_tiles;
+    } else {
+        expert = linear / p.row_tiles;
+        tile = linear % p.row_tiles;
+    }
+    const int seg_begin = p.seg[expert];
+    const int seg_end = p.seg[expert + 1];
+    if (seg_begin >= seg_end) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4, m = lane & 15;
+    const uint4* wsrc = p.codes + expert * p.code_stride + (static_cast<std::int64_t>(tile) * p.chunks * 8 + wave) * 128 + lane;
+    const __half* ssrc = p.scales + expert * p.scale_stride + (static_cast<std::int64_t>(tile) * p.chunks * 8 + wave) * 64 + lane;
+
+    for (int pass = seg_begin; pass < seg_end; pass += kPassTokens) {
+        const int live = min(kPassTokens, seg_end - pass);
+        auto run_pass = [&](auto nb_tag) {
+            constexpr int NB = decltype(nb_tag)::value;
+            const __half* xrow[NB];
+            bool xlive[NB];
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int t = (tid + 512 * j) >> 5;
+                xlive[j] = t < live;
+                const int slot = pass + min(t, live - 1);
+                const int row = p.gather ? p.gather[slot] : slot;
+                xrow[j] = p.x + static_cast<std::int64_t>(row) * p.x_stride;
+            }
+            // Weight stages live in registers; activation stages in LDS. Loads are
+            // unconditional (clamped addresses); zeros replace data past k when
+            // the activations are written to LDS.
+            struct WStage {
+                uint4 a, b;
+                unsigned short s;
+            };
+            struct XStage {
+                uint4 v[NB];
+            };
+            auto load_w = [&](int c, WStage& w) {
+                const uint4* src = wsrc + static_cast<std::int64_t>(c) * kTileCodes;
+                w.a = src[0];
+                w.b = src[64];
+                w.s = __half_as_ushort(ssrc[static_cast<std::int64_t>(c) * 512]);
+            };
+            auto load_x = [&](int c, XStage& x) {
+                const int col = c * kChunk + 8 * (tid & 31);
+#pragma unroll
+                for (int j = 0; j < NB; ++j) x.v[j] = *reinterpret_cast<const uint4*>(xrow[j] + min(col, p.k - 8));
+            };
+            auto store_x = [&](int c, const XStage& x, _Float16* buf) {
+                const int col = c * kChunk + 8 * (tid & 31);
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const int piece = tid + 512 * j;
+                    // Masking by AND keeps the body free of branches (exact wait counts).
+                    const std::uint32_t keep = (xlive[j] && col < p.k) ? 0xFFFFFFFFu : 0u;
+                    uint4 v = interleave8(x.v[j]);
+                    v.x &= keep;
+                    v.y &= keep;
+                    v.z &= keep;
+                    v.w &= keep;
+                    *reinterpret_cast<uint4*>(buf + (piece >> 5) * kXStride + 8 * (piece & 31)) = v;
+                }
+            };
+
+            float4v acc[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+            auto compute = [&](const WStage& w, const _Float16* buf) {
+                const half2v s2 = __builtin_bit_cast(half2v, static_cast<std::uint32_t>(w.s) * 0x10001u);
+                const std::uint32_t words[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
+#pragma unroll
+                for (int s = 0; s < 8; ++s) {
+                    const half8 wf = dequant8(words[s], s2);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const half8 xf = *reinterpret_cast<const half8*>(buf + (16 * b + m) * kXStride + 64 * q + 8 * s);
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf, wf, acc[b], 0, 0, 0);
+                    }
+                }
+            };
+
+            // Chunk c computes from weight stage c % 2 and LDS buffer c % 2 while
+            // the weights of c + 1 (and, once c's registers are consumed, c + 2)
+            // and the activations of c + 1 are in flight. The loop body has no
+            // branches: loads past the last chunk re-read it (clamped index) and
+            // the surplus activation stage is stored as zeros.
+            WStage w0, w1;
+            XStage xs;
+            load_w(0, w0);
+            load_w(min(1, p.chunks - 1), w1);
+            load_x(0, xs);
+            store_x(0, xs, xl[0]);
+            __syncthreads();
+            auto step = [&](int c, WStage& w) {
+                load_x(min(c + 1, p.chunks - 1), xs);
+                compute(w, xl[c & 1]);
+                load_w(min(c + 2, p.chunks - 1), w);
+                store_x(c + 1, xs, xl[(c + 1) & 1]);
+                __syncthreads();
+            };
+            int c = 0;
+            for (; c + 1 < p.chunks; c += 2) {
+                step(c, w0);
+                step(c + 1, w1);
+            }
+            if (c < p.chunks) step(c, w0);
+
+            // D layout: lane holds row slot m of the wave's block for tokens 16b + 4q + i.
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * b + 4 * q + i;
+                    const float v = acc[b][i];
+                    if (EPI == kSwiGLU) {
+                        const float other = __shfl_xor(v, 8, 64);  // lane m^8 holds the paired up/gate row
+                        const int col = tile * (kRows / 2) + 8 * wave + (m & 7);
+                        if (m < 8 && t < live && col < p.half_rows) {
+                            const float g = __half2float(from_f32<__half>(v));
+                            const float u = __half2float(from_f32<__half>(other));
+                            const float a = __half2float(from_f32<__half>(silu(g)));
+                            p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + col] =
+                                from_f32<__half>(__fmul_rn(a, u));
+                        }
+                    } else {
+                        const int row = tile * kRows + 16 * wave + m;
+                        if (t < live && row < p.n) {
+                            float y = __half2float(from_f32<__half>(v));
+                            if (EPI == kScore) y = __fmul_rn(y, __half2float(p.score[pass + t]));
+                            p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + row] = from_f32<__half>(y);
+                        }
+                    }
+                }
+            }
+        };
+        switch ((live + 15) >> 4) {
+            case 1: run_pass(std::integral_constant<int, 1>{}); break;
+            case 2: run_pass(std::integral_constant<int, 2>{}); break;
+            case 3: run_pass(std::integral_constant<int, 3>{}); break;
+            default: run_pass(std::integral_constant<int, 4>{}); break;
         }
     }
 }
 
 // Routing: one workgroup. Pair i = token * top_k + position. Pass 1 counts
 // pairs per expert (LDS atomics give each pair a rank in its expert), a scan
-// gives segment offsets, pass 2 places every pair at offset + rank.
+// gives segment offsets, pass 2 places every pair at offset + rank. Each pass
+// handles kRouteBatch pairs per thread with all loads issued up front.
+constexpr int kRouteBatch = 8;
+
 __global__ __launch_bounds__(1024) void moe_route(const std::int64_t* __restrict__ ids,
                                                   const __half* __restrict__ scores, int pairs, int top_k,
                                                   int experts, int* __restrict__ seg, int* __restrict__ status,
@@ -272,25 +471,41 @@ __global__ __launch_bounds__(1024) void moe_route(const std::int64_t* __restrict
     for (int e = tid; e < experts; e += 1024) count[e] = 0;
     if (tid == 0) invalid = 0;
     __syncthreads();
-    for (int i = tid; i < pairs; i += 1024) {
-        const std::int64_t e = ids[i];
-        if (e < 0 || e >= experts) {
-            pair_slot[i] = -1;
-            atomicAdd(&invalid, 1);
-        } else {
-            pair_slot[i] = atomicAdd(&count[e], 1);
+    // Ranks of the first batch stay in registers; later batches (more than
+    // 1024 * kRouteBatch pairs) keep theirs in pair_slot between the passes.
+    int first_rank[kRouteBatch];
+    std::int64_t first_e[kRouteBatch];
+    for (int base = 0; base < pairs; base += 1024 * kRouteBatch) {
+        std::int64_t e[kRouteBatch];
+#pragma unroll
+        for (int u = 0; u < kRouteBatch; ++u) e[u] = ids[min(base + u * 1024 + tid, pairs - 1)];
+#pragma unroll
+        for (int u = 0; u < kRouteBatch; ++u) {
+            const int i = base + u * 1024 + tid;
+            int rank = -1;
+            if (i < pairs) {
+                if (e[u] < 0 || e[u] >= experts) {
+                    atomicAdd(&invalid, 1);
+                } else {
+                    rank = atomicAdd(&count[e[u]], 1);
+                }
+                if (base > 0) pair_slot[i] = rank;
+            }
+            if (base == 0) {
+                first_rank[u] = rank;
+                first_e[u] = e[u];
+            }
         }
     }
     __syncthreads();
-    // Inclusive Hillis-Steele scan over the expert counts.
+    // Inclusive Hillis-Steele scan over the expert counts (experts <= 1024).
     for (int e = tid; e < experts; e += 1024) scan[e] = count[e];
     __syncthreads();
     for (int d = 1; d < experts; d <<= 1) {
-        int add[1] = {0};
-        const int e = tid;
-        if (e < experts && e >= d) add[0] = scan[e - d];
+        int add = 0;
+        if (tid < experts && tid >= d) add = scan[tid - d];
         __syncthreads();
-        if (e < experts) scan[e] += add[0];
+        if (tid < experts) scan[tid] += add;
         __syncthreads();
     }
     for (int e = tid; e < experts; e += 1024) seg[e + 1] = scan[e];
@@ -298,48 +513,83 @@ __global__ __launch_bounds__(1024) void moe_route(const std::int64_t* __restrict
         seg[0] = 0;
         *status = invalid;
     }
-    for (int i = tid; i < pairs; i += 1024) {
-        const int rank = pair_slot[i];
-        if (rank < 0) continue;
-        const int e = static_cast<int>(ids[i]);
-        const int slot = scan[e] - count[e] + rank;
-        pair_slot[i] = slot;
-        slot_token[slot] = i / top_k;
-        slot_score[slot] = scores[i];
+    for (int base = 0; base < pairs; base += 1024 * kRouteBatch) {
+        int rank[kRouteBatch];
+        std::int64_t e[kRouteBatch];
+        __half sc[kRouteBatch];
+#pragma unroll
+        for (int u = 0; u < kRouteBatch; ++u) {
+            const int i = min(base + u * 1024 + tid, pairs - 1);
+            rank[u] = base == 0 ? first_rank[u] : pair_slot[i];
+            e[u] = base == 0 ? first_e[u] : ids[i];
+            sc[u] = scores[i];
+        }
+#pragma unroll
+        for (int u = 0; u < kRouteBatch; ++u) {
+            const int i = base + u * 1024 + tid;
+            if (i < pairs) {
+                int slot = -1;
+                if (rank[u] >= 0) {
+                    const int ex = static_cast<int>(e[u]);
+                    slot = scan[ex] - count[ex] + rank[u];
+                    slot_token[slot] = i / top_k;
+                    slot_score[slot] = sc[u];
+                }
+                pair_slot[i] = slot;
+            }
+        }
     }
 }
 
-// Combine: one workgroup per token; each thread owns 8 consecutive columns.
+// Combine: one wave per token (4 tokens per 256-thread workgroup); each lane
+// owns 8 consecutive columns per 512-column step. The token's slots are
+// ordered by ascending expert id (stable: position order for repeated ids) and
+// added in that order from +0 with fp16 adds, as index_add_ does per expert.
+template <int K>
 __global__ __launch_bounds__(256) void moe_combine(const std::int64_t* __restrict__ ids,
                                                    const int* __restrict__ pair_slot, const __half* __restrict__ v,
-                                                   __half* __restrict__ out, int top_k, int hidden) {
-    const int token = blockIdx.x;
-    int order[16];
-    std::int64_t key[16];
+                                                   __half* __restrict__ out, int tokens, int hidden) {
+    const int token = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (token >= tokens) return;
+    int order[K];
+    std::int64_t key[K];
     int n = 0;
-    for (int pos = 0; pos < top_k; ++pos) {
-        const int slot = pair_slot[token * top_k + pos];
-        if (slot < 0) continue;
-        const std::int64_t e = ids[token * top_k + pos];
-        int at = n++;
-        while (at > 0 && key[at - 1] > e) {  // stable insertion: ascending expert, then position
-            key[at] = key[at - 1];
-            order[at] = order[at - 1];
-            --at;
-        }
-        key[at] = e;
-        order[at] = slot;
+#pragma unroll
+    for (int p = 0; p < K; ++p) {
+        order[p] = pair_slot[token * K + p];
+        key[p] = order[p] < 0 ? INT64_MAX : ids[token * K + p];  // skipped pairs sort last
+        n += order[p] >= 0;
     }
-    for (int col = 8 * threadIdx.x; col < hidden; col += 8 * 256) {
+    // Stable bubble sort with static indices (keeps the arrays in registers).
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+#pragma unroll
+        for (int j = 0; j + 1 < K - i; ++j)
+            if (key[j] > key[j + 1]) {
+                const std::int64_t tk = key[j];
+                key[j] = key[j + 1];
+                key[j + 1] = tk;
+                const int to = order[j];
+                order[j] = order[j + 1];
+                order[j + 1] = to;
+            }
+    for (int col = 8 * lane; col < hidden; col += 8 * 64) {
+        uint4 r[K];
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+            r[i] = *reinterpret_cast<const uint4*>(v + static_cast<std::int64_t>(max(order[i], 0)) * hidden + col);
         half2v acc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j] = half2v{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
-        for (int i = 0; i < n; ++i) {
-            const uint4 r = *reinterpret_cast<const uint4*>(v + static_cast<std::int64_t>(order[i]) * hidden + col);
-            acc[0] += __builtin_bit_cast(half2v, r.x);
-            acc[1] += __builtin_bit_cast(half2v, r.y);
-            acc[2] += __builtin_bit_cast(half2v, r.z);
-            acc[3] += __builtin_bit_cast(half2v, r.w);
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            if (i < n) {
+                acc[0] += __builtin_bit_cast(half2v, r[i].x);
+                acc[1] += __builtin_bit_cast(half2v, r[i].y);
+                acc[2] += __builtin_bit_cast(half2v, r[i].z);
+                acc[3] += __builtin_bit_cast(half2v, r[i].w);
+            }
         }
         uint4 o;
         o.x = __builtin_bit_cast(std::uint32_t, acc[0]);
@@ -350,10 +600,34 @@ __global__ __launch_bounds__(256) void moe_combine(const std::int64_t* __restric
     }
 }
 
+template <int K>
+void launch_combine(const std::int64_t* ids, const int* pair_slot, const __half* v, __half* out, int tokens,
+                    int hidden, hipStream_t stream) {
+    moe_combine<K><<<(tokens + 3) / 4, 256, 0, stream>>>(ids, pair_slot, v, out, tokens, hidden);
+}
+
+void combine_dispatch(int top_k, const std::int64_t* ids, const int* pair_slot, const __half* v, __half* out,
+                      int tokens, int hidden, hipStream_t stream) {
+    switch (top_k) {
+#define VT_CASE(K) \
+    case K: launch_combine<K>(ids, pair_slot, v, out, tokens, hidden, stream); break;
+        VT_CASE(1) VT_CASE(2) VT_CASE(3) VT_CASE(4) VT_CASE(5) VT_CASE(6) VT_CASE(7) VT_CASE(8)
+        VT_CASE(9) VT_CASE(10) VT_CASE(11) VT_CASE(12) VT_CASE(13) VT_CASE(14) VT_CASE(15) VT_CASE(16)
+#undef VT_CASE
+        default: throw Invalid("top_k must be in [1, 16]");
+    }
+}
+
 template <int EPI>
 void launch_q4_mfma(const Q4Gemm& p, hipStream_t stream) {
     const dim3 grid(p.experts * p.row_tiles);
     q4_mfma<EPI><<<grid, kWaves * 64, 0, stream>>>(p);
+}
+
+template <int EPI>
+void launch_q4_tiled(const Q4Tiled& p, hipStream_t stream) {
+    const dim3 grid(p.experts * p.row_tiles);
+    q4_tiled<EPI><<<grid, kWaves * 64, 0, stream>>>(p);
 }
 
 std::uint64_t align256(std::uint64_t v) { return (v + 255) / 256 * 256; }
@@ -426,7 +700,7 @@ void moe_q4_launch(const void* x, const std::int64_t* ids, const void* scores, c
     require(workspace_bytes >= l.total, "MoE workspace is too small");
     require(aligned(x, 16) && aligned(out, 16) && aligned(workspace, 256) && aligned(ids, 8) && aligned(scores, 2),
             "misaligned MoE operand");
-    require(aligned(gu_codes, 16) && aligned(dn_codes, 16) && aligned(gu_scales, 4) && aligned(dn_scales, 4),
+    require(aligned(gu_codes, 16) && aligned(dn_codes, 16) && aligned(gu_scales, 2) && aligned(dn_scales, 2),
             "misaligned Q4 expert plane");
     auto* ws = static_cast<std::uint8_t*>(workspace);
     int* seg = reinterpret_cast<int*>(ws + l.seg);
@@ -441,48 +715,48 @@ void moe_q4_launch(const void* x, const std::int64_t* ids, const void* scores, c
     moe_route<<<1, 1024, 0, stream>>>(ids, static_cast<const __half*>(scores), pairs, top_k, experts, seg, status,
                                       pair_slot, slot_token, slot_score);
 
-    const int gu_padded = static_cast<int>(padded_k(hidden));
-    const int dn_padded = static_cast<int>(padded_k(inter));
-    Q4Gemm gu{};
+    // Tiled planes: gate/up has ceil(inter/64) row tiles, down ceil(hidden/128);
+    // chunks of 256 columns over the padded K.
+    const int gu_chunks = static_cast<int>((padded_k(hidden) + kChunk - 1) / kChunk);
+    const int dn_chunks = static_cast<int>((padded_k(inter) + kChunk - 1) / kChunk);
+    Q4Tiled gu{};
     gu.x = static_cast<const __half*>(x);
     gu.gather = slot_token;
-    gu.codes = static_cast<const std::uint8_t*>(gu_codes);
+    gu.codes = static_cast<const uint4*>(gu_codes);
     gu.scales = static_cast<const __half*>(gu_scales);
-    gu.code_stride = static_cast<std::int64_t>(2 * inter) * (gu_padded / 2);
-    gu.scale_stride = static_cast<std::int64_t>(2 * inter) * (gu_padded / 64);
+    gu.row_tiles = (inter + kRows / 2 - 1) / (kRows / 2);
+    gu.code_stride = static_cast<std::int64_t>(gu.row_tiles) * gu_chunks * kTileCodes;
+    gu.scale_stride = static_cast<std::int64_t>(gu.row_tiles) * gu_chunks * 512;
     gu.seg = seg;
     gu.out = h;
-    gu.tokens = pairs;
     gu.n = 2 * inter;
     gu.k = hidden;
-    gu.padded = gu_padded;
+    gu.chunks = gu_chunks;
     gu.x_stride = hidden;
     gu.out_stride = inter;
     gu.experts = experts;
     gu.half_rows = inter;
-    gu.row_tiles = (inter + kRows / 2 - 1) / (kRows / 2);
-    launch_q4_mfma<kSwiGLU>(gu, stream);
+    launch_q4_tiled<kSwiGLU>(gu, stream);
 
-    Q4Gemm dn{};
+    Q4Tiled dn{};
     dn.x = h;
-    dn.codes = static_cast<const std::uint8_t*>(dn_codes);
+    dn.codes = static_cast<const uint4*>(dn_codes);
     dn.scales = static_cast<const __half*>(dn_scales);
-    dn.code_stride = static_cast<std::int64_t>(hidden) * (dn_padded / 2);
-    dn.scale_stride = static_cast<std::int64_t>(hidden) * (dn_padded / 64);
+    dn.row_tiles = (hidden + kRows - 1) / kRows;
+    dn.code_stride = static_cast<std::int64_t>(dn.row_tiles) * dn_chunks * kTileCodes;
+    dn.scale_stride = static_cast<std::int64_t>(dn.row_tiles) * dn_chunks * 512;
     dn.seg = seg;
     dn.score = slot_score;
     dn.out = v;
-    dn.tokens = pairs;
     dn.n = hidden;
     dn.k = inter;
-    dn.padded = dn_padded;
+    dn.chunks = dn_chunks;
     dn.x_stride = inter;
     dn.out_stride = hidden;
     dn.experts = experts;
-    dn.row_tiles = (hidden + kRows - 1) / kRows;
-    launch_q4_mfma<kScore>(dn, stream);
+    launch_q4_tiled<kScore>(dn, stream);
 
-    moe_combine<<<tokens, 256, 0, stream>>>(ids, pair_slot, v, static_cast<__half*>(out), top_k, hidden);
+    combine_dispatch(top_k, ids, pair_slot, v, static_cast<__half*>(out), tokens, hidden, stream);
 }
 
 }  // namespace vt

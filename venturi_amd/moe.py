@@ -42,23 +42,59 @@ class MoEGeometry:
             raise ValueError("hidden and intermediate sizes must be multiples of 8")
 
 
-def _stack(weights, rows, cols, device):
-    codes = torch.empty((len(weights), rows, (cols + 127) // 128 * 64), dtype=torch.uint8, device=device)
-    scales = torch.empty((len(weights), rows, (cols + 127) // 128 * 2), dtype=torch.float16, device=device)
+def _row_order(rows, half, swiglu, device):
+    """Physical row of every tile slot (-1: padding), in tile order.
+
+    Tiles hold 128 row slots; slot 16w + m belongs to wave w. Plain matrices
+    use slot -> row tile*128 + slot. Gate/up tiles pair gate and up rows: wave
+    w's slots m < 8 are gate rows tile*64 + 8w + m and slots m >= 8 the up rows
+    ``half`` further on.
+    """
+    if not swiglu:
+        tiles = (rows + 127) // 128
+        order = torch.arange(tiles * 128, device=device)
+        return torch.where(order < rows, order, -1)
+    tiles = (half + 63) // 64
+    slot = torch.arange(tiles * 128, device=device)
+    tile, w, m = slot // 128, (slot % 128) // 16, slot % 16
+    gate = tile * 64 + 8 * w + (m % 8)
+    order = torch.where(m < 8, gate, gate + half)
+    return torch.where(gate < half, order, -1)
+
+
+def _tile(weights, rows, cols, swiglu, device):
+    """Stacked tiled planes of the experts (layout read by the grouped GEMM kernels).
+
+    Codes: [E][row tile][chunk][wave w][half h][lane l = 16q + m][16 bytes], the
+    16-byte piece h of the 32 code bytes of slot row (w, m) for chunk columns
+    [64q, 64q + 64). Scales: [E][row tile][chunk][w][l] fp16 of group q of the
+    chunk. Chunks are 256 columns of the padded K; padding is zero.
+    """
+    padded = (cols + 127) // 128 * 128
+    chunks = (padded + 255) // 256
+    order = _row_order(rows, rows // 2, swiglu, device)
+    tiles = order.numel() // 128
+    valid = order >= 0
+    source = order.clamp_min(0)
+    e_count = len(weights)
+    codes = torch.zeros((e_count, tiles * 128, chunks * 128), dtype=torch.uint8, device=device)
+    scales = torch.zeros((e_count, tiles * 128, chunks * 4), dtype=torch.float16, device=device)
     for e, w in enumerate(weights):
         if not isinstance(w, Q4RowSplitWeight) or (w.out_features, w.in_features) != (rows, cols):
             raise ValueError(f"expert {e} requires a Q4RowSplitWeight of shape [{rows}, {cols}]")
         w.validate()
         if not bool(torch.isfinite(w.scales).all()):
             raise ValueError("scales must be finite")
-        codes[e].copy_(w.codes)
-        scales[e].copy_(w.scales)
+        codes[e, :, : padded // 2] = w.codes.to(device)[source] * valid[:, None].to(torch.uint8)
+        scales[e, :, : padded // 64] = w.scales.to(device)[source] * valid[:, None].to(torch.float16)
+    codes = codes.view(e_count, tiles, 8, 16, chunks, 4, 2, 16).permute(0, 1, 4, 2, 6, 5, 3, 7).contiguous()
+    scales = scales.view(e_count, tiles, 8, 16, chunks, 4).permute(0, 1, 4, 2, 5, 3).contiguous()
     return codes, scales
 
 
 @dataclass(frozen=True)
 class Q4ExpertBank:
-    """All experts resident: gate_up planes [E][2I][...] and down planes [E][H][...]."""
+    """All experts resident in the tiled layout of ``_tile`` (gate/up rows paired per wave)."""
 
     backend: object
     geometry: MoEGeometry
@@ -75,8 +111,8 @@ class Q4ExpertBank:
         target = backend.resolve_device(device)
         g = geometry
         with torch.cuda.device(target):
-            gu = _stack([e[0] for e in experts], 2 * g.intermediate_size, g.hidden_size, target)
-            dn = _stack([e[1] for e in experts], g.hidden_size, g.intermediate_size, target)
+            gu = _tile([e[0] for e in experts], 2 * g.intermediate_size, g.hidden_size, True, target)
+            dn = _tile([e[1] for e in experts], g.hidden_size, g.intermediate_size, False, target)
             torch.cuda.current_stream(target).synchronize()
         return cls(backend, geometry, gu[0], gu[1], dn[0], dn[1])
 
