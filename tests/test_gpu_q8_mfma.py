@@ -82,3 +82,10 @@ def test_mfma_route_admission(backend, device):
     with pytest.raises(ValueError, match="MFMA"):
         resident.prepare(tokens=1, route="mfma")  # k % 8 != 0
     assert resident.prepare(tokens=8).route == "venturi-q8-exact"
+    codes, scales = random_q8(8, 64, 1)
+    resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.float16, device=device)
+    assert resident.prepare(tokens=1).route == "venturi-q8-exact"
+    assert resident.prepare(tokens=2).route == "venturi-q8-mfma"
+    assert resident.prepare(tokens=17).route == "venturi-q8-exact"
+    bf = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.bfloat16, device=device)
+    assert bf.prepare(tokens=8).route == "venturi-q8-exact"

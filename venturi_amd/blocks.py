@@ -354,7 +354,7 @@ class _Q8Linear:
 
     @property
     def storage_tensors(self):
-        return self.plan.resident.storage_tensors
+        return self.plan.storage_tensors
 
     def run(self, x, *, out, workspace=None):
         if workspace is not None:

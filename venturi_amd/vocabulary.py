@@ -8,19 +8,45 @@ family once:
 * ``exact``: the reference's canonical fp32 order (bytes identical to
   ``venturi_q8_head_run`` on the reference's GPUs);
 * ``mfma``: fp16 matrix cores with per-group fp32 scaling, for larger token
-  counts (same values up to fp32 association, see ``Q8OutputHead.route``);
-* ``auto``: ``exact`` for up to 4 tokens, where it is bound by HBM anyway,
-  otherwise ``mfma`` when the library provides it.
+  counts (same values up to fp32 association, see ``Q8OutputHead.route``).
+  It reads a tiled copy of the planes (16-row blocks x 64-column chunks in
+  MFMA operand order, built once by the first ``mfma`` plan and kept with the
+  resident weight), so every wave streams contiguous 1 KB blocks;
+* ``auto``: ``exact`` for one token (bit-identical to the reference and bound
+  by HBM), ``mfma`` from two tokens when its conditions hold (the canonical
+  order needs one fp32 FMA per token and weight, so ``exact`` becomes
+  VALU-bound as tokens grow), else ``exact``.
 """
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
+import threading
 
 import torch
 
 from .blocks import _DTYPES, Q8_ROUTES, _no_overlap, _shape, _stream, _tensor
 
-EXACT_MAX_AUTO_TOKENS = 4
+EXACT_MAX_AUTO_TOKENS = 1
 MFMA_MAX_TOKENS = 16
+_TILE_LOCK = threading.Lock()
+
+
+def tile_q8(codes, scales):
+    """Tiled planes of the matrix-core route (read by ``venturi_q8_tiled_run``).
+
+    Codes [row block][chunk][lane l = 16q + m][16 bytes]: row m of the block,
+    columns 64c + 8q .. +8 (group 2c) then 64c + 32 + 8q .. +8 (group 2c + 1).
+    Scales [row block][chunk][m][2] fp16. Rows are padded to a multiple of 16
+    with zero codes and scales.
+    """
+    n, padded = codes.shape
+    blocks, chunks = (n + 15) // 16, padded // 64
+    c = torch.zeros((blocks * 16, padded), dtype=torch.int8, device=codes.device)
+    s = torch.zeros((blocks * 16, padded // 32), dtype=torch.float16, device=codes.device)
+    c[:n] = codes
+    s[:n] = scales
+    tc = c.view(blocks, 16, chunks, 2, 4, 8).permute(0, 2, 4, 1, 3, 5).contiguous()
+    ts = s.view(blocks, 16, chunks, 2).permute(0, 2, 1, 3).contiguous()
+    return tc, ts
 
 
 def _ids(ids, vocab):
@@ -72,10 +98,20 @@ class ResidentQ8Vocabulary:
     _scales: torch.Tensor
     hidden_size: int
     dtype: torch.dtype = torch.bfloat16
+    _tiles: dict = field(default_factory=dict, compare=False, repr=False)
 
     @property
     def device(self):
         return self._codes.device
+
+    def tiled_planes(self):
+        """The matrix-core route's tiled copy of the planes (built on first use)."""
+        with _TILE_LOCK:
+            if "mfma" not in self._tiles:
+                with torch.cuda.device(self.device):
+                    self._tiles["mfma"] = tile_q8(self._codes, self._scales)
+                    torch.cuda.current_stream(self.device).synchronize()
+            return self._tiles["mfma"]
 
     @property
     def vocab_size(self):
@@ -110,7 +146,8 @@ class ResidentQ8Vocabulary:
             raise ValueError(
                 f"The Q8 MFMA route takes FP16 activations, K % 8 == 0 and at most {MFMA_MAX_TOKENS} tokens"
             )
-        return Q8OutputHead(self, tokens, route)
+        tiles = self.tiled_planes() if route == "mfma" else ()
+        return Q8OutputHead(self, tokens, route, tiles)
 
 
 @dataclass(frozen=True)
@@ -145,25 +182,33 @@ class Q8OutputHead:
     resident: ResidentQ8Vocabulary
     tokens: int
     kernel: str = "exact"
+    tiles: tuple = ()
     workspace_bytes = 0
 
     @property
     def route(self):
         return "venturi-q8-exact" if self.kernel == "exact" else "venturi-q8-mfma"
 
+    @property
+    def storage_tensors(self):
+        return self.resident.storage_tensors + tuple(self.tiles)
+
     def run(self, x, *, out):
         r = self.resident
         _tensor(x, (self.tokens, r.hidden_size), r.dtype, r.device, "x")
         _tensor(out, (self.tokens, r.vocab_size), r.dtype, r.device, "out")
-        _no_overlap(out, (x,) + r.storage_tensors)
+        _no_overlap(out, (x,) + self.storage_tensors)
         lib = r.backend._native
-        entry = lib.venturi_q8_head_run if self.kernel == "exact" else lib.venturi_q8_gemm_run
+        if self.kernel == "exact":
+            entry, planes = lib.venturi_q8_head_run, (r._codes, r._scales)
+        else:
+            entry, planes = lib.venturi_q8_tiled_run, self.tiles
         with torch.cuda.device(r.device):
             r.backend._check(
                 entry(
                     x.data_ptr(),
-                    r._codes.data_ptr(),
-                    r._scales.data_ptr(),
+                    planes[0].data_ptr(),
+                    planes[1].data_ptr(),
                     out.data_ptr(),
                     self.tokens,
                     r.vocab_size,
