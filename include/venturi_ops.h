@@ -82,8 +82,22 @@ int venturi_q8_pack_run(const void* source, int8_t* codes, void* scales, int n, 
 int venturi_q8_gemm_run(const void* x, const int8_t* codes, const void* scales, void* out, int tokens, int n, int k,
                         int padded, int dtype, void* stream);
 
+/* Extension: the same projection over tiled planes: row blocks of 16 rows x
+ * 64-column chunks, 1 KB each, stored [block][chunk][lane 16q+m][16 bytes]
+ * (row m's codes of columns 64c+8q..+8, then 64c+32+8q..+8), scales
+ * [block][chunk][m][2] fp16; each wave then streams contiguous 1 KB blocks.
+ * fp16 activations, k % 8 == 0, tokens <= 16. */
+int venturi_q8_tiled_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
+                         int padded, int dtype, void* stream);
+
 /* ---- Q4 (q4_g64_fp16): codes uint8 [n][padded/2] (column 2j in the low
  * nibble of byte j, two's complement), scales fp16 [n][padded/64]. ---- */
+
+/* Extension (the reference encodes on the CPU only, flash_next_q4.py:26-52):
+ * quantize_q4_rtn of a dense fp16/bf16/fp32 [n][k] source on the device;
+ * codes/scales bytes identical to the CPU encoder. */
+int venturi_q4_pack_run(const void* source, void* codes, void* scales, int n, int k, int padded, int dtype,
+                        void* stream);
 
 /* Expert operator ABI 1 (flash_next_q4.cu:36-54). These two return a HIP error
  * code (0 = success, hipErrorInvalidValue on bad arguments), as the reference

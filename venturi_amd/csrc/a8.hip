@@ -346,7 +346,7 @@ void rms_a8_launch(const void* x, const float* w, void* workspace, std::uint64_t
 // Reference: q8_dp4a.cuh:90-92. Returns 0 on invalid geometry.
 VT_EXPORT std::uint64_t venturi_q8_dp4a_bytes(int tokens, int k, int passes) {
     std::uint64_t result = 0;
-    if (vt::guarded([&] { result = vt::a8_bytes(tokens, k, passes); }) != 0) return 0;
+    if (!vt::host_guarded([&] { result = vt::a8_bytes(tokens, k, passes); })) return 0;
     return result;
 }
 

@@ -52,6 +52,20 @@ int guarded(F&& body) {
     }
 }
 
+// Host-only variant for entry points that make no HIP call (sizes, admission):
+// maps exceptions to the message convention without touching the runtime.
+template <class F>
+bool host_guarded(F&& body) {
+    try {
+        clear_error();
+        body();
+        return true;
+    } catch (const std::exception& e) {
+        set_error(e.what());
+        return false;
+    }
+}
+
 // Activation scalar types selected by the reference's dtype codes
 // (0 = fp16, 1 = bf16, 2 = fp32).
 enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
