@@ -33,14 +33,30 @@ constexpr int kThreads = kWaves * 64;
 // at or beyond k hold +0: with finite weights they contribute
 // fma(+0, w, acc) == acc exactly (accumulators start at +0 and a
 // round-to-nearest sum is never -0), so they need no masking.
+// Weight value code * scale for the four codes of a word, exactly: with
+// u = code + 128 (code ^ 0x80 per byte), fmaf(f32(u), s, -128 s) has an exact
+// product and addend whose exact sum code * s fits fp32, so it is returned
+// unrounded; this is bit-identical to f32(code) * s and costs a byte convert
+// and one FMA per weight.
+template <int RR>
+__device__ __forceinline__ void word_weights(const std::uint32_t (&cw)[RR], const float (&s)[RR], float (&w)[RR][4]) {
+#pragma unroll
+    for (int r = 0; r < RR; ++r) {
+        const std::uint32_t u = cw[r] ^ 0x80808080u;
+        const float bias = -128.0f * s[r];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) w[r][v] = fmaf(static_cast<float>((u >> (8 * v)) & 0xFFu), s[r], bias);
+    }
+}
+
+// One chunk: 4 consecutive columns per lane, acc = fmaf(x, code*scale, acc).
+// Activations are staged as 4 x 16-bit words (uint2) or, for single-token
+// tiles, as fp32 (float4) converted once when staged.
 template <class T, int TT, int RR>
 __device__ __forceinline__ void chunk_fma(const uint2* __restrict__ xs, int stride, const std::uint32_t (&cw)[RR],
                                           const float (&s)[RR], float (&acc)[TT][RR][4]) {
     float w[RR][4];
-#pragma unroll
-    for (int r = 0; r < RR; ++r)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) w[r][v] = sbyte(cw[r], v) * s[r];
+    word_weights<RR>(cw, s, w);
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
         const uint2 xw = xs[t * stride];
@@ -55,6 +71,19 @@ __device__ __forceinline__ void chunk_fma(const uint2* __restrict__ xs, int stri
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[t][r][v] = fmaf(xv[v], w[r][v], acc[t][r][v]);
     }
+}
+
+template <int RR>
+__device__ __forceinline__ void chunk_fma_f32(const float4* __restrict__ xs, const std::uint32_t (&cw)[RR],
+                                              const float (&s)[RR], float (&acc)[1][RR][4]) {
+    float w[RR][4];
+    word_weights<RR>(cw, s, w);
+    const float4 x4 = *xs;
+    const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[0][r][v] = fmaf(xv[v], w[r][v], acc[0][r][v]);
 }
 
 // Persistent waves. Wave w owns row blocks w, w+W, w+2W, ... (RR rows each);
@@ -75,7 +104,11 @@ __global__ __launch_bounds__(kThreads) void q8_exact(const T* __restrict__ x,
                                                 const __half* __restrict__ scales,
                                                 T* __restrict__ out, int tokens, int n, int k,
                                                 int padded) {
-    extern __shared__ uint2 xs[];  // [TT][tiles*U*64] words of 4 activations
+    // [TT][tiles*U*64] groups of 4 activations: 16-bit words, or fp32 when TT == 1.
+    extern __shared__ uint4 xstage[];
+    uint2* xs = reinterpret_cast<uint2*>(xstage);
+    float4* xf = reinterpret_cast<float4*>(xstage);
+    constexpr bool kF32X = TT == 1;
     const int lane = threadIdx.x & 63;
     const int chunks = (k + 255) >> 8;
     const int tiles = (chunks + U - 1) / U;
@@ -101,7 +134,14 @@ __global__ __launch_bounds__(kThreads) void q8_exact(const T* __restrict__ x,
                     w.y = h[2] | (static_cast<std::uint32_t>(h[3]) << 16);
                 }
             }
-            xs[t * stride + i] = w;
+            if constexpr (kF32X) {
+                if constexpr (std::is_same<T, __half>::value)
+                    xf[t * stride + i] = make_float4(half_lo(w.x), half_hi(w.x), half_lo(w.y), half_hi(w.y));
+                else
+                    xf[t * stride + i] = make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+            } else {
+                xs[t * stride + i] = w;
+            }
         }
     }
     __syncthreads();
@@ -166,7 +206,10 @@ __global__ __launch_bounds__(kThreads) void q8_exact(const T* __restrict__ x,
             float s[RR];
 #pragma unroll
             for (int r = 0; r < RR; ++r) s[r] = __half2float(__ushort_as_half(tile.sb[u][r]));
-            chunk_fma<T, TT, RR>(xs + (c0 + u) * 64 + lane, stride, tile.cw[u], s, acc);
+            if constexpr (kF32X)
+                chunk_fma_f32<RR>(xf + (c0 + u) * 64 + lane, tile.cw[u], s, acc);
+            else
+                chunk_fma<T, TT, RR>(xs + (c0 + u) * 64 + lane, stride, tile.cw[u], s, acc);
         }
         if (i % tiles == tiles - 1) {
             const int row0 = (wave + (i / tiles) * waves) * RR;
@@ -200,7 +243,8 @@ __global__ __launch_bounds__(kThreads) void q8_exact(const T* __restrict__ x,
 // LDS bytes for TT tokens at width k with tiles of U chunks.
 inline std::size_t exact_lds_bytes(int tt, int u, int k) {
     const int chunks = (k + 255) >> 8;
-    return static_cast<std::size_t>(tt) * ((chunks + u - 1) / u) * u * 64 * sizeof(uint2);
+    const std::size_t group = tt == 1 ? sizeof(float4) : sizeof(uint2);  // single-token tiles stage fp32
+    return static_cast<std::size_t>(tt) * ((chunks + u - 1) / u) * u * 64 * group;
 }
 
 constexpr std::size_t kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
