@@ -58,6 +58,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-prefill", action="store_true", help="skip the config-3 A8 prefill section")
     p.add_argument("--no-moe", action="store_true", help="skip the config-4 routed-expert MoE section")
+    p.add_argument("--no-model", action="store_true", help="skip the config-5 64-layer decode section")
     return p.parse_args()
 
 
@@ -260,6 +261,91 @@ def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
     return result
 
 
+def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
+    """64 decoder layers x the config-2 projections, all resident (256 Q8 matrices).
+
+    One step chains, per layer: h -> QKV; a seeded fp16 [B, 6144] -> o_proj;
+    h -> gate+up -> SiLU*up (venturi_silu_mul_run, the native runtime's
+    SwiGLU arithmetic) -> down -> next h. The 320 launches of a step are
+    captured once in a HIP graph (checked bit-for-bit against an eager step)
+    and replayed. Projection-only tokens/s = B / step time; GB/s counts the
+    projections' algorithmic bytes (weights + activations + outputs).
+    """
+    layers = 64
+    matrices = []
+    for layer in range(layers):
+        row = []
+        for i, (name, n, k) in enumerate(PROJECTIONS):
+            gen = torch.Generator(device=device).manual_seed(7_000_000 + 16 * layer + i)
+            w = torch.randn(n, k, generator=gen, device=device) * 0.02
+            row.append(backend.upload_linear(backend.quantize_q8(w), dtype=torch.float16, device=device))
+            del w
+        matrices.append(row)
+    torch.cuda.synchronize(device)
+    weight_bytes = sum(r.storage_nbytes for row in matrices for r in row)
+    lib, stream_of = backend._native, (lambda: torch.cuda.current_stream(device).cuda_stream)
+    inter = PROJECTIONS[2][1] // 2
+    results = {}
+    for b in batches:
+        plans = [[r.prepare(tokens=b) for r in row] for row in matrices]
+        gen = torch.Generator(device=device).manual_seed(b)
+        h0 = torch.randn(b, 5120, generator=gen, device=device).half()
+        o_in = torch.randn(b, 6144, generator=gen, device=device).half()
+        h = [h0.clone(), torch.empty_like(h0)]
+        qkv = torch.empty(b, PROJECTIONS[0][1], dtype=torch.float16, device=device)
+        o = torch.empty(b, PROJECTIONS[1][1], dtype=torch.float16, device=device)
+        gu = torch.empty(b, PROJECTIONS[2][1], dtype=torch.float16, device=device)
+        act = torch.empty(b, inter, dtype=torch.float16, device=device)
+
+        def step():
+            h[0].copy_(h0)
+            for layer in range(layers):
+                p = plans[layer]
+                cur, nxt = h[layer % 2], h[(layer + 1) % 2]
+                p[0].run(cur, out=qkv)
+                p[1].run(o_in, out=o)
+                p[2].run(cur, out=gu)
+                backend._check(lib.venturi_silu_mul_run(gu.data_ptr(), act.data_ptr(), b, inter, 0, stream_of()))
+                p[3].run(act, out=nxt)
+
+        step()
+        torch.cuda.synchronize(device)
+        eager = h[layers % 2].clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        graph.replay()
+        torch.cuda.synchronize(device)
+        same = bool(torch.equal(h[layers % 2].view(torch.int16), eager.view(torch.int16)))
+        for _ in range(warmup):
+            graph.replay()
+        stream = torch.cuda.current_stream(device)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(device)
+        e0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        e1.record(stream)
+        e1.synchronize()
+        step_s = e0.elapsed_time(e1) / 1e3 / steps
+        step_bytes = layers * sum(launch_bytes(b, n, k) for _, n, k in PROJECTIONS)
+        results[f"B{b}"] = {
+            "ms_per_step": round(step_s * 1e3, 4),
+            "tokens_per_s": round(b / step_s, 1),
+            "GB/s": round(step_bytes / step_s / 1e9, 1),
+            "frac_hbm": round(step_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
+            "route": plans[0][0].route,
+            "graph_equals_eager": same,
+        }
+        del plans, graph
+    del matrices
+    return {
+        "workload": "config5: 64 layers x config-2 Q8 projections resident, chained per step (HIP graph)",
+        "weight_bytes": weight_bytes,
+        "batches": results,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -365,6 +451,9 @@ def main():
     if not args.no_moe:
         log("config-4 routed-expert MoE")
         result["moe_w4a16"] = moe_w4a16(backend, device, max(args.steps, 10), 3, 0 if args.no_cpu else 4.0)
+    if not args.no_model:
+        log("config-5 64-layer streaming decode")
+        result["model_decode"] = model_decode(backend, device, max(args.steps // 4, 3), 2)
     if not args.no_cpu:
         log("CPU baseline (reference CPU path)")
         result["cpu_baseline"] = cpu_baseline(copies, xs, args.cpu_seconds)

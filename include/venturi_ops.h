@@ -86,7 +86,7 @@ int venturi_q8_gemm_run(const void* x, const int8_t* codes, const void* scales, 
  * 64-column chunks, 1 KB each, stored [block][chunk][lane 16q+m][16 bytes]
  * (row m's codes of columns 64c+8q..+8, then 64c+32+8q..+8), scales
  * [block][chunk][m][2] fp16; each wave then streams contiguous 1 KB blocks.
- * fp16 activations, k % 8 == 0, tokens <= 16. */
+ * fp16 activations, k % 8 == 0, tokens <= 32. */
 int venturi_q8_tiled_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
                          int padded, int dtype, void* stream);
 
@@ -153,6 +153,16 @@ int venturi_moe_q4_run(const void* x, const int64_t* ids, const void* scores, co
                        const void* gate_up_scales, const void* down_codes, const void* down_scales, void* out,
                        void* workspace, uint64_t workspace_bytes, int tokens, int top_k, int experts, int hidden,
                        int inter, void* stream);
+
+/* Elementwise SwiGLU out = cast((a * sigmoid(a)) * b) with fp32 math and one
+ * rounding, and add out = cast(a + b); dtype 0/1/2. Replaces blocks.cu:741-750
+ * (ops_api.h). */
+int venturi_swiglu_run(const void* a, const void* b, void* out, int64_t count, int dtype, void* stream);
+int venturi_add_run(const void* a, const void* b, void* out, int64_t count, int dtype, void* stream);
+
+/* Extension: the same SwiGLU over one fused gate+up output [tokens][2*inter]
+ * (gate columns first) -> out [tokens][inter]; dtype 0 (fp16) or 1 (bf16). */
+int venturi_silu_mul_run(const void* gate_up, void* out, int tokens, int inter, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

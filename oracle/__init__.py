@@ -283,3 +283,17 @@ def f32_to_f16_bits(values):
     f = lib().oracle_f32_to_f16
     flat = np.asarray(values, dtype=np.float32).reshape(-1)
     return np.array([f(float(v)) for v in flat], dtype=np.uint16).reshape(np.shape(values))
+
+
+def swiglu(a, b):
+    """blocks.cu:56-70 SwiGLU: cast((x * sigmoid(x)) * y), fp32 math, stable logistic; fp16 bits in/out.
+
+    numpy's float32 exp stands in for the device exp (neither is bit-pinned).
+    """
+    x = np.asarray(a, np.float16).astype(np.float32)
+    y = np.asarray(b, np.float16).astype(np.float32)
+    with np.errstate(over="ignore"):
+        pos = np.float32(1) / (np.float32(1) + np.exp(-x))
+        neg = np.exp(x) / (np.float32(1) + np.exp(x))
+    sig = np.where(x >= 0, pos, neg).astype(np.float32)
+    return ((x * sig).astype(np.float32) * y).astype(np.float16)

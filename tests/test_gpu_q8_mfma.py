@@ -41,7 +41,7 @@ def check(out, x, codes, scales, k):
 
 
 @pytest.mark.parametrize("shape", [(1, 64), (7, 72), (33, 136), (16, 256), (257, 5120), (100, 1000)])
-@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 8, 13, 16])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 8, 13, 16, 17, 32])
 def test_mfma_tolerances_tails_and_guards(backend, device, shape, tokens):
     n, k = shape
     print(f"case q8-mfma n={n} k={k} tokens={tokens}", flush=True)
@@ -86,6 +86,7 @@ def test_mfma_route_admission(backend, device):
     resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.float16, device=device)
     assert resident.prepare(tokens=1).route == "venturi-q8-exact"
     assert resident.prepare(tokens=2).route == "venturi-q8-mfma"
-    assert resident.prepare(tokens=17).route == "venturi-q8-exact"
+    assert resident.prepare(tokens=32).route == "venturi-q8-mfma"
+    assert resident.prepare(tokens=33).route == "venturi-q8-exact"
     bf = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.bfloat16, device=device)
     assert bf.prepare(tokens=8).route == "venturi-q8-exact"

@@ -153,21 +153,27 @@ __global__ __launch_bounds__(1024) void q8_mfma_decode(const __half* __restrict_
 // fp16 (groups 2c, 2c + 1 of row m). A wave streams its chunks of a row block
 // as contiguous 1 KB loads. Padding rows/columns hold zero codes and scales.
 // Workgroup: RB consecutive row blocks; its 16 waves split the chunks, and each
-// wave reuses one activation fragment for all RB row blocks of its chunk.
-template <int STEPS, int RB>
+// wave reuses one activation fragment for all RB row blocks of its chunk. NB
+// token blocks of 16 (tokens <= 16 * NB) share every weight fragment.
+template <int STEPS, int RB, int NB>
 __global__ __launch_bounds__(1024) void q8_tiled_decode(const __half* __restrict__ x, const uint4* __restrict__ codes,
                                                         const std::uint32_t* __restrict__ scales,
                                                         __half* __restrict__ out, int tokens, int n, int k,
                                                         int chunks, int blocks) {
-    __shared__ float4v partial[kDecodeWaves][RB][64];
+    __shared__ float4v partial[kDecodeWaves][RB * NB][64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r = lane & 15;
     const int block0 = blockIdx.x * RB;
     const int per = (chunks + kDecodeWaves - 1) / kDecodeWaves;
     const int c0 = wave * per, c1 = min(c0 + per, chunks);
-    const bool live_token = r < tokens;
-    const __half* xrow = x + static_cast<std::int64_t>(min(r, tokens - 1)) * k;
+    bool live_token[NB];
+    const __half* xrow[NB];
+#pragma unroll
+    for (int tb = 0; tb < NB; ++tb) {
+        live_token[tb] = 16 * tb + r < tokens;
+        xrow[tb] = x + static_cast<std::int64_t>(min(16 * tb + r, tokens - 1)) * k;
+    }
     const uint4* wsrc[RB];
     const std::uint32_t* ssrc[RB];
 #pragma unroll
@@ -177,12 +183,14 @@ __global__ __launch_bounds__(1024) void q8_tiled_decode(const __half* __restrict
         ssrc[b] = scales + static_cast<std::int64_t>(blk) * chunks * 16 + r;
     }
 
-    float4v y[RB];
+    float4v y[RB][NB];
 #pragma unroll
-    for (int b = 0; b < RB; ++b) y[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int tb = 0; tb < NB; ++tb) y[b][tb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
     const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int c = c0; c < c1; c += STEPS) {
-        uint4 w[STEPS][RB], xa[STEPS], xb[STEPS];
+        uint4 w[STEPS][RB], xa[STEPS][NB], xb[STEPS][NB];
         std::uint32_t sc[STEPS][RB];
 #pragma unroll
         for (int i = 0; i < STEPS; ++i) {
@@ -193,15 +201,22 @@ __global__ __launch_bounds__(1024) void q8_tiled_decode(const __half* __restrict
                 w[i][b] = wsrc[b][static_cast<std::int64_t>(ch) * 64];
                 sc[i][b] = ssrc[b][static_cast<std::int64_t>(ch) * 16];
             }
-            xa[i] = *reinterpret_cast<const uint4*>(xrow + min(col, k - 8));
-            xb[i] = *reinterpret_cast<const uint4*>(xrow + min(col + 32, k - 8));
+#pragma unroll
+            for (int tb = 0; tb < NB; ++tb) {
+                xa[i][tb] = *reinterpret_cast<const uint4*>(xrow[tb] + min(col, k - 8));
+                xb[i][tb] = *reinterpret_cast<const uint4*>(xrow[tb] + min(col + 32, k - 8));
+            }
         }
 #pragma unroll
         for (int i = 0; i < STEPS; ++i) {
             if (c + i >= c1) break;
             const int col = (c + i) * 64 + 8 * q;
-            const half8 fa = live_token && col < k ? __builtin_bit_cast(half8, xa[i]) : half8{};
-            const half8 fb = live_token && col + 32 < k ? __builtin_bit_cast(half8, xb[i]) : half8{};
+            half8 fa[NB], fb[NB];
+#pragma unroll
+            for (int tb = 0; tb < NB; ++tb) {
+                fa[tb] = live_token[tb] && col < k ? __builtin_bit_cast(half8, xa[i][tb]) : half8{};
+                fb[tb] = live_token[tb] && col + 32 < k ? __builtin_bit_cast(half8, xb[i][tb]) : half8{};
+            }
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
                 std::uint32_t h0, h1, h2, h3, h4, h5, h6, h7;
@@ -209,33 +224,40 @@ __global__ __launch_bounds__(1024) void q8_tiled_decode(const __half* __restrict
                 codes_to_half4(w[i][b].y, h2, h3);
                 codes_to_half4(w[i][b].z, h4, h5);
                 codes_to_half4(w[i][b].w, h6, h7);
-                const float4v da = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa, pack8(h0, h1, h2, h3), zero, 0, 0, 0);
-                const float4v db = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb, pack8(h4, h5, h6, h7), zero, 0, 0, 0);
+                const half8 wa = pack8(h0, h1, h2, h3), wb = pack8(h4, h5, h6, h7);
                 const float sa = half_lo(sc[i][b]), sb = half_hi(sc[i][b]);  // padded groups carry scale 0
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    y[b][j] = fmaf(da[j], sa, y[b][j]);
-                    y[b][j] = fmaf(db[j], sb, y[b][j]);
+                for (int tb = 0; tb < NB; ++tb) {
+                    const float4v da = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[tb], wa, zero, 0, 0, 0);
+                    const float4v db = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[tb], wb, zero, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        y[b][tb][j] = fmaf(da[j], sa, y[b][tb][j]);
+                        y[b][tb][j] = fmaf(db[j], sb, y[b][tb][j]);
+                    }
                 }
             }
         }
     }
 #pragma unroll
-    for (int b = 0; b < RB; ++b) partial[wave][b][lane] = y[b];
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int tb = 0; tb < NB; ++tb) partial[wave][b * NB + tb][lane] = y[b][tb];
     __syncthreads();
-    // Waves 0..RB-1 each reduce one row block in wave order 0..15.
-    if (wave < RB) {
+    // Waves 0..RB*NB-1 each reduce one (row block, token block) in wave order 0..15.
+    if (wave < RB * NB) {
+        const int b = wave / NB, tb = wave % NB;
         float4v sum = partial[0][wave][lane];
         for (int w = 1; w < kDecodeWaves; ++w) {
             const float4v p = partial[w][wave][lane];
 #pragma unroll
             for (int j = 0; j < 4; ++j) sum[j] += p[j];
         }
-        // D layout: lane holds rows (tokens) 4q..4q+3 of weight row r.
+        // D layout: lane holds rows (tokens) 4q..4q+3 of the token block, weight row r.
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int t = 4 * q + j;
-            const int row = (block0 + wave) * 16 + r;
+            const int t = 16 * tb + 4 * q + j;
+            const int row = (block0 + b) * 16 + r;
             if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(sum[j]);
         }
     }
@@ -251,7 +273,7 @@ void q8_tiled_launch(const void* x, const void* codes, const void* scales, void*
     require(dtype == kF16, "the Q8 MFMA route takes FP16 activations");
     require(k % 8 == 0 && aligned(x, 16), "the Q8 MFMA route needs k % 8 == 0 and 16-byte aligned x");
     require(aligned(codes, 16) && aligned(scales, 4) && aligned(out, 2), "misaligned Q8 operand");
-    require(tokens <= 16, "the Q8 MFMA decode kernel takes at most 16 tokens");
+    require(tokens <= 32, "the tiled Q8 MFMA decode kernel takes at most 32 tokens");
     // Two row blocks per workgroup: each activation fragment feeds two MFMA
     // pairs (measured better than one or four blocks at the config-2 shapes).
     const int blocks = (n + 15) / 16;
@@ -259,7 +281,10 @@ void q8_tiled_launch(const void* x, const void* codes, const void* scales, void*
     const auto* cp = static_cast<const uint4*>(codes);
     const auto* sp = static_cast<const std::uint32_t*>(scales);
     auto* op = static_cast<__half*>(out);
-    q8_tiled_decode<4, 2><<<(blocks + 1) / 2, 1024, 0, stream>>>(xp, cp, sp, op, tokens, n, k, padded / 64, blocks);
+    if (tokens <= 16)
+        q8_tiled_decode<4, 2, 1><<<(blocks + 1) / 2, 1024, 0, stream>>>(xp, cp, sp, op, tokens, n, k, padded / 64, blocks);
+    else
+        q8_tiled_decode<4, 2, 2><<<(blocks + 1) / 2, 1024, 0, stream>>>(xp, cp, sp, op, tokens, n, k, padded / 64, blocks);
 }
 
 void q8_mfma_launch(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n,

@@ -26,7 +26,7 @@ import torch
 from .blocks import _DTYPES, Q8_ROUTES, _no_overlap, _shape, _stream, _tensor
 
 EXACT_MAX_AUTO_TOKENS = 1
-MFMA_MAX_TOKENS = 16
+MFMA_MAX_TOKENS = 32
 _TILE_LOCK = threading.Lock()
 
 
