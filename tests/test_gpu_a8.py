@@ -128,7 +128,7 @@ def test_fused_rms_a8_bytes(backend, device, passes, tokens, k):
 
 @pytest.mark.parametrize("passes", [1, 2])
 @pytest.mark.parametrize("tokens", [64, 65, 100, 257])
-@pytest.mark.parametrize("shape", [(7, 1), (33, 67), (129, 1000), (64, 5120), (100, 6144)])
+@pytest.mark.parametrize("shape", [(7, 1), (33, 67), (129, 1000), (70, 2000), (64, 5120), (100, 6144), (40, 26000)])
 def test_matrix_core_projection_bytes(backend, device, passes, tokens, shape):
     # Token counts that take the int8 matrix-core GEMM: bytes must still be the reference's.
     n, k = shape

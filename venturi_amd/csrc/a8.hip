@@ -296,7 +296,7 @@ void a8_gemv_launch(const void* workspace, std::uint64_t available, const std::i
     auto* y = static_cast<__half*>(out);
     // Both kernels produce the reference's bytes; the matrix-core GEMM takes
     // over once a 64-token tile is filled.
-    if (tokens >= kA8GemmMinTokens && (groups + 31) / 32 <= 24) {
+    if (tokens >= kA8GemmMinTokens) {
         a8_gemm_launch(workspace, codes, scales, out, tokens, n, k, padded, passes, stream);
         return;
     }

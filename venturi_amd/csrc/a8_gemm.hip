@@ -18,13 +18,25 @@
 // takes the first member of its pair and adds the second, which reproduces
 // the tree's additions exactly with 5 + 1 registers per output.
 //
+// Schedule: the work items are the (position, group) pairs in visiting order
+// (a position whose slot has no group is one item that only folds a zero
+// sum). A step takes kBatch consecutive items, possibly spanning slots, so
+// every step but the last is full whatever the number of groups per slot.
+//
 // Tiling: a 512-thread workgroup computes 128 tokens x 64 rows; wave
-// (wm, wn) in 4 x 2 computes 32 x 32 as 2 x 2 MFMA tiles of 16 x 16. Every
-// (slot, group) step stages the tile's codes (converted to fp16) and scales in
-// LDS; the next step's global loads are in flight while a step computes.
+// (wm, wn) in 4 x 2 computes 32 x 32 as 2 x 2 MFMA tiles of 16 x 16. Each
+// step's codes (converted to fp16) and scales are staged in one of two LDS
+// buffers: a step computes from one buffer while the next step's operands,
+// loaded during the previous step, are written to the other, with one barrier
+// per step. LDS rows are group-major with an 80-byte stride, so the 16-byte
+// fragment reads of 16 consecutive rows touch distinct banks. Within a step
+// the fragments of the next item are read while an item's four products and
+// its epilogue run; an item without data (past the end, or an empty slot) has
+// its weight scale zeroed in LDS, so the epilogue runs unconditionally.
 #include "common.hpp"
 
 #include <algorithm>
+#include <utility>
 
 namespace vt {
 namespace {
@@ -34,8 +46,7 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 
 constexpr int kTokTile = 128;
 constexpr int kRowTile = 64;
-constexpr int kRowHalves = 40;  // LDS row: 32 fp16 + 8 pad (80 bytes: conflict-free 16-byte reads)
-constexpr int kBatch = 4;       // groups of one slot staged per step
+constexpr int kRowHalves = 40;  // LDS row: 32 fp16 + 8 pad (80 bytes)
 
 __device__ __forceinline__ int bitrev5(int p) {
     return ((p & 1) << 4) | ((p & 2) << 2) | (p & 4) | ((p & 8) >> 2) | ((p & 16) >> 4);
@@ -51,17 +62,34 @@ __device__ __forceinline__ uint2 codes4_to_half(std::uint32_t w) {
     return make_uint2(__builtin_bit_cast(std::uint32_t, lo), __builtin_bit_cast(std::uint32_t, hi));
 }
 
+// Calls f(integral_constant<int, I>) for I = 0 .. N-1 (indices fixed at compile time).
+template <class F, int... I>
+__device__ __forceinline__ void for_each_index_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void for_each_index(F&& f) {
+    for_each_index_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Items per step: four with one pass; two with two passes (LDS budget).
+template <int P>
+struct A8Tile {
+    static constexpr int kBatch = P == 1 ? 4 : 2;
+};
+
 template <int P>
 __global__ __launch_bounds__(512) void a8_gemm(const std::int8_t* __restrict__ acodes,
                                                const float* __restrict__ ascales,
                                                const std::int8_t* __restrict__ wcodes,
                                                const __half* __restrict__ wscales, __half* __restrict__ out,
                                                int tokens, int n, int padded, int groups) {
-    // One step stages up to kBatch groups of one slot (g = slot + 32 (kBatch b + j)).
-    __shared__ __attribute__((aligned(16))) _Float16 af[P][kTokTile * kBatch * kRowHalves];
-    __shared__ __attribute__((aligned(16))) _Float16 bf[kRowTile * kBatch * kRowHalves];
-    __shared__ __attribute__((aligned(16))) float as_lds[P][kBatch][kTokTile];
-    __shared__ float ws_lds[kBatch][kRowTile];
+    constexpr int B = A8Tile<P>::kBatch;
+    static_assert(B * kTokTile <= 512 && B * kRowTile <= 512, "one scale per thread and item");
+    __shared__ __attribute__((aligned(16))) _Float16 af[2][P][B][kTokTile * kRowHalves];
+    __shared__ __attribute__((aligned(16))) _Float16 bf[2][B][kRowTile * kRowHalves];
+    __shared__ __attribute__((aligned(16))) float as_lds[2][P][B][kTokTile];
+    __shared__ float ws_lds[2][B][kRowTile];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -71,155 +99,222 @@ __global__ __launch_bounds__(512) void a8_gemm(const std::int8_t* __restrict__ a
     const int t0 = blockIdx.y * kTokTile, n0 = blockIdx.x * kRowTile;
     const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
 
-    // Staging assignment (clamped rows are computed and never stored; groups past
-    // the slot's last are clamped to it and never used):
-    // activation codes: token tid / 4, bytes 8 * (tid % 4) of every batched group;
+    // Staging assignment (clamped rows are computed and never stored):
+    // activation codes: token tid / 4, bytes 8 * (tid % 4) of every item's group;
     // weight codes: row tid / 8, bytes 4 * (tid % 8); activation scale: token
-    // tid % 128 of batched group tid / 128; weight scale: row tid % 64 of group
-    // (tid / 64) % kBatch.
+    // tid % 128 of item tid / 128; weight scale: row tid % 64 of item tid / 64.
     const std::int64_t a_tok = min(t0 + (tid >> 2), tokens - 1);
     const std::int8_t* a_src[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) a_src[p] = acodes + ((p * count) + a_tok * groups) * 32 + 8 * (tid & 3);
     const std::int8_t* b_src = wcodes + static_cast<std::int64_t>(min(n0 + (tid >> 3), n - 1)) * padded + 4 * (tid & 7);
-    static_assert(kBatch == 4, "the staging assignment assumes four groups per step");
-    const int s_group = tid >> 7;  // 0..3
-    const int w_group = (tid >> 6) & (kBatch - 1);
+    const int s_item = min(tid >> 7, B - 1);
+    const int w_item = min(tid >> 6, B - 1);
     const float* as_src[P];
 #pragma unroll
     for (int p = 0; p < P; ++p)
         as_src[p] = ascales + p * count + static_cast<std::int64_t>(min(t0 + (tid & 127), tokens - 1)) * groups;
     const __half* ws_src = wscales + static_cast<std::int64_t>(min(n0 + (tid & 63), n - 1)) * (padded / 32);
 
-    struct Stage {
-        uint2 a[P][kBatch];
-        std::uint32_t b[kBatch];
-        float as[P];
-        unsigned short ws;
+    // Schedule cursor: position p and item b within it. An item carries data
+    // when its slot has groups (group bitrev5(p) + 32 b); the slot ends with
+    // its last item (a position without groups has one item).
+    struct Cursor {
+        int p, b;
     };
-    // Groups of a step: g(j) = first + 32 j for j < kBatch, clamped to `last`.
-    auto load = [&](int first, int last, Stage& st) {
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const int g = min(first + 32 * j, last);
-#pragma unroll
-            for (int p = 0; p < P; ++p) st.a[p][j] = *reinterpret_cast<const uint2*>(a_src[p] + g * 32);
-            st.b[j] = *reinterpret_cast<const std::uint32_t*>(b_src + g * 32);
-        }
-        const int gs = min(first + 32 * s_group, last), gw = min(first + 32 * w_group, last);
-#pragma unroll
-        for (int p = 0; p < P; ++p) st.as[p] = as_src[p][gs];
-        st.ws = __half_as_ushort(ws_src[gw]);
-    };
-    auto store = [&](const Stage& st) {
-        const int tok = tid >> 2;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-#pragma unroll
-            for (int p = 0; p < P; ++p) {
-                const uint2 lo = codes4_to_half(st.a[p][j].x), hi = codes4_to_half(st.a[p][j].y);
-                *reinterpret_cast<uint4*>(&af[p][(tok * kBatch + j) * kRowHalves + 8 * (tid & 3)]) =
-                    make_uint4(lo.x, lo.y, hi.x, hi.y);
-            }
-            *reinterpret_cast<uint2*>(&bf[((tid >> 3) * kBatch + j) * kRowHalves + 4 * (tid & 7)]) =
-                codes4_to_half(st.b[j]);
-        }
-#pragma unroll
-        for (int p = 0; p < P; ++p) as_lds[p][s_group][tid & 127] = st.as[p];
-        if (tid < kBatch * kRowTile) ws_lds[w_group][tid & 63] = __half2float(__ushort_as_half(st.ws));
-    };
-
-    // The schedule: position p visits slot bitrev5(p); its groups
-    // slot, slot + 32, ... < groups are processed kBatch at a time.
-    auto slot_groups = [&](int p) {
+    auto slot_groups = [&](int p) __attribute__((always_inline)) {
         const int slot = bitrev5(p);
         return slot < groups ? (groups - slot + 31) / 32 : 0;
     };
-    auto first_position = [&](int p) {  // first position at or after p with groups
-        while (p < 32 && slot_groups(p) == 0) ++p;
-        return p;
+
+    struct Stage {
+        uint2 a[P][B];
+        std::uint32_t b[B];
+        float as[P];
+        unsigned short ws;
     };
-    auto last_group = [&](int p) { return bitrev5(p) + 32 * (slot_groups(p) - 1); };
+    // Loads the operands of the B items at cursor c, advances it and returns
+    // the step's descriptor: per item j, bits 8j (data), 8j+1 (slot ends) and
+    // 8j+2..8j+6 (position). Items past the end load group groups - 1 and
+    // have an empty descriptor.
+    auto load = [&](Cursor& c, Stage& sg) __attribute__((always_inline)) {
+        int gs = groups - 1, gw = groups - 1;
+        std::uint32_t desc = 0;
+        for_each_index<B>([&](auto J) __attribute__((always_inline)) {
+            constexpr int j = decltype(J)::value;
+            int g = groups - 1;
+            if (c.p < 32) {
+                const int cnt = slot_groups(c.p);
+                std::uint32_t d = static_cast<std::uint32_t>(c.p) << 2;
+                if (cnt > 0) {
+                    g = bitrev5(c.p) + 32 * c.b;
+                    d |= 1u;
+                }
+                if (c.b + 1 >= max(cnt, 1)) {
+                    d |= 2u;
+                    ++c.p;
+                    c.b = 0;
+                } else {
+                    ++c.b;
+                }
+                desc |= d << (8 * j);
+            }
+#pragma unroll
+            for (int p = 0; p < P; ++p) sg.a[p][j] = *reinterpret_cast<const uint2*>(a_src[p] + g * 32);
+            sg.b[j] = *reinterpret_cast<const std::uint32_t*>(b_src + g * 32);
+            gs = s_item == j ? g : gs;
+            gw = w_item == j ? g : gw;
+        });
+#pragma unroll
+        for (int p = 0; p < P; ++p) sg.as[p] = as_src[p][gs];
+        sg.ws = __half_as_ushort(ws_src[gw]);
+        return desc;
+    };
+    auto store = [&](const Stage& sg, std::uint32_t desc, int buf) __attribute__((always_inline)) {
+        const int tok = tid >> 2;
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const uint2 lo = codes4_to_half(sg.a[p][j].x), hi = codes4_to_half(sg.a[p][j].y);
+                *reinterpret_cast<uint4*>(&af[buf][p][j][tok * kRowHalves + 8 * (tid & 3)]) =
+                    make_uint4(lo.x, lo.y, hi.x, hi.y);
+            }
+            *reinterpret_cast<uint2*>(&bf[buf][j][(tid >> 3) * kRowHalves + 4 * (tid & 7)]) = codes4_to_half(sg.b[j]);
+        }
+        if (tid < B * kTokTile) {
+#pragma unroll
+            for (int p = 0; p < P; ++p) as_lds[buf][p][s_item][tid & 127] = sg.as[p];
+        }
+        // An item without data gets weight scale 0: its epilogue then adds
+        // d * 0 to the slot sum, which leaves it unchanged (d is finite).
+        if (tid < B * kRowTile)
+            ws_lds[buf][w_item][tid & 63] = (desc >> (8 * w_item)) & 1u ? __half2float(__ushort_as_half(sg.ws)) : 0.0f;
+    };
 
     float s[16], lv[5][16];
 #pragma unroll
     for (int o = 0; o < 16; ++o) s[o] = 0.0f;
-
-    Stage st;
-    int next_p = first_position(0), next_b = 0;
-    if (next_p < 32) load(bitrev5(next_p), last_group(next_p), st);
-    for (int p = 0; p < 32; ++p) {
-        const int cnt = slot_groups(p);
-        for (int b0 = 0; b0 < cnt; b0 += kBatch) {
-            const int live = min(kBatch, cnt - b0);
-            __syncthreads();
-            store(st);
-            __syncthreads();
-            // Advance the schedule and prefetch the next step's operands.
-            next_b += kBatch;
-            if (next_b >= slot_groups(next_p)) {
-                next_p = first_position(next_p + 1);
-                next_b = 0;
-            }
-            if (next_p < 32) load(bitrev5(next_p) + 32 * next_b, last_group(next_p), st);
-
-            float wsv[kBatch][2];
+    // Fold the finished slot at position p into the level accumulators: a
+    // level takes the first member of its pair and adds the second.
+    auto fold = [&](int p) __attribute__((always_inline)) {
+        if (p & 1) {
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j)
+            for (int o = 0; o < 16; ++o) lv[0][o] += s[o];
+            if (p & 2) {
 #pragma unroll
-                for (int b = 0; b < 2; ++b) wsv[j][b] = ws_lds[j][wn * 32 + 16 * b + r];
-            const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int o = 0; o < 16; ++o) lv[1][o] += lv[0][o];
+                if (p & 4) {
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
-                if (j >= live) break;  // groups in increasing order within the slot
-                half8 bfr[2];
+                    for (int o = 0; o < 16; ++o) lv[2][o] += lv[1][o];
+                    if (p & 8) {
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
-                    bfr[b] = *reinterpret_cast<const half8*>(&bf[((wn * 32 + 16 * b + r) * kBatch + j) * kRowHalves + 8 * q]);
+                        for (int o = 0; o < 16; ++o) lv[3][o] += lv[2][o];
+                        if (p & 16) {
 #pragma unroll
-                for (int p2 = 0; p2 < P; ++p2) {
+                            for (int o = 0; o < 16; ++o) lv[4][o] += lv[3][o];
+                        } else {
 #pragma unroll
-                    for (int a = 0; a < 2; ++a) {
-                        const half8 afr =
-                            *reinterpret_cast<const half8*>(&af[p2][((wm * 32 + 16 * a + r) * kBatch + j) * kRowHalves + 8 * q]);
-                        const float4 as4 = *reinterpret_cast<const float4*>(&as_lds[p2][j][wm * 32 + 16 * a + 4 * q]);
-                        const float asv[4] = {as4.x, as4.y, as4.z, as4.w};
-#pragma unroll
-                        for (int b = 0; b < 2; ++b) {
-                            const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr, bfr[b], zero, 0, 0, 0);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                float& acc = s[(a * 2 + b) * 4 + e];
-                                acc = __fmaf_rn(d[e], __fmul_rn(wsv[j][b], asv[e]), acc);
-                            }
+                            for (int o = 0; o < 16; ++o) lv[4][o] = lv[3][o];
                         }
+                    } else {
+#pragma unroll
+                        for (int o = 0; o < 16; ++o) lv[3][o] = lv[2][o];
                     }
+                } else {
+#pragma unroll
+                    for (int o = 0; o < 16; ++o) lv[2][o] = lv[1][o];
                 }
+            } else {
+#pragma unroll
+                for (int o = 0; o < 16; ++o) lv[1][o] = lv[0][o];
             }
-        }
-        // Fold slot bitrev5(p) into the level accumulators: a level takes the
-        // first member of its pair and adds the second (position bits h0..h4).
-        const int h0 = p & 1, h1 = (p >> 1) & 1, h2 = (p >> 2) & 1, h3 = (p >> 3) & 1, h4 = (p >> 4) & 1;
+        } else {
 #pragma unroll
-        for (int o = 0; o < 16; ++o) lv[0][o] = h0 ? lv[0][o] + s[o] : s[o];
-        if (h0) {
-#pragma unroll
-            for (int o = 0; o < 16; ++o) lv[1][o] = h1 ? lv[1][o] + lv[0][o] : lv[0][o];
-            if (h1) {
-#pragma unroll
-                for (int o = 0; o < 16; ++o) lv[2][o] = h2 ? lv[2][o] + lv[1][o] : lv[1][o];
-                if (h2) {
-#pragma unroll
-                    for (int o = 0; o < 16; ++o) lv[3][o] = h3 ? lv[3][o] + lv[2][o] : lv[2][o];
-                    if (h3) {
-#pragma unroll
-                        for (int o = 0; o < 16; ++o) lv[4][o] = h4 ? lv[4][o] + lv[3][o] : lv[3][o];
-                    }
-                }
-            }
+            for (int o = 0; o < 16; ++o) lv[0][o] = s[o];
         }
 #pragma unroll
         for (int o = 0; o < 16; ++o) s[o] = 0.0f;
+    };
+
+    // Fragments of one item: activation codes and scales per pass and token
+    // block, weight codes and scales per row block.
+    struct Frag {
+        half8 a[P][2];
+        half8 b[2];
+        float4 as[P][2];
+        float ws[2];
+    };
+    auto read_frag = [&](int buf, int j, Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            f.ws[b] = ws_lds[buf][j][wn * 32 + 16 * b + r];
+            f.b[b] = *reinterpret_cast<const half8*>(&bf[buf][j][(wn * 32 + 16 * b + r) * kRowHalves + 8 * q]);
+        }
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+                f.a[p][a] = *reinterpret_cast<const half8*>(&af[buf][p][j][(wm * 32 + 16 * a + r) * kRowHalves + 8 * q]);
+                f.as[p][a] = *reinterpret_cast<const float4*>(&as_lds[buf][p][j][wm * 32 + 16 * a + 4 * q]);
+            }
+    };
+    // Computes the B items of a step from LDS buffer buf. The fragments of
+    // item j + 1 are read while item j's products and epilogue run.
+    auto compute = [&](std::uint32_t desc, int buf) __attribute__((always_inline)) {
+        const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        Frag f[2];
+        read_frag(buf, 0, f[0]);
+        for_each_index<B>([&](auto J) __attribute__((always_inline)) {
+            constexpr int j = decltype(J)::value;
+            const Frag& cur = f[j & 1];
+            if constexpr (j + 1 < B) read_frag(buf, j + 1, f[(j + 1) & 1]);
+            float4v d[P][2][2];
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+                        d[p][a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.a[p][a], cur.b[b], zero, 0, 0, 0);
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+#pragma unroll
+                for (int a = 0; a < 2; ++a) {
+                    const float asv[4] = {cur.as[p][a].x, cur.as[p][a].y, cur.as[p][a].z, cur.as[p][a].w};
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float& acc = s[(a * 2 + b) * 4 + e];
+                            acc = __fmaf_rn(d[p][a][b][e], __fmul_rn(cur.ws[b], asv[e]), acc);
+                        }
+                }
+            const std::uint32_t item = desc >> (8 * j);
+            if (item & 2u) fold(static_cast<int>((item >> 2) & 31u));
+        });
+    };
+
+    // Items: one per (position, group), one per position without groups.
+    // Operands of step t are loaded during step t - 2, written to LDS during
+    // step t - 1 and consumed in step t.
+    const int steps = (max(groups, 32) + B - 1) / B;
+    static_assert(B <= 4, "four 8-bit item descriptors per word");
+    Cursor cursor = {0, 0};
+    Stage sg;
+    std::uint32_t desc_now = load(cursor, sg), desc_next = 0;
+    store(sg, desc_now, 0);
+    if (steps > 1) desc_next = load(cursor, sg);
+    __syncthreads();
+    for (int step = 0; step < steps; ++step) {
+        const int buf = step & 1;
+        compute(desc_now, buf);
+        desc_now = desc_next;
+        if (step + 1 < steps) {
+            store(sg, desc_now, buf ^ 1);  // operands of step + 1
+            if (step + 2 < steps) desc_next = load(cursor, sg);
+        }
+        __syncthreads();
     }
 
 #pragma unroll
