@@ -40,7 +40,7 @@ def check(out, x, codes, scales, k):
     return int((diff > 0).sum())
 
 
-@pytest.mark.parametrize("shape", [(1, 64), (7, 72), (33, 136), (16, 256), (257, 5120), (100, 1000)])
+@pytest.mark.parametrize("shape", [(1, 64), (7, 72), (33, 136), (16, 256), (257, 5120), (100, 1000), (16400, 136)])
 @pytest.mark.parametrize("tokens", [1, 2, 3, 4, 8, 13, 16, 17, 32])
 def test_mfma_tolerances_tails_and_guards(backend, device, shape, tokens):
     n, k = shape

@@ -149,7 +149,9 @@ __global__ __launch_bounds__(kThreads) void q8_exact(const T* __restrict__ x,
     // Wave-uniform quantities live in scalar registers, so every branch on
     // them below is a scalar branch and the prefetch is never predicated
     // (a predicated prefetch would make the compiler wait for it at once).
-    const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + (threadIdx.x >> 6));
+    // Workgroup-minor wave numbering: consecutive row blocks go to different
+    // workgroups, so every workgroup (and CU) holds the same number of rows.
+    const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) * gridDim.x + blockIdx.x);
     const int waves = gridDim.x * kWaves;
     const int blocks = (n + RR - 1) / RR;
     if (wave >= blocks) return;
@@ -254,9 +256,10 @@ void launch_tile(const void* x, const std::int8_t* codes, const __half* scales, 
                  int tokens, int n, int k, int padded, hipStream_t stream) {
     // At most two 16-wave workgroups per CU (256 CUs): each stages the
     // activations once and streams many rows; grid.y walks token tiles (each
-    // re-streams the weights).
+    // re-streams the weights). Row blocks are dealt round-robin over the
+    // workgroups, so all of them are used as soon as there are 512 blocks.
     const int blocks = (n + RR - 1) / RR;
-    const int groups = std::min((blocks + kWaves - 1) / kWaves, 512);
+    const int groups = std::min(blocks, 512);
     const dim3 grid(groups, (tokens + TT - 1) / TT);
     require(grid.y <= 65535, "token tiles exceed the launch grid");
     const std::size_t lds = exact_lds_bytes(TT, U, k);

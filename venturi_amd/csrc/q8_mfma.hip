@@ -274,14 +274,21 @@ void q8_tiled_launch(const void* x, const void* codes, const void* scales, void*
     require(k % 8 == 0 && aligned(x, 16), "the Q8 MFMA route needs k % 8 == 0 and 16-byte aligned x");
     require(aligned(codes, 16) && aligned(scales, 4) && aligned(out, 2), "misaligned Q8 operand");
     require(tokens <= 32, "the tiled Q8 MFMA decode kernel takes at most 32 tokens");
-    // Two row blocks per workgroup: each activation fragment feeds two MFMA
-    // pairs (measured better than one or four blocks at the config-2 shapes).
+    // Row blocks per workgroup: every activation fragment a wave loads feeds
+    // one MFMA pair per row block, so more blocks cut the activation traffic
+    // through the vector L1, which grows with the token count; fewer blocks
+    // keep more workgroups in flight. Two blocks (four steps of 1 KB each in
+    // flight per block) below 8 tokens or on matrices of fewer than 1024
+    // blocks; four blocks (two steps) otherwise. Both measured on the
+    // config-2 shapes.
     const int blocks = (n + 15) / 16;
     const auto* xp = static_cast<const __half*>(x);
     const auto* cp = static_cast<const uint4*>(codes);
     const auto* sp = static_cast<const std::uint32_t*>(scales);
     auto* op = static_cast<__half*>(out);
-    if (tokens <= 16)
+    if (tokens <= 16 && tokens >= 8 && blocks >= 1024)
+        q8_tiled_decode<2, 4, 1><<<(blocks + 3) / 4, 1024, 0, stream>>>(xp, cp, sp, op, tokens, n, k, padded / 64, blocks);
+    else if (tokens <= 16)
         q8_tiled_decode<4, 2, 1><<<(blocks + 1) / 2, 1024, 0, stream>>>(xp, cp, sp, op, tokens, n, k, padded / 64, blocks);
     else
         q8_tiled_decode<4, 2, 2><<<(blocks + 1) / 2, 1024, 0, stream>>>(xp, cp, sp, op, tokens, n, k, padded / 64, blocks);
