@@ -40,7 +40,7 @@ def check(out, x, codes, scales, k):
     return int((diff > 0).sum())
 
 
-@pytest.mark.parametrize("shape", [(1, 64), (7, 72), (33, 136), (16, 256), (257, 5120), (100, 1000), (16400, 136)])
+@pytest.mark.parametrize("shape", [(1, 64), (7, 72), (33, 136), (16, 256), (257, 5120), (100, 1000), (16400, 136), (40, 16392)])
 @pytest.mark.parametrize("tokens", [1, 2, 3, 4, 8, 13, 16, 17, 32])
 def test_mfma_tolerances_tails_and_guards(backend, device, shape, tokens):
     n, k = shape
@@ -84,7 +84,8 @@ def test_mfma_route_admission(backend, device):
     assert resident.prepare(tokens=8).route == "venturi-q8-exact"
     codes, scales = random_q8(8, 64, 1)
     resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.float16, device=device)
-    assert resident.prepare(tokens=1).route == "venturi-q8-exact"
+    assert resident.prepare(tokens=1).route == "venturi-q8-mfma"
+    assert resident.prepare(tokens=1, route="exact").route == "venturi-q8-exact"
     assert resident.prepare(tokens=2).route == "venturi-q8-mfma"
     assert resident.prepare(tokens=32).route == "venturi-q8-mfma"
     assert resident.prepare(tokens=33).route == "venturi-q8-exact"

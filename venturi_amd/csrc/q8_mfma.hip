@@ -150,29 +150,43 @@ __global__ __launch_bounds__(1024) void q8_mfma_decode(const __half* __restrict_
 // [b][c][lane l = 16q + m][16 bytes]; lane (m, q) holds row m's codes of
 // columns 64c + 8q .. +8 (group 2c) then 64c + 32 + 8q .. +8 (group 2c + 1),
 // exactly the two MFMA B-operand fragments it needs. Scales are [b][c][m][2]
-// fp16 (groups 2c, 2c + 1 of row m). A wave streams its chunks of a row block
-// as contiguous 1 KB loads. Padding rows/columns hold zero codes and scales.
-// Workgroup: RB consecutive row blocks; its 16 waves split the chunks, and each
-// wave reuses one activation fragment for all RB row blocks of its chunk. NB
-// token blocks of 16 (tokens <= 16 * NB) share every weight fragment.
-template <int STEPS, int RB, int NB>
-__global__ __launch_bounds__(1024) void q8_tiled_decode(const __half* __restrict__ x, const uint4* __restrict__ codes,
-                                                        const std::uint32_t* __restrict__ scales,
-                                                        __half* __restrict__ out, int tokens, int n, int k,
-                                                        int chunks, int blocks) {
-    __shared__ float4v partial[kDecodeWaves][RB * NB][64];
+// fp16 (groups 2c, 2c + 1 of row m). Padding rows hold zero codes and scales.
+//
+// Workgroup: W waves over RB consecutive row blocks. Wave w owns the chunk
+// range [w*per, (w+1)*per) of every one of them and streams it in batches of
+// STEPS chunks with a two-deep ping-pong: the codes, scales and activation
+// fragments of batch i+1 are in flight while batch i is multiplied. Each
+// activation fragment feeds one MFMA pair per row block; NB token blocks of
+// 16 (tokens <= 16 * NB) share every weight fragment. Only lanes whose token
+// row exists load activations (the others hold zeros), so small token counts
+// cost no activation traffic beyond their rows. The W partial tiles are summed
+// through LDS in wave order 0..W-1, so results are deterministic.
+template <int RB, int NB, int STEPS>
+struct TiledBatch {
+    uint4 w[STEPS][RB];
+    std::uint32_t sc[STEPS][RB];
+    uint4 xa[STEPS][NB], xb[STEPS][NB];
+};
+
+template <int W, int RB, int NB, int STEPS>
+__global__ __launch_bounds__(W * 64) void q8_tiled_decode(const __half* __restrict__ x, const uint4* __restrict__ codes,
+                                                          const std::uint32_t* __restrict__ scales,
+                                                          __half* __restrict__ out, int tokens, int n, int k,
+                                                          int chunks, int blocks) {
+    __shared__ float4v partial[W][RB * NB][64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r = lane & 15;
     const int block0 = blockIdx.x * RB;
-    const int per = (chunks + kDecodeWaves - 1) / kDecodeWaves;
-    const int c0 = wave * per, c1 = min(c0 + per, chunks);
-    bool live_token[NB];
+    const int per = (chunks + W - 1) / W;
+    const int c0 = min(wave * per, chunks), c1 = min(c0 + per, chunks);
+    const int batches = (c1 - c0 + STEPS - 1) / STEPS;
+    bool live[NB];
     const __half* xrow[NB];
 #pragma unroll
     for (int tb = 0; tb < NB; ++tb) {
-        live_token[tb] = 16 * tb + r < tokens;
-        xrow[tb] = x + static_cast<std::int64_t>(min(16 * tb + r, tokens - 1)) * k;
+        live[tb] = 16 * tb + r < tokens;
+        xrow[tb] = x + static_cast<std::int64_t>(min(16 * tb + r, tokens - 1)) * k + 8 * q;
     }
     const uint4* wsrc[RB];
     const std::uint32_t* ssrc[RB];
@@ -183,49 +197,63 @@ __global__ __launch_bounds__(1024) void q8_tiled_decode(const __half* __restrict
         ssrc[b] = scales + static_cast<std::int64_t>(blk) * chunks * 16 + r;
     }
 
+    // Batch i covers chunks c0 + i*STEPS .. ; chunks past c1 are clamped to
+    // c1 - 1 when loaded and skipped when multiplied.
+    auto fetch = [&](int i, TiledBatch<RB, NB, STEPS>& t) {
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const int ch = min(c0 + i * STEPS + s, c1 - 1);
+#pragma unroll
+            for (int b = 0; b < RB; ++b) {
+                t.w[s][b] = wsrc[b][static_cast<std::int64_t>(ch) * 64];
+                t.sc[s][b] = ssrc[b][static_cast<std::int64_t>(ch) * 16];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const int col = min(c0 + i * STEPS + s, c1 - 1) * 64;
+#pragma unroll
+            for (int tb = 0; tb < NB; ++tb) {
+                uint4 a = make_uint4(0u, 0u, 0u, 0u), bq = make_uint4(0u, 0u, 0u, 0u);
+                if (live[tb]) {
+                    a = *reinterpret_cast<const uint4*>(xrow[tb] + min(col, k - 8 - 8 * q));
+                    bq = *reinterpret_cast<const uint4*>(xrow[tb] + min(col + 32, k - 8 - 8 * q));
+                }
+                t.xa[s][tb] = a;
+                t.xb[s][tb] = bq;
+            }
+        }
+    };
+
     float4v y[RB][NB];
 #pragma unroll
     for (int b = 0; b < RB; ++b)
 #pragma unroll
         for (int tb = 0; tb < NB; ++tb) y[b][tb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
     const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c = c0; c < c1; c += STEPS) {
-        uint4 w[STEPS][RB], xa[STEPS][NB], xb[STEPS][NB];
-        std::uint32_t sc[STEPS][RB];
+
+    auto consume = [&](int i, const TiledBatch<RB, NB, STEPS>& t) {
 #pragma unroll
-        for (int i = 0; i < STEPS; ++i) {
-            const int ch = min(c + i, c1 - 1);  // clamped repeats are not accumulated
+        for (int s = 0; s < STEPS; ++s) {
+            const int ch = c0 + i * STEPS + s;
+            if (ch >= c1) break;
             const int col = ch * 64 + 8 * q;
-#pragma unroll
-            for (int b = 0; b < RB; ++b) {
-                w[i][b] = wsrc[b][static_cast<std::int64_t>(ch) * 64];
-                sc[i][b] = ssrc[b][static_cast<std::int64_t>(ch) * 16];
-            }
-#pragma unroll
-            for (int tb = 0; tb < NB; ++tb) {
-                xa[i][tb] = *reinterpret_cast<const uint4*>(xrow[tb] + min(col, k - 8));
-                xb[i][tb] = *reinterpret_cast<const uint4*>(xrow[tb] + min(col + 32, k - 8));
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < STEPS; ++i) {
-            if (c + i >= c1) break;
-            const int col = (c + i) * 64 + 8 * q;
             half8 fa[NB], fb[NB];
 #pragma unroll
             for (int tb = 0; tb < NB; ++tb) {
-                fa[tb] = live_token[tb] && col < k ? __builtin_bit_cast(half8, xa[i][tb]) : half8{};
-                fb[tb] = live_token[tb] && col + 32 < k ? __builtin_bit_cast(half8, xb[i][tb]) : half8{};
+                // Columns at or past k are zero (the clamped load read other columns).
+                fa[tb] = col < k ? __builtin_bit_cast(half8, t.xa[s][tb]) : half8{};
+                fb[tb] = col + 32 < k ? __builtin_bit_cast(half8, t.xb[s][tb]) : half8{};
             }
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
                 std::uint32_t h0, h1, h2, h3, h4, h5, h6, h7;
-                codes_to_half4(w[i][b].x, h0, h1);
-                codes_to_half4(w[i][b].y, h2, h3);
-                codes_to_half4(w[i][b].z, h4, h5);
-                codes_to_half4(w[i][b].w, h6, h7);
+                codes_to_half4(t.w[s][b].x, h0, h1);
+                codes_to_half4(t.w[s][b].y, h2, h3);
+                codes_to_half4(t.w[s][b].z, h4, h5);
+                codes_to_half4(t.w[s][b].w, h6, h7);
                 const half8 wa = pack8(h0, h1, h2, h3), wb = pack8(h4, h5, h6, h7);
-                const float sa = half_lo(sc[i][b]), sb = half_hi(sc[i][b]);  // padded groups carry scale 0
+                const float sa = half_lo(t.sc[s][b]), sb = half_hi(t.sc[s][b]);  // padded groups carry scale 0
 #pragma unroll
                 for (int tb = 0; tb < NB; ++tb) {
                     const float4v da = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[tb], wa, zero, 0, 0, 0);
@@ -238,20 +266,32 @@ __global__ __launch_bounds__(1024) void q8_tiled_decode(const __half* __restrict
                 }
             }
         }
+    };
+
+    if (batches > 0) {
+        TiledBatch<RB, NB, STEPS> ta, tb2;
+        fetch(0, ta);
+        for (int i = 0; i < batches; i += 2) {
+            if (i + 1 < batches) fetch(i + 1, tb2);
+            consume(i, ta);
+            if (i + 1 >= batches) break;
+            if (i + 2 < batches) fetch(i + 2, ta);
+            consume(i + 1, tb2);
+        }
     }
 #pragma unroll
     for (int b = 0; b < RB; ++b)
 #pragma unroll
         for (int tb = 0; tb < NB; ++tb) partial[wave][b * NB + tb][lane] = y[b][tb];
     __syncthreads();
-    // Waves 0..RB*NB-1 each reduce one (row block, token block) in wave order 0..15.
-    if (wave < RB * NB) {
-        const int b = wave / NB, tb = wave % NB;
-        float4v sum = partial[0][wave][lane];
-        for (int w = 1; w < kDecodeWaves; ++w) {
-            const float4v p = partial[w][wave][lane];
+    // Waves 0..RB*NB-1 each reduce one (row block, token block) in wave order.
+    for (int p = wave; p < RB * NB; p += W) {
+        const int b = p / NB, tb = p % NB;
+        float4v sum = partial[0][p][lane];
+        for (int w = 1; w < W; ++w) {
+            const float4v v = partial[w][p][lane];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sum[j] += p[j];
+            for (int j = 0; j < 4; ++j) sum[j] += v[j];
         }
         // D layout: lane holds rows (tokens) 4q..4q+3 of the token block, weight row r.
 #pragma unroll
@@ -261,6 +301,159 @@ __global__ __launch_bounds__(1024) void q8_tiled_decode(const __half* __restrict
             if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(sum[j]);
         }
     }
+}
+
+// The same projection with the activations staged in LDS once per workgroup
+// (used when tokens x padded columns fit). Rows 0..tokens-1 hold x with zeros
+// from column k up to the padded width, so no fragment needs masking; lanes of
+// token rows that do not exist read a 128-byte zero block. Row t's 16-byte
+// units are stored XOR-swizzled by (t & 7) inside each 128-byte span, so the
+// 16 token rows of one fragment read land in distinct banks. After the main
+// loop the LDS holds the per-wave partial tiles instead. TMAX bounds the
+// token count (1, 4 or 16): with one token only the first accumulator of each
+// lane is live, so the group scaling costs one FMA per group instead of four.
+template <int RB, int STEPS>
+struct LdsBatch {
+    uint4 w[STEPS][RB];
+    std::uint32_t sc[STEPS][RB];
+};
+
+__host__ __device__ inline std::size_t lds_x_bytes(int tokens, int chunks) {
+    return static_cast<std::size_t>(tokens) * chunks * 128 + (tokens < 16 ? 128 : 0);
+}
+
+template <int W, int RB, int STEPS, int TMAX>
+__global__ __launch_bounds__(W * 64) void q8_tiled_lds(const __half* __restrict__ x, const uint4* __restrict__ codes,
+                                                       const std::uint32_t* __restrict__ scales,
+                                                       __half* __restrict__ out, int tokens, int n, int k, int chunks,
+                                                       int blocks) {
+    extern __shared__ uint4 lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, r = lane & 15;
+    const int block0 = blockIdx.x * RB;
+    const int per = (chunks + W - 1) / W;
+    const int c0 = min(wave * per, chunks), c1 = min(c0 + per, chunks);
+    const int batches = (c1 - c0 + STEPS - 1) / STEPS;
+    const uint4* wsrc[RB];
+    const std::uint32_t* ssrc[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+        const int blk = min(block0 + b, blocks - 1);  // clamped blocks are never stored
+        wsrc[b] = codes + static_cast<std::int64_t>(blk) * chunks * 64 + lane;
+        ssrc[b] = scales + static_cast<std::int64_t>(blk) * chunks * 16 + r;
+    }
+    auto fetch = [&](int i, LdsBatch<RB, STEPS>& t) {
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const int ch = min(c0 + i * STEPS + s, c1 - 1);
+#pragma unroll
+            for (int b = 0; b < RB; ++b) {
+                t.w[s][b] = wsrc[b][static_cast<std::int64_t>(ch) * 64];
+                t.sc[s][b] = ssrc[b][static_cast<std::int64_t>(ch) * 16];
+            }
+        }
+    };
+    // The first weight batch is in flight while the activations are staged.
+    LdsBatch<RB, STEPS> ta, tb2;
+    if (batches > 0) fetch(0, ta);
+
+    const int units = chunks * 8;  // 16-byte units per staged row
+    for (int i = threadIdx.x; i < tokens * units; i += W * 64) {
+        const int t = i / units, u = i - t * units;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (8 * u < k) v = *reinterpret_cast<const uint4*>(x + static_cast<std::int64_t>(t) * k + 8 * u);
+        lds[t * units + (u ^ (t & 7))] = v;
+    }
+    if (tokens < 16 && threadIdx.x < 8) lds[tokens * units + threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+
+    // Fragment addresses (in 16-byte units): chunk ch, group half g (0 or 1)
+    // of lane (r, q) is unit ch*8 + 4g + q of row r, swizzled.
+    const bool live = r < tokens;
+    const int rowbase = live ? r * units : tokens * units;
+    const int swz = live ? (r & 7) : 0;
+    const int step = live ? 8 : 0;
+
+    float4v y[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) y[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto consume = [&](int i, const LdsBatch<RB, STEPS>& t) {
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const int ch = c0 + i * STEPS + s;
+            if (ch >= c1) break;
+            const int base = rowbase + ch * step;
+            const half8 fa = __builtin_bit_cast(half8, lds[base + ((q) ^ swz)]);
+            const half8 fb = __builtin_bit_cast(half8, lds[base + ((4 + q) ^ swz)]);
+#pragma unroll
+            for (int b = 0; b < RB; ++b) {
+                std::uint32_t h0, h1, h2, h3, h4, h5, h6, h7;
+                codes_to_half4(t.w[s][b].x, h0, h1);
+                codes_to_half4(t.w[s][b].y, h2, h3);
+                codes_to_half4(t.w[s][b].z, h4, h5);
+                codes_to_half4(t.w[s][b].w, h6, h7);
+                const half8 wa = pack8(h0, h1, h2, h3), wb = pack8(h4, h5, h6, h7);
+                const float sa = half_lo(t.sc[s][b]), sb = half_hi(t.sc[s][b]);  // padded groups carry scale 0
+                const float4v da = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa, wa, zero, 0, 0, 0);
+                const float4v db = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb, wb, zero, 0, 0, 0);
+                constexpr int live_acc = TMAX == 1 ? 1 : 4;
+#pragma unroll
+                for (int j = 0; j < live_acc; ++j) {
+                    y[b][j] = fmaf(da[j], sa, y[b][j]);
+                    y[b][j] = fmaf(db[j], sb, y[b][j]);
+                }
+            }
+        }
+    };
+    if (batches > 0) {
+        for (int i = 0; i < batches; i += 2) {
+            if (i + 1 < batches) fetch(i + 1, tb2);
+            consume(i, ta);
+            if (i + 1 >= batches) break;
+            if (i + 2 < batches) fetch(i + 2, ta);
+            consume(i + 1, tb2);
+        }
+    }
+    __syncthreads();  // every wave is done with the staged activations
+    float4v* partial = reinterpret_cast<float4v*>(lds);  // [W][RB][64]
+#pragma unroll
+    for (int b = 0; b < RB; ++b) partial[(wave * RB + b) * 64 + lane] = y[b];
+    __syncthreads();
+    for (int b = wave; b < RB; b += W) {
+        float4v sum = partial[b * 64 + lane];
+        for (int w = 1; w < W; ++w) {
+            const float4v v = partial[(w * RB + b) * 64 + lane];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sum[j] += v[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = 4 * q + j;
+            const int row = (block0 + b) * 16 + r;
+            if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(sum[j]);
+        }
+    }
+}
+
+template <int W, int RB, int STEPS, int TMAX>
+void launch_tiled_lds(const __half* x, const uint4* codes, const std::uint32_t* scales, __half* out, int tokens, int n,
+                      int k, int chunks, int blocks, hipStream_t stream) {
+    const std::size_t lds = std::max(lds_x_bytes(tokens, chunks), static_cast<std::size_t>(W) * RB * 1024);
+    require(lds <= 160 * 1024, "staged activations exceed LDS");
+    static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void*>(q8_tiled_lds<W, RB, STEPS, TMAX>),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    check(raised);
+    q8_tiled_lds<W, RB, STEPS, TMAX><<<(blocks + RB - 1) / RB, W * 64, lds, stream>>>(x, codes, scales, out, tokens, n, k,
+                                                                                     chunks, blocks);
+}
+
+template <int W, int RB, int NB, int STEPS>
+void launch_tiled(const __half* x, const uint4* codes, const std::uint32_t* scales, __half* out, int tokens, int n,
+                  int k, int chunks, int blocks, hipStream_t stream) {
+    q8_tiled_decode<W, RB, NB, STEPS><<<(blocks + RB - 1) / RB, W * 64, 0, stream>>>(x, codes, scales, out, tokens, n,
+                                                                                     k, chunks, blocks);
 }
 
 }  // namespace
@@ -274,24 +467,28 @@ void q8_tiled_launch(const void* x, const void* codes, const void* scales, void*
     require(k % 8 == 0 && aligned(x, 16), "the Q8 MFMA route needs k % 8 == 0 and 16-byte aligned x");
     require(aligned(codes, 16) && aligned(scales, 4) && aligned(out, 2), "misaligned Q8 operand");
     require(tokens <= 32, "the tiled Q8 MFMA decode kernel takes at most 32 tokens");
-    // Row blocks per workgroup: every activation fragment a wave loads feeds
-    // one MFMA pair per row block, so more blocks cut the activation traffic
-    // through the vector L1, which grows with the token count; fewer blocks
-    // keep more workgroups in flight. Two blocks (four steps of 1 KB each in
-    // flight per block) below 8 tokens or on matrices of fewer than 1024
-    // blocks; four blocks (two steps) otherwise. Both measured on the
-    // config-2 shapes.
     const int blocks = (n + 15) / 16;
+    const int chunks = padded / 64;
     const auto* xp = static_cast<const __half*>(x);
     const auto* cp = static_cast<const uint4*>(codes);
     const auto* sp = static_cast<const std::uint32_t*>(scales);
     auto* op = static_cast<__half*>(out);
-    if (tokens <= 16 && tokens >= 8 && blocks >= 1024)
-        q8_tiled_decode<2, 4, 1><<<(blocks + 3) / 4, 1024, 0, stream>>>(xp, cp, sp, op, tokens, n, k, padded / 64, blocks);
+    // Launch shapes measured on the config-2 matrices (QKV 7168x5120, o_proj
+    // 5120x6144, gate+up 34816x5120, down 5120x17408) at 1-16 tokens. One
+    // token: activations staged in LDS, 16 waves on matrices of fewer than
+    // 1024 row blocks and 8 waves otherwise. Up to four tokens at K >= 16384:
+    // LDS-staged with 16 waves. Otherwise register-loaded fragments, 8 waves
+    // over two row blocks.
+    if (tokens == 1 && blocks < 1024)
+        launch_tiled_lds<16, 2, 2, 1>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    else if (tokens == 1)
+        launch_tiled_lds<8, 2, 2, 1>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    else if (tokens <= 4 && k >= 16384 && lds_x_bytes(tokens, chunks) <= 160 * 1024)
+        launch_tiled_lds<16, 2, 2, 4>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
     else if (tokens <= 16)
-        q8_tiled_decode<4, 2, 1><<<(blocks + 1) / 2, 1024, 0, stream>>>(xp, cp, sp, op, tokens, n, k, padded / 64, blocks);
+        launch_tiled<8, 2, 1, 2>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
     else
-        q8_tiled_decode<4, 2, 2><<<(blocks + 1) / 2, 1024, 0, stream>>>(xp, cp, sp, op, tokens, n, k, padded / 64, blocks);
+        launch_tiled<8, 2, 2, 2>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
 }
 
 void q8_mfma_launch(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n,

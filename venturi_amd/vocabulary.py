@@ -12,10 +12,12 @@ family once:
   It reads a tiled copy of the planes (16-row blocks x 64-column chunks in
   MFMA operand order, built once by the first ``mfma`` plan and kept with the
   resident weight), so every wave streams contiguous 1 KB blocks;
-* ``auto``: ``exact`` for one token (bit-identical to the reference and bound
-  by HBM), ``mfma`` from two tokens when its conditions hold (the canonical
-  order needs one fp32 FMA per token and weight, so ``exact`` becomes
-  VALU-bound as tokens grow), else ``exact``.
+* ``auto``: ``mfma`` whenever its conditions hold (FP16 activations,
+  K % 8 == 0, at most 32 tokens), else ``exact``. The matrix-core kernel
+  streams the weights faster at every token count (the canonical order
+  needs one fp32 FMA per token and weight plus an exact weight conversion,
+  and its lane-per-four-columns layout issues 4-byte loads); callers that
+  need the reference's bytes ask for ``exact``.
 """
 
 from dataclasses import dataclass, field
@@ -25,7 +27,7 @@ import torch
 
 from .blocks import _DTYPES, Q8_ROUTES, _no_overlap, _shape, _stream, _tensor
 
-EXACT_MAX_AUTO_TOKENS = 1
+EXACT_MAX_AUTO_TOKENS = 0
 MFMA_MAX_TOKENS = 32
 _TILE_LOCK = threading.Lock()
 
