@@ -54,6 +54,14 @@ int venturi_q8_dp4a_quantize(const void* x, void* workspace, uint64_t available,
 int venturi_q8_dp4a_run(const void* workspace, uint64_t available, const int8_t* codes, const void* scales,
                         void* out, int tokens, int n, int k, int padded, int passes, void* stream);
 
+/* Extension (no counterpart in the reference): the same W8A8 projection on
+ * int-exact fp16 matrix cores, with the 32-column group dots exact (as the
+ * reference's int32 accumulators) and the scaled group terms summed in
+ * natural order, so outputs match the reference to fp32 association. Same
+ * arguments and workspace as venturi_q8_dp4a_run. */
+int venturi_q8_a8_gemm_run(const void* workspace, uint64_t available, const int8_t* codes, const void* scales,
+                           void* out, int tokens, int n, int k, int padded, int passes, void* stream);
+
 /* RMSNorm out = (x * 1/sqrt(mean(x^2) + eps)) * w, fp32 w.
  * Replaces ops_api.h:93-94 / blocks.cu:727-740. */
 int venturi_rms_run(const void* x, const float* w, void* out, int tokens, int features, int dtype, float epsilon,

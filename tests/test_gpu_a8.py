@@ -134,7 +134,8 @@ def test_matrix_core_projection_bytes(backend, device, passes, tokens, shape):
     n, k = shape
     print(f"case a8-gemm n={n} k={k} tokens={tokens} passes={passes}", flush=True)
     codes, scales, x, resident = _setup(backend, device, n, k, tokens)
-    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=passes == 2)
+    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=passes == 2, route="exact")
+    assert plan.route == "venturi-q8-a8"
     workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
     guard, out = guarded_out(tokens, n, torch.float16, device)
     plan.run(x.to(device), out=out, workspace=workspace)
@@ -153,13 +154,109 @@ def test_config3_prefill_sampled(backend, device, n, k):
     packed = backend.quantize_q8(torch.randn(n, k, generator=gen, device=device) * 0.02)
     x = torch.randn(tokens, k, generator=gen, device=device).half()
     resident = backend.upload_linear(packed, dtype=torch.float16, device=device)
-    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=False)
-    workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
-    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
-    plan.run(x, out=out, workspace=workspace)
     rng = np.random.default_rng(n + k)
     ts = np.sort(rng.choice(tokens, 64, replace=False))
     rows = np.sort(rng.choice(n, 128, replace=False))
     q, d = oracle.a8_quantize(bits(x[ts]), 1)
-    expected = oracle.a8_linear(q, d, packed.codes.cpu().numpy()[rows], packed.scales.cpu().numpy()[rows], k)
-    np.testing.assert_array_equal(bits(out)[ts][:, rows], expected)
+    wc, ws = packed.codes.cpu().numpy()[rows], packed.scales.cpu().numpy()[rows]
+    expected = oracle.a8_linear(q, d, wc, ws, k)
+    for route in ("exact", "mfma"):
+        plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=False, route=route)
+        workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+        out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+        plan.run(x, out=out, workspace=workspace)
+        got = bits(out)[ts][:, rows]
+        if route == "exact":
+            np.testing.assert_array_equal(got, expected)
+        else:
+            flips = check_a8_tolerance(got, q, d, wc, ws, k, expected)
+            print(f"config3 n={n} k={k} mfma: {flips} of {got.size} differ from the reference order", flush=True)
+
+
+def ulp16(v):
+    v = np.abs(v)
+    return 2.0 ** (np.floor(np.log2(np.maximum(v, 2.0**-14))) - 10)
+
+
+def check_a8_tolerance(got_bits, q, d, wcodes, wscales, k, expected_bits):
+    """The mfma route against FP64 over the exact group dots and against the reference order.
+
+    FP64: y = sum_p sum_g dot_pg * fp32(ws_g * as_pg), the reference's per-group
+    terms; the fp32 natural-order sum may differ from it by at most
+    G * 2^-24 * sum|terms| plus the final fp16 rounding (half an ulp).
+    Reference order: every output within max(2e-3, 1 fp16 ulp) and rel-L2 <= 1e-3
+    (the stated tolerance for fp16 outputs).
+    """
+    got = got_bits.view(np.float16).astype(np.float64)
+    passes, groups = q.shape[0], q.shape[2]
+    ws32 = wscales.astype(np.float32)[:, :groups]
+    y = np.zeros(got.shape)
+    mag = np.zeros(got.shape)
+    for p in range(passes):
+        dots = oracle.a8_group_dots(q[p : p + 1], wcodes, k).astype(np.float64)  # [T, N, G]
+        prod = (ws32[None, :, :] * d[p][:, None, :]).astype(np.float64)  # fp32 products, as the reference
+        terms = dots * prod
+        y += terms.sum(-1)
+        mag += np.abs(terms).sum(-1)
+    bound = 0.5 * ulp16(y) + passes * groups * 2.0**-24 * mag
+    assert (np.abs(got - y) <= bound).all()
+    ref = expected_bits.view(np.float16).astype(np.float64)
+    diff = np.abs(got - ref)
+    assert (diff <= np.maximum(2e-3, ulp16(ref))).all()
+    assert np.linalg.norm(got - ref) <= 1e-3 * max(np.linalg.norm(ref), 1e-12)
+    return int((diff > 0).sum())
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+@pytest.mark.parametrize("tokens", [1, 64, 65, 257])
+@pytest.mark.parametrize("shape", [(7, 1), (33, 67), (129, 1000), (70, 2000), (64, 5120), (300, 520), (40, 26000)])
+def test_mfma_route_tolerance(backend, device, passes, tokens, shape):
+    n, k = shape
+    print(f"case a8-mfma n={n} k={k} tokens={tokens} passes={passes}", flush=True)
+    codes, scales, x, resident = _setup(backend, device, n, k, tokens)
+    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=passes == 2, route="mfma")
+    assert plan.route == "venturi-q8-a8-mfma"
+    workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    guard, out = guarded_out(tokens, n, torch.float16, device)
+    plan.run(x.to(device), out=out, workspace=workspace)
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    q, d = oracle.a8_quantize(bits(x), passes)
+    np.testing.assert_array_equal(workspace.cpu().numpy(), oracle.a8_workspace(q, d))
+    expected = oracle.a8_linear(q, d, codes.numpy(), scales.numpy(), k)
+    flips = check_a8_tolerance(bits(out), q, d, codes.numpy(), scales.numpy(), k, expected)
+    print(f"flips={flips} of {tokens * n}", flush=True)
+
+
+@pytest.mark.parametrize("k", [32, 96, 200])
+def test_mfma_route_exact_group_dots(backend, device, k):
+    # Unit scales, weight codes in [-2, 2] and two nonzero activations per group
+    # (127, which makes the activation scale exactly 1, and one in [-2, 2]) keep
+    # every output an integer below 2048, so fp32 sums in any order and the fp16
+    # rounding are exact: any error in a group dot (a wrong lane, column or
+    # code) changes the bytes.
+    tokens, n = 130, 48
+    padded = (k + 127) // 128 * 128
+    gen = torch.Generator().manual_seed(900 + k)
+    codes = torch.randint(-2, 3, (n, padded), dtype=torch.int8, generator=gen)
+    scales = torch.ones(n, padded // 32, dtype=torch.float16)
+    x = torch.zeros(tokens, k)
+    groups = (k + 31) // 32
+    for t in range(tokens):
+        for gi in range(groups):
+            width = min(32, k - 32 * gi)
+            x[t, 32 * gi + int(torch.randint(width, (1,), generator=gen))] = 127.0  # activation scale exactly 1
+            col = 32 * gi + int(torch.randint(width, (1,), generator=gen))
+            x[t, col] += float(torch.randint(-2, 3, (1,), generator=gen)) if x[t, col] == 0 else 0.0
+    x = x.half()
+    resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, k), dtype=torch.float16, device=device)
+    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=False, route="mfma")
+    workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    plan.run(x.to(device), out=out, workspace=workspace)
+    q, d = oracle.a8_quantize(bits(x), 1)
+    assert (d == 1.0).all()
+    dots = oracle.a8_group_dots(q, codes.numpy(), k).astype(np.int64).sum(-1)
+    assert (np.abs(dots) < 2048).all()
+    np.testing.assert_array_equal(out.cpu().float().numpy(), dots.astype(np.float32))
+    np.testing.assert_array_equal(bits(out), oracle.a8_linear(q, d, codes.numpy(), scales.numpy(), k))

@@ -13,6 +13,8 @@ constexpr int kA8GemmMinTokens = 64;
 
 void a8_gemm_launch(const void* workspace, const std::int8_t* codes, const __half* scales, void* out, int tokens,
                     int n, int k, int padded, int passes, hipStream_t stream);
+void a8_fast_launch(const void* workspace, const std::int8_t* codes, const __half* scales, void* out, int tokens,
+                    int n, int k, int padded, int passes, hipStream_t stream);
 
 std::uint64_t a8_bytes(int tokens, int k, int passes) {
     // Same admission as q8_dp4a.cuh:7-13.
@@ -282,13 +284,18 @@ void a8_quantize_launch(const void* x, void* workspace, std::uint64_t available,
                                                                    tokens, k, groups, passes, vec);
 }
 
-void a8_gemv_launch(const void* workspace, std::uint64_t available, const std::int8_t* codes, const __half* scales,
-                    void* out, int tokens, int n, int k, int padded, int passes, hipStream_t stream) {
+void validate_a8_projection(const void* workspace, std::uint64_t available, const std::int8_t* codes,
+                            const __half* scales, const void* out, int tokens, int n, int k, int padded, int passes) {
     const std::uint64_t needed = a8_bytes(tokens, k, passes);
     require(workspace && available >= needed && codes && scales && out && n > 0 && n <= INT32_MAX - 3 &&
                 padded == padded_k(k) && static_cast<std::uint64_t>(tokens) * n < INT32_MAX &&
                 aligned(workspace, 16) && aligned(codes, 16) && aligned(scales, 2) && aligned(out, 2),
             "invalid A8 projection geometry/buffers");
+}
+
+void a8_gemv_launch(const void* workspace, std::uint64_t available, const std::int8_t* codes, const __half* scales,
+                    void* out, int tokens, int n, int k, int padded, int passes, hipStream_t stream) {
+    validate_a8_projection(workspace, available, codes, scales, out, tokens, n, k, padded, passes);
     const int groups = (k + 31) / 32;
     const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
     const auto* acodes = static_cast<const std::int8_t*>(workspace);
@@ -364,6 +371,20 @@ VT_EXPORT int venturi_q8_dp4a_run(const void* workspace, std::uint64_t available
                                   void* stream) {
     return vt::guarded([&] {
         vt::a8_gemv_launch(workspace, available, codes, scales, out, tokens, n, k, padded, passes,
+                           static_cast<hipStream_t>(stream));
+    });
+}
+
+// Extension: the same W8A8 projection on matrix cores with the groups summed
+// in natural order (exact int32 group dots, fp32 association differs from the
+// reference's lane-slot tree); same arguments and workspace as
+// venturi_q8_dp4a_run.
+VT_EXPORT int venturi_q8_a8_gemm_run(const void* workspace, std::uint64_t available, const std::int8_t* codes,
+                                     const __half* scales, void* out, int tokens, int n, int k, int padded,
+                                     int passes, void* stream) {
+    return vt::guarded([&] {
+        vt::validate_a8_projection(workspace, available, codes, scales, out, tokens, n, k, padded, passes);
+        vt::a8_fast_launch(workspace, codes, scales, out, tokens, n, k, padded, passes,
                            static_cast<hipStream_t>(stream));
     });
 }

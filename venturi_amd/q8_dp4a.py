@@ -4,8 +4,16 @@ Mirrors venturi.ops.q8_dp4a (reference q8_dp4a.py:43-114): the plan quantizes
 fp16 activations into a caller-owned workspace (``workspace_bytes`` bytes,
 16-byte aligned, layout int8 codes [pass][token][group][32] then fp32 scales
 [pass][token][group]) and projects them against the resident Q8 planes. Each
-32-column group's integer dot is exact; groups are combined in fp32 in the
-reference's order, so the fp16 outputs are byte-identical to the reference's.
+32-column group's integer dot is exact. Routes:
+
+* ``exact``: groups combined in fp32 in the reference's lane-slot and
+  shuffle-tree order (SIMT below 64 tokens, matrix cores above), so the fp16
+  outputs are byte-identical to the reference's;
+* ``mfma``: matrix cores with the scaled group terms summed in natural order
+  (one accumulator per output, large tiles), equal to the reference up to
+  fp32 association;
+* ``auto``: ``mfma`` from 64 tokens (prefill), ``exact`` below (decode, where
+  the projection streams the weights and the order costs nothing).
 """
 
 from dataclasses import dataclass
@@ -15,6 +23,9 @@ import torch
 from .blocks import ResidentLinear, _no_overlap, _shape, _stream, _tensor
 from .vocabulary import ResidentQ8Vocabulary
 
+A8_ROUTES = ("auto", "exact", "mfma")
+A8_MFMA_MIN_AUTO_TOKENS = 64
+
 
 @dataclass(frozen=True)
 class PreparedQ8DP4A:
@@ -23,6 +34,7 @@ class PreparedQ8DP4A:
     passes: int
     workspace_bytes: int
     _native: object
+    kernel: str = "exact"
 
     @property
     def precision_profile(self):
@@ -30,7 +42,7 @@ class PreparedQ8DP4A:
 
     @property
     def route(self):
-        return "venturi-q8-a8"
+        return "venturi-q8-a8" if self.kernel == "exact" else "venturi-q8-a8-mfma"
 
     def quantize(self, x, *, workspace):
         """Only the activation quantization step (fills ``workspace``)."""
@@ -57,9 +69,10 @@ class PreparedQ8DP4A:
         _no_overlap(out, (workspace,) + r.storage_tensors)
         if workspace.data_ptr() % 16:
             raise ValueError("A8 workspace requires 16-byte alignment")
+        entry = self._native.venturi_q8_dp4a_run if self.kernel == "exact" else self._native.venturi_q8_a8_gemm_run
         with torch.cuda.device(r.device):
             r.backend._check(
-                self._native.venturi_q8_dp4a_run(
+                entry(
                     workspace.data_ptr(), self.workspace_bytes, r._codes.data_ptr(), r._scales.data_ptr(),
                     out.data_ptr(), self.tokens, r.vocab_size, r.hidden_size, r._codes.shape[1], self.passes,
                     _stream(r.device),
@@ -80,8 +93,13 @@ class PreparedQ8DP4A:
         return self.project(out=out, workspace=workspace)
 
 
-def prepare_q8_dp4a(resident, *, tokens, residual_compensation):
-    """Opt-in A8 plan; the caller owns the workspace (q8_dp4a.py:95-114)."""
+def prepare_q8_dp4a(resident, *, tokens, residual_compensation, route="auto"):
+    """Opt-in A8 plan; the caller owns the workspace (q8_dp4a.py:95-114).
+
+    ``route`` (an addition to the reference's signature) selects the kernel
+    family: "exact", "mfma" or "auto" (see the module docstring)."""
+    if route not in A8_ROUTES:
+        raise ValueError(f"A8 route must be one of {A8_ROUTES}")
     if isinstance(resident, ResidentLinear):
         resident = resident._payload
     if not isinstance(resident, ResidentQ8Vocabulary):
@@ -99,4 +117,6 @@ def prepare_q8_dp4a(resident, *, tokens, residual_compensation):
     size = native.venturi_q8_dp4a_bytes(tokens, resident.hidden_size, passes)
     if not size:
         resident.backend._check(-1)
-    return PreparedQ8DP4A(resident, tokens, passes, size, native)
+    if route == "auto":
+        route = "mfma" if tokens >= A8_MFMA_MIN_AUTO_TOKENS else "exact"
+    return PreparedQ8DP4A(resident, tokens, passes, size, native, route)
