@@ -453,6 +453,196 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     }
 }
 
+// Grouped expert GEMM over the tiled planes with a fraction of an expert per
+// workgroup: W = 8 waves, wave v owns RB consecutive 16-row blocks (global
+// block b = tile * 8 + w of the tiled layout), so a workgroup covers 8 * RB
+// blocks and stages every activation chunk once in LDS for all of them. With
+// 128 experts and 4 parts per expert the grid is 512 workgroups, two per CU,
+// all resident at once. Weights are double-buffered in registers by half
+// chunk (1 KB per block): the loads of the next half are issued as soon as a
+// half has been multiplied, so each wave keeps RB KB in flight. Each
+// activation fragment is read from LDS once per step and multiplied by all RB
+// blocks. Passes of up to 16 * NBMAX tokens.
+template <int EPI, int W, int RB, int NBMAX>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void q4_grouped(Q4Tiled p, int parts,
+                                                                                                int blocks) {
+    __shared__ __attribute__((aligned(16))) _Float16 xl[2][16 * NBMAX * kXStride];
+    constexpr int kPass = 16 * NBMAX;
+
+    const int linear = blockIdx.x;
+    int expert, part;
+    if (p.experts % 8 == 0) {  // an expert's parts share one XCD (round-robin dispatch) and its L2
+        const int xcd = linear % 8, idx = linear / 8;
+        expert = 8 * (idx / parts) + xcd;
+        part = idx % parts;
+    } else {
+        expert = linear / parts;
+        part = linear % parts;
+    }
+    const int seg_begin = p.seg[expert];
+    const int seg_end = p.seg[expert + 1];
+    if (seg_begin >= seg_end) return;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4, m = lane & 15;
+    constexpr int T = W * 64;
+    const int b0 = (part * W + wave) * RB;  // this wave's first row block
+    // Per-block unit offsets (wave-uniform); clamped blocks are never stored.
+    std::int64_t unit[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const int b = min(b0 + r, blocks - 1);
+        unit[r] = static_cast<std::int64_t>(b >> 3) * p.chunks * 8 + (b & 7);
+    }
+    const uint4* wbase = p.codes + expert * p.code_stride + lane;
+    const __half* sbase = p.scales + expert * p.scale_stride + lane;
+
+    for (int pass = seg_begin; pass < seg_end; pass += kPass) {
+        const int live = min(kPass, seg_end - pass);
+        auto run_pass = [&](auto nb_tag) {
+            constexpr int NB = decltype(nb_tag)::value;
+            // Activation staging: XL 16-byte pieces per thread cover the NB token
+            // blocks (32 pieces per token row of a chunk).
+            constexpr int XL = (NB * 512 + T - 1) / T;
+            const __half* xrow[XL];
+            bool xlive[XL];
+#pragma unroll
+            for (int j = 0; j < XL; ++j) {
+                const int t = (tid + T * j) >> 5;
+                xlive[j] = t < live && t < 16 * NB;
+                const int slot = pass + min(t, live - 1);
+                const int row = p.gather ? p.gather[slot] : slot;
+                xrow[j] = p.x + static_cast<std::int64_t>(row) * p.x_stride;
+            }
+            struct Half {
+                uint4 w[RB];
+                unsigned short s[RB];
+            };
+            struct XStage {
+                uint4 v[XL];
+            };
+            // Half h of chunk c for every block: 16 code bytes and the group scale.
+            auto load_half = [&](int c, int h, Half& st) {
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    const std::int64_t u = unit[r] + static_cast<std::int64_t>(c) * 8;
+                    st.w[r] = wbase[u * 128 + 64 * h];
+                    if (h == 0) st.s[r] = __half_as_ushort(sbase[u * 64]);
+                }
+            };
+            auto load_x = [&](int c, XStage& x) {
+                const int col = c * kChunk + 8 * (tid & 31);
+#pragma unroll
+                for (int j = 0; j < XL; ++j) x.v[j] = *reinterpret_cast<const uint4*>(xrow[j] + min(col, p.k - 8));
+            };
+            auto store_x = [&](int c, const XStage& x, _Float16* buf) {
+                const int col = c * kChunk + 8 * (tid & 31);
+#pragma unroll
+                for (int j = 0; j < XL; ++j) {
+                    const int piece = tid + T * j;
+                    const std::uint32_t keep = (xlive[j] && col < p.k) ? 0xFFFFFFFFu : 0u;
+                    uint4 v = interleave8(x.v[j]);
+                    v.x &= keep;
+                    v.y &= keep;
+                    v.z &= keep;
+                    v.w &= keep;
+                    if (NB * 512 % T == 0 || piece < NB * 512)  // rows past the pass's token blocks are not staged
+                        *reinterpret_cast<uint4*>(buf + (piece >> 5) * kXStride + 8 * (piece & 31)) = v;
+                }
+            };
+
+            float4v acc[RB][NB];
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[r][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+            // Multiplies half h of the current chunk (code words 4h .. 4h + 3 of
+            // every block, activation columns 64q + 32h ..) from LDS buffer buf.
+            unsigned short scale[RB];
+            auto compute_half = [&](const Half& st, int h, const _Float16* buf) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    half8 xf[NB];
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+                        xf[b] = *reinterpret_cast<const half8*>(buf + (16 * b + m) * kXStride + 64 * q + 32 * h + 8 * s);
+#pragma unroll
+                    for (int r = 0; r < RB; ++r) {
+                        const std::uint32_t word = s == 0 ? st.w[r].x : s == 1 ? st.w[r].y : s == 2 ? st.w[r].z : st.w[r].w;
+                        const half8 wf = dequant8(word, __builtin_bit_cast(half2v, static_cast<std::uint32_t>(scale[r]) * 0x10001u));
+#pragma unroll
+                        for (int b = 0; b < NB; ++b)
+                            acc[r][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[b], wf, acc[r][b], 0, 0, 0);
+                    }
+                }
+            };
+
+            Half h0, h1;
+            load_half(0, 0, h0);
+            load_half(0, 1, h1);
+            XStage xs;
+            load_x(0, xs);
+            store_x(0, xs, xl[0]);
+            __syncthreads();
+            for (int c = 0; c < p.chunks; ++c) {
+                const int next = min(c + 1, p.chunks - 1);  // the last chunk re-reads itself (unused)
+                load_x(next, xs);
+                const _Float16* buf = xl[c & 1];
+#pragma unroll
+                for (int r = 0; r < RB; ++r) scale[r] = h0.s[r];
+                compute_half(h0, 0, buf);
+                load_half(next, 0, h0);
+                compute_half(h1, 1, buf);
+                load_half(next, 1, h1);
+                store_x(c + 1, xs, xl[(c + 1) & 1]);
+                __syncthreads();
+            }
+
+            // D layout: lane holds row slot m of block b for tokens 16j + 4q + i.
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const int blk = b0 + r;
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int t = 16 * b + 4 * q + i;
+                        const float v = acc[r][b][i];
+                        if (EPI == kSwiGLU) {
+                            const float other = __shfl_xor(v, 8, 64);  // lane m^8 holds the paired up/gate row
+                            const int col = (blk >> 3) * (kRows / 2) + 8 * (blk & 7) + (m & 7);
+                            if (m < 8 && t < live && blk < blocks && col < p.half_rows) {
+                                const float g = __half2float(from_f32<__half>(v));
+                                const float u = __half2float(from_f32<__half>(other));
+                                const float a = __half2float(from_f32<__half>(silu(g)));
+                                p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + col] =
+                                    from_f32<__half>(__fmul_rn(a, u));
+                            }
+                        } else {
+                            const int row = 16 * blk + m;
+                            if (t < live && blk < blocks && row < p.n) {
+                                float y = __half2float(from_f32<__half>(v));
+                                if (EPI == kScore) y = __fmul_rn(y, __half2float(p.score[pass + t]));
+                                p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + row] = from_f32<__half>(y);
+                            }
+                        }
+                    }
+                }
+            }
+        };
+        switch ((live + 15) >> 4) {
+            case 1: run_pass(std::integral_constant<int, 1>{}); break;
+            case 2: run_pass(std::integral_constant<int, (NBMAX >= 2 ? 2 : NBMAX)>{}); break;
+            case 3: run_pass(std::integral_constant<int, (NBMAX >= 3 ? 3 : NBMAX)>{}); break;
+            default: run_pass(std::integral_constant<int, NBMAX>{}); break;
+        }
+        __syncthreads();  // the next pass restages LDS
+    }
+}
+
 // Routing: one workgroup. Pair i = token * top_k + position. Pass 1 counts
 // pairs per expert (LDS atomics give each pair a rank in its expert), a scan
 // gives segment offsets, pass 2 places every pair at offset + rank. Each pass
@@ -624,6 +814,13 @@ void launch_q4_mfma(const Q4Gemm& p, hipStream_t stream) {
     q4_mfma<EPI><<<grid, kWaves * 64, 0, stream>>>(p);
 }
 
+template <int EPI, int W, int RB, int NBMAX>
+void launch_q4_grouped(const Q4Tiled& p, hipStream_t stream) {
+    const int blocks = p.row_tiles * 8;
+    const int parts = (blocks + W * RB - 1) / (W * RB);
+    q4_grouped<EPI, W, RB, NBMAX><<<dim3(p.experts * parts), W * 64, 0, stream>>>(p, parts, blocks);
+}
+
 template <int EPI>
 void launch_q4_tiled(const Q4Tiled& p, hipStream_t stream) {
     const dim3 grid(p.experts * p.row_tiles);
@@ -689,10 +886,13 @@ void q4_gemm_launch(const void* x, const void* codes, const void* scales, void* 
     launch_q4_mfma<kPlain>(p, stream);
 }
 
-void moe_q4_launch(const void* x, const std::int64_t* ids, const void* scores, const void* gu_codes,
-                   const void* gu_scales, const void* dn_codes, const void* dn_scales, void* out, void* workspace,
-                   std::uint64_t workspace_bytes, int tokens, int top_k, int experts, int hidden, int inter,
-                   hipStream_t stream) {
+// GW/GRB and DW/DRB: waves per workgroup and row blocks per wave of the
+// gate/up and down GEMMs (0 waves: one 128-row tile per workgroup, q4_tiled).
+template <int GW, int GRB, int DW, int DRB, int NBMAX>
+void moe_q4_launch_cfg(const void* x, const std::int64_t* ids, const void* scores, const void* gu_codes,
+                       const void* gu_scales, const void* dn_codes, const void* dn_scales, void* out, void* workspace,
+                       std::uint64_t workspace_bytes, int tokens, int top_k, int experts, int hidden, int inter,
+                       hipStream_t stream) {
     moe_validate(tokens, top_k, experts, hidden, inter);
     require(x && ids && scores && gu_codes && gu_scales && dn_codes && dn_scales && out && workspace,
             "null MoE operand");
@@ -736,7 +936,8 @@ void moe_q4_launch(const void* x, const std::int64_t* ids, const void* scores, c
     gu.out_stride = inter;
     gu.experts = experts;
     gu.half_rows = inter;
-    launch_q4_tiled<kSwiGLU>(gu, stream);
+    if constexpr (GW == 0) launch_q4_tiled<kSwiGLU>(gu, stream);
+    else launch_q4_grouped<kSwiGLU, GW, GRB, NBMAX>(gu, stream);
 
     Q4Tiled dn{};
     dn.x = h;
@@ -754,9 +955,18 @@ void moe_q4_launch(const void* x, const std::int64_t* ids, const void* scores, c
     dn.x_stride = inter;
     dn.out_stride = hidden;
     dn.experts = experts;
-    launch_q4_tiled<kScore>(dn, stream);
+    if constexpr (DW == 0) launch_q4_tiled<kScore>(dn, stream);
+    else launch_q4_grouped<kScore, DW, DRB, NBMAX>(dn, stream);
 
     combine_dispatch(top_k, ids, pair_slot, v, static_cast<__half*>(out), tokens, hidden, stream);
+}
+
+void moe_q4_launch(const void* x, const std::int64_t* ids, const void* scores, const void* gu_codes,
+                   const void* gu_scales, const void* dn_codes, const void* dn_scales, void* out, void* workspace,
+                   std::uint64_t workspace_bytes, int tokens, int top_k, int experts, int hidden, int inter,
+                   hipStream_t stream) {
+    moe_q4_launch_cfg<8, 2, 8, 2, 3>(x, ids, scores, gu_codes, gu_scales, dn_codes, dn_scales, out, workspace,
+                                     workspace_bytes, tokens, top_k, experts, hidden, inter, stream);
 }
 
 }  // namespace vt
