@@ -60,6 +60,8 @@ def parse():
     p.add_argument("--no-prefill", action="store_true", help="skip the config-3 A8 prefill section")
     p.add_argument("--no-moe", action="store_true", help="skip the config-4 routed-expert MoE section")
     p.add_argument("--no-model", action="store_true", help="skip the config-5 64-layer decode section")
+    p.add_argument("--eager", action="store_true",
+                   help="time config-2 launches issued from Python instead of HIP-graph replays (for counter runs)")
     return p.parse_args()
 
 
@@ -107,6 +109,27 @@ def cpu_baseline(copies, xs, seconds):
         f"torch {torch.__version__} CPU GEMM, FP32 weights materialised before timing, "
         f"{elapsed:.1f} s on {platform.processor() or platform.machine()}",
     }
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "q8_decode_traffic.json")
+
+
+def measured_traffic(route):
+    """HBM bytes per launch of the config-2 step, from the committed counter runs.
+
+    The figure comes from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over
+    this bench's eager launches, each scaled by the same counter's reading for a
+    copy of known size; the file records the commands and raw values. None when
+    the file is absent or was measured on another route.
+    """
+    try:
+        with open(TRAFFIC_FILE) as f:
+            record = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if record.get("route") != route:
+        return None
+    return record.get("traffic_bytes_per_launch")
 
 
 INT8_PEAK_TOPS = 5000.0
@@ -394,30 +417,34 @@ def main():
     # Each (projection, M) group of K rotated launches is captured once in a
     # HIP graph, so the timed region measures the kernels rather than the
     # Python launch path (a 10 us kernel is shorter than one host call).
-    graphs = {}
-    for key in launches:
-        graphs[key] = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graphs[key]):
-            run(*key, args.steps)
-    for key in launches:
-        graphs[key].replay()
-    torch.cuda.synchronize(device)
-    graph_equals_eager = True
-    for mi, pi in launches:
-        m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
-        ref = torch.empty_like(outs[(m, n)])
-        plans[(mi, pi)][(args.steps - 1) % len(plans[(mi, pi)])].run(xs[m][k], out=ref)
-        graphs[(mi, pi)].replay()
+    graphs, graph_equals_eager = {}, None
+    if not args.eager:
+        for key in launches:
+            graphs[key] = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graphs[key]):
+                run(*key, args.steps)
+        for key in launches:
+            graphs[key].replay()
         torch.cuda.synchronize(device)
-        graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
+        graph_equals_eager = True
+        for mi, pi in launches:
+            m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
+            ref = torch.empty_like(outs[(m, n)])
+            plans[(mi, pi)][(args.steps - 1) % len(plans[(mi, pi)])].run(xs[m][k], out=ref)
+            graphs[(mi, pi)].replay()
+            torch.cuda.synchronize(device)
+            graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
 
     events = {key: [torch.cuda.Event(enable_timing=True) for _ in range(2)] for key in launches}
     torch.cuda.synchronize(device)
     start = time.perf_counter()
     for key in launches:
-        events[key][0].record(stream)
-        graphs[key].replay()
-        events[key][1].record(stream)
+        if args.eager:
+            run(*key, args.steps, events[key])
+        else:
+            events[key][0].record(stream)
+            graphs[key].replay()
+            events[key][1].record(stream)
     torch.cuda.synchronize(device)
     wall = time.perf_counter() - start
 
@@ -468,10 +495,11 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.route),
         },
         "all_kernels_GBps": round(total_bytes / sum(kernel_s.values()) / 1e9, 1),
         "graph_equals_eager": graph_equals_eager,
+        "timing": "eager launches" if args.eager else "HIP-graph replays",
         "per_launch": detail,
     }
     if not args.no_prefill:
