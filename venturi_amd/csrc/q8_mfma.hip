@@ -478,13 +478,18 @@ void q8_tiled_launch(const void* x, const void* codes, const void* scales, void*
     // token: activations staged in LDS, 16 waves on matrices of fewer than
     // 1024 row blocks and 8 waves otherwise. Up to four tokens at K >= 16384:
     // LDS-staged with 16 waves. Otherwise register-loaded fragments, 8 waves
-    // over two row blocks.
+    // over two row blocks, or three on matrices of at least 1024 blocks above
+    // 8 tokens (fewer activation fragment loads per weight byte). Splitting K
+    // over workgroups with a last-arriver fix-up was measured 10-20x slower:
+    // every split needs a device-scope release fence (an L2 write-back).
     if (tokens == 1 && blocks < 1024)
         launch_tiled_lds<16, 2, 2, 1>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
     else if (tokens == 1)
         launch_tiled_lds<8, 2, 2, 1>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
     else if (tokens <= 4 && k >= 16384 && lds_x_bytes(tokens, chunks) <= 160 * 1024)
         launch_tiled_lds<16, 2, 2, 4>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    else if (tokens > 8 && tokens <= 16 && blocks >= 1024)
+        launch_tiled<8, 3, 1, 2>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
     else if (tokens <= 16)
         launch_tiled<8, 2, 1, 2>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
     else
