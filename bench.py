@@ -296,10 +296,10 @@ def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
     """64 decoder layers x the config-2 projections, all resident (256 Q8 matrices).
 
     One step chains, per layer: h -> QKV; a seeded fp16 [B, 6144] -> o_proj;
-    h -> gate+up -> SiLU*up (venturi_silu_mul_run, the native runtime's
-    SwiGLU arithmetic) -> down -> next h. The 320 launches of a step are
-    captured once in a HIP graph (checked bit-for-bit against an eager step)
-    and replayed. Projection-only tokens/s = B / step time; GB/s counts the
+    h -> gate+up fused with SiLU*up (the native runtime's SwiGLU arithmetic
+    in the projection's epilogue) -> down -> next h. The 256 launches of a
+    step are captured once in a HIP graph (checked bit-for-bit against an
+    eager step) and replayed. Projection-only tokens/s = B / step time; GB/s counts the
     projections' algorithmic bytes (weights + activations + outputs).
     """
     layers = 64
@@ -314,18 +314,19 @@ def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
         matrices.append(row)
     torch.cuda.synchronize(device)
     weight_bytes = sum(r.storage_nbytes for row in matrices for r in row)
-    lib, stream_of = backend._native, (lambda: torch.cuda.current_stream(device).cuda_stream)
     inter = PROJECTIONS[2][1] // 2
     results = {}
     for b in batches:
-        plans = [[r.prepare(tokens=b) for r in row] for row in matrices]
+        # gate+up runs fused with SiLU*up (venturi_q8_tiled_swiglu_run: the bytes of
+        # the projection followed by venturi_silu_mul_run, one launch instead of two).
+        plans = [[r.prepare_swiglu(tokens=b) if i == 2 else r.prepare(tokens=b) for i, r in enumerate(row)]
+                 for row in matrices]
         gen = torch.Generator(device=device).manual_seed(b)
         h0 = torch.randn(b, 5120, generator=gen, device=device).half()
         o_in = torch.randn(b, 6144, generator=gen, device=device).half()
         h = [h0.clone(), torch.empty_like(h0)]
         qkv = torch.empty(b, PROJECTIONS[0][1], dtype=torch.float16, device=device)
         o = torch.empty(b, PROJECTIONS[1][1], dtype=torch.float16, device=device)
-        gu = torch.empty(b, PROJECTIONS[2][1], dtype=torch.float16, device=device)
         act = torch.empty(b, inter, dtype=torch.float16, device=device)
 
         def step():
@@ -335,8 +336,7 @@ def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
                 cur, nxt = h[layer % 2], h[(layer + 1) % 2]
                 p[0].run(cur, out=qkv)
                 p[1].run(o_in, out=o)
-                p[2].run(cur, out=gu)
-                backend._check(lib.venturi_silu_mul_run(gu.data_ptr(), act.data_ptr(), b, inter, 0, stream_of()))
+                p[2].run(cur, out=act)
                 p[3].run(act, out=nxt)
 
         step()
@@ -371,7 +371,7 @@ def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
         del plans, graph
     del matrices
     return {
-        "workload": "config5: 64 layers x config-2 Q8 projections resident, chained per step (HIP graph)",
+        "workload": "config5: 64 layers x config-2 Q8 projections resident, chained per step (HIP graph, gate+up fused with SiLU*up)",
         "weight_bytes": weight_bytes,
         "batches": results,
     }

@@ -98,6 +98,16 @@ int venturi_q8_gemm_run(const void* x, const int8_t* codes, const void* scales, 
 int venturi_q8_tiled_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
                          int padded, int dtype, void* stream);
 
+/* Extension (no counterpart in the reference; the native runtime runs the
+ * gate+up projection and then SwiGLU, blocks.cu:56-86): the fused gate+up
+ * projection over paired tiled planes (16-row block b holds gate rows
+ * 8b..8b+7 then up rows n/2+8b..n/2+8b+7, built by vocabulary.tile_q8 with
+ * paired=True), writing out [tokens][n/2] = fp16(swiglu(fp16(gate), fp16(up))),
+ * the bytes of venturi_q8_tiled_run followed by venturi_silu_mul_run. fp16
+ * activations, k % 8 == 0, n even, tokens <= 32. */
+int venturi_q8_tiled_swiglu_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n,
+                                int k, int padded, int dtype, void* stream);
+
 /* ---- Q4 (q4_g64_fp16): codes uint8 [n][padded/2] (column 2j in the low
  * nibble of byte j, two's complement), scales fp16 [n][padded/64]. ---- */
 

@@ -91,3 +91,42 @@ def test_mfma_route_admission(backend, device):
     assert resident.prepare(tokens=33).route == "venturi-q8-exact"
     bf = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.bfloat16, device=device)
     assert bf.prepare(tokens=8).route == "venturi-q8-exact"
+
+
+@pytest.mark.parametrize("shape", [(16, 64), (34, 136), (200, 1000), (16400, 136), (18, 16392)])
+@pytest.mark.parametrize("tokens", [1, 3, 4, 8, 13, 16, 32])
+def test_fused_swiglu_equals_projection_then_silu_mul(backend, device, shape, tokens):
+    # The fused epilogue must give the bytes of the mfma projection followed by
+    # venturi_silu_mul_run (every row's dot is computed by the same MFMA sequence
+    # in both tilings). Shapes cover an odd intermediate size (17), >= 1024 paired
+    # blocks and K >= 16384 (the staged-activation kernels).
+    n, k = shape
+    print(f"case q8-swiglu n={n} k={k} tokens={tokens}", flush=True)
+    codes, scales = random_q8(n, k, 311 + n + tokens)
+    resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, k), dtype=torch.float16, device=device)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens + k)).half().to(device)
+    gate_up = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    resident.prepare(tokens=tokens, route="mfma").run(x, out=gate_up)
+    want = torch.empty(tokens, n // 2, dtype=torch.float16, device=device)
+    lib = backend._native
+    backend._check(lib.venturi_silu_mul_run(gate_up.data_ptr(), want.data_ptr(), tokens, n // 2, 0,
+                                            torch.cuda.current_stream(device).cuda_stream))
+    plan = resident.prepare_swiglu(tokens=tokens)
+    assert plan.route == "venturi-q8-mfma-swiglu" and plan.out_features == n // 2
+    guard = torch.full((tokens * (n // 2) + 2,), 47, dtype=torch.float16, device=device)
+    out = guard[1:-1].view(tokens, n // 2)
+    plan.run(x, out=out)
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
+def test_fused_swiglu_admission(backend, device):
+    codes, scales = random_q8(6, 64, 3)
+    bf = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError, match="SwiGLU"):
+        bf.prepare_swiglu(tokens=1)
+    codes, scales = random_q8(7, 64, 3)
+    odd = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.float16, device=device)
+    with pytest.raises(ValueError, match="even row count"):
+        odd.prepare_swiglu(tokens=1)

@@ -101,6 +101,17 @@ class ResidentLinear:
         self._backend.validate_device(self.dtype, self.device)
         return self._backend.bind_linear(self, tokens=tokens, route=route)
 
+    def prepare_swiglu(self, *, tokens):
+        """Fused gate+up projection and SwiGLU for a Q8 [2 * inter, hidden] weight, gate rows
+        first (an extension: the native runtime runs the projection, then SwiGLU). The plan's
+        output is [tokens, inter]."""
+        from .vocabulary import ResidentQ8Vocabulary
+
+        _shape(tokens, self.in_features)
+        if not isinstance(self._payload, ResidentQ8Vocabulary):
+            raise UnsupportedOperationError("The fused SwiGLU projection is defined for Q8 weights only")
+        return _Q8Linear(self._payload.prepare_swiglu(tokens=tokens))
+
 
 @dataclass(frozen=True)
 class ResidentRMSNorm:
@@ -350,7 +361,7 @@ class _Q8Linear:
 
     @property
     def out_features(self):
-        return self.plan.resident.vocab_size
+        return self.plan.out_features
 
     @property
     def storage_tensors(self):

@@ -9,14 +9,6 @@
 namespace vt {
 namespace {
 
-// The reference's stable logistic; expf is the ROCm device library's
-// (its last bit is not pinned against CUDA's; the final cast absorbs it almost
-// always).
-__device__ __forceinline__ float swiglu_value(float x, float y) {
-    const float sigmoid = x >= 0.0f ? __fdiv_rn(1.0f, 1.0f + expf(-x)) : __fdiv_rn(expf(x), 1.0f + expf(x));
-    return __fmul_rn(__fmul_rn(x, sigmoid), y);
-}
-
 template <class T, bool SWIGLU>
 __global__ __launch_bounds__(256) void elementwise(const T* __restrict__ a, const T* __restrict__ b, T* __restrict__ out,
                                                    std::int64_t count) {

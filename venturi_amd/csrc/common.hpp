@@ -112,6 +112,15 @@ __device__ __forceinline__ float sbyte(std::uint32_t w, int i) {
 // correct and is up to one ulp off, so it is not used.
 __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 
+// SwiGLU of the native runtime (blocks.cu:56-86): (x * sigmoid(x)) * y in fp32
+// with the reference's stable logistic; expf is the ROCm device library's (its
+// last bit is not pinned against CUDA's; the final cast absorbs it almost
+// always). Shared by the elementwise kernels and the fused projection epilogue.
+__device__ __forceinline__ float swiglu_value(float x, float y) {
+    const float sigmoid = x >= 0.0f ? __fdiv_rn(1.0f, 1.0f + expf(-x)) : __fdiv_rn(expf(x), 1.0f + expf(x));
+    return __fmul_rn(__fmul_rn(x, sigmoid), y);
+}
+
 // Cross-lane read of `v` from lane (lane + delta) within a 64-lane wave.
 __device__ __forceinline__ float lane_down(float v, int delta) {
     return __shfl_down(v, delta, 64);

@@ -161,6 +161,29 @@ __global__ __launch_bounds__(1024) void q8_mfma_decode(const __half* __restrict_
 // row exists load activations (the others hold zeros), so small token counts
 // cost no activation traffic beyond their rows. The W partial tiles are summed
 // through LDS in wave order 0..W-1, so results are deterministic.
+// Writes one projection output: row slot r of 16-row block blk for token t.
+// Plain: out[t][16 blk + r], n rows. SwiGLU (paired planes, n = 2 * inter):
+// slots 0..7 of block blk are gate rows 8 blk .. 8 blk + 7 and slots 8..15
+// the matching up rows; every lane fetches its partner slot's sum (lane ^ 8)
+// and lanes of gate slots write out[t][8 blk + r] = swiglu(gate, up), with
+// gate and up rounded to fp16 first as the projection would store them. All
+// lanes of the wave must call it together.
+template <bool SWIGLU>
+__device__ __forceinline__ void store_tile_value(__half* __restrict__ out, float v, int t, int blk, int r, int tokens,
+                                                 int n) {
+    if constexpr (SWIGLU) {
+        const float other = __shfl_xor(v, 8, 64);
+        const int inter = n / 2, col = 8 * blk + r;
+        if (r < 8 && t < tokens && col < inter) {
+            const float g = __half2float(from_f32<__half>(v)), u = __half2float(from_f32<__half>(other));
+            out[static_cast<std::int64_t>(t) * inter + col] = from_f32<__half>(swiglu_value(g, u));
+        }
+    } else {
+        const int row = 16 * blk + r;
+        if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(v);
+    }
+}
+
 template <int RB, int NB, int STEPS>
 struct TiledBatch {
     uint4 w[STEPS][RB];
@@ -168,7 +191,7 @@ struct TiledBatch {
     uint4 xa[STEPS][NB], xb[STEPS][NB];
 };
 
-template <int W, int RB, int NB, int STEPS>
+template <int W, int RB, int NB, int STEPS, bool SWIGLU>
 __global__ __launch_bounds__(W * 64) void q8_tiled_decode(const __half* __restrict__ x, const uint4* __restrict__ codes,
                                                           const std::uint32_t* __restrict__ scales,
                                                           __half* __restrict__ out, int tokens, int n, int k,
@@ -297,8 +320,7 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_decode(const __half* __restri
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int t = 16 * tb + 4 * q + j;
-            const int row = (block0 + b) * 16 + r;
-            if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(sum[j]);
+            store_tile_value<SWIGLU>(out, sum[j], t, block0 + b, r, tokens, n);
         }
     }
 }
@@ -322,7 +344,7 @@ __host__ __device__ inline std::size_t lds_x_bytes(int tokens, int chunks) {
     return static_cast<std::size_t>(tokens) * chunks * 128 + (tokens < 16 ? 128 : 0);
 }
 
-template <int W, int RB, int STEPS, int TMAX>
+template <int W, int RB, int STEPS, int TMAX, bool SWIGLU>
 __global__ __launch_bounds__(W * 64) void q8_tiled_lds(const __half* __restrict__ x, const uint4* __restrict__ codes,
                                                        const std::uint32_t* __restrict__ scales,
                                                        __half* __restrict__ out, int tokens, int n, int k, int chunks,
@@ -429,37 +451,60 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_lds(const __half* __restrict_
             for (int j = 0; j < 4; ++j) sum[j] += v[j];
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = 4 * q + j;
-            const int row = (block0 + b) * 16 + r;
-            if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(sum[j]);
-        }
+        for (int j = 0; j < 4; ++j) store_tile_value<SWIGLU>(out, sum[j], 4 * q + j, block0 + b, r, tokens, n);
     }
 }
 
-template <int W, int RB, int STEPS, int TMAX>
+template <int W, int RB, int STEPS, int TMAX, bool SWIGLU>
 void launch_tiled_lds(const __half* x, const uint4* codes, const std::uint32_t* scales, __half* out, int tokens, int n,
                       int k, int chunks, int blocks, hipStream_t stream) {
     const std::size_t lds = std::max(lds_x_bytes(tokens, chunks), static_cast<std::size_t>(W) * RB * 1024);
     require(lds <= 160 * 1024, "staged activations exceed LDS");
-    static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void*>(q8_tiled_lds<W, RB, STEPS, TMAX>),
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    static const hipError_t raised = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(q8_tiled_lds<W, RB, STEPS, TMAX, SWIGLU>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        160 * 1024);
     check(raised);
-    q8_tiled_lds<W, RB, STEPS, TMAX><<<(blocks + RB - 1) / RB, W * 64, lds, stream>>>(x, codes, scales, out, tokens, n, k,
-                                                                                     chunks, blocks);
+    q8_tiled_lds<W, RB, STEPS, TMAX, SWIGLU><<<(blocks + RB - 1) / RB, W * 64, lds, stream>>>(x, codes, scales, out, tokens,
+                                                                                             n, k, chunks, blocks);
 }
 
-template <int W, int RB, int NB, int STEPS>
+template <int W, int RB, int NB, int STEPS, bool SWIGLU>
 void launch_tiled(const __half* x, const uint4* codes, const std::uint32_t* scales, __half* out, int tokens, int n,
                   int k, int chunks, int blocks, hipStream_t stream) {
-    q8_tiled_decode<W, RB, NB, STEPS><<<(blocks + RB - 1) / RB, W * 64, 0, stream>>>(x, codes, scales, out, tokens, n,
-                                                                                     k, chunks, blocks);
+    q8_tiled_decode<W, RB, NB, STEPS, SWIGLU><<<(blocks + RB - 1) / RB, W * 64, 0, stream>>>(x, codes, scales, out, tokens,
+                                                                                             n, k, chunks, blocks);
+}
+
+// Launch shapes measured on the config-2 matrices (QKV 7168x5120, o_proj
+// 5120x6144, gate+up 34816x5120, down 5120x17408) at 1-16 tokens. One token:
+// activations staged in LDS, 16 waves on matrices of fewer than 1024 row
+// blocks and 8 waves otherwise. Up to four tokens at K >= 16384: LDS-staged
+// with 16 waves. Otherwise register-loaded fragments, 8 waves over two row
+// blocks, or three on matrices of at least 1024 blocks above 8 tokens (fewer
+// activation fragment loads per weight byte). Splitting K over workgroups with
+// a last-arriver fix-up was measured 10-20x slower: every split needs a
+// device-scope release fence (an L2 write-back).
+template <bool SWIGLU>
+void tiled_dispatch(const __half* xp, const uint4* cp, const std::uint32_t* sp, __half* op, int tokens, int n, int k,
+                    int chunks, int blocks, hipStream_t stream) {
+    if (tokens == 1 && blocks < 1024)
+        launch_tiled_lds<16, 2, 2, 1, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    else if (tokens == 1)
+        launch_tiled_lds<8, 2, 2, 1, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    else if (tokens <= 4 && k >= 16384 && lds_x_bytes(tokens, chunks) <= 160 * 1024)
+        launch_tiled_lds<16, 2, 2, 4, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    else if (tokens > 8 && tokens <= 16 && blocks >= 1024)
+        launch_tiled<8, 3, 1, 2, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    else if (tokens <= 16)
+        launch_tiled<8, 2, 1, 2, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    else
+        launch_tiled<8, 2, 2, 2, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
 }
 
 }  // namespace
 
 void q8_tiled_launch(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
-                     int padded, int dtype, hipStream_t stream) {
+                     int padded, int dtype, bool swiglu, hipStream_t stream) {
     require(x && codes && scales && out, "null Q8 operand");
     require(tokens > 0 && n > 0 && k > 0 && padded == padded_k(k), "invalid Q8 geometry");
     require(static_cast<std::int64_t>(tokens) * n < INT32_MAX, "Q8 output count exceeds int32");
@@ -467,33 +512,16 @@ void q8_tiled_launch(const void* x, const void* codes, const void* scales, void*
     require(k % 8 == 0 && aligned(x, 16), "the Q8 MFMA route needs k % 8 == 0 and 16-byte aligned x");
     require(aligned(codes, 16) && aligned(scales, 4) && aligned(out, 2), "misaligned Q8 operand");
     require(tokens <= 32, "the tiled Q8 MFMA decode kernel takes at most 32 tokens");
-    const int blocks = (n + 15) / 16;
+    require(!swiglu || n % 2 == 0, "the fused SwiGLU projection needs an even row count (gate rows, then up rows)");
+    // Paired planes hold 8 gate and 8 up rows per 16-row block.
+    const int blocks = swiglu ? (n / 2 + 7) / 8 : (n + 15) / 16;
     const int chunks = padded / 64;
     const auto* xp = static_cast<const __half*>(x);
     const auto* cp = static_cast<const uint4*>(codes);
     const auto* sp = static_cast<const std::uint32_t*>(scales);
     auto* op = static_cast<__half*>(out);
-    // Launch shapes measured on the config-2 matrices (QKV 7168x5120, o_proj
-    // 5120x6144, gate+up 34816x5120, down 5120x17408) at 1-16 tokens. One
-    // token: activations staged in LDS, 16 waves on matrices of fewer than
-    // 1024 row blocks and 8 waves otherwise. Up to four tokens at K >= 16384:
-    // LDS-staged with 16 waves. Otherwise register-loaded fragments, 8 waves
-    // over two row blocks, or three on matrices of at least 1024 blocks above
-    // 8 tokens (fewer activation fragment loads per weight byte). Splitting K
-    // over workgroups with a last-arriver fix-up was measured 10-20x slower:
-    // every split needs a device-scope release fence (an L2 write-back).
-    if (tokens == 1 && blocks < 1024)
-        launch_tiled_lds<16, 2, 2, 1>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
-    else if (tokens == 1)
-        launch_tiled_lds<8, 2, 2, 1>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
-    else if (tokens <= 4 && k >= 16384 && lds_x_bytes(tokens, chunks) <= 160 * 1024)
-        launch_tiled_lds<16, 2, 2, 4>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
-    else if (tokens > 8 && tokens <= 16 && blocks >= 1024)
-        launch_tiled<8, 3, 1, 2>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
-    else if (tokens <= 16)
-        launch_tiled<8, 2, 1, 2>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
-    else
-        launch_tiled<8, 2, 2, 2>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    if (swiglu) tiled_dispatch<true>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    else tiled_dispatch<false>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
 }
 
 void q8_mfma_launch(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n,
@@ -532,6 +560,19 @@ extern "C" __attribute__((visibility("default"))) int venturi_q8_tiled_run(const
                                                                           int n, int k, int padded, int dtype,
                                                                           void* stream) {
     return vt::guarded([&] {
-        vt::q8_tiled_launch(x, codes, scales, out, tokens, n, k, padded, dtype, static_cast<hipStream_t>(stream));
+        vt::q8_tiled_launch(x, codes, scales, out, tokens, n, k, padded, dtype, false, static_cast<hipStream_t>(stream));
+    });
+}
+
+// Extension: the fused gate+up projection with SwiGLU over paired tiled planes
+// (16-row block b = gate rows 8b..8b+7, then up rows inter+8b..inter+8b+7):
+// out[t][j] = fp16(swiglu(fp16(gate[t][j]), fp16(up[t][j]))), out [tokens][n/2],
+// the bytes of the projection followed by venturi_silu_mul_run.
+extern "C" __attribute__((visibility("default"))) int venturi_q8_tiled_swiglu_run(const void* x, const void* codes,
+                                                                                 const void* scales, void* out,
+                                                                                 int tokens, int n, int k, int padded,
+                                                                                 int dtype, void* stream) {
+    return vt::guarded([&] {
+        vt::q8_tiled_launch(x, codes, scales, out, tokens, n, k, padded, dtype, true, static_cast<hipStream_t>(stream));
     });
 }

@@ -32,20 +32,37 @@ MFMA_MAX_TOKENS = 32
 _TILE_LOCK = threading.Lock()
 
 
-def tile_q8(codes, scales):
+def tile_q8(codes, scales, paired=False):
     """Tiled planes of the matrix-core route (read by ``venturi_q8_tiled_run``).
 
     Codes [row block][chunk][lane l = 16q + m][16 bytes]: row m of the block,
     columns 64c + 8q .. +8 (group 2c) then 64c + 32 + 8q .. +8 (group 2c + 1).
     Scales [row block][chunk][m][2] fp16. Rows are padded to a multiple of 16
-    with zero codes and scales.
+    with zero codes and scales. ``paired`` (a fused gate+up matrix, gate rows
+    first, read by ``venturi_q8_tiled_swiglu_run``): block b holds gate rows
+    8b..8b+7 in slots 0..7 and the matching up rows in slots 8..15.
     """
     n, padded = codes.shape
-    blocks, chunks = (n + 15) // 16, padded // 64
-    c = torch.zeros((blocks * 16, padded), dtype=torch.int8, device=codes.device)
-    s = torch.zeros((blocks * 16, padded // 32), dtype=torch.float16, device=codes.device)
-    c[:n] = codes
-    s[:n] = scales
+    chunks = padded // 64
+    if paired:
+        if n % 2:
+            raise ValueError("a fused gate+up matrix needs an even row count")
+        inter = n // 2
+        blocks = (inter + 7) // 8
+        idx = torch.arange(blocks * 16, device=codes.device)
+        gate = (idx // 16) * 8 + idx % 8  # intermediate column of each slot
+        source = torch.where(idx % 16 < 8, gate, gate + inter)
+        valid = gate < inter
+        c = torch.zeros((blocks * 16, padded), dtype=torch.int8, device=codes.device)
+        s = torch.zeros((blocks * 16, padded // 32), dtype=torch.float16, device=codes.device)
+        c[valid] = codes[source[valid]]
+        s[valid] = scales[source[valid]]
+    else:
+        blocks = (n + 15) // 16
+        c = torch.zeros((blocks * 16, padded), dtype=torch.int8, device=codes.device)
+        s = torch.zeros((blocks * 16, padded // 32), dtype=torch.float16, device=codes.device)
+        c[:n] = codes
+        s[:n] = scales
     tc = c.view(blocks, 16, chunks, 2, 4, 8).permute(0, 2, 4, 1, 3, 5).contiguous()
     ts = s.view(blocks, 16, chunks, 2).permute(0, 2, 1, 3).contiguous()
     return tc, ts
@@ -106,14 +123,15 @@ class ResidentQ8Vocabulary:
     def device(self):
         return self._codes.device
 
-    def tiled_planes(self):
+    def tiled_planes(self, paired=False):
         """The matrix-core route's tiled copy of the planes (built on first use)."""
+        key = "mfma-paired" if paired else "mfma"
         with _TILE_LOCK:
-            if "mfma" not in self._tiles:
+            if key not in self._tiles:
                 with torch.cuda.device(self.device):
-                    self._tiles["mfma"] = tile_q8(self._codes, self._scales)
+                    self._tiles[key] = tile_q8(self._codes, self._scales, paired)
                     torch.cuda.current_stream(self.device).synchronize()
-            return self._tiles["mfma"]
+            return self._tiles[key]
 
     @property
     def vocab_size(self):
@@ -150,6 +168,24 @@ class ResidentQ8Vocabulary:
             )
         tiles = self.tiled_planes() if route == "mfma" else ()
         return Q8OutputHead(self, tokens, route, tiles)
+
+
+    def prepare_swiglu(self, *, tokens):
+        """Fused gate+up projection with SwiGLU (an extension; matrix cores only).
+
+        The resident matrix is [2 * inter, hidden] with the gate rows first; the
+        plan writes out [tokens, inter] = fp16(swiglu(fp16(gate), fp16(up))), the
+        bytes of the ``mfma`` projection followed by ``venturi_silu_mul_run``.
+        """
+        _shape(tokens, self.vocab_size)
+        if self.vocab_size % 2:
+            raise ValueError("a fused gate+up matrix needs an even row count")
+        if not (self.dtype == torch.float16 and self.hidden_size % 8 == 0 and tokens <= MFMA_MAX_TOKENS):
+            raise ValueError(
+                f"The fused SwiGLU projection takes FP16 activations, K % 8 == 0 and at most {MFMA_MAX_TOKENS} tokens"
+            )
+        self.backend.validate_device(self.dtype, self.device)
+        return Q8OutputHead(self, tokens, "swiglu", self.tiled_planes(paired=True))
 
 
 @dataclass(frozen=True)
@@ -189,7 +225,12 @@ class Q8OutputHead:
 
     @property
     def route(self):
-        return "venturi-q8-exact" if self.kernel == "exact" else "venturi-q8-mfma"
+        return {"exact": "venturi-q8-exact", "mfma": "venturi-q8-mfma", "swiglu": "venturi-q8-mfma-swiglu"}[self.kernel]
+
+    @property
+    def out_features(self):
+        n = self.resident.vocab_size
+        return n // 2 if self.kernel == "swiglu" else n
 
     @property
     def storage_tensors(self):
@@ -198,11 +239,13 @@ class Q8OutputHead:
     def run(self, x, *, out):
         r = self.resident
         _tensor(x, (self.tokens, r.hidden_size), r.dtype, r.device, "x")
-        _tensor(out, (self.tokens, r.vocab_size), r.dtype, r.device, "out")
+        _tensor(out, (self.tokens, self.out_features), r.dtype, r.device, "out")
         _no_overlap(out, (x,) + self.storage_tensors)
         lib = r.backend._native
         if self.kernel == "exact":
             entry, planes = lib.venturi_q8_head_run, (r._codes, r._scales)
+        elif self.kernel == "swiglu":
+            entry, planes = lib.venturi_q8_tiled_swiglu_run, self.tiles
         else:
             entry, planes = lib.venturi_q8_tiled_run, self.tiles
         with torch.cuda.device(r.device):
