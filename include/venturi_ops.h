@@ -90,13 +90,27 @@ int venturi_q8_pack_run(const void* source, int8_t* codes, void* scales, int n, 
 int venturi_q8_gemm_run(const void* x, const int8_t* codes, const void* scales, void* out, int tokens, int n, int k,
                         int padded, int dtype, void* stream);
 
+/* Extension: workspace of the tiled projections below for (tokens, n, swiglu):
+ * the exchange slots of launches that split K over two workgroups, or 0 when
+ * the launch for this shape does not split. 0 with a message on invalid
+ * arguments (tokens outside 1..32, n <= 0, odd n with swiglu). */
+size_t venturi_q8_tiled_workspace_bytes(int tokens, int n, int swiglu);
+
+/* Extension: puts a workspace of the tiled projections in its idle state (every
+ * 64-bit word 0x7f8000017f800001) with a fill kernel on `stream`. Call it once
+ * after allocating; every projection call leaves the workspace idle again.
+ * Calls that share one workspace must be ordered (one stream). */
+int venturi_q8_tiled_workspace_init(void* workspace, size_t bytes, void* stream);
+
 /* Extension: the same projection over tiled planes: row blocks of 16 rows x
  * 64-column chunks, 1 KB each, stored [block][chunk][lane 16q+m][16 bytes]
  * (row m's codes of columns 64c+8q..+8, then 64c+32+8q..+8), scales
  * [block][chunk][m][2] fp16; each wave then streams contiguous 1 KB blocks.
- * fp16 activations, k % 8 == 0, tokens <= 32. */
+ * fp16 activations, k % 8 == 0, tokens <= 32. `workspace` (8-byte aligned,
+ * initialised, at least venturi_q8_tiled_workspace_bytes) may be NULL when
+ * that size is 0. */
 int venturi_q8_tiled_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
-                         int padded, int dtype, void* stream);
+                         int padded, int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Extension (no counterpart in the reference; the native runtime runs the
  * gate+up projection and then SwiGLU, blocks.cu:56-86): the fused gate+up
@@ -104,9 +118,10 @@ int venturi_q8_tiled_run(const void* x, const void* codes, const void* scales, v
  * 8b..8b+7 then up rows n/2+8b..n/2+8b+7, built by vocabulary.tile_q8 with
  * paired=True), writing out [tokens][n/2] = fp16(swiglu(fp16(gate), fp16(up))),
  * the bytes of venturi_q8_tiled_run followed by venturi_silu_mul_run. fp16
- * activations, k % 8 == 0, n even, tokens <= 32. */
+ * activations, k % 8 == 0, n even, tokens <= 32; workspace as for
+ * venturi_q8_tiled_run, sized with swiglu = 1. */
 int venturi_q8_tiled_swiglu_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n,
-                                int k, int padded, int dtype, void* stream);
+                                int k, int padded, int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- Q4 (q4_g64_fp16): codes uint8 [n][padded/2] (column 2j in the low
  * nibble of byte j, two's complement), scales fp16 [n][padded/64]. ---- */

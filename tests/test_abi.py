@@ -59,6 +59,32 @@ def test_workspace_sizes(lib):
     assert lib.venturi_moe_q4_bytes(t, k, e, 2047, i) == 0
 
 
+def test_tiled_split_workspace_sizes(lib):
+    # The tiled Q8 projections split K over two workgroups only where that
+    # brings the grid closer to one workgroup per CU (at most 256): 8 slots of
+    # 8 bytes per (token, 16-row block) then, else no workspace.
+    def slots(tokens, blocks):
+        return tokens * blocks * 64
+
+    assert lib.venturi_q8_tiled_workspace_bytes(1, 5120, 0) == 0  # one token: unsplit
+    assert lib.venturi_q8_tiled_workspace_bytes(4, 5120, 0) == slots(4, 320)  # 107 x 2 workgroups
+    assert lib.venturi_q8_tiled_workspace_bytes(4, 7168, 0) == 0  # 224 unsplit workgroups
+    assert lib.venturi_q8_tiled_workspace_bytes(32, 7168, 0) == slots(32, 448)  # 112 x 2 above 16 tokens
+    assert lib.venturi_q8_tiled_workspace_bytes(16, 34816, 0) == 0
+    assert lib.venturi_q8_tiled_workspace_bytes(2, 16, 0) == slots(2, 1)
+    # Paired planes hold 8 gate + 8 up rows per block: same block count as the plain matrix.
+    assert lib.venturi_q8_tiled_workspace_bytes(8, 100, 1) == lib.venturi_q8_tiled_workspace_bytes(8, 100, 0) == slots(8, 7)
+    assert lib.venturi_q8_tiled_workspace_bytes(8, 34, 0) == 0  # 3 blocks: two workgroups either way, unsplit
+    assert lib.venturi_q8_tiled_workspace_bytes(8, 35, 1) == 0
+    assert "even row count" in lib.error()
+    assert lib.venturi_q8_tiled_workspace_bytes(33, 64, 0) == 0
+    assert "1..32 tokens" in lib.error()
+    # A split launch without its workspace fails on the host.
+    assert lib.venturi_q8_tiled_run(16, 16, 16, 16, 4, 5120, 64, 128, 0, None, 0, None) == -1
+    assert "initialised workspace" in lib.error()
+    assert lib.venturi_q8_tiled_workspace_init(None, 12, None) == -1
+
+
 def test_bad_arguments_fail_before_the_device(lib):
     assert lib.venturi_q8_head_run(None, None, None, None, 1, 1, 1, 128, 0, None) == -1
     assert lib.error()

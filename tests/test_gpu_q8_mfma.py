@@ -60,7 +60,7 @@ def test_mfma_tolerances_tails_and_guards(backend, device, shape, tokens):
 
 
 @pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
-@pytest.mark.parametrize("tokens", [4, 16])
+@pytest.mark.parametrize("tokens", [4, 16, 32])
 def test_mfma_config2_sampled_rows(backend, device, n, k, tokens):
     gen = torch.Generator(device=device).manual_seed(n + k)
     w = torch.randn(n, k, generator=gen, device=device) * 0.02
@@ -130,3 +130,52 @@ def test_fused_swiglu_admission(backend, device):
     odd = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.float16, device=device)
     with pytest.raises(ValueError, match="even row count"):
         odd.prepare_swiglu(tokens=1)
+
+
+SLOT_IDLE = 0x7F8000017F800001
+
+
+@pytest.mark.parametrize("n,k,tokens", [(5120, 6144, 4), (7168, 5120, 32), (200, 1000, 13), (16, 64, 2), (100, 200, 24)])
+def test_split_k_deterministic_idle_slots_and_graph_replays(backend, device, n, k, tokens):
+    # Shapes whose launch splits K over two workgroups that exchange halves
+    # through the plan's slots. Two runs give the same bytes, every slot is idle
+    # afterwards, and HIP-graph replays (eager work and synchronisation between
+    # them) match the eager result each time.
+    print(f"case q8-split n={n} k={k} tokens={tokens}", flush=True)
+    codes, scales = random_q8(n, k, 5 + n + tokens)
+    resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, k), dtype=torch.float16, device=device)
+    plan = resident.prepare(tokens=tokens, route="mfma")
+    slots = plan.plan.slots
+    assert slots is not None and slots.numel() == tokens * ((n + 15) // 16) * 64
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(n + tokens)).half()
+    xd = x.to(device)
+    first = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    second = torch.empty_like(first)
+    plan.run(xd, out=first)
+    plan.run(xd, out=second)
+    torch.cuda.synchronize(device)
+    assert torch.equal(first.view(torch.int16), second.view(torch.int16))
+    assert bool((slots.view(torch.int64) == SLOT_IDLE).all())
+    if n * k <= 200 * 1000:
+        check(first, x, codes.numpy(), scales.numpy(), k)
+    replayed = torch.full_like(first, 3.0)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run(xd, out=replayed)
+    for i in range(3):
+        replayed.fill_(3.0)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        assert torch.equal(replayed.view(torch.int16), first.view(torch.int16)), f"replay {i}"
+        plan.run(xd, out=second)  # eager work between replays
+        torch.cuda.synchronize(device)
+        assert torch.equal(second.view(torch.int16), first.view(torch.int16))
+    assert bool((slots.view(torch.int64) == SLOT_IDLE).all())
+
+
+def test_unsplit_shapes_own_no_slots(backend, device):
+    codes, scales = random_q8(7168, 128, 9)
+    resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, 128), dtype=torch.float16, device=device)
+    assert resident.prepare(tokens=1, route="mfma").plan.slots is None
+    assert resident.prepare(tokens=8, route="mfma").plan.slots is None
+    assert resident.prepare(tokens=24, route="mfma").plan.slots is not None

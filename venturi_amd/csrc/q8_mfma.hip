@@ -184,6 +184,73 @@ __device__ __forceinline__ void store_tile_value(__half* __restrict__ out, float
     }
 }
 
+// Slot state between the two K halves of a split projection: both fp32 halves
+// hold a signalling-NaN pattern, which no arithmetic result takes (NaN results
+// are quiet), so a stored partial sum never reads as empty.
+constexpr unsigned long long kSlotEmpty = 0x7f8000017f800001ull;
+
+// Writes rows r and r + 8 of 16-row block blk for token t (plain), or the
+// SwiGLU of gate slot r and up slot r + 8 (paired planes).
+template <bool SWIGLU>
+__device__ __forceinline__ void store_row_pair(__half* __restrict__ out, float lo, float hi, int t, int blk, int r,
+                                               int n) {
+    if constexpr (SWIGLU) {
+        const int inter = n / 2, col = 8 * blk + r;
+        if (col < inter) {
+            const float g = __half2float(from_f32<__half>(lo)), u = __half2float(from_f32<__half>(hi));
+            out[static_cast<std::int64_t>(t) * inter + col] = from_f32<__half>(swiglu_value(g, u));
+        }
+    } else {
+        const int row = 16 * blk + r;
+        __half* o = out + static_cast<std::int64_t>(t) * n;
+        if (row < n) o[row] = from_f32<__half>(lo);
+        if (row + 8 < n) o[row + 8] = from_f32<__half>(hi);
+    }
+}
+
+// Final sums of one 16x16 output tile in the MFMA D layout: lane (q, r) holds
+// tokens t0 + 4q + j (j = 0..3) of row slot r of block blk. All lanes of the
+// wave call it together.
+//
+// KS == 1: the tile covers all of K and is stored. KS == 2: the tile is one of
+// two K halves computed by different workgroups. Lanes r < 8 exchange the pair
+// (own sum, sum of slot r + 8) with the 64-bit slot of (t, blk, r): the first
+// half to arrive finds kSlotEmpty and leaves its pair; the second takes the
+// other pair, adds it, resets the slot and stores. The sum of two fp32 terms
+// does not depend on their order, so the output is the same whichever half
+// arrives first. Only the slot itself is shared, so the exchange needs no
+// fence, and no wave waits for another.
+template <int KS, bool SWIGLU>
+__device__ __forceinline__ void finish_tile(__half* __restrict__ out, unsigned long long* __restrict__ slots,
+                                            const float4v& sum, int t0, int q, int blk, int r, int tokens, int n,
+                                            int blocks) {
+    if constexpr (KS == 1) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) store_tile_value<SWIGLU>(out, sum[j], t0 + 4 * q + j, blk, r, tokens, n);
+    } else {
+        static_assert(KS == 2, "K is split in two at most");
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float mine = sum[j];
+            const float partner = __shfl_xor(mine, 8, 64);
+            const int t = t0 + 4 * q + j;
+            if (r < 8 && t < tokens) {
+                unsigned long long* slot = slots + (static_cast<std::int64_t>(t) * blocks + blk) * 8 + r;
+                const unsigned long long packed =
+                    (static_cast<unsigned long long>(__float_as_uint(partner)) << 32) | __float_as_uint(mine);
+                const unsigned long long old =
+                    __hip_atomic_exchange(slot, packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (old != kSlotEmpty) {
+                    __hip_atomic_store(slot, kSlotEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const float lo = mine + __uint_as_float(static_cast<std::uint32_t>(old));
+                    const float hi = partner + __uint_as_float(static_cast<std::uint32_t>(old >> 32));
+                    store_row_pair<SWIGLU>(out, lo, hi, t, blk, r, n);
+                }
+            }
+        }
+    }
+}
+
 template <int RB, int NB, int STEPS>
 struct TiledBatch {
     uint4 w[STEPS][RB];
@@ -191,18 +258,39 @@ struct TiledBatch {
     uint4 xa[STEPS][NB], xb[STEPS][NB];
 };
 
-template <int W, int RB, int NB, int STEPS, bool SWIGLU>
+// K range of a workgroup: with KS == 2 consecutive workgroups 2g and 2g + 1
+// take chunks [0, ceil(chunks/2)) and the rest of row-block group g. The W
+// waves split that range evenly.
+struct ChunkRange {
+    int k0, k1;  // the workgroup's chunks
+    int c0, c1;  // this wave's chunks
+};
+
+template <int W, int KS>
+__device__ __forceinline__ ChunkRange chunk_range(int chunks, int wave) {
+    const int ks = KS == 1 ? 0 : static_cast<int>(blockIdx.x % KS);
+    const int kper = (chunks + KS - 1) / KS;
+    ChunkRange c;
+    c.k0 = min(ks * kper, chunks);
+    c.k1 = min(c.k0 + kper, chunks);
+    const int per = (c.k1 - c.k0 + W - 1) / W;
+    c.c0 = min(c.k0 + wave * per, c.k1);
+    c.c1 = min(c.c0 + per, c.k1);
+    return c;
+}
+
+template <int W, int RB, int NB, int STEPS, int KS, bool SWIGLU>
 __global__ __launch_bounds__(W * 64) void q8_tiled_decode(const __half* __restrict__ x, const uint4* __restrict__ codes,
                                                           const std::uint32_t* __restrict__ scales,
-                                                          __half* __restrict__ out, int tokens, int n, int k,
-                                                          int chunks, int blocks) {
+                                                          __half* __restrict__ out, unsigned long long* __restrict__ slots,
+                                                          int tokens, int n, int k, int chunks, int blocks) {
     __shared__ float4v partial[W][RB * NB][64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r = lane & 15;
-    const int block0 = blockIdx.x * RB;
-    const int per = (chunks + W - 1) / W;
-    const int c0 = min(wave * per, chunks), c1 = min(c0 + per, chunks);
+    const int block0 = static_cast<int>(blockIdx.x / KS) * RB;
+    const ChunkRange range = chunk_range<W, KS>(chunks, wave);
+    const int c0 = range.c0, c1 = range.c1;
     const int batches = (c1 - c0 + STEPS - 1) / STEPS;
     bool live[NB];
     const __half* xrow[NB];
@@ -317,11 +405,7 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_decode(const __half* __restri
             for (int j = 0; j < 4; ++j) sum[j] += v[j];
         }
         // D layout: lane holds rows (tokens) 4q..4q+3 of the token block, weight row r.
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = 16 * tb + 4 * q + j;
-            store_tile_value<SWIGLU>(out, sum[j], t, block0 + b, r, tokens, n);
-        }
+        if (block0 + b < blocks) finish_tile<KS, SWIGLU>(out, slots, sum, 16 * tb, q, block0 + b, r, tokens, n, blocks);
     }
 }
 
@@ -344,18 +428,18 @@ __host__ __device__ inline std::size_t lds_x_bytes(int tokens, int chunks) {
     return static_cast<std::size_t>(tokens) * chunks * 128 + (tokens < 16 ? 128 : 0);
 }
 
-template <int W, int RB, int STEPS, int TMAX, bool SWIGLU>
+template <int W, int RB, int STEPS, int TMAX, int KS, bool SWIGLU>
 __global__ __launch_bounds__(W * 64) void q8_tiled_lds(const __half* __restrict__ x, const uint4* __restrict__ codes,
                                                        const std::uint32_t* __restrict__ scales,
-                                                       __half* __restrict__ out, int tokens, int n, int k, int chunks,
-                                                       int blocks) {
+                                                       __half* __restrict__ out, unsigned long long* __restrict__ slots,
+                                                       int tokens, int n, int k, int chunks, int blocks) {
     extern __shared__ uint4 lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r = lane & 15;
-    const int block0 = blockIdx.x * RB;
-    const int per = (chunks + W - 1) / W;
-    const int c0 = min(wave * per, chunks), c1 = min(c0 + per, chunks);
+    const int block0 = static_cast<int>(blockIdx.x / KS) * RB;
+    const ChunkRange range = chunk_range<W, KS>(chunks, wave);
+    const int c0 = range.c0, c1 = range.c1;
     const int batches = (c1 - c0 + STEPS - 1) / STEPS;
     const uint4* wsrc[RB];
     const std::uint32_t* ssrc[RB];
@@ -380,11 +464,13 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_lds(const __half* __restrict_
     LdsBatch<RB, STEPS> ta, tb2;
     if (batches > 0) fetch(0, ta);
 
-    const int units = chunks * 8;  // 16-byte units per staged row
+    // Staged row t holds columns [64 k0, 64 k1) of the workgroup's K range.
+    const int units = (range.k1 - range.k0) * 8;  // 16-byte units per staged row
     for (int i = threadIdx.x; i < tokens * units; i += W * 64) {
         const int t = i / units, u = i - t * units;
+        const int col = 64 * range.k0 + 8 * u;
         uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (8 * u < k) v = *reinterpret_cast<const uint4*>(x + static_cast<std::int64_t>(t) * k + 8 * u);
+        if (col < k) v = *reinterpret_cast<const uint4*>(x + static_cast<std::int64_t>(t) * k + col);
         lds[t * units + (u ^ (t & 7))] = v;
     }
     if (tokens < 16 && threadIdx.x < 8) lds[tokens * units + threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
@@ -406,7 +492,7 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_lds(const __half* __restrict_
         for (int s = 0; s < STEPS; ++s) {
             const int ch = c0 + i * STEPS + s;
             if (ch >= c1) break;
-            const int base = rowbase + ch * step;
+            const int base = rowbase + (ch - range.k0) * step;
             const half8 fa = __builtin_bit_cast(half8, lds[base + ((q) ^ swz)]);
             const half8 fb = __builtin_bit_cast(half8, lds[base + ((4 + q) ^ swz)]);
 #pragma unroll
@@ -450,61 +536,129 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_lds(const __half* __restrict_
 #pragma unroll
             for (int j = 0; j < 4; ++j) sum[j] += v[j];
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) store_tile_value<SWIGLU>(out, sum[j], 4 * q + j, block0 + b, r, tokens, n);
+        if (block0 + b < blocks) finish_tile<KS, SWIGLU>(out, slots, sum, 0, q, block0 + b, r, tokens, n, blocks);
     }
 }
 
-template <int W, int RB, int STEPS, int TMAX, bool SWIGLU>
-void launch_tiled_lds(const __half* x, const uint4* codes, const std::uint32_t* scales, __half* out, int tokens, int n,
-                      int k, int chunks, int blocks, hipStream_t stream) {
-    const std::size_t lds = std::max(lds_x_bytes(tokens, chunks), static_cast<std::size_t>(W) * RB * 1024);
+template <int W, int RB, int STEPS, int TMAX, int KS, bool SWIGLU>
+void launch_tiled_lds(const __half* x, const uint4* codes, const std::uint32_t* scales, __half* out,
+                      unsigned long long* slots, int tokens, int n, int k, int chunks, int blocks, hipStream_t stream) {
+    const int kper = (chunks + KS - 1) / KS;
+    const std::size_t lds = std::max(lds_x_bytes(tokens, kper), static_cast<std::size_t>(W) * RB * 1024);
     require(lds <= 160 * 1024, "staged activations exceed LDS");
-    static const hipError_t raised = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(q8_tiled_lds<W, RB, STEPS, TMAX, SWIGLU>), hipFuncAttributeMaxDynamicSharedMemorySize,
-        160 * 1024);
+    require(KS == 1 || slots, "a split projection needs its slot buffer");
+    static const hipError_t raised =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(q8_tiled_lds<W, RB, STEPS, TMAX, KS, SWIGLU>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     check(raised);
-    q8_tiled_lds<W, RB, STEPS, TMAX, SWIGLU><<<(blocks + RB - 1) / RB, W * 64, lds, stream>>>(x, codes, scales, out, tokens,
-                                                                                             n, k, chunks, blocks);
+    q8_tiled_lds<W, RB, STEPS, TMAX, KS, SWIGLU><<<(blocks + RB - 1) / RB * KS, W * 64, lds, stream>>>(
+        x, codes, scales, out, slots, tokens, n, k, chunks, blocks);
 }
 
-template <int W, int RB, int NB, int STEPS, bool SWIGLU>
-void launch_tiled(const __half* x, const uint4* codes, const std::uint32_t* scales, __half* out, int tokens, int n,
-                  int k, int chunks, int blocks, hipStream_t stream) {
-    q8_tiled_decode<W, RB, NB, STEPS, SWIGLU><<<(blocks + RB - 1) / RB, W * 64, 0, stream>>>(x, codes, scales, out, tokens,
-                                                                                             n, k, chunks, blocks);
+template <int W, int RB, int NB, int STEPS, int KS, bool SWIGLU>
+void launch_tiled(const __half* x, const uint4* codes, const std::uint32_t* scales, __half* out,
+                  unsigned long long* slots, int tokens, int n, int k, int chunks, int blocks, hipStream_t stream) {
+    require(KS == 1 || slots, "a split projection needs its slot buffer");
+    q8_tiled_decode<W, RB, NB, STEPS, KS, SWIGLU><<<(blocks + RB - 1) / RB * KS, W * 64, 0, stream>>>(
+        x, codes, scales, out, slots, tokens, n, k, chunks, blocks);
 }
 
-// Launch shapes measured on the config-2 matrices (QKV 7168x5120, o_proj
-// 5120x6144, gate+up 34816x5120, down 5120x17408) at 1-16 tokens. One token:
-// activations staged in LDS, 16 waves on matrices of fewer than 1024 row
-// blocks and 8 waves otherwise. Up to four tokens at K >= 16384: LDS-staged
-// with 16 waves. Otherwise register-loaded fragments, 8 waves over two row
-// blocks, or three on matrices of at least 1024 blocks above 8 tokens (fewer
-// activation fragment loads per weight byte). Splitting K over workgroups with
-// a last-arriver fix-up was measured 10-20x slower: every split needs a
-// device-scope release fence (an L2 write-back).
-template <bool SWIGLU>
-void tiled_dispatch(const __half* xp, const uint4* cp, const std::uint32_t* sp, __half* op, int tokens, int n, int k,
-                    int chunks, int blocks, hipStream_t stream) {
-    if (tokens == 1 && blocks < 1024)
-        launch_tiled_lds<16, 2, 2, 1, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
-    else if (tokens == 1)
-        launch_tiled_lds<8, 2, 2, 1, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
-    else if (tokens <= 4 && k >= 16384 && lds_x_bytes(tokens, chunks) <= 160 * 1024)
-        launch_tiled_lds<16, 2, 2, 4, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
-    else if (tokens > 8 && tokens <= 16 && blocks >= 1024)
-        launch_tiled<8, 3, 1, 2, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
-    else if (tokens <= 16)
-        launch_tiled<8, 2, 1, 2, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+// Launch shapes, measured on the config-2 matrices (QKV 7168x5120, o_proj
+// 5120x6144, gate+up 34816x5120, down 5120x17408) at 1-32 tokens. A workgroup
+// streams at most about 28 GB/s, so the grid should give every CU one
+// workgroup of equal work: with fewer than 1024 row blocks, two workgroups on
+// one CU finish last and set the time.
+//
+// One token: activations staged in LDS; 16 waves over two row blocks below
+// 1024 blocks, else 8 waves over three. More tokens: register fragments, 8
+// waves, one batch of chunks in flight behind the current one, and the
+// (row blocks, K halves) shape of the candidates below whose grid is largest
+// without passing 256 workgroups; ties go to the unsplit shape up to 16 tokens
+// and to more row blocks above (two token blocks load twice the activation
+// fragments per weight byte). When none fits, three blocks unsplit.
+struct TiledShape {
+    bool lds;
+    int rb, ks;
+};
+
+TiledShape tiled_shape(int tokens, int blocks) {
+    if (tokens == 1) return blocks < 1024 ? TiledShape{true, 2, 1} : TiledShape{true, 3, 1};
+    const TiledShape candidates[] = {{false, 2, 1}, {false, 3, 1}, {false, 3, 2}, {false, 4, 2}};
+    TiledShape best{false, 3, 1};
+    long best_grid = 0;
+    for (const TiledShape& c : candidates) {
+        const long grid = static_cast<long>((blocks + c.rb - 1) / c.rb) * c.ks;
+        if (grid > 256) continue;
+        const bool tie_wins = tokens <= 16 ? c.ks < best.ks : c.rb > best.rb;
+        if (grid > best_grid || (grid == best_grid && tie_wins)) {
+            best = c;
+            best_grid = grid;
+        }
+    }
+    return best;
+}
+
+std::size_t tiled_slot_bytes(int tokens, int blocks) {
+    return tiled_shape(tokens, blocks).ks > 1 ? static_cast<std::size_t>(tokens) * blocks * 8 * sizeof(unsigned long long)
+                                             : 0;
+}
+
+template <int NB, bool SWIGLU>
+void launch_tiled_shape(const TiledShape& sh, const __half* xp, const uint4* cp, const std::uint32_t* sp, __half* op,
+                        unsigned long long* slots, int tokens, int n, int k, int chunks, int blocks,
+                        hipStream_t stream) {
+    if (sh.rb == 2 && sh.ks == 1)
+        launch_tiled<8, 2, NB, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+    else if (sh.rb == 3 && sh.ks == 1)
+        launch_tiled<8, 3, NB, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+    else if (sh.rb == 3 && sh.ks == 2)
+        launch_tiled<8, 3, NB, 1, 2, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else
-        launch_tiled<8, 2, 2, 2, SWIGLU>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+        launch_tiled<8, 4, NB, 1, 2, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+}
+
+template <bool SWIGLU>
+void tiled_dispatch(const __half* xp, const uint4* cp, const std::uint32_t* sp, __half* op, unsigned long long* slots,
+                    int tokens, int n, int k, int chunks, int blocks, hipStream_t stream) {
+    const TiledShape sh = tiled_shape(tokens, blocks);
+    if (sh.lds && sh.rb == 2)
+        launch_tiled_lds<16, 2, 1, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+    else if (sh.lds)
+        launch_tiled_lds<8, 3, 2, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+    else if (tokens <= 16)
+        launch_tiled_shape<1, SWIGLU>(sh, xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+    else
+        launch_tiled_shape<2, SWIGLU>(sh, xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+}
+
+__global__ void fill_slots(unsigned long long* __restrict__ slots, std::size_t count) {
+    for (std::size_t i = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; i < count;
+         i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+        slots[i] = kSlotEmpty;
 }
 
 }  // namespace
 
+int tiled_blocks(int n, bool swiglu) { return swiglu ? (n / 2 + 7) / 8 : (n + 15) / 16; }
+
+std::size_t q8_tiled_workspace_bytes(int tokens, int n, bool swiglu) {
+    require(tokens > 0 && tokens <= 32 && n > 0, "invalid Q8 tiled geometry (1..32 tokens, n > 0)");
+    require(!swiglu || n % 2 == 0, "the fused SwiGLU projection needs an even row count (gate rows, then up rows)");
+    return tiled_slot_bytes(tokens, tiled_blocks(n, swiglu));
+}
+
+void q8_tiled_workspace_init(void* workspace, std::size_t bytes, hipStream_t stream) {
+    require(bytes % 8 == 0 && (bytes == 0 || (workspace && aligned(workspace, 8))),
+            "the Q8 tiled workspace is whole, 8-byte aligned 64-bit words");
+    const std::size_t count = bytes / 8;
+    if (count == 0) return;
+    const int grid = static_cast<int>(std::min<std::size_t>((count + 255) / 256, 1024));
+    fill_slots<<<grid, 256, 0, stream>>>(static_cast<unsigned long long*>(workspace), count);
+}
+
 void q8_tiled_launch(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
-                     int padded, int dtype, bool swiglu, hipStream_t stream) {
+                     int padded, int dtype, bool swiglu, void* workspace, std::size_t workspace_bytes,
+                     hipStream_t stream) {
     require(x && codes && scales && out, "null Q8 operand");
     require(tokens > 0 && n > 0 && k > 0 && padded == padded_k(k), "invalid Q8 geometry");
     require(static_cast<std::int64_t>(tokens) * n < INT32_MAX, "Q8 output count exceeds int32");
@@ -514,14 +668,18 @@ void q8_tiled_launch(const void* x, const void* codes, const void* scales, void*
     require(tokens <= 32, "the tiled Q8 MFMA decode kernel takes at most 32 tokens");
     require(!swiglu || n % 2 == 0, "the fused SwiGLU projection needs an even row count (gate rows, then up rows)");
     // Paired planes hold 8 gate and 8 up rows per 16-row block.
-    const int blocks = swiglu ? (n / 2 + 7) / 8 : (n + 15) / 16;
+    const int blocks = tiled_blocks(n, swiglu);
+    const std::size_t need = tiled_slot_bytes(tokens, blocks);
+    require(need == 0 || (workspace && aligned(workspace, 8) && workspace_bytes >= need),
+            "the Q8 tiled projection needs its initialised workspace (venturi_q8_tiled_workspace_bytes)");
+    auto* slots = need ? static_cast<unsigned long long*>(workspace) : nullptr;
     const int chunks = padded / 64;
     const auto* xp = static_cast<const __half*>(x);
     const auto* cp = static_cast<const uint4*>(codes);
     const auto* sp = static_cast<const std::uint32_t*>(scales);
     auto* op = static_cast<__half*>(out);
-    if (swiglu) tiled_dispatch<true>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
-    else tiled_dispatch<false>(xp, cp, sp, op, tokens, n, k, chunks, blocks, stream);
+    if (swiglu) tiled_dispatch<true>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+    else tiled_dispatch<false>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
 }
 
 void q8_mfma_launch(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n,
@@ -553,14 +711,35 @@ extern "C" __attribute__((visibility("default"))) int venturi_q8_gemm_run(const 
     });
 }
 
+// Extension: workspace of the tiled projections for (tokens, n): the exchange
+// slots of projections whose K is split over two workgroups, or 0 when the
+// launch for this shape does not split. Returns 0 with a message on invalid
+// arguments.
+extern "C" __attribute__((visibility("default"))) std::size_t venturi_q8_tiled_workspace_bytes(int tokens, int n,
+                                                                                              int swiglu) {
+    std::size_t bytes = 0;
+    vt::host_guarded([&] { bytes = vt::q8_tiled_workspace_bytes(tokens, n, swiglu != 0); });
+    return bytes;
+}
+
+// Extension: puts a tiled-projection workspace in its idle state (a fill
+// kernel on `stream`, no memset node). Every projection call leaves it idle.
+extern "C" __attribute__((visibility("default"))) int venturi_q8_tiled_workspace_init(void* workspace,
+                                                                                     std::size_t bytes,
+                                                                                     void* stream) {
+    return vt::guarded([&] { vt::q8_tiled_workspace_init(workspace, bytes, static_cast<hipStream_t>(stream)); });
+}
+
 // Extension: the matrix-core Q8 A16 projection over tiled planes (row blocks of
 // 16 x 64-column chunks, 1 KB each, lane-ordered; scales [block][chunk][row][2]).
 extern "C" __attribute__((visibility("default"))) int venturi_q8_tiled_run(const void* x, const void* codes,
                                                                           const void* scales, void* out, int tokens,
                                                                           int n, int k, int padded, int dtype,
+                                                                          void* workspace, std::size_t workspace_bytes,
                                                                           void* stream) {
     return vt::guarded([&] {
-        vt::q8_tiled_launch(x, codes, scales, out, tokens, n, k, padded, dtype, false, static_cast<hipStream_t>(stream));
+        vt::q8_tiled_launch(x, codes, scales, out, tokens, n, k, padded, dtype, false, workspace, workspace_bytes,
+                            static_cast<hipStream_t>(stream));
     });
 }
 
@@ -571,8 +750,11 @@ extern "C" __attribute__((visibility("default"))) int venturi_q8_tiled_run(const
 extern "C" __attribute__((visibility("default"))) int venturi_q8_tiled_swiglu_run(const void* x, const void* codes,
                                                                                  const void* scales, void* out,
                                                                                  int tokens, int n, int k, int padded,
-                                                                                 int dtype, void* stream) {
+                                                                                 int dtype, void* workspace,
+                                                                                 std::size_t workspace_bytes,
+                                                                                 void* stream) {
     return vt::guarded([&] {
-        vt::q8_tiled_launch(x, codes, scales, out, tokens, n, k, padded, dtype, true, static_cast<hipStream_t>(stream));
+        vt::q8_tiled_launch(x, codes, scales, out, tokens, n, k, padded, dtype, true, workspace, workspace_bytes,
+                            static_cast<hipStream_t>(stream));
     });
 }

@@ -166,8 +166,22 @@ class ResidentQ8Vocabulary:
             raise ValueError(
                 f"The Q8 MFMA route takes FP16 activations, K % 8 == 0 and at most {MFMA_MAX_TOKENS} tokens"
             )
-        tiles = self.tiled_planes() if route == "mfma" else ()
-        return Q8OutputHead(self, tokens, route, tiles)
+        if route == "exact":
+            return Q8OutputHead(self, tokens, route)
+        return Q8OutputHead(self, tokens, route, self.tiled_planes(), self._slots(tokens, swiglu=False))
+
+    def _slots(self, tokens, *, swiglu):
+        """The plan's exchange slots for launches that split K (None when this shape does not split)."""
+        lib = self.backend._native
+        nbytes = lib.venturi_q8_tiled_workspace_bytes(tokens, self.vocab_size, int(swiglu))
+        if nbytes == 0:
+            self.backend._check(-1 if lib.venturi_blocks_error() else 0)
+            return None
+        with torch.cuda.device(self.device):
+            slots = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            self.backend._check(lib.venturi_q8_tiled_workspace_init(slots.data_ptr(), nbytes, _stream(self.device)))
+            torch.cuda.current_stream(self.device).synchronize()
+        return slots
 
 
     def prepare_swiglu(self, *, tokens):
@@ -185,7 +199,7 @@ class ResidentQ8Vocabulary:
                 f"The fused SwiGLU projection takes FP16 activations, K % 8 == 0 and at most {MFMA_MAX_TOKENS} tokens"
             )
         self.backend.validate_device(self.dtype, self.device)
-        return Q8OutputHead(self, tokens, "swiglu", self.tiled_planes(paired=True))
+        return Q8OutputHead(self, tokens, "swiglu", self.tiled_planes(paired=True), self._slots(tokens, swiglu=True))
 
 
 @dataclass(frozen=True)
@@ -217,10 +231,15 @@ class Q8Embedding:
 
 @dataclass(frozen=True)
 class Q8OutputHead:
+    """A prepared projection. Matrix-core plans whose launch splits K over two
+    workgroups own an exchange-slot buffer that every run leaves idle again;
+    runs of one such plan must therefore be ordered (one stream at a time)."""
+
     resident: ResidentQ8Vocabulary
     tokens: int
     kernel: str = "exact"
     tiles: tuple = ()
+    slots: object = None
     workspace_bytes = 0
 
     @property
@@ -240,14 +259,15 @@ class Q8OutputHead:
         r = self.resident
         _tensor(x, (self.tokens, r.hidden_size), r.dtype, r.device, "x")
         _tensor(out, (self.tokens, self.out_features), r.dtype, r.device, "out")
-        _no_overlap(out, (x,) + self.storage_tensors)
+        slots = () if self.slots is None else (self.slots,)
+        _no_overlap(out, (x,) + self.storage_tensors + slots)
         lib = r.backend._native
         if self.kernel == "exact":
-            entry, planes = lib.venturi_q8_head_run, (r._codes, r._scales)
-        elif self.kernel == "swiglu":
-            entry, planes = lib.venturi_q8_tiled_swiglu_run, self.tiles
+            entry, planes, tail = lib.venturi_q8_head_run, (r._codes, r._scales), ()
         else:
-            entry, planes = lib.venturi_q8_tiled_run, self.tiles
+            entry = lib.venturi_q8_tiled_swiglu_run if self.kernel == "swiglu" else lib.venturi_q8_tiled_run
+            planes = self.tiles
+            tail = (0, 0) if self.slots is None else (self.slots.data_ptr(), self.slots.numel())
         with torch.cuda.device(r.device):
             r.backend._check(
                 entry(
@@ -260,6 +280,7 @@ class Q8OutputHead:
                     r.hidden_size,
                     r._codes.shape[1],
                     _DTYPES[r.dtype],
+                    *tail,
                     _stream(r.device),
                 )
             )
