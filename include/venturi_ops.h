@@ -62,6 +62,30 @@ int venturi_q8_dp4a_run(const void* workspace, uint64_t available, const int8_t*
 int venturi_q8_a8_gemm_run(const void* workspace, uint64_t available, const int8_t* codes, const void* scales,
                            void* out, int tokens, int n, int k, int padded, int passes, void* stream);
 
+/* One matrix of a fused projection: resident Q8 planes, its fp16 output
+ * [tokens][stride] (rows n, stride >= n). 32 bytes, as ops_api.h:8-9. */
+typedef struct VQFOutput {
+    const int8_t* codes;
+    const void* scales;
+    void* out;
+    int n, stride;
+} VQFOutput;
+
+/* Two or three Q8 matrices of one K against one A8 workspace, each output
+ * written with its own row stride; bytes equal venturi_q8_dp4a_run per matrix
+ * (reference order). One launch below 64 tokens. Replaces ops_api.h:61 /
+ * q8_fused.cuh:186-205. */
+int venturi_q8_fused_run(const void* workspace, uint64_t available, const VQFOutput* outputs, int count, int tokens,
+                         int k, int padded, int passes, void* stream);
+
+/* SwiGLU of gate and up (fp16 [tokens][k]) rounded to fp16, then two-pass A8
+ * into `workspace` (venturi_q8_dp4a_bytes(tokens, k, 2)); optional
+ * `intermediate_debug` receives the rounded SwiGLU values; threads 128 or
+ * 256. Bytes equal venturi_swiglu_run followed by venturi_q8_dp4a_quantize.
+ * Replaces ops_api.h:99-100 / q8_producer.cuh:60-82. */
+int venturi_swiglu_q8_quantize(const void* gate, const void* up, void* workspace, uint64_t available, int tokens,
+                               int k, int threads, void* intermediate_debug, void* stream);
+
 /* RMSNorm out = (x * 1/sqrt(mean(x^2) + eps)) * w, fp32 w.
  * Replaces ops_api.h:93-94 / blocks.cu:727-740. */
 int venturi_rms_run(const void* x, const float* w, void* out, int tokens, int features, int dtype, float epsilon,

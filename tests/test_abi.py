@@ -99,3 +99,23 @@ def test_bad_arguments_fail_before_the_device(lib):
     assert lib.venturi_q4_prepare(1, 1, 1, 5, 0) == -1
     assert b"invalid Q4" in lib.venturi_ada_error()
     assert lib.venturi_row_dequant_rows(None, None, None, None, 0, 1, 1, 128, 5, None) == -1
+
+
+def test_fused_entry_points_reject_bad_arguments_on_the_host(lib):
+    # venturi_q8_fused_run admission (q8_fused.cuh:188-199): count 2 or 3, a
+    # workspace of the A8 size, 16-byte alignment, padded == ceil(k/128)*128.
+    assert lib.venturi_q8_fused_run(None, 0, None, 2, 1, 64, 128, 1, None) == -1
+    assert "invalid fused DP4A" in lib.error()
+    assert lib.venturi_q8_fused_run(16, 1 << 20, 16, 1, 1, 64, 128, 1, None) == -1
+    assert lib.venturi_q8_fused_run(16, 1 << 20, 16, 4, 1, 64, 128, 1, None) == -1
+    assert lib.venturi_q8_fused_run(16, 1 << 20, 16, 2, 1, 64, 256, 1, None) == -1
+    assert lib.venturi_swiglu_q8_quantize(None, None, None, 0, 1, 64, 256, None, None) == -1
+    assert "invalid fused SwiGLU" in lib.error()
+
+
+def test_fused_plan_requires_two_or_three_matrices():
+    from venturi_amd.q8_fused import prepare_q8_fused
+
+    for values in ([], [object()], [object()] * 4):
+        with pytest.raises(ValueError, match="two or three"):
+            prepare_q8_fused(values, tokens=1, residual_compensation=True)

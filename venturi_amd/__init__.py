@@ -31,6 +31,7 @@ __all__ = [
     "UnsupportedOperationError",
     "create_backend",
     "prepare_q8_dp4a",
+    "prepare_q8_fused",
     "prepare_rms_q8",
     "quantize_q4_rtn",
     "decode_q4_fp16",
@@ -47,6 +48,10 @@ def __getattr__(name):
         from .q8_dp4a import prepare_q8_dp4a
 
         return prepare_q8_dp4a
+    if name == "prepare_q8_fused":
+        from .q8_fused import prepare_q8_fused
+
+        return prepare_q8_fused
     if name == "prepare_rms_q8":
         from .rms_quant import prepare_rms_q8
 

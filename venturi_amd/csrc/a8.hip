@@ -12,7 +12,7 @@ namespace vt {
 constexpr int kA8GemmMinTokens = 64;
 
 void a8_gemm_launch(const void* workspace, const std::int8_t* codes, const __half* scales, void* out, int tokens,
-                    int n, int k, int padded, int passes, hipStream_t stream);
+                    int n, int k, int padded, int passes, int ldo, hipStream_t stream);
 void a8_fast_launch(const void* workspace, const std::int8_t* codes, const __half* scales, void* out, int tokens,
                     int n, int k, int padded, int passes, hipStream_t stream);
 
@@ -174,20 +174,43 @@ __global__ __launch_bounds__(256) void rms_a8(const __half* __restrict__ x, cons
     }
 }
 
+// One projection of a launch: resident planes, output, its row count and the
+// output row stride (elements).
+struct A8Item {
+    const std::int8_t* codes;
+    const __half* scales;
+    __half* out;
+    int n, stride;
+};
+
+// Up to three projections of one activation pack in one launch: workgroups
+// [first[i], first[i+1]) cover item i's rows (the reference's fused
+// projection, q8_fused.cuh:5-16).
+struct A8Set {
+    A8Item item[3];
+    int first[4];
+    int count;
+};
+
 // W8A8 projection in the reference order (q8_dp4a.cuh:36-70). One reference
 // warp = one half-wave: lane l owns groups l, l+32, ... (< ceil(k/32));
 // per group the int8 dot d is exact; sum = fmaf(f32(d), ws*as, sum) over
 // passes in order; a 32-lane shfl_down tree; RNE cast to fp16. Each half-wave
-// handles RR rows and TT tokens so activation words are reused RR times.
+// handles RR rows and TT tokens so activation words are reused RR times; a
+// workgroup covers 8*RR rows of one item of the set.
 template <int TT, int RR, int P>
 __global__ __launch_bounds__(256) void a8_gemv(const std::int8_t* __restrict__ acodes,
-                                               const float* __restrict__ ascales,
-                                               const std::int8_t* __restrict__ wcodes,
-                                               const __half* __restrict__ wscales, __half* __restrict__ out,
-                                               int tokens, int n, int k, int padded, int groups) {
+                                               const float* __restrict__ ascales, const A8Set set, int tokens,
+                                               int padded, int groups) {
+    int item = 0;
+    while (item + 1 < set.count && static_cast<int>(blockIdx.x) >= set.first[item + 1]) ++item;
+    const std::int8_t* __restrict__ wcodes = set.item[item].codes;
+    const __half* __restrict__ wscales = set.item[item].scales;
+    __half* __restrict__ out = set.item[item].out;
+    const int n = set.item[item].n, ldo = set.item[item].stride;
     const int lane = threadIdx.x & 31;
     const int half = (threadIdx.x >> 5) & 1;
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int wave = (static_cast<int>(blockIdx.x) - set.first[item]) * 4 + (threadIdx.x >> 6);
     const int row0 = (wave * 2 + half) * RR;
     const int t0 = blockIdx.y * TT;
     const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
@@ -239,26 +262,96 @@ __global__ __launch_bounds__(256) void a8_gemv(const std::int8_t* __restrict__ a
         for (int r = 0; r < RR; ++r) {
             const float y = warp32_sum(sum[t][r]);
             if (lane == 0 && row0 + r < n && t0 + t < tokens)
-                out[static_cast<std::int64_t>(t0 + t) * n + row0 + r] = from_f32<__half>(y);
+                out[static_cast<std::int64_t>(t0 + t) * ldo + row0 + r] = from_f32<__half>(y);
         }
 }
 
 template <int TT, int RR, int P>
-void launch_a8_gemv(const std::int8_t* acodes, const float* ascales, const std::int8_t* codes,
-                    const __half* scales, __half* out, int tokens, int n, int k, int padded, int groups,
+void launch_a8_gemv(const std::int8_t* acodes, const float* ascales, A8Set set, int tokens, int padded, int groups,
                     hipStream_t stream) {
-    const dim3 grid((n + 8 * RR - 1) / (8 * RR), (tokens + TT - 1) / TT);
+    constexpr int rows_per_block = 8 * RR;
+    set.first[0] = 0;
+    for (int i = 0; i < set.count; ++i) set.first[i + 1] = set.first[i] + (set.item[i].n + rows_per_block - 1) / rows_per_block;
+    const dim3 grid(set.first[set.count], (tokens + TT - 1) / TT);
     require(grid.y <= 65535, "token tiles exceed the launch grid");
-    a8_gemv<TT, RR, P><<<grid, 256, 0, stream>>>(acodes, ascales, codes, scales, out, tokens, n, k, padded, groups);
+    a8_gemv<TT, RR, P><<<grid, 256, 0, stream>>>(acodes, ascales, set, tokens, padded, groups);
 }
 
 template <int P>
-void dispatch_a8_gemv(const std::int8_t* acodes, const float* ascales, const std::int8_t* codes,
-                      const __half* scales, __half* out, int tokens, int n, int k, int padded, int groups,
-                      hipStream_t stream) {
-    if (tokens == 1) launch_a8_gemv<1, 2, P>(acodes, ascales, codes, scales, out, tokens, n, k, padded, groups, stream);
-    else if (tokens == 2) launch_a8_gemv<2, 2, P>(acodes, ascales, codes, scales, out, tokens, n, k, padded, groups, stream);
-    else launch_a8_gemv<4, 2, P>(acodes, ascales, codes, scales, out, tokens, n, k, padded, groups, stream);
+void dispatch_a8_gemv(const std::int8_t* acodes, const float* ascales, const A8Set& set, int tokens, int padded,
+                      int groups, hipStream_t stream) {
+    if (tokens == 1) launch_a8_gemv<1, 2, P>(acodes, ascales, set, tokens, padded, groups, stream);
+    else if (tokens == 2) launch_a8_gemv<2, 2, P>(acodes, ascales, set, tokens, padded, groups, stream);
+    else launch_a8_gemv<4, 2, P>(acodes, ascales, set, tokens, padded, groups, stream);
+}
+
+// The projections of a set in the reference's order: one SIMT launch for all
+// items below 64 tokens, one matrix-core GEMM per item above (each fills the
+// chip on its own).
+void run_a8_set(const void* workspace, const A8Set& set, int tokens, int k, int padded, int passes,
+                hipStream_t stream) {
+    const int groups = (k + 31) / 32;
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    const auto* acodes = static_cast<const std::int8_t*>(workspace);
+    const auto* ascales = reinterpret_cast<const float*>(acodes + count * 32 * passes);
+    if (tokens >= kA8GemmMinTokens) {
+        for (int i = 0; i < set.count; ++i)
+            a8_gemm_launch(workspace, set.item[i].codes, set.item[i].scales, set.item[i].out, tokens, set.item[i].n, k,
+                           padded, passes, set.item[i].stride, stream);
+        return;
+    }
+    if (passes == 1) dispatch_a8_gemv<1>(acodes, ascales, set, tokens, padded, groups, stream);
+    else dispatch_a8_gemv<2>(acodes, ascales, set, tokens, padded, groups, stream);
+}
+
+// SwiGLU of the native runtime (blocks.cu:56-86) rounded to fp16, then the
+// two-pass quantizer, in one kernel (q8_producer.cuh:8-57): the bytes of
+// venturi_swiglu_run followed by venturi_q8_dp4a_quantize with two passes.
+// Layout and lanes as a8_quantize; `intermediate` (optional) receives the
+// rounded SwiGLU values.
+// `intermediate` may be gate or up itself (each element is read, then written,
+// by the same lane), so those pointers carry no __restrict__.
+__global__ __launch_bounds__(256) void swiglu_a8(const __half* gate, const __half* up, std::int8_t* codes,
+                                                 float* scales, __half* intermediate, int tokens, int k, int groups,
+                                                 bool vec) {
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    const std::int64_t index = (static_cast<std::int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 2;
+    const int sub = threadIdx.x & 3;
+    if (index >= count) return;  // the 4 lanes of a group exit together
+    const int token = static_cast<int>(index / groups);
+    const int g = static_cast<int>(index % groups);
+    const int col = g * 32 + sub * 8;
+    const std::int64_t row = static_cast<std::int64_t>(token) * k;
+    float r[8];
+    if (vec && col + 7 < k) {
+        const uint4 a = *reinterpret_cast<const uint4*>(gate + row + col);
+        const uint4 b = *reinterpret_cast<const uint4*>(up + row + col);
+        const std::uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+        std::uint32_t hw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const __half lo = from_f32<__half>(swiglu_value(half_lo(aw[i]), half_lo(bw[i])));
+            const __half hi = from_f32<__half>(swiglu_value(half_hi(aw[i]), half_hi(bw[i])));
+            hw[i] = static_cast<std::uint32_t>(__half_as_ushort(lo)) | (static_cast<std::uint32_t>(__half_as_ushort(hi)) << 16);
+            r[2 * i] = __half2float(lo);
+            r[2 * i + 1] = __half2float(hi);
+        }
+        if (intermediate) *reinterpret_cast<uint4*>(intermediate + row + col) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    } else {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            r[v] = 0.0f;
+            if (col + v < k) {
+                const __half h = from_f32<__half>(swiglu_value(__half2float(gate[row + col + v]), __half2float(up[row + col + v])));
+                if (intermediate) intermediate[row + col + v] = h;
+                r[v] = __half2float(h);
+            }
+        }
+    }
+    bool bad = false;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) bad |= !isfinite(r[v]);
+    quantize_group<8, 4>(r, bad, 2, codes + index * 32 + sub * 8, scales + index, count * 32, count, sub == 0);
 }
 
 bool overlap(const void* a, std::uint64_t an, const void* b, std::uint64_t bn) {
@@ -296,19 +389,71 @@ void validate_a8_projection(const void* workspace, std::uint64_t available, cons
 void a8_gemv_launch(const void* workspace, std::uint64_t available, const std::int8_t* codes, const __half* scales,
                     void* out, int tokens, int n, int k, int padded, int passes, hipStream_t stream) {
     validate_a8_projection(workspace, available, codes, scales, out, tokens, n, k, padded, passes);
-    const int groups = (k + 31) / 32;
-    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
-    const auto* acodes = static_cast<const std::int8_t*>(workspace);
-    const auto* ascales = reinterpret_cast<const float*>(acodes + count * 32 * passes);
-    auto* y = static_cast<__half*>(out);
     // Both kernels produce the reference's bytes; the matrix-core GEMM takes
     // over once a 64-token tile is filled.
-    if (tokens >= kA8GemmMinTokens) {
-        a8_gemm_launch(workspace, codes, scales, out, tokens, n, k, padded, passes, stream);
-        return;
+    A8Set set{};
+    set.item[0] = A8Item{codes, scales, static_cast<__half*>(out), n, n};
+    set.count = 1;
+    run_a8_set(workspace, set, tokens, k, padded, passes, stream);
+}
+
+// Reference fused-projection descriptor (ops_api.h:8-9).
+struct VQFOutput {
+    const std::int8_t* codes;
+    const __half* scales;
+    __half* out;
+    int n, stride;
+};
+static_assert(sizeof(VQFOutput) == 32, "the reference's descriptor is 32 bytes");
+
+void q8_fused_launch(const void* workspace, std::uint64_t available, const VQFOutput* outputs, int count, int tokens,
+                     int k, int padded, int passes, hipStream_t stream) {
+    // Admission of q8_fused.cuh:188-199 (the architecture check becomes gfx950).
+    const std::uint64_t needed = a8_bytes(tokens, k, passes);
+    require(workspace && available >= needed && outputs && (count == 2 || count == 3) && padded == padded_k(k) &&
+                aligned(workspace, 16),
+            "invalid fused DP4A input/geometry");
+    A8Set set{};
+    set.count = count;
+    std::uint64_t total = 0;
+    for (int i = 0; i < count; ++i) {
+        const VQFOutput& p = outputs[i];
+        require(p.codes && p.scales && p.out && p.n > 0 && p.n <= INT32_MAX - 16 && p.stride >= p.n &&
+                    static_cast<std::uint64_t>(tokens - 1) * p.stride + p.n < INT32_MAX && aligned(p.codes, 16) &&
+                    aligned(p.scales, 2) && aligned(p.out, 2),
+                "invalid fused DP4A descriptor");
+        total += p.n;
+        set.item[i] = A8Item{p.codes, p.scales, p.out, p.n, p.stride};
     }
-    if (passes == 1) dispatch_a8_gemv<1>(acodes, ascales, codes, scales, y, tokens, n, k, padded, groups, stream);
-    else dispatch_a8_gemv<2>(acodes, ascales, codes, scales, y, tokens, n, k, padded, groups, stream);
+    require(total < INT32_MAX - 48, "fused row sum exceeds int32");
+    run_a8_set(workspace, set, tokens, k, padded, passes, stream);
+}
+
+void swiglu_a8_launch(const void* gate, const void* up, void* workspace, std::uint64_t available, int tokens, int k,
+                      int threads, void* intermediate, hipStream_t stream) {
+    // Admission of q8_producer.cuh:62-79 (always two passes).
+    const std::uint64_t needed = a8_bytes(tokens, k, 2);
+    const std::uint64_t input_bytes = static_cast<std::uint64_t>(tokens) * k * 2;
+    require(gate && up && workspace && available >= needed && (threads == 128 || threads == 256) &&
+                aligned(workspace, 16) && aligned(gate, 2) && aligned(up, 2) && aligned(intermediate, 2) &&
+                !overlap(workspace, needed, gate, input_bytes) && !overlap(workspace, needed, up, input_bytes),
+            "invalid fused SwiGLU/two-pass Q8 operands");
+    require(!intermediate || (!overlap(workspace, needed, intermediate, input_bytes) &&
+                              (intermediate == gate || !overlap(intermediate, input_bytes, gate, input_bytes)) &&
+                              (intermediate == up || !overlap(intermediate, input_bytes, up, input_bytes))),
+            "invalid fused debug output overlap");
+    const int groups = (k + 31) / 32;
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    auto* codes = static_cast<std::int8_t*>(workspace);
+    auto* scales = reinterpret_cast<float*>(codes + count * 64);
+    const bool vec = k % 8 == 0 && aligned(gate, 16) && aligned(up, 16) && aligned(intermediate, 16);
+    const std::int64_t blocks = (count * 4 + 255) / 256;
+    require(blocks <= INT32_MAX, "A8 grid too large");
+    // `threads` selects the reference's block size; the bytes do not depend on it.
+    swiglu_a8<<<static_cast<unsigned>(blocks), 256, 0, stream>>>(static_cast<const __half*>(gate),
+                                                                 static_cast<const __half*>(up), codes, scales,
+                                                                 static_cast<__half*>(intermediate), tokens, k, groups,
+                                                                 vec);
 }
 
 void rms_launch(const void* x, const float* w, void* out, int tokens, int k, int dtype, float epsilon,
@@ -416,5 +561,25 @@ VT_EXPORT int venturi_rms_q8_quantize_passes(const void* x, const float* w, void
     return vt::guarded([&] {
         vt::rms_a8_launch(x, w, workspace, available, tokens, k, epsilon, passes, intermediate,
                           static_cast<hipStream_t>(stream));
+    });
+}
+
+// Reference fused projection (ops_api.h:61, q8_fused.cuh:186-205): two or three
+// Q8 matrices against one A8 activation pack, each output written with its
+// own row stride; bytes equal venturi_q8_dp4a_run per matrix.
+VT_EXPORT int venturi_q8_fused_run(const void* workspace, std::uint64_t available, const vt::VQFOutput* outputs,
+                                   int count, int tokens, int k, int padded, int passes, void* stream) {
+    return vt::guarded([&] {
+        vt::q8_fused_launch(workspace, available, outputs, count, tokens, k, padded, passes,
+                            static_cast<hipStream_t>(stream));
+    });
+}
+
+// Reference SwiGLU -> two-pass A8 producer (ops_api.h:99, q8_producer.cuh:60-82).
+VT_EXPORT int venturi_swiglu_q8_quantize(const void* gate, const void* up, void* workspace, std::uint64_t available,
+                                         int tokens, int k, int threads, void* intermediate_debug, void* stream) {
+    return vt::guarded([&] {
+        vt::swiglu_a8_launch(gate, up, workspace, available, tokens, k, threads, intermediate_debug,
+                             static_cast<hipStream_t>(stream));
     });
 }

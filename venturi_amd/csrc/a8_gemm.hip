@@ -83,7 +83,7 @@ __global__ __launch_bounds__(512) void a8_gemm(const std::int8_t* __restrict__ a
                                                const float* __restrict__ ascales,
                                                const std::int8_t* __restrict__ wcodes,
                                                const __half* __restrict__ wscales, __half* __restrict__ out,
-                                               int tokens, int n, int padded, int groups) {
+                                               int tokens, int n, int padded, int groups, int ldo) {
     constexpr int B = A8Tile<P>::kBatch;
     static_assert(B * kTokTile <= 512 && B * kRowTile <= 512, "one scale per thread and item");
     __shared__ __attribute__((aligned(16))) _Float16 af[2][P][B][kTokTile * kRowHalves];
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(512) void a8_gemm(const std::int8_t* __restrict__ a
             for (int e = 0; e < 4; ++e) {
                 const int t = t0 + wm * 32 + a * 16 + 4 * q + e;
                 if (t < tokens && row < n)
-                    out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(lv[4][(a * 2 + b) * 4 + e]);
+                    out[static_cast<std::int64_t>(t) * ldo + row] = from_f32<__half>(lv[4][(a * 2 + b) * 4 + e]);
             }
         }
 }
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(512) void a8_gemm(const std::int8_t* __restrict__ a
 }  // namespace
 
 void a8_gemm_launch(const void* workspace, const std::int8_t* codes, const __half* scales, void* out, int tokens,
-                    int n, int k, int padded, int passes, hipStream_t stream) {
+                    int n, int k, int padded, int passes, int ldo, hipStream_t stream) {
     const int groups = (k + 31) / 32;
     const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
     const auto* acodes = static_cast<const std::int8_t*>(workspace);
@@ -343,10 +343,10 @@ void a8_gemm_launch(const void* workspace, const std::int8_t* codes, const __hal
     require(grid.y <= 65535, "token tiles exceed the launch grid");
     if (passes == 1)
         a8_gemm<1><<<grid, 512, 0, stream>>>(acodes, ascales, codes, scales, static_cast<__half*>(out), tokens, n,
-                                              padded, groups);
+                                              padded, groups, ldo);
     else
         a8_gemm<2><<<grid, 512, 0, stream>>>(acodes, ascales, codes, scales, static_cast<__half*>(out), tokens, n,
-                                              padded, groups);
+                                              padded, groups, ldo);
 }
 
 }  // namespace vt
