@@ -173,11 +173,31 @@ int venturi_q4_linear(const void* x, const void* codes, const void* scales, void
 int venturi_q4_fused_run(const void* x, const void* codes, const void* scales, void* out, int t, int rows, int k,
                          int padded, int dtype, void* stream);
 
-/* Row-codec decode of rows [row, row+rows) into out [rows][k] fp16; bits must
- * be 4 in this library (the q5/q6 high plane is not implemented, `high` is
- * ignored). Replaces ops_api.h:98 / blocks.cu:1077-1086. */
+/* Row-codec decode of rows [row, row+rows) into out [rows][k] fp16 (ld = k),
+ * bits 4, 5 or 6: codes [n][padded/2] low nibbles, high plane
+ * [n][padded*(bits-4)/8] (LSB-first stream of the upper bits; unused for 4),
+ * scales [n][padded/64]; w = fp16(q*scale). Replaces ops_api.h:98 /
+ * blocks.cu:1077-1086, weight_dequant.cuh:16-59. */
 int venturi_row_dequant_rows(const void* codes, const void* high, const void* scales, void* out, int row, int rows,
                              int k, int padded, int bits, void* stream);
+
+/* The same decode of `count` rows named by int64 `ids` (each must be a row of
+ * the planes) into out [count][k]. Replaces ops_api.h / blocks.cu:1088-1096,
+ * weight_dequant.cuh:61-67. */
+int venturi_row_dequant_indexed(const void* codes, const void* high, const void* scales, const int64_t* ids,
+                                void* out, int count, int k, int padded, int bits, void* stream);
+
+/* W5A16 operator ABI 1 (flash_next_q5.cu:40-64): returns a HIP error code
+ * (hipErrorInvalidValue on bad arguments) like the Q4 expert ABI. */
+int venturi_q5_abi(void); /* returns 1 */
+/* fp16 decode of a q5_g64_fp16 matrix [rows][cols]. Replaces
+ * flash_next_q5.cu:42-52. */
+int venturi_q5_decode(const void* codes, const void* high, const void* scales, void* out, int rows, int cols,
+                      int padded, void* stream);
+/* W5A16 GEMV, 1..64 fp16 tokens, fp16(q*scale) weights in the lane-strided
+ * fmaf order; bytes identical. Replaces flash_next_q5.cu:53-64. */
+int venturi_q5_linear(const void* x, const void* codes, const void* high, const void* scales, void* out, int tokens,
+                      int rows, int cols, int padded, void* stream);
 
 /* Plugin ABI 2 (q4_linear.cu:60-88): its own thread-local error text. */
 int venturi_ada_abi(void); /* returns 2 */

@@ -11,9 +11,10 @@ Two layers:
 * numpy restatements of the codecs (pack/unpack/RTN) and of the MoE combine.
 
 Each function cites the reference file:line it restates (paths relative to
-/root/reference/src/venturi/). What pins each function is listed in
-tests/test_oracle_pins.py; functions that nothing pins are marked
-"parity unpinned" below.
+/root/reference/src/venturi/). The tests that pin each function against the
+reference's known answers and against closed forms are tests/test_golden.py,
+tests/test_weights.py, tests/test_oracle_q4_moe.py and tests/test_q5_codec.py;
+functions that nothing pins are marked "parity unpinned" below.
 """
 
 import ctypes as C
@@ -47,6 +48,8 @@ def lib():
         handle.oracle_q4_decode.argtypes = [P] * 3 + [I] * 3
         handle.oracle_q4_generic.argtypes = [P] * 4 + [I] * 5
         handle.oracle_q4_fused.argtypes = [P] * 4 + [I] * 4
+        handle.oracle_row_decode.argtypes = [P] * 5 + [I] * 4
+        handle.oracle_q5_linear.argtypes = [P] * 5 + [I] * 4
         _lib = handle
     return _lib
 
@@ -143,6 +146,41 @@ def q4_decode_fp16(packed, scales, k):
     signed = q4_unpack_signed(packed, packed.shape[1] * 2).astype(np.float32)
     values = signed.reshape(packed.shape[0], -1, 64) * scales.astype(np.float32)[:, :, None]
     return values.reshape(packed.shape[0], -1)[:, :k].astype(np.float16)
+
+
+def pack_high(upper, hb):
+    """High plane of a Q5/Q6 row codec (weights.py:175-190, weight_dequant.cuh:1-9).
+
+    ``upper`` [n, padded] holds each column's bits above the low nibble
+    (0 <= v < 2**hb); column c's bits go to bits [c*hb, c*hb + hb) of the
+    row's LSB-first bit stream. Returns uint8 [n, padded*hb/8].
+    """
+    upper = np.asarray(upper, dtype=np.int64)
+    n, padded = upper.shape
+    bits = ((upper[:, :, None] >> np.arange(hb)) & 1).reshape(n, padded * hb)
+    return (bits.reshape(n, -1, 8) << np.arange(8)).sum(-1).astype(np.uint8)
+
+
+def pack_row_codec(codes, scales, bits):
+    """Signed codes [n, padded] in the bits-wide range -> (codes, high) planes."""
+    codes = np.asarray(codes, dtype=np.int64)
+    u = codes & ((1 << bits) - 1)
+    low = (u & 15).astype(np.uint8)
+    packed = low[:, 0::2] | (low[:, 1::2] << 4)
+    high = pack_high(u >> 4, bits - 4) if bits > 4 else np.zeros((codes.shape[0], 0), np.uint8)
+    return packed.astype(np.uint8), high, np.asarray(scales, dtype=np.float16)
+
+
+def row_decode(codes, high, scales, k, bits, ids=None):
+    """venturi_row_dequant_rows / _indexed (weight_dequant.cuh:16-67): fp16 bits [len(ids), k]."""
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    high = np.ascontiguousarray(high, dtype=np.uint8) if bits > 4 else np.zeros(1, np.uint8)
+    n, padded = codes.shape[0], codes.shape[1] * 2
+    ids = np.arange(n, dtype=np.int64) if ids is None else np.ascontiguousarray(ids, dtype=np.int64)
+    out = np.zeros((ids.size, k), dtype=np.uint16)
+    lib().oracle_row_decode(_ptr(codes), _ptr(high), _ptr(_u16(scales)), _ptr(ids), _ptr(out), ids.size, k, padded,
+                            bits)
+    return out
 
 
 # -------------------------------------------------- device-order restatements
@@ -246,6 +284,17 @@ def q4_linear(x, packed, scales, k):
     tokens, rows, padded = xs.shape[0], packed.shape[0], packed.shape[1] * 2
     out = np.zeros((tokens, rows), dtype=np.uint16)
     lib().oracle_q4_linear(_ptr(xs), _ptr(packed), _ptr(_u16(scales)), _ptr(out), tokens, rows, k, padded)
+    return out
+
+
+def q5_linear(x, codes, high, scales, k):
+    """q5_linear (ops/csrc/flash_next_q5.cu:26-38): fp16 bits [tokens, rows]."""
+    xs = _u16(x)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    high = np.ascontiguousarray(high, dtype=np.uint8)
+    tokens, rows, padded = xs.shape[0], codes.shape[0], codes.shape[1] * 2
+    out = np.zeros((tokens, rows), dtype=np.uint16)
+    lib().oracle_q5_linear(_ptr(xs), _ptr(codes), _ptr(high), _ptr(_u16(scales)), _ptr(out), tokens, rows, k, padded)
     return out
 
 

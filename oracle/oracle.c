@@ -365,3 +365,50 @@ EXPORT void oracle_q4_fused(const uint16_t* x, const uint8_t* codes, const uint1
             out[(int64_t)t * rows + row] = f32_to_f16(warp_tree(lanes));
         }
 }
+
+/* ---- Q4/Q5/Q6 row codecs (weight_dequant.cuh:1-51, weights.py:175-190) ----
+ * Column c of a row: low four bits = nibble (c & 1) of code byte c/2; the
+ * hb = bits-4 upper bits are bits [c*hb, c*hb + hb) of the row's high plane
+ * read as one LSB-first bit stream; q is the bits-wide two's complement;
+ * w = fp16(q * scale[c / 64]), one RNE rounding. */
+static float row_weight(const uint8_t* codes, const uint8_t* high, const uint16_t* scales, int64_t row, int col,
+                        int padded, int bits) {
+    const int hb = bits - 4;
+    const uint8_t byte = codes[row * (padded / 2) + col / 2];
+    int raw = (col & 1) ? (byte >> 4) : (byte & 15);
+    for (int b = 0; b < hb; ++b) {
+        const int64_t bit = (int64_t)col * hb + b;
+        const int value = (high[row * ((int64_t)padded * hb / 8) + bit / 8] >> (bit % 8)) & 1;
+        raw |= value << (4 + b);
+    }
+    const int q = raw >= (1 << (bits - 1)) ? raw - (1 << bits) : raw;
+    return f16_to_f32(f32_to_f16((float)q * f16_to_f32(scales[row * (padded / 64) + col / 64])));
+}
+
+/* venturi_row_dequant_rows / _indexed: out[i][c] = w(ids[i], c), ld = k. */
+EXPORT void oracle_row_decode(const uint8_t* codes, const uint8_t* high, const uint16_t* scales, const int64_t* ids,
+                              uint16_t* out, int count, int k, int padded, int bits) {
+    for (int i = 0; i < count; ++i)
+        for (int c = 0; c < k; ++c)
+            out[(int64_t)i * k + c] = f32_to_f16(row_weight(codes, high, scales, ids[i], c, padded, bits));
+}
+
+/* ---- W5A16 GEMV (flash_next_q5.cu:9-38) -----------------------------------
+ * weight_at = fp16(q * scale); lane l sums columns l, l+32, ... with fmaf in
+ * increasing order (nvcc contracts sum += w*x), 32-lane shfl_down tree,
+ * fp16 output. */
+EXPORT void oracle_q5_linear(const uint16_t* x, const uint8_t* codes, const uint8_t* high, const uint16_t* scales,
+                             uint16_t* out, int tokens, int rows, int cols, int padded) {
+    for (int t = 0; t < tokens; ++t)
+        for (int row = 0; row < rows; ++row) {
+            float lanes[32];
+            for (int l = 0; l < 32; ++l) {
+                float sum = 0.0f;
+                for (int c = l; c < cols; c += 32)
+                    sum = fmaf(row_weight(codes, high, scales, row, c, padded, 5), f16_to_f32(x[(int64_t)t * cols + c]),
+                               sum);
+                lanes[l] = sum;
+            }
+            out[(int64_t)t * rows + row] = f32_to_f16(warp_tree(lanes));
+        }
+}

@@ -1,0 +1,130 @@
+"""Q5 operators and the Q4/Q5/Q6 row decode on the device, against the CPU oracle.
+
+Bytes must match: the decode is one RNE rounding of an exact product, and the
+W5A16 GEMV runs the reference's lane-strided fmaf order and 32-lane tree. The
+reference's own execution check (a relative bound against a torch fp32
+product) is kept as well.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import bits
+from venturi_amd.q5 import NativeQ5, decode_q5_fp16, quantize_q5_rtn
+from venturi_amd.weights import Q5RowSplitWeight
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def native():
+    return NativeQ5()
+
+
+@pytest.mark.parametrize("shape", [(64, 320), (33, 130), (5, 640), (1, 1), (17, 5120)])
+@pytest.mark.parametrize("tokens", [1, 3, 17, 64])
+def test_decode_and_linear_bytes(native, device, shape, tokens):
+    n, k = shape
+    print(f"case q5 n={n} k={k} tokens={tokens}", flush=True)
+    torch.manual_seed(31 + n + k)
+    q = quantize_q5_rtn(torch.randn(n, k))
+    prepared = native.prepare(q, device=device)
+    assert torch.equal(native.decode(prepared).cpu(), decode_q5_fp16(q))
+    x = torch.randn(tokens, k).half()
+    got = native.linear(x.to(device), prepared).cpu()
+    want = oracle.q5_linear(bits(x), q.codes.numpy(), q.high.numpy(), q.scales.numpy(), k)
+    np.testing.assert_array_equal(bits(got), want)
+    # The reference's execution bound (tests/test_flash_next_q5.py:125-131).
+    expected = (x.float() @ decode_q5_fp16(q).float().t()).half()
+    peak = expected.float().abs().max().clamp_min(1e-6)
+    assert float((got.float() - expected.float()).abs().max() / peak) < 1e-3
+
+
+def test_linear_bounds_and_status(native, device):
+    torch.manual_seed(32)
+    q = quantize_q5_rtn(torch.randn(8, 128))
+    prepared = native.prepare(q, device=device)
+    with pytest.raises(ValueError):
+        native.linear(torch.randn(65, 128, dtype=torch.float16).to(device), prepared)
+    w = prepared.weight
+    lib = native.lib
+    s = torch.cuda.current_stream(device).cuda_stream
+    out = torch.empty(1, 8, dtype=torch.float16, device=device)
+    x = torch.ones(1, 128, dtype=torch.float16, device=device)
+    # hipErrorInvalidValue (1) for bad geometry, as the reference's cudaErrorInvalidValue.
+    assert lib.venturi_q5_linear(x.data_ptr(), w.codes.data_ptr(), w.high.data_ptr(), w.scales.data_ptr(),
+                                 out.data_ptr(), 65, 8, 128, 128, s) == 1
+    assert lib.venturi_q5_linear(x.data_ptr(), w.codes.data_ptr(), w.high.data_ptr(), w.scales.data_ptr(),
+                                 out.data_ptr(), 1, 8, 128, 64, s) == 1
+    assert lib.venturi_q5_decode(w.codes.data_ptr(), None, w.scales.data_ptr(), out.data_ptr(), 8, 128, 128, s) == 1
+    torch.cuda.synchronize(device)
+
+
+def _planes(n, k, nbits, seed):
+    padded = (k + 127) // 128 * 128
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(-(1 << (nbits - 1)), 1 << (nbits - 1), size=(n, padded))
+    codes[:, k:] = 0
+    scales = (rng.random((n, padded // 64)) * 0.02).astype(np.float16)
+    return oracle.pack_row_codec(codes, scales, nbits)
+
+
+@pytest.mark.parametrize("nbits", [4, 5, 6])
+@pytest.mark.parametrize("k,padded_extra", [(1, 0), (63, 0), (130, 128), (2049, 0), (5120, 0)])
+def test_row_dequant_rows_and_indexed(backend, device, nbits, k, padded_extra):
+    print(f"case row-decode bits={nbits} k={k}", flush=True)
+    n = 37
+    packed, high, scales = _planes(n, k, nbits, nbits * 1000 + k)
+    if padded_extra:  # a wider padded K than the minimum is accepted (blocks.cu:1079)
+        packed = np.pad(packed, ((0, 0), (0, padded_extra // 2)))
+        high = np.pad(high, ((0, 0), (0, padded_extra * (nbits - 4) // 8)))
+        scales = np.pad(scales, ((0, 0), (0, padded_extra // 64)))
+    padded = packed.shape[1] * 2
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    dc = torch.from_numpy(packed).to(device)
+    dh = torch.from_numpy(high if nbits > 4 else np.zeros((n, 1), np.uint8)).to(device)
+    ds = torch.from_numpy(scales).to(device)
+    row0, rows = 5, 29
+    guard = torch.full((rows * k + 2,), 47, dtype=torch.float16, device=device)
+    out = guard[1:-1]
+    backend._check(lib.venturi_row_dequant_rows(dc.data_ptr(), dh.data_ptr(), ds.data_ptr(), out.data_ptr(), row0, rows,
+                                                k, padded, nbits, s))
+    want = oracle.row_decode(packed, high, scales, k, nbits, np.arange(row0, row0 + rows))
+    g = guard.cpu()
+    assert g[0] == g[-1] == 47
+    np.testing.assert_array_equal(bits(out.view(rows, k)), want)
+    ids = np.array([36, 0, 5, 5, 17], dtype=np.int64)
+    dids = torch.from_numpy(ids).to(device)
+    out2 = torch.empty(len(ids), k, dtype=torch.float16, device=device)
+    backend._check(lib.venturi_row_dequant_indexed(dc.data_ptr(), dh.data_ptr(), ds.data_ptr(), dids.data_ptr(),
+                                                   out2.data_ptr(), len(ids), k, padded, nbits, s))
+    np.testing.assert_array_equal(bits(out2), oracle.row_decode(packed, high, scales, k, nbits, ids))
+
+
+def test_row_decode_q5_equals_native_decode(backend, native, device):
+    torch.manual_seed(3)
+    q = Q5RowSplitWeight.from_dense(torch.randn(12, 300))
+    prepared = native.prepare(q, device=device)
+    w = prepared.weight
+    out = torch.empty(12, 300, dtype=torch.float16, device=device)
+    backend._check(backend._native.venturi_row_dequant_rows(
+        w.codes.data_ptr(), w.high.data_ptr(), w.scales.data_ptr(), out.data_ptr(), 0, 12, 300, 384, 5,
+        torch.cuda.current_stream(device).cuda_stream))
+    assert torch.equal(out.cpu(), native.decode(prepared).cpu())
+    assert torch.equal(out.cpu(), decode_q5_fp16(q))
+
+
+def test_row_decode_rejects_bad_arguments(backend, device):
+    lib = backend._native
+    x = torch.zeros(64, dtype=torch.uint8, device=device)
+    o = torch.empty(128, dtype=torch.float16, device=device)
+    s = torch.cuda.current_stream(device).cuda_stream
+    assert lib.venturi_row_dequant_rows(x.data_ptr(), x.data_ptr(), x.data_ptr(), o.data_ptr(), 0, 1, 128, 128, 7, s) == -1
+    assert "4, 5 or 6" in backend._native.error()
+    assert lib.venturi_row_dequant_rows(x.data_ptr(), None, x.data_ptr(), o.data_ptr(), 0, 1, 128, 128, 5, s) == -1
+    assert lib.venturi_row_dequant_indexed(x.data_ptr(), x.data_ptr(), x.data_ptr(), None, o.data_ptr(), 1, 128, 128,
+                                           5, s) == -1
+    torch.cuda.synchronize(device)

@@ -261,16 +261,6 @@ VT_EXPORT int venturi_q4_linear(const void* x, const void* codes, const void* sc
     return static_cast<int>(hipGetLastError());
 }
 
-// ---- row-codec decode (blocks.cu:1077-1086), 4-bit rows only in this build
-VT_EXPORT int venturi_row_dequant_rows(const void* codes, const void* high, const void* scales, void* out, int row,
-                                       int rows, int k, int padded, int bits, void* stream) {
-    return vt::guarded([&] {
-        vt::require(bits == 4, "only 4-bit row codecs are executed by this build");
-        (void)high;
-        vt::q4_decode_launch(codes, scales, out, row, rows, k, padded, static_cast<hipStream_t>(stream));
-    });
-}
-
 // ---- research fused Q4 GEMV (blocks.cu:1067-1076)
 VT_EXPORT int venturi_q4_fused_run(const void* x, const void* codes, const void* scales, void* out, int t, int rows,
                                    int k, int padded, int dtype, void* stream) {

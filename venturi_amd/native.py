@@ -48,6 +48,10 @@ SIGNATURES = {
     "venturi_q4_linear": ([_P] * 4 + [_I] * 4 + [_P], _I),
     "venturi_q4_fused_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
     "venturi_row_dequant_rows": ([_P] * 4 + [_I] * 5 + [_P], _I),
+    "venturi_row_dequant_indexed": ([_P] * 5 + [_I] * 4 + [_P], _I),
+    "venturi_q5_abi": ([], _I),
+    "venturi_q5_decode": ([_P] * 4 + [_I] * 3 + [_P], _I),
+    "venturi_q5_linear": ([_P] * 5 + [_I] * 4 + [_P], _I),
     "venturi_ada_abi": ([], _I),
     "venturi_ada_error": ([], C.c_char_p),
     "venturi_q4_prepare": ([_I] * 5, _I),

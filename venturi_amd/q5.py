@@ -1,0 +1,162 @@
+"""Q5 (q5_g64_fp16) codec helpers and the W5A16 operator object.
+
+``quantize_q5_rtn`` and ``decode_q5_fp16`` mirror the reference's experimental
+W5A16 codec (models/flash_next/flash_next_q5.py:19-70): fp16 scale =
+fp16(max|w|/15) floored at 2^-24 and rounded before the codes, codes =
+round_half_even(w / scale) in [-16, 15] (a +16 produced by the scale rounding
+saturates to +15), and the W5A16 weight value fp16(q * scale). ``NativeQ5``
+mirrors ops/flash_next_q5.py over this library's Q5 ABI 1 with gfx950
+qualification instead of SM70.
+"""
+
+from dataclasses import dataclass
+from pathlib import Path
+
+import torch
+from torch.nn import functional as F
+
+from .weights import Q5RowSplitWeight
+
+CODEC = "rtn_symmetric15_g64_fp16_row_split_k128_v1"
+
+
+def quantize_q5_rtn(weight, *, max_elements=16 * 2**20):
+    """CPU round-to-nearest-even Q5 with the fp16 scale rounded before the codes."""
+    if (
+        not isinstance(weight, torch.Tensor)
+        or weight.device.type != "cpu"
+        or weight.ndim != 2
+        or weight.dtype not in (torch.float16, torch.bfloat16, torch.float32)
+        or min(weight.shape) < 1
+    ):
+        raise ValueError("Explicit nonempty CPU floating weight required")
+    if type(max_elements) is not int or max_elements <= 0 or weight.numel() > max_elements:
+        raise ValueError("Q5 quantization exceeds explicit element budget")
+    value = weight.float()
+    if not torch.isfinite(value).all():
+        raise ValueError("Finite source weights required")
+    rows, cols = weight.shape
+    padded = (cols + 127) // 128 * 128
+    blocks = F.pad(value, (0, padded - cols)).reshape(rows, padded // 64, 64)
+    scales = (blocks.abs().amax(-1) / 15).clamp_min(2**-24).half()
+    if not torch.isfinite(scales).all():
+        raise ValueError("Source scale overflows FP16")
+    codes = (blocks / scales.float().unsqueeze(-1)).round().clamp(-16, 16).to(torch.int8)
+    # A +16 appears only where rounding the scale moved the group boundary.
+    codes = torch.where(codes == 16, torch.full_like(codes, 15), codes)
+    if not torch.isfinite((codes.float() * scales.float().unsqueeze(-1)).half()).all():
+        raise ValueError("Quantized weight overflows FP16 execution")
+    return Q5RowSplitWeight.from_codes(codes.reshape(rows, padded)[:, :cols], scales[:, : (cols + 63) // 64])
+
+
+def decode_q5_fp16(weight):
+    """fp16 matrix of fp16(q * scale) values (diagnostic; no retained cache)."""
+    weight.validate()
+    low = torch.stack((weight.codes & 15, weight.codes >> 4), -1).reshape(weight.out_features, weight.padded_k)
+    bits = (weight.high.to(torch.int16).unsqueeze(-1) >> torch.arange(8, dtype=torch.int16)) & 1
+    unsigned = low.to(torch.int16) | (bits.reshape(weight.out_features, weight.padded_k) << 4)
+    signed = torch.where(unsigned < 16, unsigned, unsigned - 32)
+    values = signed.float().reshape(weight.out_features, -1, 64) * weight.scales.float().unsqueeze(-1)
+    return values.reshape(weight.out_features, -1)[:, : weight.in_features].half()
+
+
+@dataclass(frozen=True)
+class PreparedQ5:
+    weight: Q5RowSplitWeight
+    ready: object
+
+
+class NativeQ5:
+    """W5A16 operators of Q5 ABI 1 (reference ops/flash_next_q5.py:17-89).
+
+    ``linear`` is the reference GEMV order (fp16(q*scale) weights,
+    lane-strided fmaf, 32-lane tree) for 1..64 fp16 tokens; ``decode`` writes
+    the fp16 matrix.
+    """
+
+    def __init__(self, library=None, *, max_output_bytes=64 * 2**20):
+        from . import native
+
+        if type(max_output_bytes) is not int or max_output_bytes <= 0:
+            raise ValueError("Positive explicit output budget required")
+        self.max_output_bytes = max_output_bytes
+        self.lib = native.load(library)
+        self.library = Path(self.lib.path)
+        if self.lib.venturi_q5_abi() != 1:
+            raise ValueError("Unsupported Q5 operator ABI")
+
+    def prepare(self, weight, *, device):
+        from .blocks import is_gfx950
+
+        if not isinstance(weight, Q5RowSplitWeight) or weight.codes.device.type != "cpu":
+            raise ValueError("Explicit CPU Q5 descriptor required for preparation")
+        weight.validate()
+        if (
+            not torch.isfinite(weight.scales).all()
+            or (weight.scales < 0).any()
+            or weight.out_features * weight.in_features * 2 > self.max_output_bytes
+        ):
+            raise ValueError("Finite nonnegative Q5 scales and bounded matrix required")
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise ValueError("Explicit GPU device required")
+        with torch.cuda.device(device):
+            if not is_gfx950(device):
+                raise ValueError("This operator is qualified only for gfx950")
+            result = Q5RowSplitWeight(
+                weight.codes.to(device), weight.high.to(device), weight.scales.to(device), weight.in_features
+            )
+            ready = torch.cuda.Event()
+            ready.record(torch.cuda.current_stream(device))
+        return PreparedQ5(result, ready)
+
+    def _lease(self, prepared):
+        if not isinstance(prepared, PreparedQ5) or prepared.weight.codes.device.type != "cuda":
+            raise ValueError("Explicit prepared GPU Q5 weight required")
+        w = prepared.weight
+        w.validate()
+        stream = torch.cuda.current_stream(w.codes.device)
+        stream.wait_event(prepared.ready)
+        for plane in (w.codes, w.high, w.scales):
+            plane.record_stream(stream)
+        return w, stream
+
+    def decode(self, prepared):
+        with torch.cuda.device(prepared.weight.codes.device):
+            w, stream = self._lease(prepared)
+            if w.out_features * w.in_features * 2 > self.max_output_bytes:
+                raise ValueError("Q5 decode exceeds output budget")
+            out = torch.empty((w.out_features, w.in_features), device=w.codes.device, dtype=torch.float16)
+            status = self.lib.venturi_q5_decode(
+                w.codes.data_ptr(), w.high.data_ptr(), w.scales.data_ptr(), out.data_ptr(), w.out_features,
+                w.in_features, w.padded_k, stream.cuda_stream,
+            )
+            if status:
+                raise RuntimeError(f"Q5 decode HIP launch failed: {status}")
+            return out
+
+    def linear(self, x, prepared):
+        if not isinstance(prepared, PreparedQ5):
+            raise ValueError("Explicit prepared GPU Q5 weight required")
+        w = prepared.weight
+        if (
+            x.ndim != 2
+            or not 1 <= len(x) <= 64
+            or x.shape[1] != w.in_features
+            or x.dtype != torch.float16
+            or x.device != w.codes.device
+            or not x.is_contiguous()
+        ):
+            raise ValueError("Bounded contiguous FP16 GPU input required")
+        if len(x) * w.out_features * 2 > self.max_output_bytes:
+            raise ValueError("Q5 linear exceeds output budget")
+        with torch.cuda.device(x.device):
+            w, stream = self._lease(prepared)
+            out = torch.empty((len(x), w.out_features), device=x.device, dtype=x.dtype)
+            status = self.lib.venturi_q5_linear(
+                x.data_ptr(), w.codes.data_ptr(), w.high.data_ptr(), w.scales.data_ptr(), out.data_ptr(), len(x),
+                w.out_features, w.in_features, w.padded_k, stream.cuda_stream,
+            )
+            if status:
+                raise RuntimeError(f"Q5 GEMV HIP launch failed: {status}")
+            return out

@@ -167,6 +167,139 @@ class Q4RowSplitWeight:
 
 
 @dataclass(frozen=True)
+class Q5RowSplitWeight:
+    """Signed 5-bit codes, group-64 fp16 scales, K padded to 128 (weights.py:175-336).
+
+    codes is uint8 [N, padded_K/2] with the low four bits of weight 2j in the
+    low nibble of byte j; high is uint8 [N, padded_K/8] with the fifth bit of
+    column c at bit c % 8 of byte c / 8 (inside each K64 group lane L reads
+    byte L//8, bit L%8); scales is float16 [N, padded_K/64]. Values are
+    q * scale with q in [-16, 15], no zero point.
+    """
+
+    codes: torch.Tensor
+    high: torch.Tensor
+    scales: torch.Tensor
+    in_features: int
+
+    format = "q5_g64_fp16"
+    layout = "row_split_k128_v1"
+    group_size = 64
+
+    def __post_init__(self):
+        self.validate()
+
+    @property
+    def out_features(self) -> int:
+        return self.codes.shape[0]
+
+    @property
+    def padded_k(self) -> int:
+        return _padded(self.in_features)
+
+    @property
+    def nbytes(self) -> int:
+        return self.codes.numel() + self.high.numel() + 2 * self.scales.numel()
+
+    def validate(self) -> None:
+        if type(self.in_features) is not int or not 0 < self.in_features < 2**31:
+            raise ValueError("in_features must be a positive int32")
+        if self.padded_k >= 2**31:
+            raise ValueError("padded K must fit int32")
+        if self.codes.ndim != 2 or not 0 < self.codes.shape[0] < 2**31:
+            raise ValueError("codes must be a nonempty [N, padded_K/2] matrix")
+        if self.codes.dtype != torch.uint8 or self.high.dtype != torch.uint8 or self.scales.dtype != torch.float16:
+            raise ValueError("Q5 requires uint8 codes/high and float16 scales")
+        if self.codes.shape[1] != self.padded_k // 2:
+            raise ValueError("codes width must match K padded to 128")
+        if self.high.shape != (self.out_features, self.padded_k // 8):
+            raise ValueError("high plane shape must be [N, padded_K/8]")
+        if self.scales.shape != (self.out_features, self.padded_k // 64):
+            raise ValueError("scales shape must be [N, padded_K/64]")
+        if not (self.codes.is_contiguous() and self.high.is_contiguous() and self.scales.is_contiguous()):
+            raise ValueError("Q5 planes must be contiguous")
+        if not (self.codes.device == self.high.device == self.scales.device):
+            raise ValueError("Q5 planes must share one device")
+        if self.codes.device.type not in ("cpu", "cuda"):
+            raise ValueError("Q5 planes require CPU or CUDA storage")
+        if self.scales.data_ptr() % 2:
+            raise ValueError("FP16 scales must be aligned")
+
+    @classmethod
+    def from_codes(cls, codes: torch.Tensor, scales: torch.Tensor):
+        """Packs CPU integer codes in [-16, 15] exactly; no float quantization."""
+        if codes.device.type != "cpu" or scales.device.type != "cpu":
+            raise ValueError("from_codes is an explicit CPU preparation operation")
+        if codes.dtype not in (torch.int8, torch.int16, torch.int32, torch.int64):
+            raise ValueError("codes must contain signed integers")
+        if codes.ndim != 2 or min(codes.shape) <= 0:
+            raise ValueError("codes must be a nonempty [N, K] matrix")
+        n, k = codes.shape
+        if scales.dtype != torch.float16 or scales.shape != (n, (k + 63) // 64):
+            raise ValueError("scales must be float16 [N, ceil(K/64)]")
+        if bool(((codes < -16) | (codes > 15)).any()):
+            raise ValueError("Q5 codes must be in [-16, 15]")
+        if not bool(torch.isfinite(scales).all()):
+            raise ValueError("scales must be finite")
+        padded = _padded(k)
+        unsigned = torch.zeros((n, padded), dtype=torch.int16)
+        unsigned[:, :k] = codes.to(torch.int16) & 31
+        low = (unsigned & 15).to(torch.uint8)
+        packed = low[:, 0::2] | (low[:, 1::2] << 4)
+        fifth = (unsigned >> 4).view(n, padded // 8, 8)
+        high = (fifth << torch.arange(8, dtype=torch.int16)).sum(-1).to(torch.uint8)
+        plane = torch.zeros((n, padded // 64), dtype=torch.float16)
+        plane[:, : scales.shape[1]] = scales
+        return cls(packed.contiguous(), high.contiguous(), plane, k)
+
+    @classmethod
+    def from_dense(cls, source, *, rows_per_chunk=256):
+        """Nearest-even RTN with the stored fp16 scale fp16(max|group|/15), codes in
+        [-16, 15], over K64 groups, chunked by rows; the source is not modified."""
+        dense = DenseWeight(source)
+        if source.device.type != "cpu":
+            raise ValueError("Q5 quantization requires an explicit CPU source")
+        if type(rows_per_chunk) is not int or not 0 < rows_per_chunk < 2**31:
+            raise ValueError("rows_per_chunk must be a positive int32")
+        n, k = dense.out_features, dense.in_features
+        padded = _padded(k)
+        if padded >= 2**31:
+            raise ValueError("Padded Q5 K must fit int32")
+        codes = torch.zeros(n, padded, dtype=torch.int16)
+        scales = torch.zeros(n, padded // 64, dtype=torch.float16)
+        work = torch.float64 if source.dtype == torch.float64 else torch.float32
+        with torch.no_grad():
+            for begin in range(0, n, rows_per_chunk):
+                end = min(n, begin + rows_per_chunk)
+                values = torch.zeros(end - begin, padded, dtype=work)
+                values[:, :k].copy_(source[begin:end].detach())
+                if not bool(torch.isfinite(values).all()):
+                    raise ValueError("Q5 source must be finite")
+                groups = values.view(end - begin, -1, 64)
+                stored = (groups.abs().amax(-1) / 15).to(torch.float16)
+                if not bool(torch.isfinite(stored).all()):
+                    raise ValueError("Q5 group scale overflows FP16")
+                divisor = stored.to(work).unsqueeze(-1)
+                safe = torch.where(divisor > 0, divisor, torch.ones_like(divisor))
+                quantized = torch.where(divisor > 0, (groups / safe).round().clamp(-16, 15), 0)
+                codes[begin:end].copy_(quantized.reshape(end - begin, padded))
+                scales[begin:end].copy_(stored)
+        return cls.from_codes(codes[:, :k], scales[:, : (k + 63) // 64])
+
+    def dequantize_reference(self) -> torch.Tensor:
+        """CPU FP64 values q * scale (diagnostic; never used by device execution)."""
+        self.validate()
+        if self.codes.device.type != "cpu":
+            raise ValueError("reference decoding requires explicit CPU weights")
+        low = torch.stack((self.codes & 15, self.codes >> 4), dim=-1).reshape(self.out_features, self.padded_k)
+        bits = (self.high.to(torch.int16).unsqueeze(-1) >> torch.arange(8, dtype=torch.int16)) & 1
+        unsigned = low.to(torch.int16) | (bits.reshape(self.out_features, self.padded_k) << 4)
+        signed = torch.where(unsigned < 16, unsigned, unsigned - 32)
+        dense = signed.to(torch.float64) * self.scales.to(torch.float64).repeat_interleave(64, 1)
+        return dense[:, : self.in_features]
+
+
+@dataclass(frozen=True)
 class Q8RowSplitWeight:
     """Signed Q8 codes in [-127, 127] with group-32 fp16 scales, K padded to 128."""
 
