@@ -223,7 +223,9 @@ uint64_t venturi_moe_q4_bytes(int tokens, int top_k, int experts, int hidden, in
 /* Extension: routed-expert Q4 W4A16 MoE, replacing the per-expert host loop of
  * flash_next_moe.py:139-161 / flash_next_q4.py:204-224. x fp16 [tokens][hidden];
  * ids int64 [tokens][top_k]; scores fp16 [tokens][top_k]; gate_up planes stacked
- * [experts][2*inter][...] (gate rows first), down planes [experts][hidden][...];
+ * [experts][2*inter][...] (gate rows first), down planes [experts][hidden][...],
+ * both in the tiled layout built by moe.Q4ExpertBank.upload (128-row x
+ * 256-column tiles, gate/up rows paired per wave, nibbles stored as q + 8);
  * out fp16 [tokens][hidden]; workspace 256-byte aligned. Ids outside
  * [0, experts) are skipped and counted in the workspace status word. */
 int venturi_moe_q4_run(const void* x, const int64_t* ids, const void* scores, const void* gate_up_codes,

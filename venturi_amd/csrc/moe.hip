@@ -79,6 +79,43 @@ __device__ __forceinline__ half8 dequant8(std::uint32_t word, half2v s2) {
     return w;
 }
 
+// The same eight weights from a pre-biased word (nibble = q + 8, stored so by
+// the tiled bank): a mask-and-or per pair of nibbles 16 bits apart places u
+// (low nibble) or 16u (high nibble) in the mantissa of 1024 (0x6400); q is
+// then one exact fp16 add (low: h - 1032) or fma (high: h/16 - 72), and q * s
+// the contract's single rounding. Columns come out as c, c+4, c+1, c+5, c+2,
+// c+6, c+3, c+7 (activations staged by interleave_biased to match).
+__device__ __forceinline__ half8 dequant8_biased(std::uint32_t u, half2v s2) {
+    const std::uint32_t v = u >> 8;
+    const half2v lo_bias = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const half2v sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+    const half2v hi_bias = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+    const half2v a = __builtin_bit_cast(half2v, (u & 0x000F000Fu) | 0x64006400u);  // c, c+4
+    const half2v b = __builtin_bit_cast(half2v, (u & 0x00F000F0u) | 0x64006400u);  // c+1, c+5 (times 16)
+    const half2v c = __builtin_bit_cast(half2v, (v & 0x000F000Fu) | 0x64006400u);  // c+2, c+6
+    const half2v d = __builtin_bit_cast(half2v, (v & 0x00F000F0u) | 0x64006400u);  // c+3, c+7 (times 16)
+    const half2v q[4] = {a + lo_bias, b * sixteenth + hi_bias, c + lo_bias, d * sixteenth + hi_bias};  // exact
+    half8 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v x = q[i] * s2;  // one fp16 rounding of q * s
+        w[2 * i] = x[0];
+        w[2 * i + 1] = x[1];
+    }
+    return w;
+}
+
+// Eight consecutive activations x0..x7 -> x0, x4, x1, x5, x2, x6, x3, x7
+// (the column order of dequant8_biased).
+__device__ __forceinline__ uint4 interleave_biased(uint4 v) {
+    uint4 r;
+    r.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+    r.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+    r.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+    r.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+    return r;
+}
+
 // Eight consecutive activations x0..x7 -> x0, x2, x4, x6, x1, x3, x5, x7.
 __device__ __forceinline__ uint4 interleave8(uint4 v) {
     uint4 r;
@@ -280,7 +317,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 // columns [64q, 64q + 64) (group q) as two 1 KB contiguous wave loads. Scales:
 // [row tile][chunk][w][l] fp16, one 128-byte wave load. For gate/up, row block
 // w holds gate rows 8w..8w+7 of the tile's 64 (m < 8) and the matching up rows
-// (m >= 8). Padding rows and columns hold zero codes and scales.
+// (m >= 8). Codes are stored pre-biased: every nibble holds q + 8 (the
+// dequant then needs no sign fix). Padding rows and columns hold q = 0 and
+// zero scales.
 struct Q4Tiled {
     const __half* x;            // activation rows (x_stride halves apart)
     const int* gather;          // slot -> x row (null: slot itself)
@@ -295,163 +334,6 @@ struct Q4Tiled {
 };
 
 constexpr int kTileCodes = 8 * 128;  // uint4 per (tile, chunk): 8 row blocks x 2 KB
-
-template <int EPI>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void q4_tiled(Q4Tiled p) {
-    __shared__ __attribute__((aligned(16))) _Float16 xl[2][kPassTokens * kXStride];
-
-    const int linear = blockIdx.x;
-    int expert, tile;
-    if (p.experts % 8 == 0) {  // an expert's tiles share one XCD (round-robin dispatch) and its L2
-        const int xcd = linear % 8, idx = linear / 8;
-        expert = 8 * (idx / p.row_tiles) + xcd;
-        tile = idx % p.row_tiles;
-    } else {
-        expert = linear / p.row_tiles;
-        tile = linear % p.row_tiles;
-    }
-    const int seg_begin = p.seg[expert];
-    const int seg_end = p.seg[expert + 1];
-    if (seg_begin >= seg_end) return;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int q = lane >> 4, m = lane & 15;
-    const uint4* wsrc = p.codes + expert * p.code_stride + (static_cast<std::int64_t>(tile) * p.chunks * 8 + wave) * 128 + lane;
-    const __half* ssrc = p.scales + expert * p.scale_stride + (static_cast<std::int64_t>(tile) * p.chunks * 8 + wave) * 64 + lane;
-
-    for (int pass = seg_begin; pass < seg_end; pass += kPassTokens) {
-        const int live = min(kPassTokens, seg_end - pass);
-        auto run_pass = [&](auto nb_tag) {
-            constexpr int NB = decltype(nb_tag)::value;
-            const __half* xrow[NB];
-            bool xlive[NB];
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const int t = (tid + 512 * j) >> 5;
-                xlive[j] = t < live;
-                const int slot = pass + min(t, live - 1);
-                const int row = p.gather ? p.gather[slot] : slot;
-                xrow[j] = p.x + static_cast<std::int64_t>(row) * p.x_stride;
-            }
-            // Weight stages live in registers; activation stages in LDS. Loads are
-            // unconditional (clamped addresses); zeros replace data past k when
-            // the activations are written to LDS.
-            struct WStage {
-                uint4 a, b;
-                unsigned short s;
-            };
-            struct XStage {
-                uint4 v[NB];
-            };
-            auto load_w = [&](int c, WStage& w) {
-                const uint4* src = wsrc + static_cast<std::int64_t>(c) * kTileCodes;
-                w.a = src[0];
-                w.b = src[64];
-                w.s = __half_as_ushort(ssrc[static_cast<std::int64_t>(c) * 512]);
-            };
-            auto load_x = [&](int c, XStage& x) {
-                const int col = c * kChunk + 8 * (tid & 31);
-#pragma unroll
-                for (int j = 0; j < NB; ++j) x.v[j] = *reinterpret_cast<const uint4*>(xrow[j] + min(col, p.k - 8));
-            };
-            auto store_x = [&](int c, const XStage& x, _Float16* buf) {
-                const int col = c * kChunk + 8 * (tid & 31);
-#pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    const int piece = tid + 512 * j;
-                    // Masking by AND keeps the body free of branches (exact wait counts).
-                    const std::uint32_t keep = (xlive[j] && col < p.k) ? 0xFFFFFFFFu : 0u;
-                    uint4 v = interleave8(x.v[j]);
-                    v.x &= keep;
-                    v.y &= keep;
-                    v.z &= keep;
-                    v.w &= keep;
-                    *reinterpret_cast<uint4*>(buf + (piece >> 5) * kXStride + 8 * (piece & 31)) = v;
-                }
-            };
-
-            float4v acc[NB];
-#pragma unroll
-            for (int b = 0; b < NB; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-
-            auto compute = [&](const WStage& w, const _Float16* buf) {
-                const half2v s2 = __builtin_bit_cast(half2v, static_cast<std::uint32_t>(w.s) * 0x10001u);
-                const std::uint32_t words[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
-#pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    const half8 wf = dequant8(words[s], s2);
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) {
-                        const half8 xf = *reinterpret_cast<const half8*>(buf + (16 * b + m) * kXStride + 64 * q + 8 * s);
-                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf, wf, acc[b], 0, 0, 0);
-                    }
-                }
-            };
-
-            // Chunk c computes from weight stage c % 2 and LDS buffer c % 2 while
-            // the weights of c + 1 (and, once c's registers are consumed, c + 2)
-            // and the activations of c + 1 are in flight. The loop body has no
-            // branches: loads past the last chunk re-read it (clamped index) and
-            // the surplus activation stage is stored as zeros.
-            WStage w0, w1;
-            XStage xs;
-            load_w(0, w0);
-            load_w(min(1, p.chunks - 1), w1);
-            load_x(0, xs);
-            store_x(0, xs, xl[0]);
-            __syncthreads();
-            auto step = [&](int c, WStage& w) {
-                load_x(min(c + 1, p.chunks - 1), xs);
-                compute(w, xl[c & 1]);
-                load_w(min(c + 2, p.chunks - 1), w);
-                store_x(c + 1, xs, xl[(c + 1) & 1]);
-                __syncthreads();
-            };
-            int c = 0;
-            for (; c + 1 < p.chunks; c += 2) {
-                step(c, w0);
-                step(c + 1, w1);
-            }
-            if (c < p.chunks) step(c, w0);
-
-            // D layout: lane holds row slot m of the wave's block for tokens 16b + 4q + i.
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = 16 * b + 4 * q + i;
-                    const float v = acc[b][i];
-                    if (EPI == kSwiGLU) {
-                        const float other = __shfl_xor(v, 8, 64);  // lane m^8 holds the paired up/gate row
-                        const int col = tile * (kRows / 2) + 8 * wave + (m & 7);
-                        if (m < 8 && t < live && col < p.half_rows) {
-                            const float g = __half2float(from_f32<__half>(v));
-                            const float u = __half2float(from_f32<__half>(other));
-                            const float a = __half2float(from_f32<__half>(silu(g)));
-                            p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + col] =
-                                from_f32<__half>(__fmul_rn(a, u));
-                        }
-                    } else {
-                        const int row = tile * kRows + 16 * wave + m;
-                        if (t < live && row < p.n) {
-                            float y = __half2float(from_f32<__half>(v));
-                            if (EPI == kScore) y = __fmul_rn(y, __half2float(p.score[pass + t]));
-                            p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + row] = from_f32<__half>(y);
-                        }
-                    }
-                }
-            }
-        };
-        switch ((live + 15) >> 4) {
-            case 1: run_pass(std::integral_constant<int, 1>{}); break;
-            case 2: run_pass(std::integral_constant<int, 2>{}); break;
-            case 3: run_pass(std::integral_constant<int, 3>{}); break;
-            default: run_pass(std::integral_constant<int, 4>{}); break;
-        }
-    }
-}
 
 // Grouped expert GEMM over the tiled planes with a fraction of an expert per
 // workgroup: W = 8 waves, wave v owns RB consecutive 16-row blocks (global
@@ -543,7 +425,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
                 for (int j = 0; j < XL; ++j) {
                     const int piece = tid + T * j;
                     const std::uint32_t keep = (xlive[j] && col < p.k) ? 0xFFFFFFFFu : 0u;
-                    uint4 v = interleave8(x.v[j]);
+                    uint4 v = interleave_biased(x.v[j]);
                     v.x &= keep;
                     v.y &= keep;
                     v.z &= keep;
@@ -572,7 +454,8 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
 #pragma unroll
                     for (int r = 0; r < RB; ++r) {
                         const std::uint32_t word = s == 0 ? st.w[r].x : s == 1 ? st.w[r].y : s == 2 ? st.w[r].z : st.w[r].w;
-                        const half8 wf = dequant8(word, __builtin_bit_cast(half2v, static_cast<std::uint32_t>(scale[r]) * 0x10001u));
+                        const half2v s2 = __builtin_bit_cast(half2v, static_cast<std::uint32_t>(scale[r]) * 0x10001u);
+                        const half8 wf = dequant8_biased(word, s2);
 #pragma unroll
                         for (int b = 0; b < NB; ++b)
                             acc[r][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[b], wf, acc[r][b], 0, 0, 0);
@@ -821,12 +704,6 @@ void launch_q4_grouped(const Q4Tiled& p, hipStream_t stream) {
     q4_grouped<EPI, W, RB, NBMAX><<<dim3(p.experts * parts), W * 64, 0, stream>>>(p, parts, blocks);
 }
 
-template <int EPI>
-void launch_q4_tiled(const Q4Tiled& p, hipStream_t stream) {
-    const dim3 grid(p.experts * p.row_tiles);
-    q4_tiled<EPI><<<grid, kWaves * 64, 0, stream>>>(p);
-}
-
 std::uint64_t align256(std::uint64_t v) { return (v + 255) / 256 * 256; }
 
 }  // namespace
@@ -887,7 +764,7 @@ void q4_gemm_launch(const void* x, const void* codes, const void* scales, void* 
 }
 
 // GW/GRB and DW/DRB: waves per workgroup and row blocks per wave of the
-// gate/up and down GEMMs (0 waves: one 128-row tile per workgroup, q4_tiled).
+// gate/up and down GEMMs.
 template <int GW, int GRB, int DW, int DRB, int NBMAX>
 void moe_q4_launch_cfg(const void* x, const std::int64_t* ids, const void* scores, const void* gu_codes,
                        const void* gu_scales, const void* dn_codes, const void* dn_scales, void* out, void* workspace,
@@ -936,8 +813,7 @@ void moe_q4_launch_cfg(const void* x, const std::int64_t* ids, const void* score
     gu.out_stride = inter;
     gu.experts = experts;
     gu.half_rows = inter;
-    if constexpr (GW == 0) launch_q4_tiled<kSwiGLU>(gu, stream);
-    else launch_q4_grouped<kSwiGLU, GW, GRB, NBMAX>(gu, stream);
+    launch_q4_grouped<kSwiGLU, GW, GRB, NBMAX>(gu, stream);
 
     Q4Tiled dn{};
     dn.x = h;
@@ -955,8 +831,7 @@ void moe_q4_launch_cfg(const void* x, const std::int64_t* ids, const void* score
     dn.x_stride = inter;
     dn.out_stride = hidden;
     dn.experts = experts;
-    if constexpr (DW == 0) launch_q4_tiled<kScore>(dn, stream);
-    else launch_q4_grouped<kScore, DW, DRB, NBMAX>(dn, stream);
+    launch_q4_grouped<kScore, DW, DRB, NBMAX>(dn, stream);
 
     combine_dispatch(top_k, ids, pair_slot, v, static_cast<__half*>(out), tokens, hidden, stream);
 }

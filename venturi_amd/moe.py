@@ -67,8 +67,9 @@ def _tile(weights, rows, cols, swiglu, device):
 
     Codes: [E][row tile][chunk][wave w][half h][lane l = 16q + m][16 bytes], the
     16-byte piece h of the 32 code bytes of slot row (w, m) for chunk columns
-    [64q, 64q + 64). Scales: [E][row tile][chunk][w][l] fp16 of group q of the
-    chunk. Chunks are 256 columns of the padded K; padding is zero.
+    [64q, 64q + 64), every nibble stored as q + 8. Scales: [E][row tile][chunk][w][l]
+    fp16 of group q of the chunk. Chunks are 256 columns of the padded K; padding
+    holds q = 0 and zero scales.
     """
     padded = (cols + 127) // 128 * 128
     chunks = (padded + 255) // 256
@@ -87,6 +88,7 @@ def _tile(weights, rows, cols, swiglu, device):
             raise ValueError("scales must be finite")
         codes[e, :, : padded // 2] = w.codes.to(device)[source] * valid[:, None].to(torch.uint8)
         scales[e, :, : padded // 64] = w.scales.to(device)[source] * valid[:, None].to(torch.float16)
+    codes ^= 0x88  # pre-biased nibbles: q + 8 (padding becomes q = 0)
     codes = codes.view(e_count, tiles, 8, 16, chunks, 4, 2, 16).permute(0, 1, 4, 2, 6, 5, 3, 7).contiguous()
     scales = scales.view(e_count, tiles, 8, 16, chunks, 4).permute(0, 1, 4, 2, 5, 3).contiguous()
     return codes, scales
