@@ -217,6 +217,14 @@ int venturi_q4_run(const void* x, const void* codes, const void* scales, void* o
 int venturi_q4_gemm_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
                         int padded, int dtype, void* stream);
 
+/* Extension: the same contract GEMM for 4-, 5- and 6-bit row codecs (bits
+ * 4/5/6; `high` = the q5/q6 high plane [n][padded*(bits-4)/8], 16-byte
+ * aligned, unused for 4 bits). Stands where the reference dequantizes q4/q5/q6
+ * rows to an fp16 shadow chunk and calls a dense GEMM
+ * (row_codec_dispatch.cuh:41-46, weight_dequant.cuh:1-9). */
+int venturi_row_gemm_run(const void* x, const void* codes, const void* high, const void* scales, void* out, int tokens,
+                         int n, int k, int padded, int bits, int dtype, void* stream);
+
 /* Extension: workspace bytes of venturi_moe_q4_run (0 on invalid geometry). */
 uint64_t venturi_moe_q4_bytes(int tokens, int top_k, int experts, int hidden, int inter);
 

@@ -128,3 +128,65 @@ def test_row_decode_rejects_bad_arguments(backend, device):
     assert lib.venturi_row_dequant_indexed(x.data_ptr(), x.data_ptr(), x.data_ptr(), None, o.data_ptr(), 1, 128, 128,
                                            5, s) == -1
     torch.cuda.synchronize(device)
+
+
+def _ulp16(v):
+    v = np.abs(v)
+    return 2.0 ** (np.floor(np.log2(np.maximum(v, 2.0**-14))) - 10)
+
+
+@pytest.mark.parametrize("nbits", [4, 5, 6])
+@pytest.mark.parametrize("shape", [(1, 8), (37, 136), (130, 768), (300, 2048)])
+@pytest.mark.parametrize("tokens", [1, 16, 33, 130])
+def test_row_gemm_contract_tolerances(backend, device, nbits, shape, tokens):
+    # The W*A16 contract: weights fp16(q * scale) (the oracle's row decode),
+    # fp32 accumulation; |y - exact| <= 0.5 ulp_fp16 + 2^-19 sum|x w| against
+    # FP64, and against the reference-order Q5 GEMV within 2e-3 / one ulp,
+    # rel-L2 1e-3.
+    n, k = shape
+    print(f"case row-gemm bits={nbits} n={n} k={k} tokens={tokens}", flush=True)
+    packed, high, scales = _planes(n, k, nbits, 77 * nbits + n + tokens)
+    padded = packed.shape[1] * 2
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens + k)).half()
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    dc = torch.from_numpy(packed).to(device)
+    dh = torch.from_numpy(high if nbits > 4 else np.zeros((1, 16), np.uint8)).to(device)
+    ds = torch.from_numpy(scales).to(device)
+    guard = torch.full((tokens * n + 2,), 47, dtype=torch.float16, device=device)
+    out = guard[1:-1].view(tokens, n)
+    backend._check(lib.venturi_row_gemm_run(x.to(device).data_ptr(), dc.data_ptr(), dh.data_ptr(), ds.data_ptr(),
+                                            out.data_ptr(), tokens, n, k, padded, nbits, 0, s))
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    wd = oracle.row_decode(packed, high, scales, k, nbits).view(np.float16).astype(np.float64)
+    xd = x.float().numpy().astype(np.float64)
+    exact = xd @ wd.T
+    got = out.cpu().float().numpy().astype(np.float64)
+    bound = 0.5 * _ulp16(exact) + 2.0**-19 * (np.abs(xd) @ np.abs(wd).T)
+    assert (np.abs(got - exact) <= bound).all()
+    if nbits == 5 and tokens <= 64:
+        ref = oracle.q5_linear(bits(x), packed, high, scales, k).view(np.float16).astype(np.float64)
+        diff = np.abs(got - ref)
+        assert (diff <= np.maximum(2e-3, _ulp16(ref))).all()
+        assert np.linalg.norm(got - ref) <= 1e-3 * max(np.linalg.norm(ref), 1e-12)
+    if nbits == 4:
+        same = torch.empty_like(out)
+        backend._check(lib.venturi_q4_gemm_run(x.to(device).data_ptr(), dc.data_ptr(), ds.data_ptr(), same.data_ptr(),
+                                               tokens, n, k, padded, 0, s))
+        assert torch.equal(same.view(torch.int16), out.view(torch.int16))
+
+
+def test_row_gemm_rejects_bad_arguments(backend, device):
+    lib = backend._native
+    x = torch.zeros(1, 64, dtype=torch.float16, device=device)
+    c = torch.zeros(1, 64, dtype=torch.uint8, device=device)
+    o = torch.empty(1, 1, dtype=torch.float16, device=device)
+    s = torch.cuda.current_stream(device).cuda_stream
+    assert lib.venturi_row_gemm_run(x.data_ptr(), c.data_ptr(), None, c.data_ptr(), o.data_ptr(), 1, 1, 64, 128, 5, 0,
+                                    s) == -1
+    assert "null" in lib.error()
+    assert lib.venturi_row_gemm_run(x.data_ptr(), c.data_ptr(), c.data_ptr(), c.data_ptr(), o.data_ptr(), 1, 1, 64, 128,
+                                    7, 0, s) == -1
+    assert "4, 5 or 6" in lib.error()
+    torch.cuda.synchronize(device)

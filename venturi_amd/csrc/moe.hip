@@ -52,8 +52,11 @@ struct Q4Gemm {
     const int* seg;            // [experts+1] slot offsets (null: one segment [0, tokens))
     const __half* score;       // per-slot fp16 factor (kScore)
     __half* out;               // out[slot][out_stride]
+    const std::uint8_t* high;  // Q5/Q6 high plane [n][padded*hb/8] (hb = bits - 4 > 0)
     int tokens, n, k, padded, x_stride, out_stride, experts, row_tiles, half_rows;
 };
+
+constexpr int kHStride = 80;  // LDS bytes per row of a chunk's high-plane slice (up to 64 + 16 pad)
 
 // Eight signed nibbles (one code word: columns c..c+7, even columns in the
 // low nibbles) -> eight fp16 weights fp16(q * s), in the K order
@@ -116,6 +119,43 @@ __device__ __forceinline__ uint4 interleave_biased(uint4 v) {
     return r;
 }
 
+// Eight (4 + HB)-bit codes of a Q5 (HB = 1) / Q6 (HB = 2) row: the low
+// nibbles as in dequant8 and `h` holding the 8 * HB upper bits of the eight
+// columns (column c + j's at bit HB * j, the high plane's LSB-first stream).
+// The upper bits are placed above each nibble, the sign bit of the
+// (4 + HB)-bit code is flipped (u = q + 2^(3+HB)) and 1024 + u converts
+// exactly as for Q4; fp16(q * s) is the one rounding. Same K order as dequant8.
+template <int HB>
+__device__ __forceinline__ half8 dequant8_high(std::uint32_t word, std::uint32_t h, half2v s2) {
+    constexpr std::uint32_t mask = (1u << HB) - 1u;
+    std::uint32_t lo = word & 0x0F0F0F0Fu;         // columns c, c+2, c+4, c+6
+    std::uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;  // columns c+1, c+3, c+5, c+7
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        lo |= ((h >> (HB * 2 * j)) & mask) << (8 * j + 4);
+        hi |= ((h >> (HB * (2 * j + 1))) & mask) << (8 * j + 4);
+    }
+    constexpr std::uint32_t flip = 0x01010101u << (3 + HB);
+    lo ^= flip;
+    hi ^= flip;
+    const half2v bias = {static_cast<_Float16>(-1024.0f - (1 << (3 + HB))),
+                         static_cast<_Float16>(-1024.0f - (1 << (3 + HB)))};
+    half2v p[4];
+    p[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u));
+    p[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u));
+    p[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u));
+    p[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u));
+    half8 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v q = p[i] + bias;  // exact: q in [-2^(3+HB), 2^(3+HB))
+        const half2v v = q * s2;       // one fp16 rounding of q * s
+        w[2 * i] = v[0];
+        w[2 * i + 1] = v[1];
+    }
+    return w;
+}
+
 // Eight consecutive activations x0..x7 -> x0, x2, x4, x6, x1, x3, x5, x7.
 __device__ __forceinline__ uint4 interleave8(uint4 v) {
     uint4 r;
@@ -128,9 +168,10 @@ __device__ __forceinline__ uint4 interleave8(uint4 v) {
 
 __device__ __forceinline__ float silu(float g) { return __fdiv_rn(g, 1.0f + expf(-g)); }
 
-template <int EPI>
+template <int EPI, int HB>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void q4_mfma(Q4Gemm p) {
     __shared__ __attribute__((aligned(16))) std::uint8_t wl[kRows * kWStride];
+    __shared__ __attribute__((aligned(16))) std::uint8_t hl[HB ? kRows * kHStride : 16];
     __shared__ std::uint32_t sl[kRows][2];
     __shared__ __attribute__((aligned(16))) _Float16 xl[kPassTokens * kXStride];
 
@@ -180,6 +221,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     for (int i = 0; i < 2; ++i)
         wsrc[i] = codes + static_cast<std::int64_t>(weight_row((tid + 512 * i) >> 3)) * row_bytes + 16 * (tid & 7);
     const __half* ssrc = scales + static_cast<std::int64_t>(weight_row((tid & 255) >> 1)) * groups + 2 * (tid & 1);
+    // High-plane piece: row tid / 4, bytes 8 * HB * (tid % 4) of the chunk's 32 * HB.
+    const std::uint8_t* hsrc =
+        HB ? p.high + static_cast<std::int64_t>(weight_row(tid >> 2)) * (p.padded * HB / 8) + 8 * HB * (tid & 3)
+           : nullptr;
 
     for (int pass = seg_begin; pass < seg_end; pass += kPassTokens) {
         const int live = min(kPassTokens, seg_end - pass);
@@ -204,9 +249,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
             // destination registers early, which would force a wait per load.
             struct Stage {
                 uint4 w[2];
+                uint4 h;
                 std::uint32_t s;
                 uint4 x[NB];
-                bool wok, sok, xok[NB];
+                bool wok, hok, sok, xok[NB];
             };
             auto load = [&](int c, Stage& st) {
                 const int col0 = c * kChunk;
@@ -215,6 +261,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
                 const int wofs = second_half ? col0 / 2 : col0 / 2 - 64 * ((tid & 7) >> 2);
 #pragma unroll
                 for (int i = 0; i < 2; ++i) st.w[i] = *reinterpret_cast<const uint4*>(wsrc[i] + wofs);
+                if constexpr (HB > 0) {
+                    // Pieces 2, 3 cover chunk columns 128..255, absent past padded K.
+                    st.hok = second_half || (tid & 3) < 2;
+                    const int hofs = col0 * HB / 8 - (st.hok ? 0 : 16 * HB);
+                    if constexpr (HB == 1) {
+                        const uint2 v = *reinterpret_cast<const uint2*>(hsrc + hofs);
+                        st.h = make_uint4(v.x, v.y, 0u, 0u);
+                    } else {
+                        st.h = *reinterpret_cast<const uint4*>(hsrc + hofs);
+                    }
+                }
                 st.sok = col0 / 64 + 2 * (tid & 1) < groups;
                 st.s = *reinterpret_cast<const std::uint32_t*>(ssrc + col0 / 64 - (st.sok ? 0 : 2 * (tid & 1)));
                 const int col = col0 + 8 * (tid & 31);
@@ -232,6 +289,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
                     *reinterpret_cast<uint4*>(wl + (piece >> 3) * kWStride + 16 * (piece & 7)) = st.wok ? st.w[i] : zero;
                 }
                 if (tid < 256) sl[tid >> 1][tid & 1] = st.sok ? st.s : 0u;
+                if constexpr (HB == 1)
+                    *reinterpret_cast<uint2*>(hl + (tid >> 2) * kHStride + 8 * (tid & 3)) =
+                        st.hok ? make_uint2(st.h.x, st.h.y) : make_uint2(0u, 0u);
+                if constexpr (HB == 2)
+                    *reinterpret_cast<uint4*>(hl + (tid >> 2) * kHStride + 16 * (tid & 3)) = st.hok ? st.h : zero;
 #pragma unroll
                 for (int j = 0; j < NB; ++j) {
                     const int piece = tid + 512 * j;
@@ -259,9 +321,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
                 const std::uint32_t sbits = (q & 1) ? (spair >> 16) : (spair & 0xFFFFu);
                 const half2v s2 = __builtin_bit_cast(half2v, sbits | (sbits << 16));
                 const std::uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                // Group q's upper bits: 8 * HB bytes, HB per word of 8 columns.
+                std::uint32_t hw[4] = {0u, 0u, 0u, 0u};
+                if constexpr (HB == 1) {
+                    const uint2 v = *reinterpret_cast<const uint2*>(hl + my_slot * kHStride + 8 * q);
+                    hw[0] = v.x;
+                    hw[1] = v.y;
+                }
+                if constexpr (HB == 2) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(hl + my_slot * kHStride + 16 * q);
+                    hw[0] = v.x;
+                    hw[1] = v.y;
+                    hw[2] = v.z;
+                    hw[3] = v.w;
+                }
 #pragma unroll
                 for (int s = 0; s < 8; ++s) {
-                    const half8 wf = dequant8(words[s], s2);
+                    half8 wf;
+                    if constexpr (HB == 0) wf = dequant8(words[s], s2);
+                    else wf = dequant8_high<HB>(words[s], (hw[(HB * s) >> 2] >> (8 * ((HB * s) & 3))) & ((1u << (8 * HB)) - 1u), s2);
 #pragma unroll
                     for (int b = 0; b < NB; ++b) {
                         const half8 xf = *reinterpret_cast<const half8*>(xl + (16 * b + m) * kXStride + 64 * q + 8 * s);
@@ -691,10 +769,10 @@ void combine_dispatch(int top_k, const std::int64_t* ids, const int* pair_slot, 
     }
 }
 
-template <int EPI>
+template <int EPI, int HB>
 void launch_q4_mfma(const Q4Gemm& p, hipStream_t stream) {
     const dim3 grid(p.experts * p.row_tiles);
-    q4_mfma<EPI><<<grid, kWaves * 64, 0, stream>>>(p);
+    q4_mfma<EPI, HB><<<grid, kWaves * 64, 0, stream>>>(p);
 }
 
 template <int EPI, int W, int RB, int NBMAX>
@@ -739,17 +817,20 @@ void moe_validate(int tokens, int top_k, int experts, int hidden, int inter) {
             "MoE routed rows exceed int32 geometry");
 }
 
-void q4_gemm_launch(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
-                    int padded, int dtype, hipStream_t stream) {
-    require(x && codes && scales && out, "null Q4 operand");
-    require(tokens > 0 && n > 0 && k > 0 && padded == padded_k(k), "invalid Q4 geometry");
-    require(static_cast<std::int64_t>(tokens) * n < INT32_MAX, "Q4 output count exceeds int32");
-    require(dtype == kF16, "the Q4 matrix-core route takes FP16 activations");
-    require(k % 8 == 0 && aligned(x, 16), "the Q4 matrix-core route needs k % 8 == 0 and 16-byte aligned x");
-    require(aligned(codes, 16) && aligned(scales, 4) && aligned(out, 2), "misaligned Q4 operand");
+void row_gemm_launch(const void* x, const void* codes, const void* high, const void* scales, void* out, int tokens,
+                     int n, int k, int padded, int bits, int dtype, hipStream_t stream) {
+    require(bits == 4 || bits == 5 || bits == 6, "row codecs are 4, 5 or 6 bits");
+    require(x && codes && scales && out && (bits == 4 || high), "null Q4/Q5/Q6 operand");
+    require(tokens > 0 && n > 0 && k > 0 && padded == padded_k(k), "invalid Q4/Q5/Q6 geometry");
+    require(static_cast<std::int64_t>(tokens) * n < INT32_MAX, "Q4/Q5/Q6 output count exceeds int32");
+    require(dtype == kF16, "the W4/5/6A16 matrix-core route takes FP16 activations");
+    require(k % 8 == 0 && aligned(x, 16), "the W4/5/6A16 matrix-core route needs k % 8 == 0 and 16-byte aligned x");
+    require(aligned(codes, 16) && aligned(scales, 4) && aligned(out, 2) && (bits == 4 || aligned(high, 16)),
+            "misaligned Q4/Q5/Q6 operand");
     Q4Gemm p{};
     p.x = static_cast<const __half*>(x);
     p.codes = static_cast<const std::uint8_t*>(codes);
+    p.high = static_cast<const std::uint8_t*>(high);
     p.scales = static_cast<const __half*>(scales);
     p.out = static_cast<__half*>(out);
     p.tokens = tokens;
@@ -760,7 +841,9 @@ void q4_gemm_launch(const void* x, const void* codes, const void* scales, void* 
     p.out_stride = n;
     p.experts = 1;
     p.row_tiles = (n + kRows - 1) / kRows;
-    launch_q4_mfma<kPlain>(p, stream);
+    if (bits == 4) launch_q4_mfma<kPlain, 0>(p, stream);
+    else if (bits == 5) launch_q4_mfma<kPlain, 1>(p, stream);
+    else launch_q4_mfma<kPlain, 2>(p, stream);
 }
 
 // GW/GRB and DW/DRB: waves per workgroup and row blocks per wave of the
@@ -852,7 +935,19 @@ void moe_q4_launch(const void* x, const std::int64_t* ids, const void* scores, c
 VT_EXPORT int venturi_q4_gemm_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n,
                                   int k, int padded, int dtype, void* stream) {
     return vt::guarded([&] {
-        vt::q4_gemm_launch(x, codes, scales, out, tokens, n, k, padded, dtype, static_cast<hipStream_t>(stream));
+        vt::row_gemm_launch(x, codes, nullptr, scales, out, tokens, n, k, padded, 4, dtype,
+                            static_cast<hipStream_t>(stream));
+    });
+}
+
+// Extension: the W4A16 / W5A16 / W6A16 contract GEMM (fp16(q*scale) weights,
+// fp32 accumulation on fp16 matrix cores) for 4-, 5- and 6-bit row codecs
+// (q5/q6 read their high plane; `high` is unused for 4 bits).
+VT_EXPORT int venturi_row_gemm_run(const void* x, const void* codes, const void* high, const void* scales, void* out,
+                                   int tokens, int n, int k, int padded, int bits, int dtype, void* stream) {
+    return vt::guarded([&] {
+        vt::row_gemm_launch(x, codes, high, scales, out, tokens, n, k, padded, bits, dtype,
+                            static_cast<hipStream_t>(stream));
     });
 }
 
