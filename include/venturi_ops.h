@@ -251,6 +251,36 @@ int venturi_add_run(const void* a, const void* b, void* out, int64_t count, int 
  * (gate columns first) -> out [tokens][inter]; dtype 0 (fp16) or 1 (bf16). */
 int venturi_silu_mul_run(const void* gate_up, void* out, int tokens, int inter, int dtype, void* stream);
 
+/* ---- Native-runtime plan table and per-matrix dispatch (no exported
+ * counterpart in the reference: its runtime compiles rowcodec::prepare,
+ * row_codec_dispatch.cuh:6-64, and Model::project, qwen_runtime.cuh:348-390,
+ * into the model). ---- */
+
+/* A QuantLinear plan: codec (bits, group), precision 0 = WxA16, 1 = WxA8,
+ * 2 = WxA8 with the residual pass; dtype 0 fp16 / 1 bf16; implementation
+ * 0 = auto, 1 = dequant, 2 = fused research; path 0 = direct, 1 = chunked
+ * dense (the W*A16 contract), 2 = quantized (A8); passes = A8 passes. */
+typedef struct VRCPlan {
+    int bits, group, precision, dtype, implementation, path, passes;
+} VRCPlan;
+
+/* rowcodec::prepare for gfx950: fills `plan` or returns -1 with a message
+ * when no kernel family is admitted (q8_g32 Auto only, A8 fp16 only; q4/q5/q6
+ * fp16 WxA16 only; fused research for q4 only). */
+int venturi_rowcodec_prepare(int bits, int group, int precision, int dtype, int implementation, VRCPlan* plan);
+
+/* Workspace of venturi_rowcodec_project for `tokens` rows of K = k: the A8
+ * activation pack for quantized plans (venturi_q8_dp4a_bytes), 0 otherwise
+ * (and 0 with a message for an invalid plan). */
+uint64_t venturi_rowcodec_workspace_bytes(const VRCPlan* plan, int tokens, int k);
+
+/* One matrix of Model::project: out [tokens][n] = x [tokens][k] times the
+ * row-split planes (codes, q5/q6 `high`, scales). Quantized plans quantize x
+ * into `workspace` first unless `packed` = 1 (the caller filled it). */
+int venturi_rowcodec_project(const VRCPlan* plan, const void* x, const void* codes, const void* high,
+                             const void* scales, void* out, void* workspace, uint64_t available, int tokens, int n,
+                             int k, int padded, int packed, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

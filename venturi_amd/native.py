@@ -58,6 +58,9 @@ SIGNATURES = {
     "venturi_q4_run": ([_P] * 4 + [_I] * 6 + [_P], _I),
     "venturi_q4_gemm_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
     "venturi_row_gemm_run": ([_P] * 5 + [_I] * 6 + [_P], _I),
+    "venturi_rowcodec_prepare": ([_I] * 5 + [_P], _I),
+    "venturi_rowcodec_workspace_bytes": ([_P, _I, _I], _U64),
+    "venturi_rowcodec_project": ([_P] * 7 + [_U64] + [_I] * 5 + [_P], _I),
     "venturi_moe_q4_bytes": ([_I] * 5, _U64),
     "venturi_moe_q4_run": ([_P] * 9 + [_U64] + [_I] * 5 + [_P], _I),
     "venturi_silu_mul_run": ([_P] * 2 + [_I] * 3 + [_P], _I),
