@@ -210,6 +210,56 @@ def prefill_a8(backend, device, steps, warmup):
 FP16_PEAK_TFLOPS = 2500.0
 
 
+def prefill_a16(backend, device, steps, warmup):
+    """fp16-activation prefill GEMMs at the config-2 shapes, M = 2048 (the metric's
+    "fp16 TOPS (M >= 256)" leg): W8A16 (q8_g32, venturi_q8_prefill_run) and W4A16
+    (q4_g64, venturi_q4_gemm_run), both on their plans' auto route.
+
+    Weights N(0, 0.02) packed on the device; x fp16 N(0, 1). Each GEMM runs
+    `steps` times back to back between one pair of events; TFLOP/s =
+    2*M*N*K / average time, against the 2.5 PFLOP/s dense fp16 peak.
+    """
+    m = 2048
+    gen = torch.Generator(device=device).manual_seed(11)
+    stream = torch.cuda.current_stream(device)
+
+    def timed(fn, reps):
+        for _ in range(warmup):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        b.synchronize()
+        return a.elapsed_time(b) / 1e3 / reps
+
+    sections = {}
+    for codec, quantize in (("w8a16", backend.quantize_q8), ("w4a16", backend.quantize_q4)):
+        stages, total_flops, total_s, route = {}, 0, 0.0, None
+        for name, n, k in PROJECTIONS:
+            packed = quantize(torch.randn(n, k, generator=gen, device=device) * 0.02)
+            resident = backend.upload_linear(packed, dtype=torch.float16, device=device)
+            del packed
+            plan = resident.prepare(tokens=m)
+            route = plan.route
+            x = torch.randn(m, k, generator=gen, device=device).half()
+            out = torch.empty(m, n, dtype=torch.float16, device=device)
+            t = timed(lambda: plan.run(x, out=out), steps)
+            flops = 2 * m * n * k
+            total_flops += flops
+            total_s += t
+            stages[name] = {"us": round(t * 1e6, 1), "TFLOP/s": round(flops / t / 1e12, 1),
+                            "frac_fp16_peak": round(flops / t / 1e12 / FP16_PEAK_TFLOPS, 4)}
+            del resident, plan, x, out
+        tf = total_flops / total_s / 1e12
+        sections[codec] = {"route": route, "TFLOP/s": round(tf, 1),
+                           "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": FP16_PEAK_TFLOPS,
+                                        "unit": "TFLOP/s", "frac": round(tf / FP16_PEAK_TFLOPS, 4)},
+                           "stages": stages}
+    return {"workload": "fp16-activation prefill GEMMs at the config-2 shapes, M=2048", **sections}
+
+
 def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
     """routed-expert Q4 W4A16 MoE, 128 experts, H 2048, I 768, 512 tokens top-8.
 
@@ -506,6 +556,8 @@ def main():
         del plans, graphs
         log("config-3 A8 prefill")
         result["prefill_a8"] = prefill_a8(backend, device, max(args.steps // 2, 3), 2)
+        log("fp16-activation prefill GEMMs (W8A16, W4A16)")
+        result["prefill_a16"] = prefill_a16(backend, device, max(args.steps // 4, 3), 1)
     if not args.no_moe:
         log("config-4 routed-expert MoE")
         result["moe_w4a16"] = moe_w4a16(backend, device, max(args.steps, 10), 3, 0 if args.no_cpu else 4.0)

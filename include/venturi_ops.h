@@ -114,6 +114,13 @@ int venturi_q8_pack_run(const void* source, int8_t* codes, void* scales, int n, 
 int venturi_q8_gemm_run(const void* x, const int8_t* codes, const void* scales, void* out, int tokens, int n, int k,
                         int padded, int dtype, void* stream);
 
+/* Extension: the same projection for many tokens (prefill) on fp16 matrix
+ * cores over the row-major planes: LDS-staged 256-token x 128-row tiles,
+ * codes converted to fp16 once per tile, one fp32 scale FMA per 32-column
+ * group. fp16 activations, k % 8 == 0, 16-byte aligned x; any token count. */
+int venturi_q8_prefill_run(const void* x, const int8_t* codes, const void* scales, void* out, int tokens, int n, int k,
+                           int padded, int dtype, void* stream);
+
 /* Extension: workspace of the tiled projections below for (tokens, n, swiglu):
  * the exchange slots of launches that split K over two workgroups, or 0 when
  * the launch for this shape does not split. 0 with a message on invalid

@@ -137,7 +137,7 @@ def _ulp16(v):
 
 @pytest.mark.parametrize("nbits", [4, 5, 6])
 @pytest.mark.parametrize("shape", [(1, 8), (37, 136), (130, 768), (300, 2048)])
-@pytest.mark.parametrize("tokens", [1, 16, 33, 130])
+@pytest.mark.parametrize("tokens", [1, 16, 33, 130, 300])
 def test_row_gemm_contract_tolerances(backend, device, nbits, shape, tokens):
     # The W*A16 contract: weights fp16(q * scale) (the oracle's row decode),
     # fp32 accumulation; |y - exact| <= 0.5 ulp_fp16 + 2^-19 sum|x w| against

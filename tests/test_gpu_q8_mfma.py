@@ -59,6 +59,45 @@ def test_mfma_tolerances_tails_and_guards(backend, device, shape, tokens):
     print(f"flips={flips} of {tokens * n}", flush=True)
 
 
+@pytest.mark.parametrize("shape", [(1, 64), (7, 72), (33, 136), (129, 1000), (257, 5120), (300, 2056)])
+@pytest.mark.parametrize("tokens", [33, 64, 100, 256, 300])
+def test_prefill_gemm_tolerances_tails_and_guards(backend, device, shape, tokens):
+    # venturi_q8_prefill_run: the same contract as the decode kernels (exact
+    # group dots on matrix cores, fp32 group scaling), 256 x 128 tiles.
+    n, k = shape
+    print(f"case q8-prefill n={n} k={k} tokens={tokens}", flush=True)
+    codes, scales = random_q8(n, k, 901 + n + tokens)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens + 3)).half()
+    plan = backend.upload_linear(Q8RowSplitWeight(codes, scales, k), dtype=torch.float16, device=device).prepare(
+        tokens=tokens)
+    assert plan.route == "venturi-q8-mfma" and plan.plan.kernel == "prefill"
+    guard = torch.full((tokens * n + 2,), 47, dtype=torch.float16, device=device)
+    out = guard[1:-1].view(tokens, n)
+    plan.run(x.to(device), out=out)
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    flips = check(out, x, codes.numpy(), scales.numpy(), k)
+    print(f"flips={flips} of {tokens * n}", flush=True)
+
+
+@pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 17408)])
+def test_prefill_config2_m2048_sampled_rows(backend, device, n, k):
+    gen = torch.Generator(device=device).manual_seed(n + k + 1)
+    w = torch.randn(n, k, generator=gen, device=device) * 0.02
+    packed = backend.quantize_q8(w)
+    del w
+    tokens = 2048
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(5)).half()
+    plan = backend.upload_linear(packed, dtype=torch.float16, device=device).prepare(tokens=tokens)
+    assert plan.plan.kernel == "prefill"
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    plan.run(x.to(device), out=out)
+    rows = np.sort(np.random.default_rng(n).choice(n, 32, replace=False))
+    codes, scales = packed.codes.cpu().numpy()[rows], packed.scales.cpu().numpy()[rows]
+    flips = check(out[:, rows], x, codes, scales, k)
+    print(f"prefill config2 n={n} k={k}: flips={flips} of {tokens * 32}", flush=True)
+
+
 @pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
 @pytest.mark.parametrize("tokens", [4, 16, 32])
 def test_mfma_config2_sampled_rows(backend, device, n, k, tokens):
@@ -88,7 +127,10 @@ def test_mfma_route_admission(backend, device):
     assert resident.prepare(tokens=1, route="exact").route == "venturi-q8-exact"
     assert resident.prepare(tokens=2).route == "venturi-q8-mfma"
     assert resident.prepare(tokens=32).route == "venturi-q8-mfma"
-    assert resident.prepare(tokens=33).route == "venturi-q8-exact"
+    assert resident.prepare(tokens=32).plan.kernel == "mfma"
+    assert resident.prepare(tokens=33).route == "venturi-q8-mfma"  # prefill GEMM above 32 tokens
+    assert resident.prepare(tokens=33).plan.kernel == "prefill"
+    assert resident.prepare(tokens=4096).plan.slots is None
     bf = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.bfloat16, device=device)
     assert bf.prepare(tokens=8).route == "venturi-q8-exact"
 

@@ -784,6 +784,187 @@ void launch_q4_grouped(const Q4Tiled& p, hipStream_t stream) {
 
 std::uint64_t align256(std::uint64_t v) { return (v + 255) / 256 * 256; }
 
+// ---------------------------------------------------------------------------
+// W4/5/6A16 prefill GEMM (many tokens): out[t][n] = fp16(sum_k x[t][k] * w[n][k])
+// with the contract weights w = fp16(q * scale) (one rounding each, as the
+// reference's fp16 shadow). Once the weights are fp16 the product is a plain
+// fp16 GEMM: the matrix cores accumulate across groups and no per-group VALU
+// work remains. A workgroup of WM x WN waves computes (WM*TI*16) tokens x
+// (WN*TJ*16) rows; one 64-column group per stage: the tile's activation rows
+// (64 halves, staged in dequant8's column order) and weight rows (dequantized
+// once per workgroup into fp16) in two LDS buffers. Rows are eight 16-byte
+// units XOR-swizzled by (row >> 1) & 7, so 16 consecutive rows' fragment reads
+// cover all 64 banks once. Global loads run PF groups ahead in registers.
+template <int WM, int WN, int TI, int TJ>
+struct RowPrefillGeom {
+    static constexpr int kThreads = WM * WN * 64;
+    static constexpr int kTM = WM * TI * 16;
+    static constexpr int kTN = WN * TJ * 16;
+    static constexpr int kAUnits = kTM * 8;  // 16-byte activation loads per group (64 halves a row)
+    static constexpr int kBUnits = kTN * 2;  // 16-byte code loads per group (32 code bytes a row)
+    static constexpr int kAPer = (kAUnits + kThreads - 1) / kThreads;
+    static constexpr int kBPer = (kBUnits + kThreads - 1) / kThreads;
+    static_assert(kAUnits % kThreads == 0, "whole activation loads per thread");
+    static_assert(kBUnits % kThreads == 0 || kBUnits < kThreads, "whole code loads per thread");
+};
+
+__device__ __forceinline__ int swizzle8(int row) { return (row >> 1) & 7; }
+
+template <int HB, int WM, int WN, int TI, int TJ, int PF>
+__global__ __launch_bounds__(WM * WN * 64) void row_prefill(const __half* __restrict__ x,
+                                                           const std::uint8_t* __restrict__ codes,
+                                                           const std::uint8_t* __restrict__ high,
+                                                           const __half* __restrict__ scales, __half* __restrict__ out,
+                                                           int tokens, int n, int k, int padded) {
+    using G = RowPrefillGeom<WM, WN, TI, TJ>;
+    constexpr int TM = G::kTM, TN = G::kTN, T = G::kThreads;
+    struct Stage {
+        uint4 a[G::kAPer];
+        uint4 b[G::kBPer];
+        std::uint32_t h[G::kBPer][HB ? HB : 1];
+        unsigned short s[G::kBPer];
+    };
+    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][TM * 8];
+    __shared__ __attribute__((aligned(16))) uint4 b_lds[2][TN * 8];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    const int q = lane >> 4, r = lane & 15;
+    const int t0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+    const int groups = padded / 64;
+
+    // Activation unit i = tid + u*T: token i / 8, columns 8 * (i % 8) of the group.
+    const __half* a_src[G::kAPer];
+    bool a_row_ok[G::kAPer];
+#pragma unroll
+    for (int u = 0; u < G::kAPer; ++u) {
+        const int tok = (tid + u * T) / 8;
+        a_row_ok[u] = t0 + tok < tokens;
+        a_src[u] = x + static_cast<std::int64_t>(min(t0 + tok, tokens - 1)) * k + 8 * ((tid + u * T) & 7);
+    }
+    // Code unit i: row i / 2, code bytes 16 * (i % 2) of the group (columns 32 * (i % 2) ..).
+    std::int64_t b_row[G::kBPer];
+#pragma unroll
+    for (int u = 0; u < G::kBPer; ++u) b_row[u] = min(n0 + min((tid + u * T) / 2, TN - 1), n - 1);
+
+    auto load = [&](int g, Stage& st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < G::kAPer; ++u)
+            st.a[u] = *reinterpret_cast<const uint4*>(a_src[u] - 8 * ((tid + u * T) & 7) +
+                                                       min(64 * g + 8 * ((tid + u * T) & 7), k - 8));
+#pragma unroll
+        for (int u = 0; u < G::kBPer; ++u) {
+            if (G::kBUnits < T && tid >= G::kBUnits) break;
+            const int half = (tid + u * T) & 1;
+            st.b[u] = *reinterpret_cast<const uint4*>(codes + b_row[u] * (padded / 2) + 32 * g + 16 * half);
+            st.s[u] = __half_as_ushort(scales[b_row[u] * groups + g]);
+            if constexpr (HB > 0) {
+                // 32 columns x HB bits = 4 * HB bytes of the row's high stream.
+                const std::uint8_t* hp = high + b_row[u] * (padded * HB / 8) + (64 * g + 32 * half) * HB / 8;
+#pragma unroll
+                for (int w = 0; w < HB; ++w) st.h[u][w] = reinterpret_cast<const std::uint32_t*>(hp)[w];
+            }
+        }
+    };
+    auto store = [&](const Stage& st, int g, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < G::kAPer; ++u) {
+            const int i = tid + u * T;
+            const int tok = i / 8, unit = i & 7;
+            const bool ok = a_row_ok[u] && 64 * g + 8 * unit < k;  // k % 8 == 0: a unit is all in or all out
+            a_lds[buf][tok * 8 + (unit ^ swizzle8(tok))] = ok ? interleave8(st.a[u]) : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < G::kBPer; ++u) {
+            const int i = tid + u * T;
+            if (G::kBUnits < T && i >= G::kBUnits) break;
+            const int row = i / 2, half = i & 1;
+            const half2v s2 = __builtin_bit_cast(half2v, static_cast<std::uint32_t>(st.s[u]) * 0x10001u);
+            const std::uint32_t words[4] = {st.b[u].x, st.b[u].y, st.b[u].z, st.b[u].w};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                half8 v;
+                if constexpr (HB == 0) {
+                    v = dequant8(words[w], s2);
+                } else {
+                    // Word w covers 8 columns: bits 8 * HB * w .. of the 32 * HB loaded.
+                    const std::uint32_t hbits = (st.h[u][(HB * w) >> 2] >> (8 * ((HB * w) & 3))) & ((1u << (8 * HB)) - 1u);
+                    v = dequant8_high<HB>(words[w], hbits, s2);
+                }
+                b_lds[buf][row * 8 + ((4 * half + w) ^ swizzle8(row))] = __builtin_bit_cast(uint4, v);
+            }
+        }
+    };
+
+    float4v acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) {  // two 32-column slices of the group
+            half8 fb[TJ];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const int row = wn * TJ * 16 + j * 16 + r;
+                fb[j] = __builtin_bit_cast(half8, b_lds[buf][row * 8 + ((4 * sl + q) ^ swizzle8(row))]);
+            }
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                const int tok = wm * TI * 16 + i * 16 + r;
+                const half8 fa = __builtin_bit_cast(half8, a_lds[buf][tok * 8 + ((4 * sl + q) ^ swizzle8(tok))]);
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa, fb[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+
+    Stage st[PF];
+#pragma unroll
+    for (int s = 0; s < PF; ++s) load(min(s, groups - 1), st[s]);
+    store(st[0], 0, 0);
+    if (PF < groups) load(PF, st[0]);
+    __syncthreads();
+    for (int g0 = 0; g0 < groups; g0 += PF) {
+#pragma unroll
+        for (int s = 0; s < PF; ++s) {
+            const int g = g0 + s;
+            if (g >= groups) break;
+            compute(g & 1);
+            if (g + 1 < groups) {
+                store(st[(s + 1) % PF], g + 1, (g + 1) & 1);
+                if (g + 1 + PF < groups) load(g + 1 + PF, st[(s + 1) % PF]);
+            }
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int row = n0 + wn * TJ * 16 + j * 16 + r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = t0 + wm * TI * 16 + i * 16 + 4 * q + e;
+                if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(acc[i][j][e]);
+            }
+        }
+}
+
+template <int HB, int WM, int WN, int TI, int TJ, int PF>
+void launch_row_prefill(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
+                        __half* out, int tokens, int n, int k, int padded, hipStream_t stream) {
+    using G = RowPrefillGeom<WM, WN, TI, TJ>;
+    const dim3 grid((n + G::kTN - 1) / G::kTN, (tokens + G::kTM - 1) / G::kTM);
+    require(grid.y <= 65535, "token tiles exceed the launch grid");
+    row_prefill<HB, WM, WN, TI, TJ, PF><<<grid, G::kThreads, 0, stream>>>(x, codes, high, scales, out, tokens, n, k,
+                                                                         padded);
+}
+
 }  // namespace
 
 // Workspace of one MoE call (offsets in bytes, each section 256-byte aligned):
@@ -817,6 +998,12 @@ void moe_validate(int tokens, int top_k, int experts, int hidden, int inter) {
             "MoE routed rows exceed int32 geometry");
 }
 
+// Token count from which the W4/5/6A16 GEMM uses the prefill tiles (128 tokens
+// x 128 rows, measured faster than the 128-row x 64-token kernel from 32
+// tokens at the config-2 shapes; that kernel reads each weight once per 64
+// tokens).
+constexpr int kRowPrefillMinTokens = 32;
+
 void row_gemm_launch(const void* x, const void* codes, const void* high, const void* scales, void* out, int tokens,
                      int n, int k, int padded, int bits, int dtype, hipStream_t stream) {
     require(bits == 4 || bits == 5 || bits == 6, "row codecs are 4, 5 or 6 bits");
@@ -841,6 +1028,15 @@ void row_gemm_launch(const void* x, const void* codes, const void* high, const v
     p.out_stride = n;
     p.experts = 1;
     p.row_tiles = (n + kRows - 1) / kRows;
+    if (tokens >= kRowPrefillMinTokens) {
+        // Prefill: 128-token tiles that read each weight once per tile.
+        const auto* xp = static_cast<const __half*>(x);
+        auto* op = static_cast<__half*>(out);
+        if (bits == 4) launch_row_prefill<0, 4, 2, 2, 4, 2>(xp, p.codes, p.high, p.scales, op, tokens, n, k, padded, stream);
+        else if (bits == 5) launch_row_prefill<1, 4, 2, 2, 4, 2>(xp, p.codes, p.high, p.scales, op, tokens, n, k, padded, stream);
+        else launch_row_prefill<2, 4, 2, 2, 4, 2>(xp, p.codes, p.high, p.scales, op, tokens, n, k, padded, stream);
+        return;
+    }
     if (bits == 4) launch_q4_mfma<kPlain, 0>(p, stream);
     else if (bits == 5) launch_q4_mfma<kPlain, 1>(p, stream);
     else launch_q4_mfma<kPlain, 2>(p, stream);

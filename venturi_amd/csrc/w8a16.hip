@@ -1,0 +1,245 @@
+// Q8 A16 projection for many tokens (prefill) on fp16 matrix cores: the
+// "mfma" route above the decode kernels' 32 tokens.
+//
+// out[t][n] = fp16( sum_g D[t][n][g] * ws[n][g] ),  D = sum_{k in g} x[t][k] * code[n][k]
+//
+// Each 32-column group's D is one v_mfma_f32_16x16x32_f16 on the fp16
+// activations and the int8 codes converted to fp16 exactly (every x * code
+// product is exact in fp32); the group scale is one fp32 FMA per (t, n, g),
+// groups summed in natural order, so outputs agree with the canonical order
+// (blocks.cu:306-321) to fp32 association, like the decode route.
+//
+// Tiling: a workgroup of WM x WN waves computes (WM*TI*16) tokens x
+// (WN*TJ*16) rows, each wave TI x TJ tiles of 16 x 16. Groups are staged one
+// at a time in two LDS buffers: the tile's activation rows (32 halves each)
+// and weight rows (32 codes converted to fp16 once per workgroup) plus the
+// weight scales. Global loads run PF groups ahead in registers; one barrier
+// per group. LDS rows are four 16-byte units XOR-swizzled by (row >> 1) & 3
+// so that 16 consecutive rows' fragment reads fall on distinct banks.
+#include "common.hpp"
+
+namespace vt {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Sixteen int8 codes -> sixteen fp16 values, exactly (u = c + 128 as the
+// mantissa of 1024 + u, then -1152).
+__device__ __forceinline__ void codes16_to_fp16(const uint4 w, uint4& lo, uint4& hi) {
+    const half2v bias = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+    std::uint32_t h[8];
+    const std::uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const std::uint32_t u = words[i] ^ 0x80808080u;
+        const half2v a = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x05010400u)) + bias;
+        const half2v b = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x05030402u)) + bias;
+        h[2 * i] = __builtin_bit_cast(std::uint32_t, a);
+        h[2 * i + 1] = __builtin_bit_cast(std::uint32_t, b);
+    }
+    lo = make_uint4(h[0], h[1], h[2], h[3]);
+    hi = make_uint4(h[4], h[5], h[6], h[7]);
+}
+
+__device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 3; }
+
+template <int WM, int WN, int TI, int TJ>
+struct PrefillGeom {
+    static constexpr int kThreads = WM * WN * 64;
+    static constexpr int kTM = WM * TI * 16;  // tokens per workgroup
+    static constexpr int kTN = WN * TJ * 16;  // weight rows per workgroup
+    static constexpr int kAUnits = kTM * 4;   // 16-byte activation loads per group (32 halves a row)
+    static constexpr int kBUnits = kTN * 2;   // 16-byte code loads per group (32 codes a row)
+    static constexpr int kAPer = (kAUnits + kThreads - 1) / kThreads;
+    static constexpr int kBPer = (kBUnits + kThreads - 1) / kThreads;
+    static_assert(kAUnits % kThreads == 0 || kAUnits < kThreads, "whole loads per thread");
+    static_assert(kBUnits % kThreads == 0 || kBUnits < kThreads, "whole loads per thread");
+    static_assert(kTN <= kThreads, "one scale per thread");
+};
+
+template <int WM, int WN, int TI, int TJ>
+struct PrefillStage {
+    using G = PrefillGeom<WM, WN, TI, TJ>;
+    uint4 a[G::kAPer];
+    uint4 b[G::kBPer];
+    unsigned short ws;
+};
+
+template <int WM, int WN, int TI, int TJ, int PF>
+__global__ __launch_bounds__(WM * WN * 64) void q8_prefill(const __half* __restrict__ x,
+                                                          const std::int8_t* __restrict__ codes,
+                                                          const __half* __restrict__ scales, __half* __restrict__ out,
+                                                          int tokens, int n, int k, int padded, int groups) {
+    using G = PrefillGeom<WM, WN, TI, TJ>;
+    using Stage = PrefillStage<WM, WN, TI, TJ>;
+    constexpr int TM = G::kTM, TN = G::kTN, T = G::kThreads;
+    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][TM * 4];
+    __shared__ __attribute__((aligned(16))) uint4 b_lds[2][TN * 4];
+    __shared__ __attribute__((aligned(16))) float ws_lds[2][TN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    const int q = lane >> 4, r = lane & 15;
+    const int t0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+
+    // Activation load u of a thread: unit i = tid + u*T, token i / 4 of the
+    // tile, columns 8 * (i % 4) .. +8 of the group (zero past k or past the
+    // last token: the address is clamped and the value replaced at the store).
+    const __half* a_src[G::kAPer];
+    int a_col[G::kAPer];
+    bool a_row_ok[G::kAPer];
+#pragma unroll
+    for (int u = 0; u < G::kAPer; ++u) {
+        const int i = tid + u * T;
+        const int tok = i / 4;
+        a_row_ok[u] = t0 + tok < tokens;
+        a_src[u] = x + static_cast<std::int64_t>(min(t0 + tok, tokens - 1)) * k;
+        a_col[u] = 8 * (i & 3);
+    }
+    const std::int8_t* b_src[G::kBPer];
+#pragma unroll
+    for (int u = 0; u < G::kBPer; ++u) {
+        const int i = tid + u * T;
+        b_src[u] = codes + static_cast<std::int64_t>(min(n0 + min(i / 2, TN - 1), n - 1)) * padded + 16 * (i & 1);
+    }
+    const int sid = T - 1 - tid;  // scales are staged by the last threads
+    const __half* ws_src = scales + static_cast<std::int64_t>(min(n0 + sid % TN, n - 1)) * (padded / 32);
+
+    auto load = [&](int g, Stage& s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < G::kAPer; ++u)
+            if (G::kAUnits >= T || tid < G::kAUnits)
+                s.a[u] = *reinterpret_cast<const uint4*>(a_src[u] + min(g * 32 + a_col[u], k - 8));
+#pragma unroll
+        for (int u = 0; u < G::kBPer; ++u)
+            if (G::kBUnits >= T || tid < G::kBUnits) s.b[u] = *reinterpret_cast<const uint4*>(b_src[u] + g * 32);
+        s.ws = __half_as_ushort(ws_src[g]);
+    };
+    auto store = [&](const Stage& s, int g, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < G::kAPer; ++u) {
+            const int i = tid + u * T;
+            if (G::kAUnits < T && i >= G::kAUnits) break;
+            const int tok = i / 4;
+            const bool ok = a_row_ok[u] && g * 32 + a_col[u] < k;  // k % 8 == 0: a unit is all in or all out
+            a_lds[buf][tok * 4 + ((i & 3) ^ swizzle(tok))] = ok ? s.a[u] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < G::kBPer; ++u) {
+            const int i = tid + u * T;
+            if (G::kBUnits < T && i >= G::kBUnits) break;
+            const int row = i / 2;
+            uint4 lo, hi;
+            codes16_to_fp16(s.b[u], lo, hi);
+            b_lds[buf][row * 4 + ((2 * (i & 1)) ^ swizzle(row))] = lo;
+            b_lds[buf][row * 4 + ((2 * (i & 1) + 1) ^ swizzle(row))] = hi;
+        }
+        if (sid < TN) ws_lds[buf][sid] = __half2float(__ushort_as_half(s.ws));
+    };
+
+    float4v y[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) y[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](int buf) __attribute__((always_inline)) {
+        const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        half8 fb[TJ];
+        float wsv[TJ];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int row = wn * TJ * 16 + j * 16 + r;
+            fb[j] = __builtin_bit_cast(half8, b_lds[buf][row * 4 + (q ^ swizzle(row))]);
+            wsv[j] = ws_lds[buf][row];
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const int tok = wm * TI * 16 + i * 16 + r;
+            const half8 fa = __builtin_bit_cast(half8, a_lds[buf][tok * 4 + (q ^ swizzle(tok))]);
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa, fb[j], zero, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[i][j][e] = fmaf(d[e], wsv[j], y[i][j][e]);
+            }
+        }
+    };
+
+    // Group g is loaded PF groups ahead, written to LDS buffer g % 2 during
+    // the compute of group g - 1, and consumed after the barrier that ends it.
+    Stage st[PF];
+#pragma unroll
+    for (int s = 0; s < PF; ++s) load(min(s, groups - 1), st[s]);
+    store(st[0], 0, 0);
+    if (PF < groups) load(PF, st[0]);
+    __syncthreads();
+    for (int g0 = 0; g0 < groups; g0 += PF) {
+#pragma unroll
+        for (int s = 0; s < PF; ++s) {
+            const int g = g0 + s;
+            if (g >= groups) break;
+            compute(g & 1);
+            if (g + 1 < groups) {
+                store(st[(s + 1) % PF], g + 1, (g + 1) & 1);
+                if (g + 1 + PF < groups) load(g + 1 + PF, st[(s + 1) % PF]);
+            }
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int row = n0 + wn * TJ * 16 + j * 16 + r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = t0 + wm * TI * 16 + i * 16 + 4 * q + e;
+                if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(y[i][j][e]);
+            }
+        }
+}
+
+template <int WM, int WN, int TI, int TJ, int PF>
+void launch_prefill(const __half* x, const std::int8_t* codes, const __half* scales, __half* out, int tokens, int n,
+                    int k, int padded, hipStream_t stream) {
+    using G = PrefillGeom<WM, WN, TI, TJ>;
+    const int groups = (k + 31) / 32;
+    const dim3 grid((n + G::kTN - 1) / G::kTN, (tokens + G::kTM - 1) / G::kTM);
+    require(grid.y <= 65535, "token tiles exceed the launch grid");
+    q8_prefill<WM, WN, TI, TJ, PF><<<grid, G::kThreads, 0, stream>>>(x, codes, scales, out, tokens, n, k, padded,
+                                                                    groups);
+}
+
+}  // namespace
+
+void q8_prefill_launch(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n,
+                       int k, int padded, int dtype, hipStream_t stream) {
+    require(x && codes && scales && out, "null Q8 operand");
+    require(tokens > 0 && n > 0 && k > 0 && padded == padded_k(k), "invalid Q8 geometry");
+    require(static_cast<std::int64_t>(tokens) * n < INT32_MAX, "Q8 output count exceeds int32");
+    require(dtype == kF16, "the Q8 prefill GEMM takes FP16 activations");
+    require(k % 8 == 0 && aligned(x, 16), "the Q8 prefill GEMM needs k % 8 == 0 and 16-byte aligned x");
+    require(aligned(codes, 16) && aligned(scales, 2) && aligned(out, 2), "misaligned Q8 operand");
+    launch_prefill<4, 2, 4, 4, 4>(static_cast<const __half*>(x), codes, scales, static_cast<__half*>(out), tokens, n, k,
+                                  padded, stream);
+}
+
+}  // namespace vt
+
+// Extension: the Q8 A16 projection for many tokens on fp16 matrix cores (same
+// arguments as venturi_q8_head_run; fp16 activations, k % 8 == 0, any token
+// count; intended for prefill, M >= 33).
+extern "C" __attribute__((visibility("default"))) int venturi_q8_prefill_run(const void* x, const std::int8_t* codes,
+                                                                            const __half* scales, void* out,
+                                                                            int tokens, int n, int k, int padded,
+                                                                            int dtype, void* stream) {
+    return vt::guarded([&] {
+        vt::q8_prefill_launch(x, codes, scales, out, tokens, n, k, padded, dtype, static_cast<hipStream_t>(stream));
+    });
+}

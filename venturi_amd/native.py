@@ -38,6 +38,7 @@ SIGNATURES = {
     "venturi_rms_q8_quantize_passes": ([_P] * 3 + [_U64, _I, _I, _F, _I, _P, _P], _I),
     "venturi_q8_pack_run": ([_P] * 3 + [_I] * 4 + [_P], _I),
     "venturi_q8_gemm_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
+    "venturi_q8_prefill_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
     "venturi_q8_tiled_workspace_bytes": ([_I] * 3, _U64),
     "venturi_q8_tiled_workspace_init": ([_P, _U64, _P], _I),
     "venturi_q8_tiled_run": ([_P] * 4 + [_I] * 5 + [_P, _U64, _P], _I),

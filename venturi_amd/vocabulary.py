@@ -7,17 +7,19 @@ family once:
 
 * ``exact``: the reference's canonical fp32 order (bytes identical to
   ``venturi_q8_head_run`` on the reference's GPUs);
-* ``mfma``: fp16 matrix cores with per-group fp32 scaling, for larger token
-  counts (same values up to fp32 association, see ``Q8OutputHead.route``).
-  It reads a tiled copy of the planes (16-row blocks x 64-column chunks in
-  MFMA operand order, built once by the first ``mfma`` plan and kept with the
-  resident weight), so every wave streams contiguous 1 KB blocks;
+* ``mfma``: fp16 matrix cores with per-group fp32 scaling (same values up to
+  fp32 association, see ``Q8OutputHead.route``). Up to 32 tokens (decode)
+  it reads a tiled copy of the planes (16-row blocks x 64-column chunks in
+  MFMA operand order, built once by the first such plan and kept with the
+  resident weight), so every wave streams contiguous 1 KB blocks; above 32
+  tokens (prefill) it runs ``venturi_q8_prefill_run`` on the row-major planes
+  (LDS-staged 256-token x 128-row tiles);
 * ``auto``: ``mfma`` whenever its conditions hold (FP16 activations,
-  K % 8 == 0, at most 32 tokens), else ``exact``. The matrix-core kernel
-  streams the weights faster at every token count (the canonical order
-  needs one fp32 FMA per token and weight plus an exact weight conversion,
-  and its lane-per-four-columns layout issues 4-byte loads); callers that
-  need the reference's bytes ask for ``exact``.
+  K % 8 == 0), else ``exact``. The matrix-core kernels are faster at every
+  token count (the canonical order needs one fp32 FMA per token and weight
+  plus an exact weight conversion, and its lane-per-four-columns layout
+  issues 4-byte loads); callers that need the reference's bytes ask for
+  ``exact``.
 """
 
 from dataclasses import dataclass, field
@@ -159,15 +161,15 @@ class ResidentQ8Vocabulary:
         if route not in Q8_ROUTES:
             raise ValueError(f"Q8 route must be one of {Q8_ROUTES}")
         self.backend.validate_device(self.dtype, self.device)
-        mfma_ok = self.dtype == torch.float16 and self.hidden_size % 8 == 0 and tokens <= MFMA_MAX_TOKENS
+        mfma_ok = self.dtype == torch.float16 and self.hidden_size % 8 == 0
         if route == "auto":
             route = "mfma" if mfma_ok and tokens > EXACT_MAX_AUTO_TOKENS else "exact"
         if route == "mfma" and not mfma_ok:
-            raise ValueError(
-                f"The Q8 MFMA route takes FP16 activations, K % 8 == 0 and at most {MFMA_MAX_TOKENS} tokens"
-            )
+            raise ValueError("The Q8 MFMA route takes FP16 activations and K % 8 == 0")
         if route == "exact":
             return Q8OutputHead(self, tokens, route)
+        if tokens > MFMA_MAX_TOKENS:
+            return Q8OutputHead(self, tokens, "prefill")
         return Q8OutputHead(self, tokens, route, self.tiled_planes(), self._slots(tokens, swiglu=False))
 
     def _slots(self, tokens, *, swiglu):
@@ -244,7 +246,12 @@ class Q8OutputHead:
 
     @property
     def route(self):
-        return {"exact": "venturi-q8-exact", "mfma": "venturi-q8-mfma", "swiglu": "venturi-q8-mfma-swiglu"}[self.kernel]
+        return {
+            "exact": "venturi-q8-exact",
+            "mfma": "venturi-q8-mfma",
+            "prefill": "venturi-q8-mfma",
+            "swiglu": "venturi-q8-mfma-swiglu",
+        }[self.kernel]
 
     @property
     def out_features(self):
@@ -264,6 +271,8 @@ class Q8OutputHead:
         lib = r.backend._native
         if self.kernel == "exact":
             entry, planes, tail = lib.venturi_q8_head_run, (r._codes, r._scales), ()
+        elif self.kernel == "prefill":
+            entry, planes, tail = lib.venturi_q8_prefill_run, (r._codes, r._scales), ()
         else:
             entry = lib.venturi_q8_tiled_swiglu_run if self.kernel == "swiglu" else lib.venturi_q8_tiled_run
             planes = self.tiles
