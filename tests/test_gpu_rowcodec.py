@@ -27,7 +27,7 @@ def _dev(a, device):
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
-@pytest.mark.parametrize("tokens", [1, 7, 16, 40])
+@pytest.mark.parametrize("tokens", [1, 7, 16, 40, 300])
 @pytest.mark.parametrize("k", [64, 200, 1000])
 def test_q8_a16_plan(backend, device, dtype, tokens, k):
     n = 70
@@ -46,6 +46,9 @@ def test_q8_a16_plan(backend, device, dtype, tokens, k):
     if dtype == 0 and k % 8 == 0 and tokens <= 16:
         backend._check(lib.venturi_q8_gemm_run(x.data_ptr(), dc.data_ptr(), ds.data_ptr(), want.data_ptr(), tokens, n,
                                                k, padded, dtype, s))
+    elif dtype == 0 and k % 8 == 0 and tokens > 32:
+        backend._check(lib.venturi_q8_prefill_run(x.data_ptr(), dc.data_ptr(), ds.data_ptr(), want.data_ptr(), tokens,
+                                                  n, k, padded, dtype, s))
     else:
         backend._check(lib.venturi_q8_head_run(x.data_ptr(), dc.data_ptr(), ds.data_ptr(), want.data_ptr(), tokens, n,
                                                k, padded, dtype, s))
