@@ -20,8 +20,9 @@ event-measured time, against the 8 TB/s HBM peak; `all_kernels_GBps` is the
 same over every launch; `per_launch` gives each kernel's average launch
 duration; `cpu_baseline` times the reference's CPU path (torch FP32 GEMM over
 materialised weights) on a bounded sample of the same workload. The
-`prefill_a8` (config 3) and `moe_w4a16` (config 4) sections carry their own
-roofline objects.
+`q4_decode` (the metric's Q4 leg at M <= 16: config-2 shapes with q4_g64_fp16
+weights), `prefill_a8` (config 3), `prefill_a16` (W8A16 / W4A16 at M = 2048)
+and `moe_w4a16` (config 4) sections carry their own roofline objects.
 """
 
 import argparse
@@ -57,6 +58,7 @@ def parse():
     p.add_argument("--copy-mb", type=float, default=600.0, help="minimum rotated weight bytes per projection")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-q4", action="store_true", help="skip the Q4 W4A16 decode section")
     p.add_argument("--no-prefill", action="store_true", help="skip the config-3 A8 prefill section")
     p.add_argument("--no-moe", action="store_true", help="skip the config-4 routed-expert MoE section")
     p.add_argument("--no-model", action="store_true", help="skip the config-5 64-layer decode section")
@@ -258,6 +260,92 @@ def prefill_a16(backend, device, steps, warmup):
                                         "unit": "TFLOP/s", "frac": round(tf / FP16_PEAK_TFLOPS, 4)},
                            "stages": stages}
     return {"workload": "fp16-activation prefill GEMMs at the config-2 shapes, M=2048", **sections}
+
+
+def q4_launch_bytes(m, n, k):
+    padded = (k + 127) // 128 * 128
+    return n * padded // 2 + n * (padded // 64) * 2 + m * k * 2 + m * n * 2
+
+
+def q4_decode(backend, device, steps, warmup, copy_mb):
+    """The metric's Q4 leg at M <= 16: the config-2 projection set with weights
+    packed to q4_g64_fp16 (the W4A16 contract, plan route auto), M in {1,4,8,16}.
+
+    Same method as the Q8 decode timing: per (projection, M), `steps` launches
+    rotating >= `copy_mb` MB of independent weight copies captured in one HIP
+    graph, replayed between one pair of events; algorithmic bytes per launch =
+    codes N*Kp/2 + scales N*(Kp/64)*2 + activations M*K*2 + outputs M*N*2.
+    """
+    copies = []
+    for i, (name, n, k) in enumerate(PROJECTIONS):
+        count = max(2, -(-int(copy_mb * 1e6) // q4_launch_bytes(0, n, k)))
+        residents = []
+        for c in range(count):
+            gen = torch.Generator(device=device).manual_seed(5000 + 1000 * c + i)
+            w = torch.randn(n, k, generator=gen, device=device, dtype=torch.float32) * 0.02
+            packed = backend.quantize_q4(w)
+            del w
+            residents.append(backend.upload_linear(packed, dtype=torch.float16, device=device))
+            del packed
+        copies.append(residents)
+    gen = torch.Generator(device=device).manual_seed(17)
+    xs = {m: {k: torch.randn(m, k, generator=gen, device=device).half() for k in {p[2] for p in PROJECTIONS}}
+          for m in TOKENS}
+    outs = {(m, n): torch.empty(m, n, dtype=torch.float16, device=device) for m in TOKENS for (_, n, _) in PROJECTIONS}
+    launches = [(mi, pi) for mi in range(len(TOKENS)) for pi in range(len(PROJECTIONS))]
+    plans = {(mi, pi): [r.prepare(tokens=TOKENS[mi]) for r in copies[pi]] for mi, pi in launches}
+    stream = torch.cuda.current_stream(device)
+
+    def run(mi, pi, reps):
+        m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
+        rotation = plans[(mi, pi)]
+        for s in range(reps):
+            rotation[s % len(rotation)].run(xs[m][k], out=outs[(m, n)])
+
+    for key in launches:
+        run(*key, warmup)
+    torch.cuda.synchronize(device)
+    graphs = {}
+    for key in launches:
+        graphs[key] = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graphs[key]):
+            run(*key, steps)
+    graph_equals_eager = True
+    for mi, pi in launches:
+        m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
+        ref = torch.empty_like(outs[(m, n)])
+        plans[(mi, pi)][(steps - 1) % len(plans[(mi, pi)])].run(xs[m][k], out=ref)
+        graphs[(mi, pi)].replay()
+        torch.cuda.synchronize(device)
+        graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
+    events = {key: [torch.cuda.Event(enable_timing=True) for _ in range(2)] for key in launches}
+    torch.cuda.synchronize(device)
+    start = time.perf_counter()
+    for key in launches:
+        events[key][0].record(stream)
+        graphs[key].replay()
+        events[key][1].record(stream)
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - start
+    detail, total_bytes, kernel_total = {}, 0, 0.0
+    for mi, pi in launches:
+        m, (name, n, k) = TOKENS[mi], PROJECTIONS[pi]
+        t = events[(mi, pi)][0].elapsed_time(events[(mi, pi)][1]) / 1e3
+        b = steps * q4_launch_bytes(m, n, k)
+        total_bytes += b
+        kernel_total += t
+        detail[f"{name}_m{m}"] = {"us": round(t / steps * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+    achieved = total_bytes / kernel_total / 1e9
+    return {
+        "workload": "config-2 projection set with q4_g64_fp16 weights (W4A16 contract), M in {1,4,8,16}",
+        "route": plans[(0, 0)][0].route,
+        "GB/s": round(total_bytes / wall / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": "row_decode_gemm (fp16 MFMA, W4A16 contract)", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4)},
+        "weight_copies": {p[0]: len(c) for p, c in zip(PROJECTIONS, copies)},
+        "graph_equals_eager": graph_equals_eager,
+        "per_launch": detail,
+    }
 
 
 def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
@@ -552,8 +640,11 @@ def main():
         "timing": "eager launches" if args.eager else "HIP-graph replays",
         "per_launch": detail,
     }
-    if not args.no_prefill:
+    if not args.no_q4:
         del plans, graphs
+        log("Q4 W4A16 decode at the config-2 shapes")
+        result["q4_decode"] = q4_decode(backend, device, args.steps, args.warmup, args.copy_mb)
+    if not args.no_prefill:
         log("config-3 A8 prefill")
         result["prefill_a8"] = prefill_a8(backend, device, max(args.steps // 2, 3), 2)
         log("fp16-activation prefill GEMMs (W8A16, W4A16)")

@@ -136,13 +136,15 @@ def _ulp16(v):
 
 
 @pytest.mark.parametrize("nbits", [4, 5, 6])
-@pytest.mark.parametrize("shape", [(1, 8), (37, 136), (130, 768), (300, 2048)])
-@pytest.mark.parametrize("tokens", [1, 16, 33, 130, 300])
+@pytest.mark.parametrize("shape", [(1, 8), (37, 136), (130, 768), (300, 2048), (6200, 136), (16400, 264)])
+@pytest.mark.parametrize("tokens", [1, 5, 16, 24, 33, 130, 300])
 def test_row_gemm_contract_tolerances(backend, device, nbits, shape, tokens):
     # The W*A16 contract: weights fp16(q * scale) (the oracle's row decode),
     # fp32 accumulation; |y - exact| <= 0.5 ulp_fp16 + 2^-19 sum|x w| against
     # FP64, and against the reference-order Q5 GEMV within 2e-3 / one ulp,
-    # rel-L2 1e-3.
+    # rel-L2 1e-3. Token counts cover the decode kernel's one and two token
+    # blocks and the prefill tiles; row counts cover each decode launch shape
+    # (up to 384, up to 1023 and from 1024 row blocks of 16).
     n, k = shape
     print(f"case row-gemm bits={nbits} n={n} k={k} tokens={tokens}", flush=True)
     packed, high, scales = _planes(n, k, nbits, 77 * nbits + n + tokens)

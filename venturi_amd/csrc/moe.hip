@@ -1,6 +1,6 @@
-// Q4 W4A16 on fp16 matrix cores: a grouped (routed-expert) GEMM and the
-// plain W4A16 GEMM, plus the device routing and per-token combine of the
-// routed-expert MoE.
+// Q4 W4A16 on fp16 matrix cores: a grouped (routed-expert) GEMM, the plain
+// W4/5/6A16 GEMMs (decode and prefill), plus the device routing and per-token
+// combine of the routed-expert MoE.
 //
 // Weight contract (flash_next_q4.cu:7-14, quantization/linear.py:86-95):
 // w = fp16_RNE(q * scale). In registers: the nibble u = q + 8 becomes the
@@ -32,31 +32,12 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
-constexpr int kRows = 128;        // weight rows per workgroup tile
-constexpr int kWaves = 8;         // 512 threads; wave w owns 16 rows
+constexpr int kRows = 128;        // weight rows per expert tile
 constexpr int kChunk = 256;       // K columns staged per iteration (128 code bytes per row)
-constexpr int kPassTokens = 64;   // tokens per pass: four 16-token MFMA blocks
-constexpr int kWStride = 144;     // LDS bytes per weight row (128 + 16 pad)
 constexpr int kXStride = 264;     // LDS halves per token row (256 + 8 pad)
 constexpr int kMaxExperts = 1024;
 
-enum Epilogue { kPlain = 0, kSwiGLU = 1, kScore = 2 };
-
-struct Q4Gemm {
-    const __half* x;           // activation rows, row stride x_stride halves
-    const int* gather;         // slot -> x row (null: slot itself)
-    const std::uint8_t* codes; // expert 0 codes [n][padded/2]
-    const __half* scales;      // expert 0 scales [n][padded/64]
-    std::int64_t code_stride;  // bytes between experts
-    std::int64_t scale_stride; // halves between experts
-    const int* seg;            // [experts+1] slot offsets (null: one segment [0, tokens))
-    const __half* score;       // per-slot fp16 factor (kScore)
-    __half* out;               // out[slot][out_stride]
-    const std::uint8_t* high;  // Q5/Q6 high plane [n][padded*hb/8] (hb = bits - 4 > 0)
-    int tokens, n, k, padded, x_stride, out_stride, experts, row_tiles, half_rows;
-};
-
-constexpr int kHStride = 80;  // LDS bytes per row of a chunk's high-plane slice (up to 64 + 16 pad)
+enum Epilogue { kSwiGLU = 1, kScore = 2 };
 
 // Eight signed nibbles (one code word: columns c..c+7, even columns in the
 // low nibbles) -> eight fp16 weights fp16(q * s), in the K order
@@ -167,224 +148,6 @@ __device__ __forceinline__ uint4 interleave8(uint4 v) {
 }
 
 __device__ __forceinline__ float silu(float g) { return __fdiv_rn(g, 1.0f + expf(-g)); }
-
-template <int EPI, int HB>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void q4_mfma(Q4Gemm p) {
-    __shared__ __attribute__((aligned(16))) std::uint8_t wl[kRows * kWStride];
-    __shared__ __attribute__((aligned(16))) std::uint8_t hl[HB ? kRows * kHStride : 16];
-    __shared__ std::uint32_t sl[kRows][2];
-    __shared__ __attribute__((aligned(16))) _Float16 xl[kPassTokens * kXStride];
-
-    // Workgroup -> (expert, row tile); with experts % 8 == 0 every expert's
-    // tiles run on one XCD (round-robin dispatch), so its routed activation
-    // rows are fetched into one L2.
-    const int linear = blockIdx.x;
-    int expert, tile;
-    if (p.experts % 8 == 0) {
-        const int xcd = linear % 8, idx = linear / 8;
-        expert = 8 * (idx / p.row_tiles) + xcd;
-        tile = idx % p.row_tiles;
-    } else {
-        expert = linear / p.row_tiles;
-        tile = linear % p.row_tiles;
-    }
-    const int seg_begin = p.seg ? p.seg[expert] : 0;
-    const int seg_end = p.seg ? p.seg[expert + 1] : p.tokens;
-    if (seg_begin >= seg_end) return;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int q = lane >> 4, m = lane & 15;
-    const std::uint8_t* codes = p.codes + expert * p.code_stride;
-    const __half* scales = p.scales + expert * p.scale_stride;
-    const int row_bytes = p.padded / 2, groups = p.padded / 64;
-    const int chunks = (p.padded + kChunk - 1) / kChunk;
-
-    // Tile row slot -> weight row (clamped; clamped rows are never stored).
-    auto weight_row = [&](int slot) {
-        if (EPI == kSwiGLU) {
-            const int r = tile * (kRows / 2) + (slot & 63);
-            return slot < 64 ? min(r, p.half_rows - 1) : min(p.half_rows + r, p.n - 1);
-        }
-        return min(tile * kRows + slot, p.n - 1);
-    };
-    // This lane's MFMA column (weight row slot): plain waves own 16 consecutive
-    // slots; SwiGLU waves own 8 gate slots and the 8 matching up slots.
-    const int my_slot = EPI == kSwiGLU ? (m < 8 ? 8 * wave + m : 64 + 8 * wave + (m - 8)) : 16 * wave + m;
-
-    // Staging assignment: code piece i covers row (tid + 512 i) / 8, bytes 16 * (tid % 8);
-    // scale pair: row tid / 2 (tid < 256), groups 2 * (tid % 2) .. +1;
-    // activation piece j: token (tid + 512 j) / 32, columns 8 * (tid % 32).
-    const std::uint8_t* wsrc[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-        wsrc[i] = codes + static_cast<std::int64_t>(weight_row((tid + 512 * i) >> 3)) * row_bytes + 16 * (tid & 7);
-    const __half* ssrc = scales + static_cast<std::int64_t>(weight_row((tid & 255) >> 1)) * groups + 2 * (tid & 1);
-    // High-plane piece: row tid / 4, bytes 8 * HB * (tid % 4) of the chunk's 32 * HB.
-    const std::uint8_t* hsrc =
-        HB ? p.high + static_cast<std::int64_t>(weight_row(tid >> 2)) * (p.padded * HB / 8) + 8 * HB * (tid & 3)
-           : nullptr;
-
-    for (int pass = seg_begin; pass < seg_end; pass += kPassTokens) {
-        const int live = min(kPassTokens, seg_end - pass);
-        // Token blocks of 16 (activation load j feeds block j), fixed at compile
-        // time so that no load sits behind a branch.
-        auto run_pass = [&](auto nb_tag) {
-            constexpr int NB = decltype(nb_tag)::value;
-            const __half* xrow[NB];
-            bool xlive[NB];
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const int t = (tid + 512 * j) >> 5;
-                xlive[j] = t < live;
-                const int slot = pass + min(t, live - 1);
-                const int row = p.gather ? p.gather[slot] : slot;
-                xrow[j] = p.x + static_cast<std::int64_t>(row) * p.x_stride;
-            }
-
-            // Every load is unconditional from a valid (clamped) address; data past
-            // the matrix is replaced by zeros when the stage is stored to LDS (after
-            // the wait that store needs anyway), never by writing the load's
-            // destination registers early, which would force a wait per load.
-            struct Stage {
-                uint4 w[2];
-                uint4 h;
-                std::uint32_t s;
-                uint4 x[NB];
-                bool wok, hok, sok, xok[NB];
-            };
-            auto load = [&](int c, Stage& st) {
-                const int col0 = c * kChunk;
-                const bool second_half = col0 + 128 < p.padded;  // chunk tail past padded K is absent
-                st.wok = second_half || (tid & 7) < 4;
-                const int wofs = second_half ? col0 / 2 : col0 / 2 - 64 * ((tid & 7) >> 2);
-#pragma unroll
-                for (int i = 0; i < 2; ++i) st.w[i] = *reinterpret_cast<const uint4*>(wsrc[i] + wofs);
-                if constexpr (HB > 0) {
-                    // Pieces 2, 3 cover chunk columns 128..255, absent past padded K.
-                    st.hok = second_half || (tid & 3) < 2;
-                    const int hofs = col0 * HB / 8 - (st.hok ? 0 : 16 * HB);
-                    if constexpr (HB == 1) {
-                        const uint2 v = *reinterpret_cast<const uint2*>(hsrc + hofs);
-                        st.h = make_uint4(v.x, v.y, 0u, 0u);
-                    } else {
-                        st.h = *reinterpret_cast<const uint4*>(hsrc + hofs);
-                    }
-                }
-                st.sok = col0 / 64 + 2 * (tid & 1) < groups;
-                st.s = *reinterpret_cast<const std::uint32_t*>(ssrc + col0 / 64 - (st.sok ? 0 : 2 * (tid & 1)));
-                const int col = col0 + 8 * (tid & 31);
-#pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    st.x[j] = *reinterpret_cast<const uint4*>(xrow[j] + min(col, p.k - 8));
-                    st.xok[j] = xlive[j] && col < p.k;
-                }
-            };
-            auto store = [&](const Stage& st) {
-                const uint4 zero = make_uint4(0, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const int piece = tid + 512 * i;
-                    *reinterpret_cast<uint4*>(wl + (piece >> 3) * kWStride + 16 * (piece & 7)) = st.wok ? st.w[i] : zero;
-                }
-                if (tid < 256) sl[tid >> 1][tid & 1] = st.sok ? st.s : 0u;
-                if constexpr (HB == 1)
-                    *reinterpret_cast<uint2*>(hl + (tid >> 2) * kHStride + 8 * (tid & 3)) =
-                        st.hok ? make_uint2(st.h.x, st.h.y) : make_uint2(0u, 0u);
-                if constexpr (HB == 2)
-                    *reinterpret_cast<uint4*>(hl + (tid >> 2) * kHStride + 16 * (tid & 3)) = st.hok ? st.h : zero;
-#pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    const int piece = tid + 512 * j;
-                    *reinterpret_cast<uint4*>(xl + (piece >> 5) * kXStride + 8 * (piece & 31)) =
-                        st.xok[j] ? interleave8(st.x[j]) : zero;
-                }
-            };
-
-            float4v acc[NB];
-#pragma unroll
-            for (int b = 0; b < NB; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-
-            Stage st;
-            load(0, st);
-            for (int c = 0; c < chunks; ++c) {
-                __syncthreads();
-                store(st);
-                __syncthreads();
-                if (c + 1 < chunks) load(c + 1, st);  // in flight while chunk c computes
-
-                // Lane (m, q): weight slot my_slot, chunk columns [64q, 64q + 64) = group q.
-                const uint4* wrow = reinterpret_cast<const uint4*>(wl + my_slot * kWStride + 32 * q);
-                const uint4 w0 = wrow[0], w1 = wrow[1];
-                const std::uint32_t spair = sl[my_slot][q >> 1];
-                const std::uint32_t sbits = (q & 1) ? (spair >> 16) : (spair & 0xFFFFu);
-                const half2v s2 = __builtin_bit_cast(half2v, sbits | (sbits << 16));
-                const std::uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-                // Group q's upper bits: 8 * HB bytes, HB per word of 8 columns.
-                std::uint32_t hw[4] = {0u, 0u, 0u, 0u};
-                if constexpr (HB == 1) {
-                    const uint2 v = *reinterpret_cast<const uint2*>(hl + my_slot * kHStride + 8 * q);
-                    hw[0] = v.x;
-                    hw[1] = v.y;
-                }
-                if constexpr (HB == 2) {
-                    const uint4 v = *reinterpret_cast<const uint4*>(hl + my_slot * kHStride + 16 * q);
-                    hw[0] = v.x;
-                    hw[1] = v.y;
-                    hw[2] = v.z;
-                    hw[3] = v.w;
-                }
-#pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    half8 wf;
-                    if constexpr (HB == 0) wf = dequant8(words[s], s2);
-                    else wf = dequant8_high<HB>(words[s], (hw[(HB * s) >> 2] >> (8 * ((HB * s) & 3))) & ((1u << (8 * HB)) - 1u), s2);
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) {
-                        const half8 xf = *reinterpret_cast<const half8*>(xl + (16 * b + m) * kXStride + 64 * q + 8 * s);
-                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf, wf, acc[b], 0, 0, 0);
-                    }
-                }
-            }
-
-            // D layout: lane holds weight slot my_slot for tokens 16b + 4q + i.
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = 16 * b + 4 * q + i;
-                    const float v = acc[b][i];
-                    if (EPI == kSwiGLU) {
-                        const float other = __shfl_xor(v, 8, 64);  // lane m^8 holds the paired up/gate row
-                        const int col = tile * (kRows / 2) + 8 * wave + (m & 7);
-                        if (m < 8 && t < live && col < p.half_rows) {
-                            const float g = __half2float(from_f32<__half>(v));
-                            const float u = __half2float(from_f32<__half>(other));
-                            const float a = __half2float(from_f32<__half>(silu(g)));
-                            p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + col] =
-                                from_f32<__half>(__fmul_rn(a, u));
-                        }
-                    } else {
-                        const int row = tile * kRows + my_slot;
-                        if (t < live && row < p.n) {
-                            float y = __half2float(from_f32<__half>(v));
-                            if (EPI == kScore) y = __fmul_rn(y, __half2float(p.score[pass + t]));
-                            p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + row] = from_f32<__half>(y);
-                        }
-                    }
-                }
-            }
-        };
-        switch ((live + 15) >> 4) {
-            case 1: run_pass(std::integral_constant<int, 1>{}); break;
-            case 2: run_pass(std::integral_constant<int, 2>{}); break;
-            case 3: run_pass(std::integral_constant<int, 3>{}); break;
-            default: run_pass(std::integral_constant<int, 4>{}); break;
-        }
-        __syncthreads();  // the next pass restages LDS
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Tiled expert planes (built at upload): a matrix is cut into tiles of 128 rows
@@ -769,12 +532,6 @@ void combine_dispatch(int top_k, const std::int64_t* ids, const int* pair_slot, 
     }
 }
 
-template <int EPI, int HB>
-void launch_q4_mfma(const Q4Gemm& p, hipStream_t stream) {
-    const dim3 grid(p.experts * p.row_tiles);
-    q4_mfma<EPI, HB><<<grid, kWaves * 64, 0, stream>>>(p);
-}
-
 template <int EPI, int W, int RB, int NBMAX>
 void launch_q4_grouped(const Q4Tiled& p, hipStream_t stream) {
     const int blocks = p.row_tiles * 8;
@@ -965,6 +722,168 @@ void launch_row_prefill(const __half* x, const std::uint8_t* codes, const std::u
                                                                          padded);
 }
 
+// ---------------------------------------------------------------------------
+// W4/5/6A16 decode GEMM (fewer tokens than the prefill tiles) over the
+// row-major planes: out[t][n] = fp16(sum_k x[t][k] * fp16(q * scale)), fp32
+// accumulation. A workgroup of W waves owns RB blocks of 16 weight rows and its
+// waves split the K range; a lane (r, q) of a wave reads, per 128-column chunk,
+// the 16 code bytes of row r holding columns 32q .. 32q+31 (a row block's chunk
+// is one 1 KB wave load of 64-byte row segments), the pair of group scales of
+// the chunk and, for Q5/Q6, the 4 * HB high-plane bytes of those columns. The
+// four code words become four half8 B fragments (dequant8 order) for four
+// v_mfma_f32_16x16x32_f16 whose A fragments are the matching activations of
+// token r (interleave8), loaded only by lanes whose token exists. Chunks are
+// fetched in a two-deep ping-pong; partial tiles are summed across waves
+// through LDS in wave order and stored by one wave per (row block, token block).
+template <int HB, int RB, int NB, int STEPS>
+struct RowDecodeBatch {
+    uint4 w[STEPS][RB];
+    std::uint32_t s[STEPS][RB];
+    std::uint32_t h[STEPS][RB][HB ? HB : 1];
+    uint4 x[STEPS][NB][4];
+};
+
+template <int HB, int W, int RB, int NB, int STEPS>
+__global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restrict__ x,
+                                                          const std::uint8_t* __restrict__ codes,
+                                                          const std::uint8_t* __restrict__ high,
+                                                          const __half* __restrict__ scales, __half* __restrict__ out,
+                                                          int tokens, int n, int k, int padded) {
+    __shared__ float4v partial[W][RB * NB][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, r = lane & 15;
+    const int block0 = blockIdx.x * RB;
+    const int chunks = padded / 128;
+    const int c0 = wave * chunks / W, c1 = (wave + 1) * chunks / W;
+    const std::int64_t cstride = padded / 2, sstride = padded / 64, hstride = padded * HB / 8;
+    const std::uint8_t* cp[RB];
+    const std::uint32_t* sp[RB];
+    const std::uint8_t* hp[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+        const std::int64_t row = min((block0 + b) * 16 + r, n - 1);  // clamped rows are never stored
+        cp[b] = codes + row * cstride + 16 * q;
+        sp[b] = reinterpret_cast<const std::uint32_t*>(scales + row * sstride);
+        hp[b] = HB ? high + row * hstride + 4 * HB * q : nullptr;
+    }
+    bool live[NB];
+    const __half* xr[NB];
+#pragma unroll
+    for (int tb = 0; tb < NB; ++tb) {
+        const int t = 16 * tb + r;
+        live[tb] = t < tokens;
+        xr[tb] = x + static_cast<std::int64_t>(min(t, tokens - 1)) * k + 32 * q;
+    }
+    using Batch = RowDecodeBatch<HB, RB, NB, STEPS>;
+    const int batches = (c1 - c0 + STEPS - 1) / STEPS;
+    // Batch i holds chunks c0 + i * STEPS + s; chunks past c1 are clamped to c1 - 1
+    // when loaded and skipped when multiplied.
+    auto fetch = [&](int i, Batch& t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+            const int c = min(c0 + i * STEPS + st, c1 - 1);
+#pragma unroll
+            for (int b = 0; b < RB; ++b) {
+                t.w[st][b] = *reinterpret_cast<const uint4*>(cp[b] + 64 * c);
+                t.s[st][b] = sp[b][c];
+                if constexpr (HB > 0) {
+#pragma unroll
+                    for (int h = 0; h < HB; ++h)
+                        t.h[st][b][h] = reinterpret_cast<const std::uint32_t*>(hp[b] + 16 * HB * c)[h];
+                }
+            }
+            const int col = 128 * c + 32 * q;  // k % 8 == 0: a fragment is all in or all out
+#pragma unroll
+            for (int tb = 0; tb < NB; ++tb)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+                    if (live[tb] && col + 8 * j < k) v = *reinterpret_cast<const uint4*>(xr[tb] + 128 * c + 8 * j);
+                    t.x[st][tb][j] = v;
+                }
+        }
+    };
+    float4v acc[RB][NB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int tb = 0; tb < NB; ++tb) acc[b][tb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    auto consume = [&](int i, const Batch& t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+        if (c0 + i * STEPS + st >= c1) break;
+        half8 fa[NB][4];
+#pragma unroll
+        for (int tb = 0; tb < NB; ++tb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fa[tb][j] = __builtin_bit_cast(half8, interleave8(t.x[st][tb][j]));
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            // Columns 32q .. 32q+31 of the chunk lie in its group q / 2.
+            const std::uint32_t s = (t.s[st][b] >> (16 * (q >> 1))) & 0xFFFFu;
+            const half2v s2 = __builtin_bit_cast(half2v, s * 0x10001u);
+            const std::uint32_t words[4] = {t.w[st][b].x, t.w[st][b].y, t.w[st][b].z, t.w[st][b].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                half8 wf;
+                if constexpr (HB == 0) {
+                    wf = dequant8(words[j], s2);
+                } else {
+                    // Word j's eight columns own bits 8 * HB * j .. of the lane's 32 * HB.
+                    const std::uint32_t hbits =
+                        (t.h[st][b][(HB * j) >> 2] >> (8 * ((HB * j) & 3))) & ((1u << (8 * HB)) - 1u);
+                    wf = dequant8_high<HB>(words[j], hbits, s2);
+                }
+#pragma unroll
+                for (int tb = 0; tb < NB; ++tb)
+                    acc[b][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[tb][j], wf, acc[b][tb], 0, 0, 0);
+            }
+        }
+        }
+    };
+    if (batches > 0) {
+        Batch ta, tb2;
+        fetch(0, ta);
+        for (int i = 0; i < batches; i += 2) {
+            if (i + 1 < batches) fetch(i + 1, tb2);
+            consume(i, ta);
+            if (i + 1 >= batches) break;
+            if (i + 2 < batches) fetch(i + 2, ta);
+            consume(i + 1, tb2);
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int tb = 0; tb < NB; ++tb) partial[wave][b * NB + tb][lane] = acc[b][tb];
+    __syncthreads();
+    for (int p = wave; p < RB * NB; p += W) {
+        const int b = p / NB, tb = p % NB;
+        float4v sum = partial[0][p][lane];
+        for (int w = 1; w < W; ++w) {
+            const float4v v = partial[w][p][lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum[e] += v[e];
+        }
+        // D layout: lane (r, q) holds tokens 4q .. 4q+3 of the token block for weight row r.
+        const int row = (block0 + b) * 16 + r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = 16 * tb + 4 * q + e;
+            if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(sum[e]);
+        }
+    }
+}
+
+template <int HB, int W, int RB, int NB, int STEPS>
+void launch_row_decode(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
+                       __half* out, int tokens, int n, int k, int padded, hipStream_t stream) {
+    const int blocks = (n + 15) / 16;
+    row_decode_gemm<HB, W, RB, NB, STEPS><<<(blocks + RB - 1) / RB, W * 64, 0, stream>>>(x, codes, high, scales, out,
+                                                                                        tokens, n, k, padded);
+}
+
 }  // namespace
 
 // Workspace of one MoE call (offsets in bytes, each section 256-byte aligned):
@@ -998,10 +917,23 @@ void moe_validate(int tokens, int top_k, int experts, int hidden, int inter) {
             "MoE routed rows exceed int32 geometry");
 }
 
+// Decode launch shapes, measured at the config-2 matrices (QKV 448 row blocks,
+// o_proj and down 320, gate+up 2176) at 1-24 tokens: 16 waves over two row
+// blocks for up to 384 blocks, 8 waves over two up to 1023 and over three
+// from 1024; two token blocks (17-31 tokens) take 8 waves over two.
+template <int HB>
+void row_decode_dispatch(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
+                         __half* out, int tokens, int n, int k, int padded, hipStream_t stream) {
+    const int blocks = (n + 15) / 16;
+    if (tokens > 16) launch_row_decode<HB, 8, 2, 2, 1>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+    else if (blocks <= 384) launch_row_decode<HB, 16, 2, 1, 1>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+    else if (blocks < 1024) launch_row_decode<HB, 8, 2, 1, 1>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+    else launch_row_decode<HB, 8, 3, 1, 1>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+}
+
 // Token count from which the W4/5/6A16 GEMM uses the prefill tiles (128 tokens
-// x 128 rows, measured faster than the 128-row x 64-token kernel from 32
-// tokens at the config-2 shapes; that kernel reads each weight once per 64
-// tokens).
+// x 128 rows, which read each weight once per 128 tokens; below it the decode
+// GEMM reads each weight once per 16 or 32 tokens).
 constexpr int kRowPrefillMinTokens = 32;
 
 void row_gemm_launch(const void* x, const void* codes, const void* high, const void* scales, void* out, int tokens,
@@ -1014,32 +946,21 @@ void row_gemm_launch(const void* x, const void* codes, const void* high, const v
     require(k % 8 == 0 && aligned(x, 16), "the W4/5/6A16 matrix-core route needs k % 8 == 0 and 16-byte aligned x");
     require(aligned(codes, 16) && aligned(scales, 4) && aligned(out, 2) && (bits == 4 || aligned(high, 16)),
             "misaligned Q4/Q5/Q6 operand");
-    Q4Gemm p{};
-    p.x = static_cast<const __half*>(x);
-    p.codes = static_cast<const std::uint8_t*>(codes);
-    p.high = static_cast<const std::uint8_t*>(high);
-    p.scales = static_cast<const __half*>(scales);
-    p.out = static_cast<__half*>(out);
-    p.tokens = tokens;
-    p.n = n;
-    p.k = k;
-    p.padded = padded;
-    p.x_stride = k;
-    p.out_stride = n;
-    p.experts = 1;
-    p.row_tiles = (n + kRows - 1) / kRows;
+    const auto* xp = static_cast<const __half*>(x);
+    const auto* cp = static_cast<const std::uint8_t*>(codes);
+    const auto* hp = static_cast<const std::uint8_t*>(high);
+    const auto* sp = static_cast<const __half*>(scales);
+    auto* op = static_cast<__half*>(out);
     if (tokens >= kRowPrefillMinTokens) {
         // Prefill: 128-token tiles that read each weight once per tile.
-        const auto* xp = static_cast<const __half*>(x);
-        auto* op = static_cast<__half*>(out);
-        if (bits == 4) launch_row_prefill<0, 4, 2, 2, 4, 2>(xp, p.codes, p.high, p.scales, op, tokens, n, k, padded, stream);
-        else if (bits == 5) launch_row_prefill<1, 4, 2, 2, 4, 2>(xp, p.codes, p.high, p.scales, op, tokens, n, k, padded, stream);
-        else launch_row_prefill<2, 4, 2, 2, 4, 2>(xp, p.codes, p.high, p.scales, op, tokens, n, k, padded, stream);
+        if (bits == 4) launch_row_prefill<0, 4, 2, 2, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
+        else if (bits == 5) launch_row_prefill<1, 4, 2, 2, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
+        else launch_row_prefill<2, 4, 2, 2, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
         return;
     }
-    if (bits == 4) launch_q4_mfma<kPlain, 0>(p, stream);
-    else if (bits == 5) launch_q4_mfma<kPlain, 1>(p, stream);
-    else launch_q4_mfma<kPlain, 2>(p, stream);
+    if (bits == 4) row_decode_dispatch<0>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
+    else if (bits == 5) row_decode_dispatch<1>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
+    else row_decode_dispatch<2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
 }
 
 // GW/GRB and DW/DRB: waves per workgroup and row blocks per wave of the
