@@ -162,6 +162,48 @@ def test_mfma_w4a16_tolerances(backend, device, shape, tokens):
         print(f"flips={int((diff > 0).sum())} of {tokens * n}", flush=True)
 
 
+@pytest.mark.parametrize("shape", [(1, 8), (37, 136), (300, 2048), (6200, 264), (16400, 136)])
+@pytest.mark.parametrize("tokens", [1, 5, 16, 24, 31])
+def test_tiled_decode_equals_row_major(backend, device, shape, tokens):
+    # Decode plans read the resident's tiled copy; the arithmetic and its order
+    # are those of venturi_q4_gemm_run on the row-major planes, so the bits match.
+    n, k = shape
+    print(f"case q4-tiled n={n} k={k} tokens={tokens}", flush=True)
+    w = random_q4(n, k, 900 + n + tokens, scale=0.02)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens + 3 * k)).half().to(device)
+    resident = backend.upload_linear(w, dtype=torch.float16, device=device)
+    plan = resident.prepare(tokens=tokens)
+    assert plan.route == "venturi-q4-mfma"
+    guard = torch.full((tokens * n + 2,), 47, dtype=torch.float16, device=device)
+    out = guard[1:-1].view(tokens, n)
+    plan.run(x, out=out)
+    want = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    dw = resident._payload.weight
+    backend._check(backend._native.venturi_q4_gemm_run(
+        x.data_ptr(), dw.codes.data_ptr(), dw.scales.data_ptr(), want.data_ptr(), tokens, n, k, dw.padded_k, 0,
+        torch.cuda.current_stream(device).cuda_stream))
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
+def test_tiled_decode_rejects_bad_arguments(backend, device):
+    lib = backend._native
+    resident = backend.upload_linear(random_q4(16, 128, 5), dtype=torch.float16, device=device)
+    resident.prepare(tokens=1)
+    tc, ts = resident._payload.tiled
+    x = torch.zeros(32, 128, dtype=torch.float16, device=device)
+    o = torch.empty(32, 16, dtype=torch.float16, device=device)
+    s = torch.cuda.current_stream(device).cuda_stream
+    assert lib.venturi_q4_tiled_run(x.data_ptr(), tc.data_ptr(), ts.data_ptr(), o.data_ptr(), 32, 16, 128, 128, 0, s) == -1
+    assert "1 to 31 tokens" in lib.error()
+    assert lib.venturi_q4_tiled_run(x.data_ptr(), tc.data_ptr(), ts.data_ptr(), o.data_ptr(), 1, 16, 128, 128, 1, s) == -1
+    assert "FP16" in lib.error()
+    assert lib.venturi_q4_tiled_run(x.data_ptr(), None, ts.data_ptr(), o.data_ptr(), 1, 16, 128, 128, 0, s) == -1
+    assert lib.venturi_q4_tiled_run(x.data_ptr(), tc.data_ptr(), ts.data_ptr(), o.data_ptr(), 1, 16, 128, 256, 0, s) == -1
+    torch.cuda.synchronize(device)
+
+
 def test_expert_abi_objects(device):
     """NativeQ4 (ops/flash_next_q4.py:17-89): prepare / linear / decode."""
     from venturi_amd.q4 import NativeQ4

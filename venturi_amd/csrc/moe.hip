@@ -735,6 +735,13 @@ void launch_row_prefill(const __half* x, const std::uint8_t* codes, const std::u
 // token r (interleave8), loaded only by lanes whose token exists. Chunks are
 // fetched in a two-deep ping-pong; partial tiles are summed across waves
 // through LDS in wave order and stored by one wave per (row block, token block).
+//
+// TILED (Q4 only) reads the decode copy built by q4.tile_q4 instead: codes
+// [row block][chunk][lane 16q + r][16 bytes] holding exactly the bytes lane
+// (r, q) reads from the row-major planes, and scales [row block][chunk][r][2]
+// (the chunk's two groups); each load is then one contiguous 1 KB (codes) or
+// 64-byte (scales) wave access. The arithmetic and its order are the same, so
+// both layouts give the same bits.
 template <int HB, int RB, int NB, int STEPS>
 struct RowDecodeBatch {
     uint4 w[STEPS][RB];
@@ -743,7 +750,7 @@ struct RowDecodeBatch {
     uint4 x[STEPS][NB][4];
 };
 
-template <int HB, int W, int RB, int NB, int STEPS>
+template <int HB, int W, int RB, int NB, int STEPS, bool TILED>
 __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restrict__ x,
                                                           const std::uint8_t* __restrict__ codes,
                                                           const std::uint8_t* __restrict__ high,
@@ -762,10 +769,17 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
     const std::uint8_t* hp[RB];
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
-        const std::int64_t row = min((block0 + b) * 16 + r, n - 1);  // clamped rows are never stored
-        cp[b] = codes + row * cstride + 16 * q;
-        sp[b] = reinterpret_cast<const std::uint32_t*>(scales + row * sstride);
-        hp[b] = HB ? high + row * hstride + 4 * HB * q : nullptr;
+        if constexpr (TILED) {
+            const std::int64_t blk = min(block0 + b, (n + 15) / 16 - 1);  // clamped blocks are never stored
+            cp[b] = codes + blk * chunks * 1024 + 16 * lane;
+            sp[b] = reinterpret_cast<const std::uint32_t*>(scales) + blk * chunks * 16 + r;
+            hp[b] = nullptr;
+        } else {
+            const std::int64_t row = min((block0 + b) * 16 + r, n - 1);  // clamped rows are never stored
+            cp[b] = codes + row * cstride + 16 * q;
+            sp[b] = reinterpret_cast<const std::uint32_t*>(scales + row * sstride);
+            hp[b] = HB ? high + row * hstride + 4 * HB * q : nullptr;
+        }
     }
     bool live[NB];
     const __half* xr[NB];
@@ -785,8 +799,8 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
             const int c = min(c0 + i * STEPS + st, c1 - 1);
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
-                t.w[st][b] = *reinterpret_cast<const uint4*>(cp[b] + 64 * c);
-                t.s[st][b] = sp[b][c];
+                t.w[st][b] = *reinterpret_cast<const uint4*>(cp[b] + (TILED ? 1024 : 64) * c);
+                t.s[st][b] = sp[b][TILED ? 16 * c : c];
                 if constexpr (HB > 0) {
 #pragma unroll
                     for (int h = 0; h < HB; ++h)
@@ -876,12 +890,13 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
     }
 }
 
-template <int HB, int W, int RB, int NB, int STEPS>
+template <int HB, int W, int RB, int NB, int STEPS, bool TILED>
 void launch_row_decode(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
                        __half* out, int tokens, int n, int k, int padded, hipStream_t stream) {
+    static_assert(!TILED || HB == 0, "the tiled decode copy is built for Q4 rows");
     const int blocks = (n + 15) / 16;
-    row_decode_gemm<HB, W, RB, NB, STEPS><<<(blocks + RB - 1) / RB, W * 64, 0, stream>>>(x, codes, high, scales, out,
-                                                                                        tokens, n, k, padded);
+    row_decode_gemm<HB, W, RB, NB, STEPS, TILED><<<(blocks + RB - 1) / RB, W * 64, 0, stream>>>(
+        x, codes, high, scales, out, tokens, n, k, padded);
 }
 
 }  // namespace
@@ -921,14 +936,18 @@ void moe_validate(int tokens, int top_k, int experts, int hidden, int inter) {
 // o_proj and down 320, gate+up 2176) at 1-24 tokens: 16 waves over two row
 // blocks for up to 384 blocks, 8 waves over two up to 1023 and over three
 // from 1024; two token blocks (17-31 tokens) take 8 waves over two.
-template <int HB>
+template <int HB, bool TILED = false>
 void row_decode_dispatch(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
                          __half* out, int tokens, int n, int k, int padded, hipStream_t stream) {
     const int blocks = (n + 15) / 16;
-    if (tokens > 16) launch_row_decode<HB, 8, 2, 2, 1>(x, codes, high, scales, out, tokens, n, k, padded, stream);
-    else if (blocks <= 384) launch_row_decode<HB, 16, 2, 1, 1>(x, codes, high, scales, out, tokens, n, k, padded, stream);
-    else if (blocks < 1024) launch_row_decode<HB, 8, 2, 1, 1>(x, codes, high, scales, out, tokens, n, k, padded, stream);
-    else launch_row_decode<HB, 8, 3, 1, 1>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+    if (tokens > 16)
+        launch_row_decode<HB, 8, 2, 2, 1, TILED>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+    else if (blocks <= 384)
+        launch_row_decode<HB, 16, 2, 1, 1, TILED>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+    else if (blocks < 1024)
+        launch_row_decode<HB, 8, 2, 1, 1, TILED>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+    else
+        launch_row_decode<HB, 8, 3, 1, 1, TILED>(x, codes, high, scales, out, tokens, n, k, padded, stream);
 }
 
 // Token count from which the W4/5/6A16 GEMM uses the prefill tiles (128 tokens
@@ -1054,6 +1073,25 @@ VT_EXPORT int venturi_q4_gemm_run(const void* x, const void* codes, const void* 
     return vt::guarded([&] {
         vt::row_gemm_launch(x, codes, nullptr, scales, out, tokens, n, k, padded, 4, dtype,
                             static_cast<hipStream_t>(stream));
+    });
+}
+
+// Extension: the W4A16 contract GEMM at decode token counts (1..31) over the
+// tiled decode copy of q4.tile_q4 (same arithmetic and bits as
+// venturi_q4_gemm_run on the row-major planes, contiguous wave loads).
+VT_EXPORT int venturi_q4_tiled_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n,
+                                   int k, int padded, int dtype, void* stream) {
+    return vt::guarded([&] {
+        vt::require(x && codes && scales && out, "null Q4 tiled operand");
+        vt::require(tokens > 0 && tokens < vt::kRowPrefillMinTokens, "the tiled Q4 decode takes 1 to 31 tokens");
+        vt::require(n > 0 && k > 0 && padded == vt::padded_k(k), "invalid Q4 geometry");
+        vt::require(dtype == vt::kF16, "the tiled Q4 decode takes FP16 activations");
+        vt::require(k % 8 == 0 && vt::aligned(x, 16), "the tiled Q4 decode needs k % 8 == 0 and 16-byte aligned x");
+        vt::require(vt::aligned(codes, 16) && vt::aligned(scales, 4) && vt::aligned(out, 2),
+                    "misaligned Q4 tiled operand");
+        vt::row_decode_dispatch<0, true>(static_cast<const __half*>(x), static_cast<const std::uint8_t*>(codes), nullptr,
+                                         static_cast<const __half*>(scales), static_cast<__half*>(out), tokens, n, k,
+                                         padded, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -58,6 +58,7 @@ SIGNATURES = {
     "venturi_q4_prepare": ([_I] * 5, _I),
     "venturi_q4_run": ([_P] * 4 + [_I] * 6 + [_P], _I),
     "venturi_q4_gemm_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
+    "venturi_q4_tiled_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
     "venturi_row_gemm_run": ([_P] * 5 + [_I] * 6 + [_P], _I),
     "venturi_rowcodec_prepare": ([_I] * 5 + [_P], _I),
     "venturi_rowcodec_workspace_bytes": ([_P, _I, _I], _U64),

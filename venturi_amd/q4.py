@@ -7,6 +7,7 @@ W4A16 weight value fp16(q * scale).
 """
 
 from dataclasses import dataclass
+from functools import cached_property
 from pathlib import Path
 
 import torch
@@ -16,12 +17,34 @@ from .blocks import _DTYPES, _no_overlap, _shape, _stream, _tensor
 from .weights import Q4RowSplitWeight
 
 # Plan routes of a resident Q4 linear:
-#   mfma    W4A16 contract (fp16(q*scale) weights) on fp16 matrix cores, any tokens;
+#   mfma    W4A16 contract (fp16(q*scale) weights) on fp16 matrix cores, any tokens
+#           (below DECODE_TILED_TOKENS over the resident's tiled decode copy);
 #   generic the plugin order of q4_linear.cu:21-56 (FP32 weights), fp16/bf16;
 #   exact   the expert order of flash_next_q4.cu:23-34 (fp16 weights), fp16, <= 64 tokens;
 #   fused   the research order of q4_fused.cuh:10-89 (FP32 weights), fp16.
 # auto: mfma for fp16 activations, generic for bf16.
 Q4_ROUTES = ("auto", "mfma", "generic", "exact", "fused")
+DECODE_TILED_TOKENS = 32
+
+
+def tile_q4(codes, scales):
+    """Tiled decode copy of row-major Q4 planes (read by ``venturi_q4_tiled_run``).
+
+    Codes [row block][chunk][lane l = 16q + r][16 bytes]: row r of the 16-row
+    block, code bytes 16q .. 16q+15 of the 128-column chunk (columns
+    128c + 32q .. +32). Scales [row block][chunk][r][2] fp16: the chunk's two
+    groups. Rows past n are zero codes and scales.
+    """
+    n, row_bytes = codes.shape
+    chunks = row_bytes // 64
+    blocks = (n + 15) // 16
+    c = torch.zeros((blocks * 16, row_bytes), dtype=torch.uint8, device=codes.device)
+    s = torch.zeros((blocks * 16, chunks * 2), dtype=torch.float16, device=codes.device)
+    c[:n] = codes
+    s[:n] = scales
+    tc = c.view(blocks, 16, chunks, 4, 16).permute(0, 2, 3, 1, 4).contiguous()
+    ts = s.view(blocks, 16, chunks, 2).permute(0, 2, 1, 3).contiguous()
+    return tc, ts
 
 
 def quantize_q4_rtn(weight, *, max_elements=16 * 2**20):
@@ -85,6 +108,11 @@ class ResidentQ4Linear:
     def storage_tensors(self):
         return (self.weight.codes, self.weight.scales)
 
+    @cached_property
+    def tiled(self):
+        """The tiled decode copy (``tile_q4``), built on first use by a decode plan."""
+        return tile_q4(self.weight.codes, self.weight.scales)
+
     @property
     def in_features(self):
         return self.weight.in_features
@@ -111,6 +139,8 @@ class ResidentQ4Linear:
         if route == "generic" and tokens > 4 * 65535:
             raise ValueError("The generic Q4 route takes at most 262140 tokens")
         self.backend.validate_device(self.dtype, self.device)
+        if route == "mfma" and tokens < DECODE_TILED_TOKENS:
+            self.tiled  # built once here, so that run allocates nothing
         return Q4LinearPlan(self, tokens, route)
 
     def decode(self, *, out, row=0):
@@ -162,7 +192,8 @@ class Q4LinearPlan:
 
     @property
     def storage_tensors(self):
-        return self.resident.storage_tensors
+        r = self.resident
+        return r.storage_tensors + (r.tiled if self.kernel == "mfma" and self.tokens < DECODE_TILED_TOKENS else ())
 
     def run(self, x, *, out, workspace=None):
         if workspace is not None:
@@ -170,11 +201,17 @@ class Q4LinearPlan:
         r = self.resident
         _tensor(x, (self.tokens, r.in_features), r.dtype, r.device, "x")
         _tensor(out, (self.tokens, r.out_features), r.dtype, r.device, "out")
-        _no_overlap(out, (x,) + r.storage_tensors)
+        _no_overlap(out, (x,) + self.storage_tensors)
         w, lib, stream = r.weight, r.backend._native, _stream(r.device)
         args = (x.data_ptr(), w.codes.data_ptr(), w.scales.data_ptr(), out.data_ptr())
         with torch.cuda.device(r.device):
-            if self.kernel == "mfma":
+            if self.kernel == "mfma" and self.tokens < DECODE_TILED_TOKENS:
+                tc, ts = r.tiled
+                status = lib.venturi_q4_tiled_run(
+                    x.data_ptr(), tc.data_ptr(), ts.data_ptr(), out.data_ptr(), self.tokens, w.out_features,
+                    w.in_features, w.padded_k, _DTYPES[r.dtype], stream
+                )
+            elif self.kernel == "mfma":
                 status = lib.venturi_q4_gemm_run(
                     *args, self.tokens, w.out_features, w.in_features, w.padded_k, _DTYPES[r.dtype], stream
                 )
