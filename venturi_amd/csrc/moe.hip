@@ -89,6 +89,39 @@ __device__ __forceinline__ half8 dequant8_biased(std::uint32_t u, half2v s2) {
     return w;
 }
 
+// dequant8_biased with its three bit constants held in registers: a VOP3
+// v_and_or_b32 takes no literal, so with literal constants the compiler splits
+// each mask-and-or into two instructions (17 instead of 13 per word).
+struct BiasedMasks {
+    std::uint32_t lo, hi, one;  // 0x000F000F, 0x00F000F0, 0x64006400
+};
+
+__device__ __forceinline__ BiasedMasks biased_masks() {
+    BiasedMasks m{0x000F000Fu, 0x00F000F0u, 0x64006400u};
+    asm volatile("" : "+v"(m.lo), "+v"(m.hi), "+v"(m.one));  // opaque: kept in VGPRs, not re-folded to literals
+    return m;
+}
+
+__device__ __forceinline__ half8 dequant8_biased(std::uint32_t u, half2v s2, const BiasedMasks& m) {
+    const std::uint32_t v = u >> 8;
+    const half2v lo_bias = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const half2v sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+    const half2v hi_bias = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+    const half2v a = __builtin_bit_cast(half2v, (u & m.lo) | m.one);
+    const half2v b = __builtin_bit_cast(half2v, (u & m.hi) | m.one);
+    const half2v c = __builtin_bit_cast(half2v, (v & m.lo) | m.one);
+    const half2v d = __builtin_bit_cast(half2v, (v & m.hi) | m.one);
+    const half2v q[4] = {a + lo_bias, b * sixteenth + hi_bias, c + lo_bias, d * sixteenth + hi_bias};  // exact
+    half8 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v x = q[i] * s2;  // one fp16 rounding of q * s
+        w[2 * i] = x[0];
+        w[2 * i + 1] = x[1];
+    }
+    return w;
+}
+
 // Eight consecutive activations x0..x7 -> x0, x4, x1, x5, x2, x6, x3, x7
 // (the column order of dequant8_biased).
 __device__ __forceinline__ uint4 interleave_biased(uint4 v) {
@@ -732,15 +765,20 @@ void launch_row_prefill(const __half* x, const std::uint8_t* codes, const std::u
 // the chunk and, for Q5/Q6, the 4 * HB high-plane bytes of those columns. The
 // four code words become four half8 B fragments (dequant8 order) for four
 // v_mfma_f32_16x16x32_f16 whose A fragments are the matching activations of
-// token r (interleave8), loaded only by lanes whose token exists. Chunks are
+// token r (interleave8); lanes of absent tokens load the last token's row and
+// feed output rows that are never stored. Chunks are
 // fetched in a two-deep ping-pong; partial tiles are summed across waves
 // through LDS in wave order and stored by one wave per (row block, token block).
 //
 // TILED (Q4 only) reads the decode copy built by q4.tile_q4 instead: codes
-// [row block][chunk][lane 16q + r][16 bytes] holding exactly the bytes lane
-// (r, q) reads from the row-major planes, and scales [row block][chunk][r][2]
-// (the chunk's two groups); each load is then one contiguous 1 KB (codes) or
-// 64-byte (scales) wave access. The arithmetic and its order are the same, so
+// [row block][chunk][lane 16q + r][16 bytes] holding the code bytes lane (r, q)
+// reads from the row-major planes, and scales [row block][chunk][r][2] (the
+// chunk's two groups); each load is then one contiguous 1 KB (codes) or
+// 64-byte (scales) wave access. The copy stores each word's nibbles pre-biased
+// (q + 8) and reordered (nibble j holds column 2j, nibble 4 + j column 2j + 1)
+// so that dequant8_biased yields the eight columns in natural order: the
+// activation fragments need no interleave. Every product and sum is the same
+// as in the row-major path (the MFMA's k slots hold the same column pairs), so
 // both layouts give the same bits.
 template <int HB, int RB, int NB, int STEPS>
 struct RowDecodeBatch {
@@ -781,14 +819,11 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
             hp[b] = HB ? high + row * hstride + 4 * HB * q : nullptr;
         }
     }
-    bool live[NB];
     const __half* xr[NB];
 #pragma unroll
-    for (int tb = 0; tb < NB; ++tb) {
-        const int t = 16 * tb + r;
-        live[tb] = t < tokens;
-        xr[tb] = x + static_cast<std::int64_t>(min(t, tokens - 1)) * k + 32 * q;
-    }
+    for (int tb = 0; tb < NB; ++tb)
+        xr[tb] = x + static_cast<std::int64_t>(min(16 * tb + r, tokens - 1)) * k + 32 * q;
+    const BiasedMasks masks = biased_masks();
     using Batch = RowDecodeBatch<HB, RB, NB, STEPS>;
     const int batches = (c1 - c0 + STEPS - 1) / STEPS;
     // Batch i holds chunks c0 + i * STEPS + s; chunks past c1 are clamped to c1 - 1
@@ -807,15 +842,28 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
                         t.h[st][b][h] = reinterpret_cast<const std::uint32_t*>(hp[b] + 16 * HB * c)[h];
                 }
             }
-            const int col = 128 * c + 32 * q;  // k % 8 == 0: a fragment is all in or all out
+            // A chunk wholly inside k loads every lane's fragments unmasked: lanes of
+            // absent tokens read the last token's row (valid memory) and feed only
+            // output rows that are never stored. The chunk that crosses k
+            // (k % 128 != 0) zeroes columns at or past k (k % 8 == 0: a fragment is
+            // all in or all out).
+            const int col = 128 * c + 32 * q;
+            if (128 * c + 128 <= k) {
 #pragma unroll
-            for (int tb = 0; tb < NB; ++tb)
+                for (int tb = 0; tb < NB; ++tb)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-                    if (live[tb] && col + 8 * j < k) v = *reinterpret_cast<const uint4*>(xr[tb] + 128 * c + 8 * j);
-                    t.x[st][tb][j] = v;
-                }
+                    for (int j = 0; j < 4; ++j)
+                        t.x[st][tb][j] = *reinterpret_cast<const uint4*>(xr[tb] + 128 * c + 8 * j);
+            } else {
+#pragma unroll
+                for (int tb = 0; tb < NB; ++tb)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+                        if (col + 8 * j < k) v = *reinterpret_cast<const uint4*>(xr[tb] + 128 * c + 8 * j);
+                        t.x[st][tb][j] = v;
+                    }
+            }
         }
     };
     float4v acc[RB][NB];
@@ -831,7 +879,8 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
 #pragma unroll
         for (int tb = 0; tb < NB; ++tb)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) fa[tb][j] = __builtin_bit_cast(half8, interleave8(t.x[st][tb][j]));
+            for (int j = 0; j < 4; ++j)
+                fa[tb][j] = __builtin_bit_cast(half8, TILED ? t.x[st][tb][j] : interleave8(t.x[st][tb][j]));
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             // Columns 32q .. 32q+31 of the chunk lie in its group q / 2.
@@ -841,7 +890,9 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 half8 wf;
-                if constexpr (HB == 0) {
+                if constexpr (TILED) {
+                    wf = dequant8_biased(words[j], s2, masks);
+                } else if constexpr (HB == 0) {
                     wf = dequant8(words[j], s2);
                 } else {
                     // Word j's eight columns own bits 8 * HB * j .. of the lane's 32 * HB.

@@ -31,16 +31,22 @@ def tile_q4(codes, scales):
     """Tiled decode copy of row-major Q4 planes (read by ``venturi_q4_tiled_run``).
 
     Codes [row block][chunk][lane l = 16q + r][16 bytes]: row r of the 16-row
-    block, code bytes 16q .. 16q+15 of the 128-column chunk (columns
-    128c + 32q .. +32). Scales [row block][chunk][r][2] fp16: the chunk's two
-    groups. Rows past n are zero codes and scales.
+    block, columns 128c + 32q .. +32 of the chunk (the bytes 16q .. 16q+15 of
+    the row-major chunk). Inside each 4-byte word (8 columns c .. c+7) the
+    nibbles are stored biased (q + 8) and reordered: nibble j holds column
+    c + 2j, nibble 4 + j column c + 2j + 1, the order in which the kernel's
+    mask-and-or dequant yields natural column order. Scales [row block][chunk]
+    [r][2] fp16: the chunk's two groups. Rows past n are zero.
     """
     n, row_bytes = codes.shape
     chunks = row_bytes // 64
     blocks = (n + 15) // 16
+    nib = torch.stack((codes & 15, codes >> 4), -1).reshape(n, row_bytes // 4, 8) ^ 8  # biased, column order
+    nib = nib[:, :, [0, 2, 4, 6, 1, 3, 5, 7]].reshape(n, row_bytes, 2)
+    packed = nib[..., 0] | (nib[..., 1] << 4)
     c = torch.zeros((blocks * 16, row_bytes), dtype=torch.uint8, device=codes.device)
     s = torch.zeros((blocks * 16, chunks * 2), dtype=torch.float16, device=codes.device)
-    c[:n] = codes
+    c[:n] = packed
     s[:n] = scales
     tc = c.view(blocks, 16, chunks, 4, 16).permute(0, 2, 3, 1, 4).contiguous()
     ts = s.view(blocks, 16, chunks, 2).permute(0, 2, 1, 3).contiguous()
