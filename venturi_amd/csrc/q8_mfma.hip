@@ -323,15 +323,25 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_decode(const __half* __restri
 #pragma unroll
         for (int s = 0; s < STEPS; ++s) {
             const int col = min(c0 + i * STEPS + s, c1 - 1) * 64;
+            if (col + 64 <= k) {
+                // Inside k every lane loads unmasked: lanes of absent tokens read
+                // the last token's row and feed only output rows never stored.
 #pragma unroll
-            for (int tb = 0; tb < NB; ++tb) {
-                uint4 a = make_uint4(0u, 0u, 0u, 0u), bq = make_uint4(0u, 0u, 0u, 0u);
-                if (live[tb]) {
-                    a = *reinterpret_cast<const uint4*>(xrow[tb] + min(col, k - 8 - 8 * q));
-                    bq = *reinterpret_cast<const uint4*>(xrow[tb] + min(col + 32, k - 8 - 8 * q));
+                for (int tb = 0; tb < NB; ++tb) {
+                    t.xa[s][tb] = *reinterpret_cast<const uint4*>(xrow[tb] + col);
+                    t.xb[s][tb] = *reinterpret_cast<const uint4*>(xrow[tb] + col + 32);
                 }
-                t.xa[s][tb] = a;
-                t.xb[s][tb] = bq;
+            } else {
+#pragma unroll
+                for (int tb = 0; tb < NB; ++tb) {
+                    uint4 a = make_uint4(0u, 0u, 0u, 0u), bq = make_uint4(0u, 0u, 0u, 0u);
+                    if (live[tb]) {
+                        a = *reinterpret_cast<const uint4*>(xrow[tb] + min(col, k - 8 - 8 * q));
+                        bq = *reinterpret_cast<const uint4*>(xrow[tb] + min(col + 32, k - 8 - 8 * q));
+                    }
+                    t.xa[s][tb] = a;
+                    t.xb[s][tb] = bq;
+                }
             }
         }
     };
@@ -349,12 +359,14 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_decode(const __half* __restri
             const int ch = c0 + i * STEPS + s;
             if (ch >= c1) break;
             const int col = ch * 64 + 8 * q;
+            const bool inside = ch * 64 + 64 <= k;  // wave-uniform
             half8 fa[NB], fb[NB];
 #pragma unroll
             for (int tb = 0; tb < NB; ++tb) {
-                // Columns at or past k are zero (the clamped load read other columns).
-                fa[tb] = col < k ? __builtin_bit_cast(half8, t.xa[s][tb]) : half8{};
-                fb[tb] = col + 32 < k ? __builtin_bit_cast(half8, t.xb[s][tb]) : half8{};
+                // In the chunk that crosses k, columns at or past k are zero (the
+                // clamped load read other columns).
+                fa[tb] = inside || col < k ? __builtin_bit_cast(half8, t.xa[s][tb]) : half8{};
+                fb[tb] = inside || col + 32 < k ? __builtin_bit_cast(half8, t.xb[s][tb]) : half8{};
             }
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
