@@ -226,13 +226,19 @@ int venturi_q4_gemm_run(const void* x, const void* codes, const void* scales, vo
 
 /* Extension: the same contract GEMM at decode token counts (1..31) over the
  * tiled decode copy of the planes (q4.tile_q4: codes [ceil(n/16)][padded/128]
- * [64 lanes][16 bytes], scales [ceil(n/16)][padded/128][16][2] fp16, rows
- * past n zero); fp16 activations, k % 8 == 0, x and codes 16-byte aligned,
- * scales 4-byte aligned. Outputs have the bits of venturi_q4_gemm_run on the
- * row-major planes. No counterpart in the reference (which streams its Q4
- * shadow through cuBLAS); for callers that decode from a resident tiled copy. */
+ * [64 lanes][16 bytes] of biased, reordered nibbles, scales
+ * [ceil(n/16)][padded/128][16][2] fp16, rows past n zero); fp16 activations,
+ * k % 8 == 0, x and codes 16-byte aligned, scales 4-byte aligned. Shapes that
+ * split K over two workgroups (venturi_q4_tiled_workspace_bytes > 0) need a
+ * slot buffer of that size, put idle once by venturi_q4_tiled_workspace_init;
+ * calls sharing it run on one stream. Unsplit shapes give the bits of
+ * venturi_q4_gemm_run on the row-major planes. No counterpart in the reference
+ * (which streams its Q4 shadow through cuBLAS); for callers that decode from a
+ * resident tiled copy. */
+uint64_t venturi_q4_tiled_workspace_bytes(int tokens, int n, int k);
+int venturi_q4_tiled_workspace_init(void* workspace, uint64_t bytes, void* stream);
 int venturi_q4_tiled_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
-                         int padded, int dtype, void* stream);
+                         int padded, int dtype, void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* Extension: the same contract GEMM for 4-, 5- and 6-bit row codecs (bits
  * 4/5/6; `high` = the q5/q6 high plane [n][padded*(bits-4)/8], 16-byte

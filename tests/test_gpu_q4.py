@@ -195,13 +195,61 @@ def test_tiled_decode_rejects_bad_arguments(backend, device):
     x = torch.zeros(32, 128, dtype=torch.float16, device=device)
     o = torch.empty(32, 16, dtype=torch.float16, device=device)
     s = torch.cuda.current_stream(device).cuda_stream
-    assert lib.venturi_q4_tiled_run(x.data_ptr(), tc.data_ptr(), ts.data_ptr(), o.data_ptr(), 32, 16, 128, 128, 0, s) == -1
+    args = (x.data_ptr(), tc.data_ptr(), ts.data_ptr(), o.data_ptr())
+    assert lib.venturi_q4_tiled_run(*args, 32, 16, 128, 128, 0, None, 0, s) == -1
     assert "1 to 31 tokens" in lib.error()
-    assert lib.venturi_q4_tiled_run(x.data_ptr(), tc.data_ptr(), ts.data_ptr(), o.data_ptr(), 1, 16, 128, 128, 1, s) == -1
+    assert lib.venturi_q4_tiled_run(*args, 1, 16, 128, 128, 1, None, 0, s) == -1
     assert "FP16" in lib.error()
-    assert lib.venturi_q4_tiled_run(x.data_ptr(), None, ts.data_ptr(), o.data_ptr(), 1, 16, 128, 128, 0, s) == -1
-    assert lib.venturi_q4_tiled_run(x.data_ptr(), tc.data_ptr(), ts.data_ptr(), o.data_ptr(), 1, 16, 128, 256, 0, s) == -1
+    assert lib.venturi_q4_tiled_run(x.data_ptr(), None, ts.data_ptr(), o.data_ptr(), 1, 16, 128, 128, 0, None, 0, s) == -1
+    assert lib.venturi_q4_tiled_run(*args, 1, 16, 128, 256, 0, None, 0, s) == -1
+    # A shape that splits K (<= 384 row blocks, >= 64 chunks) refuses to run without its slots.
+    assert lib.venturi_q4_tiled_workspace_bytes(3, 16, 8192) == 3 * 1 * 8 * 8
+    assert lib.venturi_q4_tiled_workspace_bytes(3, 16, 8064) == 0  # 63 chunks: unsplit
+    assert lib.venturi_q4_tiled_workspace_bytes(17, 16, 8192) == 0  # two token blocks: unsplit
+    assert lib.venturi_q4_tiled_workspace_bytes(3, 6160, 8192) == 0  # 385 row blocks: unsplit
+    assert lib.venturi_q4_tiled_run(*args, 1, 16, 8192, 8192, 0, None, 0, s) == -1
+    assert "slot buffer" in lib.error()
     torch.cuda.synchronize(device)
+
+
+@pytest.mark.parametrize("shape", [(16, 8192), (130, 8320), (5120, 17408)])
+@pytest.mark.parametrize("tokens", [1, 3, 16])
+def test_tiled_decode_split_k(backend, device, shape, tokens):
+    # Shapes that split K over two workgroups: the two halves meet in fp32 (an
+    # order-free add), so outputs are deterministic and graph replays agree; the
+    # W4A16 contract bound against FP64 holds, and the plan's slots end idle.
+    n, k = shape
+    print(f"case q4-tiled-split n={n} k={k} tokens={tokens}", flush=True)
+    w = random_q4(n, k, 300 + n + tokens, scale=0.02)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(5 * tokens + k)).half()
+    resident = backend.upload_linear(w, dtype=torch.float16, device=device)
+    plan = resident.prepare(tokens=tokens)
+    slots = plan._plan.slots if hasattr(plan, "_plan") else plan.slots
+    assert slots is not None and slots.numel() == tokens * ((n + 15) // 16) * 64
+    idle = slots.clone()
+    xd_dev = x.to(device)
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    plan.run(xd_dev, out=out)
+    again = torch.empty_like(out)
+    plan.run(xd_dev, out=again)
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    assert torch.equal(slots, idle)
+    graph_out = torch.empty_like(out)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        plan.run(xd_dev, out=graph_out)
+    for _ in range(3):
+        graph_out.fill_(0)
+        g.replay()
+        torch.cuda.synchronize(device)
+        assert torch.equal(graph_out.view(torch.int16), out.view(torch.int16))
+    codes, scales = planes(w)
+    wd = oracle.q4_decode_fp16(codes, scales, k).astype(np.float64)
+    xd = x.float().numpy().astype(np.float64)
+    exact = xd @ wd.T
+    got = out.cpu().float().numpy().astype(np.float64)
+    bound = 0.5 * ulp16(exact) + 2.0**-19 * (np.abs(xd) @ np.abs(wd).T)
+    assert (np.abs(got - exact) <= bound).all()
 
 
 def test_expert_abi_objects(device):

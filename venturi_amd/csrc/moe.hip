@@ -788,19 +788,29 @@ struct RowDecodeBatch {
     uint4 x[STEPS][NB][4];
 };
 
-template <int HB, int W, int RB, int NB, int STEPS, bool TILED>
+// Idle pattern of a split-K exchange slot: two signalling NaNs, which no
+// arithmetic result takes.
+constexpr unsigned long long kRowSlotEmpty = 0x7f8000017f800001ull;
+
+template <int HB, int W, int RB, int NB, int STEPS, bool TILED, int KS>
 __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restrict__ x,
                                                           const std::uint8_t* __restrict__ codes,
                                                           const std::uint8_t* __restrict__ high,
                                                           const __half* __restrict__ scales, __half* __restrict__ out,
-                                                          int tokens, int n, int k, int padded) {
+                                                          unsigned long long* __restrict__ slots, int tokens, int n,
+                                                          int k, int padded) {
     __shared__ float4v partial[W][RB * NB][64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r = lane & 15;
-    const int block0 = blockIdx.x * RB;
+    const int block0 = static_cast<int>(blockIdx.x / KS) * RB;
     const int chunks = padded / 128;
-    const int c0 = wave * chunks / W, c1 = (wave + 1) * chunks / W;
+    // KS == 2: workgroups 2g and 2g + 1 take the first and second half of the
+    // chunks of row-block group g; the W waves split that range evenly.
+    const int kper = (chunks + KS - 1) / KS;
+    const int k0 = KS == 1 ? 0 : min(static_cast<int>(blockIdx.x % KS) * kper, chunks);
+    const int k1 = KS == 1 ? chunks : min(k0 + kper, chunks);
+    const int c0 = k0 + wave * (k1 - k0) / W, c1 = k0 + (wave + 1) * (k1 - k0) / W;
     const std::int64_t cstride = padded / 2, sstride = padded / 64, hstride = padded * HB / 8;
     const std::uint8_t* cp[RB];
     const std::uint32_t* sp[RB];
@@ -932,22 +942,60 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
             for (int e = 0; e < 4; ++e) sum[e] += v[e];
         }
         // D layout: lane (r, q) holds tokens 4q .. 4q+3 of the token block for weight row r.
-        const int row = (block0 + b) * 16 + r;
+        const int blk = block0 + b, row = blk * 16 + r;
+        if constexpr (KS == 1) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int t = 16 * tb + 4 * q + e;
-            if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(sum[e]);
+            for (int e = 0; e < 4; ++e) {
+                const int t = 16 * tb + 4 * q + e;
+                if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(sum[e]);
+            }
+        } else {
+            // Pairwise exchange of the two K halves through a 64-bit slot per
+            // (token, block, row pair r, r + 8): the first half leaves its pair, the
+            // second adds (two fp32 terms: the result does not depend on the
+            // arrival order), stores and returns the slot to idle. Only the slot is
+            // shared, so no fence is needed, and every call leaves the slots idle.
+            const int blocks = (n + 15) / 16;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float mine = sum[e];
+                const float partner = __shfl_xor(mine, 8, 64);
+                const int t = 16 * tb + 4 * q + e;
+                if (r < 8 && t < tokens && blk < blocks) {
+                    unsigned long long* slot = slots + (static_cast<std::int64_t>(t) * blocks + blk) * 8 + r;
+                    const unsigned long long packed =
+                        (static_cast<unsigned long long>(__float_as_uint(partner)) << 32) | __float_as_uint(mine);
+                    const unsigned long long old =
+                        __hip_atomic_exchange(slot, packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (old != kRowSlotEmpty) {
+                        __hip_atomic_store(slot, kRowSlotEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const float lo = mine + __uint_as_float(static_cast<std::uint32_t>(old));
+                        const float hi = partner + __uint_as_float(static_cast<std::uint32_t>(old >> 32));
+                        __half* o = out + static_cast<std::int64_t>(t) * n;
+                        if (row < n) o[row] = from_f32<__half>(lo);
+                        if (row + 8 < n) o[row + 8] = from_f32<__half>(hi);
+                    }
+                }
+            }
         }
     }
 }
 
-template <int HB, int W, int RB, int NB, int STEPS, bool TILED>
+__global__ void fill_row_slots(unsigned long long* __restrict__ slots, std::size_t count) {
+    for (std::size_t i = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; i < count;
+         i += static_cast<std::size_t>(gridDim.x) * blockDim.x)
+        slots[i] = kRowSlotEmpty;
+}
+
+template <int HB, int W, int RB, int NB, int STEPS, bool TILED, int KS = 1>
 void launch_row_decode(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
-                       __half* out, int tokens, int n, int k, int padded, hipStream_t stream) {
+                       __half* out, int tokens, int n, int k, int padded, hipStream_t stream,
+                       unsigned long long* slots = nullptr) {
     static_assert(!TILED || HB == 0, "the tiled decode copy is built for Q4 rows");
+    require(KS == 1 || slots, "a split decode needs its slot buffer");
     const int blocks = (n + 15) / 16;
-    row_decode_gemm<HB, W, RB, NB, STEPS, TILED><<<(blocks + RB - 1) / RB, W * 64, 0, stream>>>(
-        x, codes, high, scales, out, tokens, n, k, padded);
+    row_decode_gemm<HB, W, RB, NB, STEPS, TILED, KS><<<(blocks + RB - 1) / RB * KS, W * 64, 0, stream>>>(
+        x, codes, high, scales, out, slots, tokens, n, k, padded);
 }
 
 }  // namespace
@@ -987,11 +1035,29 @@ void moe_validate(int tokens, int top_k, int experts, int hidden, int inter) {
 // o_proj and down 320, gate+up 2176) at 1-24 tokens: 16 waves over two row
 // blocks for up to 384 blocks, 8 waves over two up to 1023 and over three
 // from 1024; two token blocks (17-31 tokens) take 8 waves over two.
+// The tiled Q4 decode splits K over two workgroups (8 waves over 3 row blocks
+// each, slots exchanged pairwise) for up to 384 row blocks with at least 64
+// chunks of 128 columns: there the unsplit grid leaves most CUs with one long
+// workgroup (down 17408 -> 5120: 16.4 -> 14.3 us at one token, 24.1 -> 18.8 at
+// 16); with shorter K (o_proj, 48 chunks) the split measured no faster.
+bool row_decode_splits(int tokens, int n, int padded) {
+    return tokens <= 16 && (n + 15) / 16 <= 384 && padded / 128 >= 64;
+}
+
+std::uint64_t row_decode_slot_bytes(int tokens, int n, int padded) {
+    return row_decode_splits(tokens, n, padded)
+               ? static_cast<std::uint64_t>(tokens) * ((n + 15) / 16) * 8 * sizeof(unsigned long long)
+               : 0;
+}
+
 template <int HB, bool TILED = false>
 void row_decode_dispatch(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
-                         __half* out, int tokens, int n, int k, int padded, hipStream_t stream) {
+                         __half* out, int tokens, int n, int k, int padded, hipStream_t stream,
+                         unsigned long long* slots = nullptr) {
     const int blocks = (n + 15) / 16;
-    if (tokens > 16)
+    if (TILED && row_decode_splits(tokens, n, padded))
+        launch_row_decode<HB, 8, 3, 1, 1, TILED, 2>(x, codes, high, scales, out, tokens, n, k, padded, stream, slots);
+    else if (tokens > 16)
         launch_row_decode<HB, 8, 2, 2, 1, TILED>(x, codes, high, scales, out, tokens, n, k, padded, stream);
     else if (blocks <= 384)
         launch_row_decode<HB, 16, 2, 1, 1, TILED>(x, codes, high, scales, out, tokens, n, k, padded, stream);
@@ -1127,11 +1193,32 @@ VT_EXPORT int venturi_q4_gemm_run(const void* x, const void* codes, const void* 
     });
 }
 
+// Extension: exchange-slot bytes of venturi_q4_tiled_run (0 when the shape
+// does not split K).
+VT_EXPORT std::uint64_t venturi_q4_tiled_workspace_bytes(int tokens, int n, int k) {
+    if (tokens <= 0 || n <= 0 || k <= 0) return 0;
+    return vt::row_decode_slot_bytes(tokens, n, static_cast<int>(vt::padded_k(k)));
+}
+
+// Extension: puts a slot buffer in its idle state (once, before the first run;
+// every run leaves its slots idle again).
+VT_EXPORT int venturi_q4_tiled_workspace_init(void* workspace, std::uint64_t bytes, void* stream) {
+    return vt::guarded([&] {
+        vt::require(workspace && vt::aligned(workspace, 8) && bytes % 8 == 0, "invalid Q4 slot buffer");
+        const std::size_t count = bytes / 8;
+        if (count)
+            vt::fill_row_slots<<<static_cast<unsigned>(std::min<std::size_t>((count + 255) / 256, 1024)), 256, 0,
+                                 static_cast<hipStream_t>(stream)>>>(static_cast<unsigned long long*>(workspace),
+                                                                     count);
+    });
+}
+
 // Extension: the W4A16 contract GEMM at decode token counts (1..31) over the
-// tiled decode copy of q4.tile_q4 (same arithmetic and bits as
-// venturi_q4_gemm_run on the row-major planes, contiguous wave loads).
+// tiled decode copy of q4.tile_q4 (contiguous wave loads; without a K split
+// the same arithmetic and bits as venturi_q4_gemm_run on the row-major planes).
 VT_EXPORT int venturi_q4_tiled_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n,
-                                   int k, int padded, int dtype, void* stream) {
+                                   int k, int padded, int dtype, void* workspace, std::uint64_t workspace_bytes,
+                                   void* stream) {
     return vt::guarded([&] {
         vt::require(x && codes && scales && out, "null Q4 tiled operand");
         vt::require(tokens > 0 && tokens < vt::kRowPrefillMinTokens, "the tiled Q4 decode takes 1 to 31 tokens");
@@ -1140,9 +1227,13 @@ VT_EXPORT int venturi_q4_tiled_run(const void* x, const void* codes, const void*
         vt::require(k % 8 == 0 && vt::aligned(x, 16), "the tiled Q4 decode needs k % 8 == 0 and 16-byte aligned x");
         vt::require(vt::aligned(codes, 16) && vt::aligned(scales, 4) && vt::aligned(out, 2),
                     "misaligned Q4 tiled operand");
+        const std::uint64_t need = vt::row_decode_slot_bytes(tokens, n, padded);
+        vt::require(workspace_bytes >= need && (need == 0 || (workspace && vt::aligned(workspace, 8))),
+                    "the Q4 tiled decode needs its slot buffer (venturi_q4_tiled_workspace_bytes)");
         vt::row_decode_dispatch<0, true>(static_cast<const __half*>(x), static_cast<const std::uint8_t*>(codes), nullptr,
                                          static_cast<const __half*>(scales), static_cast<__half*>(out), tokens, n, k,
-                                         padded, static_cast<hipStream_t>(stream));
+                                         padded, static_cast<hipStream_t>(stream),
+                                         need ? static_cast<unsigned long long*>(workspace) : nullptr);
     });
 }
 

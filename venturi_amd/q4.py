@@ -145,9 +145,20 @@ class ResidentQ4Linear:
         if route == "generic" and tokens > 4 * 65535:
             raise ValueError("The generic Q4 route takes at most 262140 tokens")
         self.backend.validate_device(self.dtype, self.device)
+        slots = None
         if route == "mfma" and tokens < DECODE_TILED_TOKENS:
             self.tiled  # built once here, so that run allocates nothing
-        return Q4LinearPlan(self, tokens, route)
+            lib = self.backend._native
+            size = int(lib.venturi_q4_tiled_workspace_bytes(tokens, self.out_features, self.in_features))
+            if size:
+                # A decode that splits K exchanges its halves through slots the
+                # plan owns; every run leaves them idle, so runs of one plan must
+                # be ordered (one stream), and concurrent streams prepare a plan each.
+                slots = torch.empty(size, dtype=torch.uint8, device=self.device)
+                with torch.cuda.device(self.device):
+                    self.backend._check(lib.venturi_q4_tiled_workspace_init(slots.data_ptr(), size,
+                                                                              _stream(self.device)))
+        return Q4LinearPlan(self, tokens, route, slots)
 
     def decode(self, *, out, row=0):
         """fp16 rows fp16(q * scale) of [row, row + len(out)) into ``out`` (blocks.cu:1077-1086)."""
@@ -174,6 +185,7 @@ class Q4LinearPlan:
     resident: ResidentQ4Linear
     tokens: int
     kernel: str
+    slots: object = None  # exchange slots of a decode that splits K (plan-owned)
     workspace_bytes = 0
 
     @property
@@ -213,9 +225,11 @@ class Q4LinearPlan:
         with torch.cuda.device(r.device):
             if self.kernel == "mfma" and self.tokens < DECODE_TILED_TOKENS:
                 tc, ts = r.tiled
+                slots = self.slots
                 status = lib.venturi_q4_tiled_run(
                     x.data_ptr(), tc.data_ptr(), ts.data_ptr(), out.data_ptr(), self.tokens, w.out_features,
-                    w.in_features, w.padded_k, _DTYPES[r.dtype], stream
+                    w.in_features, w.padded_k, _DTYPES[r.dtype], None if slots is None else slots.data_ptr(),
+                    0 if slots is None else slots.numel(), stream
                 )
             elif self.kernel == "mfma":
                 status = lib.venturi_q4_gemm_run(
