@@ -109,17 +109,49 @@ __global__ __launch_bounds__(256) void a8_quantize(const __half* __restrict__ x,
 // two-level tree; inv = 1/sqrt(sum/k + eps) with IEEE division and square
 // root. (The reference uses rsqrtf, an approximation its tests pin only by
 // tolerance; this library fixes the correctly rounded form.)
+// Four consecutive 16-bit values as f32, one 8-byte load (p 8-byte aligned).
 template <class T>
-__device__ __forceinline__ float row_inverse_rms(const T* src, int k, float epsilon, int lane) {
+__device__ __forceinline__ void load4_f32(const T* p, float (&v)[4]) {
+    if constexpr (sizeof(T) == 2) {
+        const uint2 u = *reinterpret_cast<const uint2*>(p);
+        const unsigned short h[4] = {static_cast<unsigned short>(u.x), static_cast<unsigned short>(u.x >> 16),
+                                     static_cast<unsigned short>(u.y), static_cast<unsigned short>(u.y >> 16)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = to_f32(__builtin_bit_cast(T, h[i]));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = to_f32(p[i]);  // (rows_vec4 keeps wider types off this path)
+    }
+}
+
+// Whether a row's four-value pieces can be read as 8-byte words: rows start
+// 8-byte aligned when k % 4 == 0 and the base is.
+template <class T>
+__device__ __forceinline__ bool rows_vec4(const T* base, int k) {
+    return sizeof(T) == 2 && k % 4 == 0 && (reinterpret_cast<std::uintptr_t>(base) & 7) == 0;
+}
+
+template <class T>
+__device__ __forceinline__ float row_inverse_rms(const T* src, int k, float epsilon, int lane, bool vec) {
     float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Unrolled so that several pieces of the row are in flight at once; each
+    // chain a[v] still runs over base in ascending order.
+#pragma unroll 8
     for (int base = 0; base < k; base += 256) {
         const int col = base + 4 * lane;
+        if (vec && col + 3 < k) {
+            float xv[4];
+            load4_f32(src + col, xv);
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-            if (col + v < k) {
-                const float x = to_f32(src[col + v]);
-                a[v] = fmaf(x, x, a[v]);
-            }
+            for (int v = 0; v < 4; ++v) a[v] = fmaf(xv[v], xv[v], a[v]);
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (col + v < k) {
+                    const float x = to_f32(src[col + v]);
+                    a[v] = fmaf(x, x, a[v]);
+                }
+        }
     }
     const float sum = __shfl(canonical_sum(a[0], a[1], a[2], a[3]), 0, 64);
     return __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(sum, static_cast<float>(k)) + epsilon));
@@ -134,36 +166,77 @@ __global__ __launch_bounds__(256) void rms_norm(const T* __restrict__ x, const f
     if (token >= tokens) return;
     const T* src = x + static_cast<std::int64_t>(token) * k;
     T* dst = out + static_cast<std::int64_t>(token) * k;
-    const float inv = row_inverse_rms(src, k, epsilon, lane);
+    const float inv = row_inverse_rms(src, k, epsilon, lane, rows_vec4(x, k));
     for (int col = lane; col < k; col += 64) dst[col] = from_f32<T>((to_f32(src[col]) * inv) * w[col]);
 }
 
 // RMSNorm fused with A8 quantization (q8_rms_producer.cuh:8-53 for two
 // passes): the quantizer sees exactly the fp16-rounded normalised values.
-// One wave per token; 8 lanes x 4 values form each group of 32.
+// One 4-wave workgroup per token: thread c runs the reference's chain c
+// (fmaf over columns c, c + 256, ...), wave 0 folds the 256 chains through the
+// same two-level tree as row_inverse_rms (so inv has the same bits), and the
+// four waves then quantize every fourth 256-column piece; 8 lanes x 4 values
+// form each group of 32.
 __global__ __launch_bounds__(256) void rms_a8(const __half* __restrict__ x, const float* __restrict__ w,
                                               std::int8_t* codes, float* scales, __half* intermediate,
                                               int tokens, int k, int groups, int passes, float epsilon) {
-    const int lane = threadIdx.x & 63;
-    const int token = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (token >= tokens) return;
+    __shared__ float chains[256];
+    __shared__ float inv_shared;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int token = blockIdx.x;
     const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
     const __half* src = x + static_cast<std::int64_t>(token) * k;
-    const float inv = row_inverse_rms(src, k, epsilon, lane);
-    for (int base = 0; base < groups * 32; base += 256) {
+    float chain = 0.0f;
+#pragma unroll 4
+    for (int col = tid; col < k; col += 256) {
+        const float v = __half2float(src[col]);
+        chain = fmaf(v, v, chain);
+    }
+    chains[tid] = chain;
+    __syncthreads();
+    if (wave == 0) {
+        const float sum = canonical_sum(chains[4 * lane], chains[4 * lane + 1], chains[4 * lane + 2],
+                                        chains[4 * lane + 3]);
+        if (lane == 0) inv_shared = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(sum, static_cast<float>(k)) + epsilon));
+    }
+    __syncthreads();
+    const float inv = inv_shared;
+    // Vector path: 8-byte x and intermediate pieces, 16-byte gamma pieces.
+    const bool vec = rows_vec4(x, k) && (reinterpret_cast<std::uintptr_t>(w) & 15) == 0 &&
+                     (!intermediate || (reinterpret_cast<std::uintptr_t>(intermediate) & 7) == 0);
+    for (int base = 256 * wave; base < groups * 32; base += 1024) {
         const int col = base + 4 * lane;
         const int g = col >> 5;
         float r[4];
         bool bad = false;
+        if (vec && col + 3 < k) {
+            float xv[4];
+            load4_f32(src + col, xv);
+            const float4 wv = *reinterpret_cast<const float4*>(w + col);
+            const float wa[4] = {wv.x, wv.y, wv.z, wv.w};
+            unsigned short yb[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            r[v] = 0.0f;
-            if (col + v < k) {
-                const __half y = from_f32<__half>((__half2float(src[col + v]) * inv) * w[col + v]);
-                if (intermediate) intermediate[static_cast<std::int64_t>(token) * k + col + v] = y;
+            for (int v = 0; v < 4; ++v) {
+                const __half y = from_f32<__half>((xv[v] * inv) * wa[v]);
+                yb[v] = __half_as_ushort(y);
                 r[v] = __half2float(y);
+                bad |= !isfinite(r[v]);
             }
-            bad |= !isfinite(r[v]);
+            if (intermediate)
+                *reinterpret_cast<uint2*>(intermediate + static_cast<std::int64_t>(token) * k + col) =
+                    make_uint2(yb[0] | (static_cast<std::uint32_t>(yb[1]) << 16),
+                               yb[2] | (static_cast<std::uint32_t>(yb[3]) << 16));
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                r[v] = 0.0f;
+                if (col + v < k) {
+                    const __half y = from_f32<__half>((__half2float(src[col + v]) * inv) * w[col + v]);
+                    if (intermediate) intermediate[static_cast<std::int64_t>(token) * k + col + v] = y;
+                    r[v] = __half2float(y);
+                }
+                bad |= !isfinite(r[v]);
+            }
         }
         const std::int64_t index = static_cast<std::int64_t>(token) * groups + min(g, groups - 1);
         // The 8 lanes of a group share g, so skipping whole groups keeps every
@@ -486,9 +559,8 @@ void rms_a8_launch(const void* x, const float* w, void* workspace, std::uint64_t
     const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
     auto* codes = static_cast<std::int8_t*>(workspace);
     auto* scales = reinterpret_cast<float*>(codes + count * 32 * passes);
-    rms_a8<<<(tokens + 3) / 4, 256, 0, stream>>>(static_cast<const __half*>(x), w, codes, scales,
-                                                 static_cast<__half*>(intermediate), tokens, k, groups, passes,
-                                                 epsilon);
+    rms_a8<<<tokens, 256, 0, stream>>>(static_cast<const __half*>(x), w, codes, scales,
+                                       static_cast<__half*>(intermediate), tokens, k, groups, passes, epsilon);
 }
 
 }  // namespace vt
