@@ -10,12 +10,12 @@
 // (blocks.cu:306-321) to fp32 association, like the decode route.
 //
 // Tiling: a workgroup of WM x WN waves computes (WM*TI*16) tokens x
-// (WN*TJ*16) rows, each wave TI x TJ tiles of 16 x 16. Groups are staged one
-// at a time in two LDS buffers: the tile's activation rows (32 halves each)
-// and weight rows (32 codes converted to fp16 once per workgroup) plus the
-// weight scales. Global loads run PF groups ahead in registers; one barrier
-// per group. LDS rows are four 16-byte units XOR-swizzled by (row >> 1) & 3
-// so that 16 consecutive rows' fragment reads fall on distinct banks.
+// (WN*TJ*16) rows, each wave TI x TJ tiles of 16 x 16. GS groups are staged at
+// a time in two LDS buffers: the tile's activation rows (32 GS halves each)
+// and weight rows (32 GS codes converted to fp16 once per workgroup) plus the
+// weight scales. Global loads run PF stages ahead in registers; one barrier
+// per stage. LDS rows are 4 GS 16-byte units XOR-swizzled by (row >> 1) so
+// that 16 consecutive rows' fragment reads fall on distinct banks.
 #include "common.hpp"
 
 namespace vt {
@@ -43,41 +43,47 @@ __device__ __forceinline__ void codes16_to_fp16(const uint4 w, uint4& lo, uint4&
     hi = make_uint4(h[4], h[5], h[6], h[7]);
 }
 
-__device__ __forceinline__ int swizzle(int row) { return (row >> 1) & 3; }
+// XOR swizzle of the 16-byte units of a staged row of U units (4 or 8), so
+// that 16 consecutive rows' fragment reads fall on distinct banks.
+template <int U>
+__device__ __forceinline__ int swizzle(int row) { return (row >> 1) & (U - 1); }
 
-template <int WM, int WN, int TI, int TJ>
+// GS groups of 32 columns per stage.
+template <int WM, int WN, int TI, int TJ, int GS>
 struct PrefillGeom {
     static constexpr int kThreads = WM * WN * 64;
-    static constexpr int kTM = WM * TI * 16;  // tokens per workgroup
-    static constexpr int kTN = WN * TJ * 16;  // weight rows per workgroup
-    static constexpr int kAUnits = kTM * 4;   // 16-byte activation loads per group (32 halves a row)
-    static constexpr int kBUnits = kTN * 2;   // 16-byte code loads per group (32 codes a row)
+    static constexpr int kTM = WM * TI * 16;      // tokens per workgroup
+    static constexpr int kTN = WN * TJ * 16;      // weight rows per workgroup
+    static constexpr int kU = 4 * GS;             // 16-byte fp16 units per staged row
+    static constexpr int kAUnits = kTM * kU;      // 16-byte activation loads per stage
+    static constexpr int kBUnits = kTN * 2 * GS;  // 16-byte code loads per stage (32 codes a row a group)
     static constexpr int kAPer = (kAUnits + kThreads - 1) / kThreads;
     static constexpr int kBPer = (kBUnits + kThreads - 1) / kThreads;
     static_assert(kAUnits % kThreads == 0 || kAUnits < kThreads, "whole loads per thread");
     static_assert(kBUnits % kThreads == 0 || kBUnits < kThreads, "whole loads per thread");
-    static_assert(kTN <= kThreads, "one scale per thread");
+    static_assert(kTN * GS <= kThreads, "one scale per thread");
 };
 
-template <int WM, int WN, int TI, int TJ>
+template <int WM, int WN, int TI, int TJ, int GS>
 struct PrefillStage {
-    using G = PrefillGeom<WM, WN, TI, TJ>;
+    using G = PrefillGeom<WM, WN, TI, TJ, GS>;
     uint4 a[G::kAPer];
     uint4 b[G::kBPer];
     unsigned short ws;
 };
 
-template <int WM, int WN, int TI, int TJ, int PF>
+template <int WM, int WN, int TI, int TJ, int PF, int GS>
 __global__ __launch_bounds__(WM * WN * 64) void q8_prefill(const __half* __restrict__ x,
                                                           const std::int8_t* __restrict__ codes,
                                                           const __half* __restrict__ scales, __half* __restrict__ out,
                                                           int tokens, int n, int k, int padded, int groups) {
-    using G = PrefillGeom<WM, WN, TI, TJ>;
-    using Stage = PrefillStage<WM, WN, TI, TJ>;
-    constexpr int TM = G::kTM, TN = G::kTN, T = G::kThreads;
-    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][TM * 4];
-    __shared__ __attribute__((aligned(16))) uint4 b_lds[2][TN * 4];
-    __shared__ __attribute__((aligned(16))) float ws_lds[2][TN];
+    using G = PrefillGeom<WM, WN, TI, TJ, GS>;
+    using Stage = PrefillStage<WM, WN, TI, TJ, GS>;
+    constexpr int TM = G::kTM, TN = G::kTN, T = G::kThreads, U = G::kU;
+    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][TM * U];
+    __shared__ __attribute__((aligned(16))) uint4 b_lds[2][TN * U];
+    __shared__ __attribute__((aligned(16))) float ws_lds[2][GS][TN];
+    const int stages = (groups + GS - 1) / GS;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -86,59 +92,70 @@ __global__ __launch_bounds__(WM * WN * 64) void q8_prefill(const __half* __restr
     const int q = lane >> 4, r = lane & 15;
     const int t0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
 
-    // Activation load u of a thread: unit i = tid + u*T, token i / 4 of the
-    // tile, columns 8 * (i % 4) .. +8 of the group (zero past k or past the
-    // last token: the address is clamped and the value replaced at the store).
+    // Stage s covers groups GS*s .. GS*s + GS - 1 (columns 32 GS s ..). Activation
+    // load u of a thread: unit i = tid + u*T, token i / U of the tile, columns
+    // 8 * (i % U) .. +8 of the stage (zero past k or past the last token: the
+    // address is clamped and the value replaced at the store).
     const __half* a_src[G::kAPer];
     int a_col[G::kAPer];
     bool a_row_ok[G::kAPer];
 #pragma unroll
     for (int u = 0; u < G::kAPer; ++u) {
         const int i = tid + u * T;
-        const int tok = i / 4;
+        const int tok = i / U;
         a_row_ok[u] = t0 + tok < tokens;
         a_src[u] = x + static_cast<std::int64_t>(min(t0 + tok, tokens - 1)) * k;
-        a_col[u] = 8 * (i & 3);
+        a_col[u] = 8 * (i % U);
     }
+    // Code load u: unit i, row i / (2 GS), code bytes 16 * (i % (2 GS)) of the stage.
     const std::int8_t* b_src[G::kBPer];
 #pragma unroll
     for (int u = 0; u < G::kBPer; ++u) {
         const int i = tid + u * T;
-        b_src[u] = codes + static_cast<std::int64_t>(min(n0 + min(i / 2, TN - 1), n - 1)) * padded + 16 * (i & 1);
+        b_src[u] = codes + static_cast<std::int64_t>(min(n0 + min(i / (2 * GS), TN - 1), n - 1)) * padded +
+                   16 * (i % (2 * GS));
     }
-    const int sid = T - 1 - tid;  // scales are staged by the last threads
+    // Scale slot sid = T - 1 - tid (staged by the last threads): row sid % TN,
+    // group sid / TN of the stage.
+    const int sid = T - 1 - tid;
+    const int s_grp = sid / TN;
     const __half* ws_src = scales + static_cast<std::int64_t>(min(n0 + sid % TN, n - 1)) * (padded / 32);
 
-    auto load = [&](int g, Stage& s) __attribute__((always_inline)) {
+    auto load = [&](int st, Stage& s) __attribute__((always_inline)) {
+        const int c0 = st * 32 * GS;
 #pragma unroll
         for (int u = 0; u < G::kAPer; ++u)
             if (G::kAUnits >= T || tid < G::kAUnits)
-                s.a[u] = *reinterpret_cast<const uint4*>(a_src[u] + min(g * 32 + a_col[u], k - 8));
+                s.a[u] = *reinterpret_cast<const uint4*>(a_src[u] + min(c0 + a_col[u], k - 8));
 #pragma unroll
         for (int u = 0; u < G::kBPer; ++u)
-            if (G::kBUnits >= T || tid < G::kBUnits) s.b[u] = *reinterpret_cast<const uint4*>(b_src[u] + g * 32);
-        s.ws = __half_as_ushort(ws_src[g]);
+            if (G::kBUnits >= T || tid < G::kBUnits)
+                s.b[u] = *reinterpret_cast<const uint4*>(b_src[u] + min(c0, padded - 32 * GS));
+        s.ws = __half_as_ushort(ws_src[min(st * GS + (s_grp < GS ? s_grp : 0), groups - 1)]);
     };
-    auto store = [&](const Stage& s, int g, int buf) __attribute__((always_inline)) {
+    auto store = [&](const Stage& s, int st, int buf) __attribute__((always_inline)) {
+        const int c0 = st * 32 * GS;
 #pragma unroll
         for (int u = 0; u < G::kAPer; ++u) {
             const int i = tid + u * T;
             if (G::kAUnits < T && i >= G::kAUnits) break;
-            const int tok = i / 4;
-            const bool ok = a_row_ok[u] && g * 32 + a_col[u] < k;  // k % 8 == 0: a unit is all in or all out
-            a_lds[buf][tok * 4 + ((i & 3) ^ swizzle(tok))] = ok ? s.a[u] : make_uint4(0u, 0u, 0u, 0u);
+            const int tok = i / U;
+            const bool ok = a_row_ok[u] && c0 + a_col[u] < k;  // k % 8 == 0: a unit is all in or all out
+            a_lds[buf][tok * U + ((i % U) ^ swizzle<U>(tok))] = ok ? s.a[u] : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
         for (int u = 0; u < G::kBPer; ++u) {
             const int i = tid + u * T;
             if (G::kBUnits < T && i >= G::kBUnits) break;
-            const int row = i / 2;
+            const int row = i / (2 * GS), piece = i % (2 * GS);
             uint4 lo, hi;
             codes16_to_fp16(s.b[u], lo, hi);
-            b_lds[buf][row * 4 + ((2 * (i & 1)) ^ swizzle(row))] = lo;
-            b_lds[buf][row * 4 + ((2 * (i & 1) + 1) ^ swizzle(row))] = hi;
+            b_lds[buf][row * U + ((2 * piece) ^ swizzle<U>(row))] = lo;
+            b_lds[buf][row * U + ((2 * piece + 1) ^ swizzle<U>(row))] = hi;
         }
-        if (sid < TN) ws_lds[buf][sid] = __half2float(__ushort_as_half(s.ws));
+        // A group past the last one (groups % GS != 0) carries scale 0.
+        if (sid < TN * GS)
+            ws_lds[buf][s_grp][sid % TN] = st * GS + s_grp < groups ? __half2float(__ushort_as_half(s.ws)) : 0.0f;
     };
 
     float4v y[TI][TJ];
@@ -149,44 +166,47 @@ __global__ __launch_bounds__(WM * WN * 64) void q8_prefill(const __half* __restr
 
     auto compute = [&](int buf) __attribute__((always_inline)) {
         const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
-        half8 fb[TJ];
-        float wsv[TJ];
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            const int row = wn * TJ * 16 + j * 16 + r;
-            fb[j] = __builtin_bit_cast(half8, b_lds[buf][row * 4 + (q ^ swizzle(row))]);
-            wsv[j] = ws_lds[buf][row];
-        }
-#pragma unroll
-        for (int i = 0; i < TI; ++i) {
-            const int tok = wm * TI * 16 + i * 16 + r;
-            const half8 fa = __builtin_bit_cast(half8, a_lds[buf][tok * 4 + (q ^ swizzle(tok))]);
+        for (int gg = 0; gg < GS; ++gg) {  // groups in natural order
+            half8 fb[TJ];
+            float wsv[TJ];
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
-                const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa, fb[j], zero, 0, 0, 0);
+                const int row = wn * TJ * 16 + j * 16 + r;
+                fb[j] = __builtin_bit_cast(half8, b_lds[buf][row * U + ((4 * gg + q) ^ swizzle<U>(row))]);
+                wsv[j] = ws_lds[buf][gg][row];
+            }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) y[i][j][e] = fmaf(d[e], wsv[j], y[i][j][e]);
+            for (int i = 0; i < TI; ++i) {
+                const int tok = wm * TI * 16 + i * 16 + r;
+                const half8 fa = __builtin_bit_cast(half8, a_lds[buf][tok * U + ((4 * gg + q) ^ swizzle<U>(tok))]);
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) {
+                    const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa, fb[j], zero, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) y[i][j][e] = fmaf(d[e], wsv[j], y[i][j][e]);
+                }
             }
         }
     };
 
-    // Group g is loaded PF groups ahead, written to LDS buffer g % 2 during
-    // the compute of group g - 1, and consumed after the barrier that ends it.
+    // Stage s is loaded PF stages ahead, written to LDS buffer s % 2 during
+    // the compute of stage s - 1, and consumed after the barrier that ends it.
     Stage st[PF];
 #pragma unroll
-    for (int s = 0; s < PF; ++s) load(min(s, groups - 1), st[s]);
+    for (int s = 0; s < PF; ++s) load(min(s, stages - 1), st[s]);
     store(st[0], 0, 0);
-    if (PF < groups) load(PF, st[0]);
+    if (PF < stages) load(PF, st[0]);
     __syncthreads();
-    for (int g0 = 0; g0 < groups; g0 += PF) {
+    for (int g0 = 0; g0 < stages; g0 += PF) {
 #pragma unroll
         for (int s = 0; s < PF; ++s) {
             const int g = g0 + s;
-            if (g >= groups) break;
+            if (g >= stages) break;
             compute(g & 1);
-            if (g + 1 < groups) {
+            if (g + 1 < stages) {
                 store(st[(s + 1) % PF], g + 1, (g + 1) & 1);
-                if (g + 1 + PF < groups) load(g + 1 + PF, st[(s + 1) % PF]);
+                if (g + 1 + PF < stages) load(g + 1 + PF, st[(s + 1) % PF]);
             }
             __syncthreads();
         }
@@ -205,15 +225,15 @@ __global__ __launch_bounds__(WM * WN * 64) void q8_prefill(const __half* __restr
         }
 }
 
-template <int WM, int WN, int TI, int TJ, int PF>
+template <int WM, int WN, int TI, int TJ, int PF, int GS = 1>
 void launch_prefill(const __half* x, const std::int8_t* codes, const __half* scales, __half* out, int tokens, int n,
                     int k, int padded, hipStream_t stream) {
-    using G = PrefillGeom<WM, WN, TI, TJ>;
+    using G = PrefillGeom<WM, WN, TI, TJ, GS>;
     const int groups = (k + 31) / 32;
     const dim3 grid((n + G::kTN - 1) / G::kTN, (tokens + G::kTM - 1) / G::kTM);
     require(grid.y <= 65535, "token tiles exceed the launch grid");
-    q8_prefill<WM, WN, TI, TJ, PF><<<grid, G::kThreads, 0, stream>>>(x, codes, scales, out, tokens, n, k, padded,
-                                                                    groups);
+    q8_prefill<WM, WN, TI, TJ, PF, GS><<<grid, G::kThreads, 0, stream>>>(x, codes, scales, out, tokens, n, k,
+                                                                        padded, groups);
 }
 
 }  // namespace
@@ -226,8 +246,18 @@ void q8_prefill_launch(const void* x, const std::int8_t* codes, const __half* sc
     require(dtype == kF16, "the Q8 prefill GEMM takes FP16 activations");
     require(k % 8 == 0 && aligned(x, 16), "the Q8 prefill GEMM needs k % 8 == 0 and 16-byte aligned x");
     require(aligned(codes, 16) && aligned(scales, 2) && aligned(out, 2), "misaligned Q8 operand");
-    launch_prefill<4, 2, 4, 4, 4>(static_cast<const __half*>(x), codes, scales, static_cast<__half*>(out), tokens, n, k,
-                                  padded, stream);
+    // 256 x 128 tiles, one group per stage, unless that grid leaves CUs with
+    // uneven shares (fewer than 384 workgroups: n = 5120 at 2048 tokens gives
+    // 320); then 128 x 128 tiles with two groups per stage (o_proj and down at
+    // M = 2048: 383 -> 436 and 401 -> 467 TFLOP/s; same bits either way, the
+    // groups being summed in natural order).
+    const auto* xp = static_cast<const __half*>(x);
+    auto* op = static_cast<__half*>(out);
+    const long big_grid = static_cast<long>((n + 127) / 128) * ((tokens + 255) / 256);
+    if (big_grid < 384)
+        launch_prefill<2, 4, 4, 2, 2, 2>(xp, codes, scales, op, tokens, n, k, padded, stream);
+    else
+        launch_prefill<4, 2, 4, 4, 4, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
 }
 
 }  // namespace vt
