@@ -8,9 +8,12 @@ q8_g32_fp16 on the device and fp16 N(0, 1) activations, run at token counts
 M in {1, 4, 8, 16}. A step is one pass of the 16 (projection, M) launches.
 For every (projection, M), K launches rotating independent weight copies (at
 least 600 MB per projection, so that no launch is served from the 256 MB
-Infinity Cache) are captured once in a HIP graph; the timed region replays
-the 16 graphs back to back, each between one pair of HIP events on the
-launch stream (the graphs' outputs are checked against eager launches).
+Infinity Cache) are captured once in a HIP graph; the whole job (the 16
+groups in turn) is also captured as one graph, whose replay is the timed
+region of `value`, as a decode step runs in production; the 16 group graphs
+are then replayed back to back, each between one pair of HIP events on the
+launch stream, for the per-launch durations (all graphs' outputs are checked
+against eager launches).
 
 Printed JSON (one line): `value` is the whole-job algorithmic throughput in
 GB/s (weights N*Kp*(1+2/32) + activations M*K*2 + outputs M*N*2, per launch)
@@ -273,7 +276,8 @@ def q4_decode(backend, device, steps, warmup, copy_mb):
 
     Same method as the Q8 decode timing: per (projection, M), `steps` launches
     rotating >= `copy_mb` MB of independent weight copies captured in one HIP
-    graph, replayed between one pair of events; algorithmic bytes per launch =
+    graph, replayed between one pair of events (per-launch durations), and the
+    whole job as one graph (`GB/s`); algorithmic bytes per launch =
     codes N*Kp/2 + scales N*(Kp/64)*2 + activations M*K*2 + outputs M*N*2.
     """
     copies = []
@@ -318,15 +322,32 @@ def q4_decode(backend, device, steps, warmup, copy_mb):
         graphs[(mi, pi)].replay()
         torch.cuda.synchronize(device)
         graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
+    # As in the Q8 timing: the whole job as one graph for `GB/s`, the group
+    # graphs between events for the per-launch durations.
+    step_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(step_graph):
+        for key in launches:
+            run(*key, steps)
+    step_graph.replay()
+    torch.cuda.synchronize(device)
+    last_writer = {(TOKENS[mi], PROJECTIONS[pi][1]): (mi, pi) for mi, pi in launches}
+    for mi, pi in last_writer.values():
+        m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
+        ref = torch.empty_like(outs[(m, n)])
+        plans[(mi, pi)][(steps - 1) % len(plans[(mi, pi)])].run(xs[m][k], out=ref)
+        torch.cuda.synchronize(device)
+        graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
     events = {key: [torch.cuda.Event(enable_timing=True) for _ in range(2)] for key in launches}
     torch.cuda.synchronize(device)
     start = time.perf_counter()
+    step_graph.replay()
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - start
     for key in launches:
         events[key][0].record(stream)
         graphs[key].replay()
         events[key][1].record(stream)
     torch.cuda.synchronize(device)
-    wall = time.perf_counter() - start
     detail, total_bytes, kernel_total = {}, 0, 0.0
     for mi, pi in launches:
         m, (name, n, k) = TOKENS[mi], PROJECTIONS[pi]
@@ -573,8 +594,35 @@ def main():
             torch.cuda.synchronize(device)
             graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
 
+    # The whole job (K steps of the 16 launch groups) is also captured as one
+    # graph, as a decode step runs in production; its replay is the timed
+    # region of `value`. The per-group graphs, each between a pair of events,
+    # give the per-launch durations and the roofline.
+    step_graph = None
+    if not args.eager:
+        step_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(step_graph):
+            for key in launches:
+                run(*key, args.steps)
+        step_graph.replay()
+        torch.cuda.synchronize(device)
+        # Output buffers are shared by projections of one shape (o_proj and down
+        # are both [M, 5120]): each holds its last writer's result.
+        last_writer = {(TOKENS[mi], PROJECTIONS[pi][1]): (mi, pi) for mi, pi in launches}
+        for mi, pi in last_writer.values():
+            m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
+            ref = torch.empty_like(outs[(m, n)])
+            plans[(mi, pi)][(args.steps - 1) % len(plans[(mi, pi)])].run(xs[m][k], out=ref)
+            torch.cuda.synchronize(device)
+            graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
+
     events = {key: [torch.cuda.Event(enable_timing=True) for _ in range(2)] for key in launches}
     torch.cuda.synchronize(device)
+    if step_graph is not None:
+        start = time.perf_counter()
+        step_graph.replay()
+        torch.cuda.synchronize(device)
+        wall = time.perf_counter() - start
     start = time.perf_counter()
     for key in launches:
         if args.eager:
@@ -584,7 +632,8 @@ def main():
             graphs[key].replay()
             events[key][1].record(stream)
     torch.cuda.synchronize(device)
-    wall = time.perf_counter() - start
+    if step_graph is None:
+        wall = time.perf_counter() - start
 
     kernel_s = {key: e[0].elapsed_time(e[1]) / 1e3 for key, e in events.items()}
     total_bytes = args.steps * step_bytes
@@ -637,7 +686,9 @@ def main():
         },
         "all_kernels_GBps": round(total_bytes / sum(kernel_s.values()) / 1e9, 1),
         "graph_equals_eager": graph_equals_eager,
-        "timing": "eager launches" if args.eager else "HIP-graph replays",
+        "timing": ("eager launches" if args.eager else
+                   "value: one HIP graph of the whole job (K steps x 16 launch groups), wall clock of its replay; "
+                   "per_launch: one graph per group between HIP events"),
         "per_launch": detail,
     }
     if not args.no_q4:
