@@ -158,6 +158,8 @@ class ResidentQ4Linear:
                 with torch.cuda.device(self.device):
                     self.backend._check(lib.venturi_q4_tiled_workspace_init(slots.data_ptr(), size,
                                                                               _stream(self.device)))
+            # The copy and the slots were written on this stream; a plan may run on another.
+            torch.cuda.current_stream(self.device).synchronize()
         return Q4LinearPlan(self, tokens, route, slots)
 
     def decode(self, *, out, row=0):
