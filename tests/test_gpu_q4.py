@@ -212,7 +212,7 @@ def test_tiled_decode_rejects_bad_arguments(backend, device):
     torch.cuda.synchronize(device)
 
 
-@pytest.mark.parametrize("shape", [(16, 8192), (130, 8320), (5120, 17408)])
+@pytest.mark.parametrize("shape", [(16, 8192), (130, 8320), (37, 8200), (5120, 17408)])
 @pytest.mark.parametrize("tokens", [1, 3, 16])
 def test_tiled_decode_split_k(backend, device, shape, tokens):
     # Shapes that split K over two workgroups: the two halves meet in fp32 (an
