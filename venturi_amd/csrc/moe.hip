@@ -496,9 +496,10 @@ template <int K>
 __global__ __launch_bounds__(256) void moe_combine(const std::int64_t* __restrict__ ids,
                                                    const int* __restrict__ pair_slot, const __half* __restrict__ v,
                                                    __half* __restrict__ out, int tokens, int hidden) {
-    const int token = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (token >= tokens) return;
+    // One 4-wave workgroup per token, each wave a quarter of the columns (every
+    // wave sorts the token's K pairs itself).
+    const int token = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int order[K];
     std::int64_t key[K];
     int n = 0;
@@ -521,7 +522,7 @@ __global__ __launch_bounds__(256) void moe_combine(const std::int64_t* __restric
                 order[j] = order[j + 1];
                 order[j + 1] = to;
             }
-    for (int col = 8 * lane; col < hidden; col += 8 * 64) {
+    for (int col = 8 * lane + 512 * wave; col < hidden; col += 4 * 512) {
         uint4 r[K];
 #pragma unroll
         for (int i = 0; i < K; ++i)
@@ -550,7 +551,7 @@ __global__ __launch_bounds__(256) void moe_combine(const std::int64_t* __restric
 template <int K>
 void launch_combine(const std::int64_t* ids, const int* pair_slot, const __half* v, __half* out, int tokens,
                     int hidden, hipStream_t stream) {
-    moe_combine<K><<<(tokens + 3) / 4, 256, 0, stream>>>(ids, pair_slot, v, out, tokens, hidden);
+    moe_combine<K><<<tokens, 256, 0, stream>>>(ids, pair_slot, v, out, tokens, hidden);
 }
 
 void combine_dispatch(int top_k, const std::int64_t* ids, const int* pair_slot, const __half* v, __half* out,
