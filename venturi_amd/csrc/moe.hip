@@ -422,10 +422,15 @@ __global__ __launch_bounds__(1024) void moe_route(const std::int64_t* __restrict
     // 1024 * kRouteBatch pairs) keep theirs in pair_slot between the passes.
     int first_rank[kRouteBatch];
     std::int64_t first_e[kRouteBatch];
+    __half first_sc[kRouteBatch];  // the first batch's scores, fetched with its ids
     for (int base = 0; base < pairs; base += 1024 * kRouteBatch) {
         std::int64_t e[kRouteBatch];
 #pragma unroll
         for (int u = 0; u < kRouteBatch; ++u) e[u] = ids[min(base + u * 1024 + tid, pairs - 1)];
+        if (base == 0) {
+#pragma unroll
+            for (int u = 0; u < kRouteBatch; ++u) first_sc[u] = scores[min(u * 1024 + tid, pairs - 1)];
+        }
 #pragma unroll
         for (int u = 0; u < kRouteBatch; ++u) {
             const int i = base + u * 1024 + tid;
@@ -469,7 +474,7 @@ __global__ __launch_bounds__(1024) void moe_route(const std::int64_t* __restrict
             const int i = min(base + u * 1024 + tid, pairs - 1);
             rank[u] = base == 0 ? first_rank[u] : pair_slot[i];
             e[u] = base == 0 ? first_e[u] : ids[i];
-            sc[u] = scores[i];
+            sc[u] = base == 0 ? first_sc[u] : scores[i];
         }
 #pragma unroll
         for (int u = 0; u < kRouteBatch; ++u) {
