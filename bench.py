@@ -61,7 +61,7 @@ def parse():
     p.add_argument("--copy-mb", type=float, default=600.0, help="minimum rotated weight bytes per projection")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--no-q4", action="store_true", help="skip the Q4 W4A16 decode section")
+    p.add_argument("--no-q4", action="store_true", help="skip the Q4 W4A16 and Q5/Q6 decode sections")
     p.add_argument("--no-prefill", action="store_true", help="skip the config-3 A8 prefill section")
     p.add_argument("--no-moe", action="store_true", help="skip the config-4 routed-expert MoE section")
     p.add_argument("--no-model", action="store_true", help="skip the config-5 64-layer decode section")
@@ -367,6 +367,98 @@ def q4_decode(backend, device, steps, warmup, copy_mb):
         "graph_equals_eager": graph_equals_eager,
         "per_launch": detail,
     }
+
+
+def row_codec_decode(backend, device, steps, warmup, copy_mb, bits_list=(5, 6)):
+    """Q5/Q6 row codecs (q5_g64 / q6_g64) at the config-2 shapes and M in {1, 4, 8, 16}:
+    the W5A16 / W6A16 contract GEMM (`venturi_row_gemm_run`, reading the high plane)
+    over the row-major planes.
+
+    Planes are synthetic bytes (random low nibbles and high bits, fp16 scales in
+    [1e-4, 1e-2)); per (projection, M) `steps` launches rotate over >= `copy_mb`
+    MB of copies inside one HIP graph; the whole job is one graph (GB/s).
+    Algorithmic bytes per launch = N*Kp/2 + N*Kp*hb/8 + N*(Kp/64)*2 + M*K*2 + M*N*2.
+    """
+    lib = backend._native
+    stream = torch.cuda.current_stream(device)
+    gen = torch.Generator(device=device).manual_seed(23)
+    result = {"workload": "config-2 projection set with q5_g64 / q6_g64 planes, M in {1,4,8,16}",
+              "kernel": "row_decode_gemm (fp16 MFMA, W*A16 contract)"}
+    for bits in bits_list:
+        hb = bits - 4
+
+        def launch_bytes_rc(m, n, k):
+            padded = (k + 127) // 128 * 128
+            return n * padded // 2 + n * padded * hb // 8 + n * (padded // 64) * 2 + m * k * 2 + m * n * 2
+
+        copies = []
+        for name, n, k in PROJECTIONS:
+            padded = (k + 127) // 128 * 128
+            count = max(2, -(-int(copy_mb * 1e6) // launch_bytes_rc(0, n, k)))
+            planes = []
+            for _ in range(count):
+                codes = torch.randint(0, 256, (n, padded // 2), dtype=torch.uint8, device=device, generator=gen)
+                high = torch.randint(0, 256, (n, padded * hb // 8), dtype=torch.uint8, device=device, generator=gen)
+                scales = (torch.rand(n, padded // 64, device=device, generator=gen) * 0.0099 + 1e-4).half()
+                planes.append((codes, high, scales))
+            copies.append(planes)
+        xs = {m: {k: torch.randn(m, k, generator=gen, device=device).half() for k in {p[2] for p in PROJECTIONS}}
+              for m in TOKENS}
+        outs = {(m, pi): torch.empty(m, PROJECTIONS[pi][1], dtype=torch.float16, device=device)
+                for m in TOKENS for pi in range(len(PROJECTIONS))}
+        launches = [(mi, pi) for mi in range(len(TOKENS)) for pi in range(len(PROJECTIONS))]
+
+        def run(mi, pi, reps):
+            m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
+            padded = (k + 127) // 128 * 128
+            launch_stream = torch.cuda.current_stream(device).cuda_stream  # the capture stream inside a graph
+            for r in range(reps):
+                codes, high, scales = copies[pi][r % len(copies[pi])]
+                backend._check(lib.venturi_row_gemm_run(
+                    xs[m][k].data_ptr(), codes.data_ptr(), high.data_ptr(), scales.data_ptr(),
+                    outs[(m, pi)].data_ptr(), m, n, k, padded, bits, 0, launch_stream))
+
+        for key in launches:
+            run(*key, warmup)
+        torch.cuda.synchronize(device)
+        graphs = {}
+        for key in launches:
+            graphs[key] = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graphs[key]):
+                run(*key, steps)
+        step_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(step_graph):
+            for key in launches:
+                run(*key, steps)
+        step_graph.replay()
+        torch.cuda.synchronize(device)
+        start = time.perf_counter()
+        step_graph.replay()
+        torch.cuda.synchronize(device)
+        wall = time.perf_counter() - start
+        events = {key: [torch.cuda.Event(enable_timing=True) for _ in range(2)] for key in launches}
+        for key in launches:
+            events[key][0].record(stream)
+            graphs[key].replay()
+            events[key][1].record(stream)
+        torch.cuda.synchronize(device)
+        detail, total_bytes, kernel_total = {}, 0, 0.0
+        for mi, pi in launches:
+            m, (name, n, k) = TOKENS[mi], PROJECTIONS[pi]
+            t = events[(mi, pi)][0].elapsed_time(events[(mi, pi)][1]) / 1e3
+            b = steps * launch_bytes_rc(m, n, k)
+            total_bytes += b
+            kernel_total += t
+            detail[f"{name}_m{m}"] = {"us": round(t / steps * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+        achieved = total_bytes / kernel_total / 1e9
+        result[f"q{bits}"] = {
+            "GB/s": round(total_bytes / wall / 1e9, 1),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4)},
+            "per_launch": detail,
+        }
+        del copies, graphs, step_graph
+    return result
 
 
 def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
@@ -695,6 +787,8 @@ def main():
         del plans, graphs
         log("Q4 W4A16 decode at the config-2 shapes")
         result["q4_decode"] = q4_decode(backend, device, args.steps, args.warmup, args.copy_mb)
+        log("Q5/Q6 row-codec decode at the config-2 shapes")
+        result["q56_decode"] = row_codec_decode(backend, device, args.steps, args.warmup, args.copy_mb)
     if not args.no_prefill:
         log("config-3 A8 prefill")
         result["prefill_a8"] = prefill_a8(backend, device, max(args.steps // 2, 3), 2)
