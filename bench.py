@@ -371,19 +371,21 @@ def q4_decode(backend, device, steps, warmup, copy_mb):
 
 def row_codec_decode(backend, device, steps, warmup, copy_mb, bits_list=(5, 6)):
     """Q5/Q6 row codecs (q5_g64 / q6_g64) at the config-2 shapes and M in {1, 4, 8, 16}:
-    the W5A16 / W6A16 contract GEMM (`venturi_row_gemm_run`, reading the high plane)
-    over the row-major planes.
+    the W5A16 / W6A16 contract GEMM over tiled decode copies (`q5.tile_row_codec`,
+    `venturi_row_tiled_run`, with exchange slots where K is split).
 
     Planes are synthetic bytes (random low nibbles and high bits, fp16 scales in
     [1e-4, 1e-2)); per (projection, M) `steps` launches rotate over >= `copy_mb`
     MB of copies inside one HIP graph; the whole job is one graph (GB/s).
     Algorithmic bytes per launch = N*Kp/2 + N*Kp*hb/8 + N*(Kp/64)*2 + M*K*2 + M*N*2.
     """
+    from venturi_amd.q5 import tile_row_codec
+
     lib = backend._native
     stream = torch.cuda.current_stream(device)
     gen = torch.Generator(device=device).manual_seed(23)
-    result = {"workload": "config-2 projection set with q5_g64 / q6_g64 planes, M in {1,4,8,16}",
-              "kernel": "row_decode_gemm (fp16 MFMA, W*A16 contract)"}
+    result = {"workload": "config-2 projection set with q5_g64 / q6_g64 planes (tiled decode copies), M in {1,4,8,16}",
+              "kernel": "row_decode_gemm (fp16 MFMA, W*A16 contract, tiled copy)"}
     for bits in bits_list:
         hb = bits - 4
 
@@ -400,23 +402,33 @@ def row_codec_decode(backend, device, steps, warmup, copy_mb, bits_list=(5, 6)):
                 codes = torch.randint(0, 256, (n, padded // 2), dtype=torch.uint8, device=device, generator=gen)
                 high = torch.randint(0, 256, (n, padded * hb // 8), dtype=torch.uint8, device=device, generator=gen)
                 scales = (torch.rand(n, padded // 64, device=device, generator=gen) * 0.0099 + 1e-4).half()
-                planes.append((codes, high, scales))
+                planes.append(tile_row_codec(codes, high, scales, bits))
+                del codes, high, scales
             copies.append(planes)
         xs = {m: {k: torch.randn(m, k, generator=gen, device=device).half() for k in {p[2] for p in PROJECTIONS}}
               for m in TOKENS}
         outs = {(m, pi): torch.empty(m, PROJECTIONS[pi][1], dtype=torch.float16, device=device)
                 for m in TOKENS for pi in range(len(PROJECTIONS))}
         launches = [(mi, pi) for mi in range(len(TOKENS)) for pi in range(len(PROJECTIONS))]
+        slots = {}
+        for mi, pi in launches:
+            size = int(lib.venturi_q4_tiled_workspace_bytes(TOKENS[mi], PROJECTIONS[pi][1], PROJECTIONS[pi][2]))
+            if size:
+                slots[(mi, pi)] = torch.empty(size, dtype=torch.uint8, device=device)
+                backend._check(lib.venturi_q4_tiled_workspace_init(slots[(mi, pi)].data_ptr(), size,
+                                                                   stream.cuda_stream))
 
         def run(mi, pi, reps):
             m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
             padded = (k + 127) // 128 * 128
+            slot = slots.get((mi, pi))
             launch_stream = torch.cuda.current_stream(device).cuda_stream  # the capture stream inside a graph
             for r in range(reps):
                 codes, high, scales = copies[pi][r % len(copies[pi])]
-                backend._check(lib.venturi_row_gemm_run(
+                backend._check(lib.venturi_row_tiled_run(
                     xs[m][k].data_ptr(), codes.data_ptr(), high.data_ptr(), scales.data_ptr(),
-                    outs[(m, pi)].data_ptr(), m, n, k, padded, bits, 0, launch_stream))
+                    outs[(m, pi)].data_ptr(), m, n, k, padded, bits, 0, None if slot is None else slot.data_ptr(),
+                    0 if slot is None else slot.numel(), launch_stream))
 
         for key in launches:
             run(*key, warmup)

@@ -240,6 +240,17 @@ int venturi_q4_tiled_workspace_init(void* workspace, uint64_t bytes, void* strea
 int venturi_q4_tiled_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
                          int padded, int dtype, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* Extension: venturi_q4_tiled_run for 4-, 5- and 6-bit row codecs: bits 4 reads
+ * the copy described above; bits 5/6 read q5.tile_row_codec's copy (codes tiled
+ * as for Q4 but with the row-major nibbles, high plane [ceil(n/16)][padded/128]
+ * [64 lanes][4*(bits-4) bytes], scales as for Q4; high 4-byte aligned). Same
+ * slot buffer rule; unsplit shapes give the bits of venturi_row_gemm_run on the
+ * row-major planes. No counterpart in the reference; for callers that decode
+ * q5/q6 rows from a resident tiled copy. */
+int venturi_row_tiled_run(const void* x, const void* codes, const void* high, const void* scales, void* out,
+                          int tokens, int n, int k, int padded, int bits, int dtype, void* workspace,
+                          uint64_t workspace_bytes, void* stream);
+
 /* Extension: the same contract GEMM for 4-, 5- and 6-bit row codecs (bits
  * 4/5/6; `high` = the q5/q6 high plane [n][padded*(bits-4)/8], 16-byte
  * aligned, unused for 4 bits). Stands where the reference dequantizes q4/q5/q6

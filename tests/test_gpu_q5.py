@@ -192,3 +192,37 @@ def test_row_gemm_rejects_bad_arguments(backend, device):
                                     7, 0, s) == -1
     assert "4, 5 or 6" in lib.error()
     torch.cuda.synchronize(device)
+
+
+@pytest.mark.parametrize("nbits", [4, 5, 6])
+@pytest.mark.parametrize("shape", [(37, 136), (300, 2048), (6200, 264)])
+@pytest.mark.parametrize("tokens", [1, 5, 16, 24])
+def test_row_tiled_decode_equals_row_major(backend, device, nbits, shape, tokens):
+    # The tiled copies (q4.tile_q4 for 4 bits, q5.tile_row_codec for 5/6) give the
+    # bits of the row-major decode GEMM for shapes that do not split K.
+    from venturi_amd.q4 import tile_q4
+    from venturi_amd.q5 import tile_row_codec
+
+    n, k = shape
+    print(f"case row-tiled bits={nbits} n={n} k={k} tokens={tokens}", flush=True)
+    packed, high, scales = _planes(n, k, nbits, 11 * nbits + n + tokens)
+    padded = packed.shape[1] * 2
+    lib = backend._native
+    assert lib.venturi_q4_tiled_workspace_bytes(tokens, n, k) == 0
+    s = torch.cuda.current_stream(device).cuda_stream
+    dc = torch.from_numpy(packed).to(device)
+    dh = torch.from_numpy(high if nbits > 4 else np.zeros((1, 16), np.uint8)).to(device)
+    ds = torch.from_numpy(scales).to(device)
+    if nbits == 4:
+        tc, ts = tile_q4(dc, ds)
+        th = dh
+    else:
+        tc, th, ts = tile_row_codec(dc, dh, ds, nbits)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens * 3 + k)).half().to(device)
+    want = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    backend._check(lib.venturi_row_gemm_run(x.data_ptr(), dc.data_ptr(), dh.data_ptr(), ds.data_ptr(), want.data_ptr(),
+                                            tokens, n, k, padded, nbits, 0, s))
+    got = torch.empty_like(want)
+    backend._check(lib.venturi_row_tiled_run(x.data_ptr(), tc.data_ptr(), th.data_ptr(), ts.data_ptr(), got.data_ptr(),
+                                             tokens, n, k, padded, nbits, 0, None, 0, s))
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))

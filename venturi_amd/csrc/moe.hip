@@ -776,14 +776,16 @@ void launch_row_prefill(const __half* x, const std::uint8_t* codes, const std::u
 // fetched in a two-deep ping-pong; partial tiles are summed across waves
 // through LDS in wave order and stored by one wave per (row block, token block).
 //
-// TILED (Q4 only) reads the decode copy built by q4.tile_q4 instead: codes
+// TILED reads the decode copy built by q4.tile_q4 / q5.tile_row_codec instead: codes
 // [row block][chunk][lane 16q + r][16 bytes] holding the code bytes lane (r, q)
 // reads from the row-major planes, and scales [row block][chunk][r][2] (the
 // chunk's two groups); each load is then one contiguous 1 KB (codes) or
 // 64-byte (scales) wave access. The copy stores each word's nibbles pre-biased
 // (q + 8) and reordered (nibble j holds column 2j, nibble 4 + j column 2j + 1)
 // so that dequant8_biased yields the eight columns in natural order: the
-// activation fragments need no interleave. Every product and sum is the same
+// activation fragments need no interleave (Q5/Q6 copies keep the row-major
+// nibbles and tile the high plane [row block][chunk][lane][4 * HB bytes], the
+// bits lane (r, q) reads from the row-major plane). Every product and sum is the same
 // as in the row-major path (the MFMA's k slots hold the same column pairs), so
 // both layouts give the same bits.
 template <int HB, int RB, int NB, int STEPS>
@@ -827,7 +829,7 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
             const std::int64_t blk = min(block0 + b, (n + 15) / 16 - 1);  // clamped blocks are never stored
             cp[b] = codes + blk * chunks * 1024 + 16 * lane;
             sp[b] = reinterpret_cast<const std::uint32_t*>(scales) + blk * chunks * 16 + r;
-            hp[b] = nullptr;
+            hp[b] = HB ? high + blk * chunks * 256 * HB + 4 * HB * lane : nullptr;
         } else {
             const std::int64_t row = min((block0 + b) * 16 + r, n - 1);  // clamped rows are never stored
             cp[b] = codes + row * cstride + 16 * q;
@@ -855,7 +857,8 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
                 if constexpr (HB > 0) {
 #pragma unroll
                     for (int h = 0; h < HB; ++h)
-                        t.h[st][b][h] = reinterpret_cast<const std::uint32_t*>(hp[b] + 16 * HB * c)[h];
+                        t.h[st][b][h] =
+                            reinterpret_cast<const std::uint32_t*>(hp[b] + (TILED ? 256 * HB : 16 * HB) * c)[h];
                 }
             }
             // A chunk wholly inside k loads every lane's fragments unmasked: lanes of
@@ -896,7 +899,7 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
         for (int tb = 0; tb < NB; ++tb)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                fa[tb][j] = __builtin_bit_cast(half8, TILED ? t.x[st][tb][j] : interleave8(t.x[st][tb][j]));
+                fa[tb][j] = __builtin_bit_cast(half8, TILED && HB == 0 ? t.x[st][tb][j] : interleave8(t.x[st][tb][j]));
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             // Columns 32q .. 32q+31 of the chunk lie in its group q / 2.
@@ -906,7 +909,7 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 half8 wf;
-                if constexpr (TILED) {
+                if constexpr (TILED && HB == 0) {
                     wf = dequant8_biased(words[j], s2, masks);
                 } else if constexpr (HB == 0) {
                     wf = dequant8(words[j], s2);
@@ -997,7 +1000,6 @@ template <int HB, int W, int RB, int NB, int STEPS, bool TILED, int KS = 1>
 void launch_row_decode(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
                        __half* out, int tokens, int n, int k, int padded, hipStream_t stream,
                        unsigned long long* slots = nullptr) {
-    static_assert(!TILED || HB == 0, "the tiled decode copy is built for Q4 rows");
     require(KS == 1 || slots, "a split decode needs its slot buffer");
     const int blocks = (n + 15) / 16;
     row_decode_gemm<HB, W, RB, NB, STEPS, TILED, KS><<<(blocks + RB - 1) / RB * KS, W * 64, 0, stream>>>(
@@ -1240,6 +1242,39 @@ VT_EXPORT int venturi_q4_tiled_run(const void* x, const void* codes, const void*
                                          static_cast<const __half*>(scales), static_cast<__half*>(out), tokens, n, k,
                                          padded, static_cast<hipStream_t>(stream),
                                          need ? static_cast<unsigned long long*>(workspace) : nullptr);
+    });
+}
+
+// Extension: venturi_q4_tiled_run for 4-, 5- and 6-bit row codecs (bits 4 reads
+// the biased Q4 copy of q4.tile_q4, bits 5/6 the copy of q5.tile_row_codec with
+// its tiled high plane); the slot buffer is sized by
+// venturi_q4_tiled_workspace_bytes.
+VT_EXPORT int venturi_row_tiled_run(const void* x, const void* codes, const void* high, const void* scales, void* out,
+                                    int tokens, int n, int k, int padded, int bits, int dtype, void* workspace,
+                                    std::uint64_t workspace_bytes, void* stream) {
+    return vt::guarded([&] {
+        vt::require(bits == 4 || bits == 5 || bits == 6, "row codecs are 4, 5 or 6 bits");
+        vt::require(x && codes && scales && out && (bits == 4 || high), "null row-codec tiled operand");
+        vt::require(tokens > 0 && tokens < vt::kRowPrefillMinTokens, "the tiled decode takes 1 to 31 tokens");
+        vt::require(n > 0 && k > 0 && padded == vt::padded_k(k), "invalid row-codec geometry");
+        vt::require(dtype == vt::kF16, "the tiled decode takes FP16 activations");
+        vt::require(k % 8 == 0 && vt::aligned(x, 16), "the tiled decode needs k % 8 == 0 and 16-byte aligned x");
+        vt::require(vt::aligned(codes, 16) && vt::aligned(scales, 4) && vt::aligned(out, 2) &&
+                        (bits == 4 || vt::aligned(high, 4)),
+                    "misaligned row-codec tiled operand");
+        const std::uint64_t need = vt::row_decode_slot_bytes(tokens, n, padded);
+        vt::require(workspace_bytes >= need && (need == 0 || (workspace && vt::aligned(workspace, 8))),
+                    "the tiled decode needs its slot buffer (venturi_q4_tiled_workspace_bytes)");
+        auto* slots = need ? static_cast<unsigned long long*>(workspace) : nullptr;
+        const auto* xp = static_cast<const __half*>(x);
+        const auto* cp = static_cast<const std::uint8_t*>(codes);
+        const auto* hp = static_cast<const std::uint8_t*>(high);
+        const auto* sp = static_cast<const __half*>(scales);
+        auto* op = static_cast<__half*>(out);
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        if (bits == 4) vt::row_decode_dispatch<0, true>(xp, cp, nullptr, sp, op, tokens, n, k, padded, st, slots);
+        else if (bits == 5) vt::row_decode_dispatch<1, true>(xp, cp, hp, sp, op, tokens, n, k, padded, st, slots);
+        else vt::row_decode_dispatch<2, true>(xp, cp, hp, sp, op, tokens, n, k, padded, st, slots);
     });
 }
 

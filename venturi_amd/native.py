@@ -60,6 +60,7 @@ SIGNATURES = {
     "venturi_q4_gemm_run": ([_P] * 4 + [_I] * 5 + [_P], _I),
     "venturi_q4_tiled_run": ([_P] * 4 + [_I] * 5 + [_P, _U64, _P], _I),
     "venturi_q4_tiled_workspace_bytes": ([_I] * 3, _U64),
+    "venturi_row_tiled_run": ([_P] * 5 + [_I] * 6 + [_P, _U64, _P], _I),
     "venturi_q4_tiled_workspace_init": ([_P, _U64, _P], _I),
     "venturi_row_gemm_run": ([_P] * 5 + [_I] * 6 + [_P], _I),
     "venturi_rowcodec_prepare": ([_I] * 5 + [_P], _I),

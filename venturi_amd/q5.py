@@ -49,6 +49,33 @@ def quantize_q5_rtn(weight, *, max_elements=16 * 2**20):
     return Q5RowSplitWeight.from_codes(codes.reshape(rows, padded)[:, :cols], scales[:, : (cols + 63) // 64])
 
 
+def tile_row_codec(codes, high, scales, bits):
+    """Tiled decode copy of q5_g64 / q6_g64 planes (read by ``venturi_row_tiled_run``).
+
+    Codes [row block][chunk][lane l = 16q + r][16 bytes] as for Q4 (row r of the
+    16-row block, code bytes 16q .. 16q+15 of the 128-column chunk) but with the
+    row-major nibbles; high plane [row block][chunk][lane][4 * hb bytes] (the
+    lane's 32 columns' upper hb = bits - 4 bits, LSB-first as in the row-major
+    stream); scales [row block][chunk][r][2]. Rows past n are zero.
+    """
+    if bits not in (5, 6):
+        raise ValueError("tile_row_codec takes 5- or 6-bit planes")
+    hb = bits - 4
+    n, row_bytes = codes.shape
+    chunks = row_bytes // 64
+    blocks = (n + 15) // 16
+    c = torch.zeros((blocks * 16, row_bytes), dtype=torch.uint8, device=codes.device)
+    h = torch.zeros((blocks * 16, chunks * 16 * hb), dtype=torch.uint8, device=codes.device)
+    s = torch.zeros((blocks * 16, chunks * 2), dtype=torch.float16, device=codes.device)
+    c[:n] = codes
+    h[:n] = high
+    s[:n] = scales
+    tc = c.view(blocks, 16, chunks, 4, 16).permute(0, 2, 3, 1, 4).contiguous()
+    th = h.view(blocks, 16, chunks, 4, 4 * hb).permute(0, 2, 3, 1, 4).contiguous()
+    ts = s.view(blocks, 16, chunks, 2).permute(0, 2, 1, 3).contiguous()
+    return tc, th, ts
+
+
 def decode_q5_fp16(weight):
     """fp16 matrix of fp16(q * scale) values (diagnostic; no retained cache)."""
     weight.validate()
