@@ -473,6 +473,56 @@ def row_codec_decode(backend, device, steps, warmup, copy_mb, bits_list=(5, 6)):
     return result
 
 
+def codecs(backend, device, steps, warmup):
+    """Row-codec pack and unpack on the device at the gate+up shape [34816 x 5120]:
+    Q8 and Q4 packers from fp16 weights (`venturi_q8_pack_run`, `venturi_q4_pack_run`,
+    bytes = fp16 read + codes and scales written), the Q4 row decoder to fp16
+    (`venturi_row_dequant_rows`, planes read + fp16 written) and the Q8 embedding
+    row gather (`venturi_q8_embedding_run`, 4096 ids). Each runs `steps` times
+    back to back between one pair of events; inputs resident, outputs preallocated.
+    """
+    lib = backend._native
+    n, k = 34816, 5120
+    padded = (k + 127) // 128 * 128
+    gen = torch.Generator(device=device).manual_seed(29)
+    w = (torch.randn(n, k, generator=gen, device=device) * 0.02).half()
+    c8 = torch.empty(n, padded, dtype=torch.int8, device=device)
+    s8 = torch.empty(n, padded // 32, dtype=torch.float16, device=device)
+    c4 = torch.empty(n, padded // 2, dtype=torch.uint8, device=device)
+    s4 = torch.empty(n, padded // 64, dtype=torch.float16, device=device)
+    dense = torch.empty(n, k, dtype=torch.float16, device=device)
+    ids = torch.randint(0, n, (4096,), generator=gen, device=device, dtype=torch.int64)
+    emb = torch.empty(4096, k, dtype=torch.float16, device=device)
+    stream = torch.cuda.current_stream(device)
+    s = stream.cuda_stream
+    calls = {
+        "q8_pack": (lambda: lib.venturi_q8_pack_run(w.data_ptr(), c8.data_ptr(), s8.data_ptr(), n, k, padded, 0, s),
+                    n * k * 2 + n * padded + n * (padded // 32) * 2),
+        "q4_pack": (lambda: lib.venturi_q4_pack_run(w.data_ptr(), c4.data_ptr(), s4.data_ptr(), n, k, padded, 0, s),
+                    n * k * 2 + n * padded // 2 + n * (padded // 64) * 2),
+        "q4_row_decode": (lambda: lib.venturi_row_dequant_rows(c4.data_ptr(), None, s4.data_ptr(), dense.data_ptr(), 0, n,
+                                                               k, padded, 4, s),
+                          n * padded // 2 + n * (padded // 64) * 2 + n * k * 2),
+        "q8_embedding": (lambda: lib.venturi_q8_embedding_run(c8.data_ptr(), s8.data_ptr(), ids.data_ptr(),
+                                                              emb.data_ptr(), 4096, n, k, padded, 0, s),
+                         4096 * (padded + (padded // 32) * 2 + 8 + k * 2)),
+    }
+    out = {"workload": "device row-codec pack/unpack at [34816 x 5120] (fp16 source), embedding of 4096 rows"}
+    for name, (fn, nbytes) in calls.items():
+        for _ in range(warmup):
+            backend._check(fn())
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(steps):
+            backend._check(fn())
+        b.record(stream)
+        b.synchronize()
+        t = a.elapsed_time(b) / 1e3 / steps
+        out[name] = {"us": round(t * 1e6, 1), "GB/s": round(nbytes / t / 1e9, 1),
+                     "frac_hbm": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
     """routed-expert Q4 W4A16 MoE, 128 experts, H 2048, I 768, 512 tokens top-8.
 
@@ -801,6 +851,8 @@ def main():
         result["q4_decode"] = q4_decode(backend, device, args.steps, args.warmup, args.copy_mb)
         log("Q5/Q6 row-codec decode at the config-2 shapes")
         result["q56_decode"] = row_codec_decode(backend, device, args.steps, args.warmup, args.copy_mb)
+    log("row-codec pack/unpack on the device")
+    result["codecs"] = codecs(backend, device, max(args.steps // 2, 3), 2)
     if not args.no_prefill:
         log("config-3 A8 prefill")
         result["prefill_a8"] = prefill_a8(backend, device, max(args.steps // 2, 3), 2)
