@@ -12,34 +12,41 @@ Infinity Cache) are captured once in a HIP graph; the whole job (the 16
 groups in turn) is also captured as one graph, whose replay is the timed
 region of `value`, as a decode step runs in production; the 16 group graphs
 are then replayed back to back, each between one pair of HIP events on the
-launch stream, for the per-launch durations (all graphs' outputs are checked
-against eager launches).
+launch stream, for the per-launch durations (every graph's output is checked
+against an eager launch).
 
 Printed JSON (one line): `value` is the whole-job algorithmic throughput in
 GB/s (weights N*Kp*(1+2/32) + activations M*K*2 + outputs M*N*2, per launch)
-over the timed region's wall clock; `roofline` is the dominant kernel's (the
-route with the largest share of kernel time) algorithmic bytes over its own
-event-measured time, against the 8 TB/s HBM peak; `all_kernels_GBps` is the
-same over every launch; `per_launch` gives each kernel's average launch
-duration; `cpu_baseline` times the reference's CPU path (torch FP32 GEMM over
-materialised weights) on a bounded sample of the same workload. The
-`q4_decode` (the metric's Q4 leg at M <= 16: config-2 shapes with q4_g64_fp16
-weights), `prefill_a8` (config 3), `prefill_a16` (W8A16 / W4A16 at M = 2048)
-and `moe_w4a16` (config 4) sections carry their own roofline objects.
+over the timed region's wall clock; `roofline` is the dominant kernel's
+algorithmic bytes over its own event-measured time, against the 8 TB/s HBM
+peak; `per_launch` gives each launch's average duration; `parity` compares
+every timed launch's output with the library's canonical-order route
+(venturi_q8_head_run, byte-identical to the reference's kernel order: raw
+max-abs, largest difference in fp16 ulps, outputs that differ, outputs more
+than 2e-3 off, rel-L2); `exact_route` times that canonical route on the same
+job; `cpu_baseline` times the reference's CPU path (torch FP32 GEMM over
+materialised weights) on a bounded sample of the same workload. Further
+sections of the same line carry their own roofline objects: `config1`
+(4096 x 4096 at one token, rotated copies), `q4_decode`
+(the metric's Q4 leg), `q56_decode`, `codecs`, `prefill_a8` (config 3),
+`prefill_a16` (W8A16 / W4A16 at M = 2048), `moe_w4a16` (config 4) and
+`model_decode` (config 5).
 """
 
 import argparse
 import json
 import os
-import platform
 import sys
 import time
 
 import torch
 
+ROOT = os.path.dirname(os.path.abspath(__file__))
 PROJECTIONS = (("qkv", 7168, 5120), ("o_proj", 5120, 6144), ("gate_up", 34816, 5120), ("down", 5120, 17408))
 TOKENS = (1, 4, 8, 16)
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+FP16_PEAK_TFLOPS = 2500.0
 
 
 def log(message):
@@ -47,9 +54,18 @@ def log(message):
     print(f"[bench] {message}", file=sys.stderr, flush=True)
 
 
+def padded_k(k):
+    return (k + 127) // 128 * 128
+
+
 def launch_bytes(m, n, k):
-    padded = (k + 127) // 128 * 128
+    padded = padded_k(k)
     return n * padded + n * (padded // 32) * 2 + m * k * 2 + m * n * 2
+
+
+def q4_launch_bytes(m, n, k):
+    padded = padded_k(k)
+    return n * padded // 2 + n * (padded // 64) * 2 + m * k * 2 + m * n * 2
 
 
 def parse():
@@ -60,24 +76,152 @@ def parse():
     p.add_argument("--route", default="auto", choices=("auto", "exact", "mfma"))
     p.add_argument("--copy-mb", type=float, default=600.0, help="minimum rotated weight bytes per projection")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     p.add_argument("--no-q4", action="store_true", help="skip the Q4 W4A16 and Q5/Q6 decode sections")
-    p.add_argument("--no-prefill", action="store_true", help="skip the config-3 A8 prefill section")
+    p.add_argument("--no-prefill", action="store_true", help="skip the config-3 A8 and A16 prefill sections")
     p.add_argument("--no-moe", action="store_true", help="skip the config-4 routed-expert MoE section")
     p.add_argument("--no-model", action="store_true", help="skip the config-5 64-layer decode section")
+    p.add_argument("--only", default=None,
+                   help="comma-separated extra sections to run (config1,q4,q56,codecs,a8,a16,moe,model)")
     p.add_argument("--eager", action="store_true",
                    help="time config-2 launches issued from Python instead of HIP-graph replays (for counter runs)")
     return p.parse_args()
 
 
-def build_copies(backend, device, copy_mb):
-    """Per projection, enough independent packed copies to exceed `copy_mb` MB."""
+# ---------------------------------------------------------------- helpers
+
+
+def agreement(got, ref):
+    """Raw agreement of fp16 outputs with reference-order fp16 outputs (device tensors).
+
+    max_abs, max_ulp (largest difference in fp16 ulps of the reference value),
+    flips (outputs that differ at all), over_2e-3, rel_l2, count.
+    """
+    g, r = got.double(), ref.double()
+    diff = (g - r).abs()
+    ulp = torch.exp2(torch.floor(torch.log2(r.abs().clamp_min(2.0**-14))) - 10)
+    denom = float(torch.linalg.vector_norm(r))
+    return {
+        "max_abs": float(diff.max()),
+        "max_ulp": float((diff / ulp).max()),
+        "flips": int((diff > 0).sum()),
+        "over_2e-3": int((diff > 2e-3).sum()),
+        "rel_l2": float(torch.linalg.vector_norm(g - r)) / max(denom, 1e-30),
+        "count": r.numel(),
+    }
+
+
+def merge_agreement(items):
+    """Worst-case summary of several agreement records."""
+    items = list(items)
+    return {
+        "max_abs": max(i["max_abs"] for i in items),
+        "max_ulp": max(i["max_ulp"] for i in items),
+        "flips": sum(i["flips"] for i in items),
+        "over_2e-3": sum(i["over_2e-3"] for i in items),
+        "max_rel_l2": max(i.get("rel_l2", i.get("max_rel_l2", 0.0)) for i in items),
+        "count": sum(i["count"] for i in items),
+    }
+
+
+def compact(stats):
+    return {k: (float(f"{v:.4g}") if isinstance(v, float) else v) for k, v in stats.items()}
+
+
+def event_time(fn, reps, warmup, stream):
+    """Average seconds of fn() over `reps` back-to-back calls between two events on `stream`."""
+    for _ in range(warmup):
+        fn()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        fn()
+    b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) / 1e3 / reps
+
+
+def graph_timing(groups, steps, warmup, device, eager=False):
+    """Times launch groups through HIP graphs.
+
+    ``groups`` maps a key to (run, verify): run(reps) issues `reps` launches
+    (rotating weight copies); verify() re-runs the group's last launch eagerly
+    and returns whether the group's output equals it. Each group's `steps`
+    launches are captured in one graph, and the whole job (every group in
+    turn) in another. Returns (seconds per group from events around its graph
+    replay, wall seconds of one replay of the whole-job graph, graphs equal
+    eager). With eager=True the launches are issued from Python between the
+    events instead, and the wall time is that of the eager pass.
+    """
+    stream = torch.cuda.current_stream(device)
+    for run, _ in groups.values():
+        run(warmup)
+    torch.cuda.synchronize(device)
+    events = {key: [torch.cuda.Event(enable_timing=True) for _ in range(2)] for key in groups}
+    if eager:
+        start = time.perf_counter()
+        for key, (run, _) in groups.items():
+            events[key][0].record(stream)
+            run(steps)
+            events[key][1].record(stream)
+        torch.cuda.synchronize(device)
+        wall = time.perf_counter() - start
+        return {k: e[0].elapsed_time(e[1]) / 1e3 for k, e in events.items()}, wall, None
+    graphs = {}
+    for key, (run, _) in groups.items():
+        graphs[key] = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graphs[key]):
+            run(steps)
+    same = True
+    for key, (_, verify) in groups.items():
+        graphs[key].replay()
+        torch.cuda.synchronize(device)
+        same &= bool(verify())
+    step_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(step_graph):
+        for run, _ in groups.values():
+            run(steps)
+    step_graph.replay()
+    torch.cuda.synchronize(device)
+    for _, verify in groups.values():
+        same &= bool(verify())
+    start = time.perf_counter()
+    step_graph.replay()
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - start
+    for key in groups:
+        events[key][0].record(stream)
+        graphs[key].replay()
+        events[key][1].record(stream)
+    torch.cuda.synchronize(device)
+    del graphs, step_graph
+    return {k: e[0].elapsed_time(e[1]) / 1e3 for k, e in events.items()}, wall, same
+
+
+def rotated_group(plans, x, out, steps):
+    """(run, verify) of one launch group over rotated plans writing `out`."""
+
+    def run(reps):
+        for s in range(reps):
+            plans[s % len(plans)].run(x, out=out)
+
+    def verify():
+        ref = torch.empty_like(out)
+        plans[(steps - 1) % len(plans)].run(x, out=ref)
+        torch.cuda.synchronize(out.device)
+        return torch.equal(ref.view(torch.int16), out.view(torch.int16))
+
+    return run, verify
+
+
+def q8_copies(backend, device, shapes, copy_mb, seed):
+    """Per (name, n, k), independent Q8 residents whose bytes exceed `copy_mb` MB."""
     copies = []
-    for i, (name, n, k) in enumerate(PROJECTIONS):
+    for i, (name, n, k) in enumerate(shapes):
         count = max(2, -(-int(copy_mb * 1e6) // launch_bytes(0, n, k)))
         residents = []
         for c in range(count):
-            gen = torch.Generator(device=device).manual_seed(1000 * c + i)
+            gen = torch.Generator(device=device).manual_seed(seed + 1000 * c + i)
             w = torch.randn(n, k, generator=gen, device=device, dtype=torch.float32) * 0.02
             packed = backend.quantize_q8(w)
             del w
@@ -88,35 +232,123 @@ def build_copies(backend, device, copy_mb):
     return copies
 
 
-def cpu_baseline(copies, xs, seconds):
-    """Reference CPU path on copy 0 of the weights; same M values and inputs."""
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle.cpu_path import CpuQuantizedLinear, cpu_threads, time_calls
+def cpu_description(threads):
+    from oracle.cpu_path import cpu_model
 
-    threads = cpu_threads()
-    layers = []
-    for residents, (_, n, k) in zip(copies, PROJECTIONS):
-        resident = residents[0]
-        codes, scales = (t.cpu() for t in resident.storage_tensors)
-        layers.append((CpuQuantizedLinear(codes, scales, k), n, k))
-    calls, step_bytes = [], 0
+    return f"{threads} threads on {cpu_model()}, torch {torch.__version__}"
+
+
+# ---------------------------------------------------------------- config 2
+
+
+def decode_job(backend, device, copies, route, steps, warmup, eager):
+    """The config-2 job on one route: per-launch seconds, wall seconds, graph check, outputs of copy 0."""
+    gen = torch.Generator(device=device).manual_seed(7)
+    xs = {m: {k: torch.randn(m, k, generator=gen, device=device).half() for k in {p[2] for p in PROJECTIONS}}
+          for m in TOKENS}
+    groups, outs, plans = {}, {}, {}
     for m in TOKENS:
-        for layer, n, k in layers:
-            calls.append(lambda layer=layer, x=xs[m][k].cpu(): layer.run(x))
-            step_bytes += launch_bytes(m, n, k)
-    reps, elapsed = time_calls(calls, seconds)
-    return {
-        "value": round(reps * step_bytes / elapsed / 1e9, 3),
+        for pi, (name, n, k) in enumerate(PROJECTIONS):
+            key = (m, name)
+            plans[key] = [r.prepare(tokens=m, route=route) for r in copies[pi]]
+            outs[key] = torch.empty(m, n, dtype=torch.float16, device=device)
+            groups[key] = rotated_group(plans[key], xs[m][k], outs[key], steps)
+    seconds, wall, same = graph_timing(groups, steps, warmup, device, eager)
+    first = {}
+    for (m, name), p in plans.items():
+        k = dict((q[0], q[2]) for q in PROJECTIONS)[name]
+        o = torch.empty_like(outs[(m, name)])
+        p[0].run(xs[m][k], out=o)
+        first[(m, name)] = o
+    torch.cuda.synchronize(device)
+    routes = {key: p[0].route for key, p in plans.items()}
+    return seconds, wall, same, first, routes
+
+
+def config2(backend, device, args):
+    log("packing config-2 weight copies")
+    copies = q8_copies(backend, device, PROJECTIONS, args.copy_mb, 0)
+    step_bytes = sum(launch_bytes(m, n, k) for m in TOKENS for _, n, k in PROJECTIONS)
+    log("config-2 decode: warm-up, graph capture and timed region")
+    seconds, wall, same, outputs, routes = decode_job(backend, device, copies, args.route, args.steps, args.warmup,
+                                                      args.eager)
+    log("config-2 decode on the canonical-order route (timing and parity reference)")
+    ex_seconds, ex_wall, ex_same, ex_outputs, _ = decode_job(backend, device, copies, "exact", args.steps,
+                                                             max(1, args.warmup // 2), args.eager)
+    total_bytes = args.steps * step_bytes
+    detail, ex_detail, parity = {}, {}, {}
+    by_route = {}
+    for m in TOKENS:
+        for name, n, k in PROJECTIONS:
+            key, label = (m, name), f"{name}_m{m}"
+            avg = seconds[key] / args.steps
+            b = launch_bytes(m, n, k)
+            detail[label] = {"us": round(avg * 1e6, 2), "GB/s": round(b / avg / 1e9, 1), "route": routes[key]}
+            ex_avg = ex_seconds[key] / args.steps
+            ex_detail[label] = {"us": round(ex_avg * 1e6, 2), "GB/s": round(b / ex_avg / 1e9, 1)}
+            parity[label] = compact(agreement(outputs[key], ex_outputs[key]))
+            bt = by_route.get(routes[key], (0, 0.0))
+            by_route[routes[key]] = (bt[0] + args.steps * b, bt[1] + seconds[key])
+    dominant = max(by_route, key=lambda r: by_route[r][1])
+    achieved = by_route[dominant][0] / by_route[dominant][1] / 1e9
+    kernels = {"venturi-q8-exact": "q8_exact (canonical order)",
+               "venturi-q8-mfma": "q8_tiled_lds / q8_tiled_decode (fp16 MFMA)"}
+    summary = merge_agreement(parity.values())
+    result = {
+        "metric": "Q8 quantlinear decode GB/s (M<=16), config-2 projection set",
+        "value": round(total_bytes / wall / 1e9, 2),
         "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{reps} repetitions of the full config-2 step (4 projections x M in {list(TOKENS)}), "
-        f"torch {torch.__version__} CPU GEMM, FP32 weights materialised before timing, "
-        f"{elapsed:.1f} s on {platform.processor() or platform.machine()}",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: weights N(0,0.02) packed to q8_g32_fp16 on device, activations N(0,1) fp16",
+        "config": {
+            "workload": "config2: Qwen-27B-class Q8 decode projection set, hidden 5120, M in {1,4,8,16}",
+            "projections": {p[0]: [p[1], p[2]] for p in PROJECTIONS},
+            "tokens": list(TOKENS),
+            "weight_copies": {p[0]: len(c) for p, c in zip(PROJECTIONS, copies)},
+            "routes": sorted(set(routes.values())),
+            "bytes_per_step": step_bytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": kernels.get(dominant, dominant),
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(args.route),
+        },
+        "all_kernels_GBps": round(total_bytes / sum(seconds.values()) / 1e9, 1),
+        "graph_equals_eager": same,
+        "timing": ("eager launches" if args.eager else
+                   "value: one HIP graph of the whole job (K steps x 16 launch groups), wall clock of its replay; "
+                   "per_launch: one graph per group between HIP events"),
+        "parity": {
+            "against": "venturi_q8_head_run (canonical order, byte-identical to the reference's q8_head order; "
+                       "checked against the oracle by tests/test_gpu_q8_exact.py)",
+            "tolerance": "max-abs 2e-3 where |y| < 4; one fp16 ulp (3.9e-3) at |y| >= 4",
+            "summary": compact(summary),
+            "per_launch": parity,
+        },
+        "exact_route": {
+            "kernel": "q8_exact (venturi_q8_head_run)",
+            "GB/s": round(total_bytes / ex_wall / 1e9, 1),
+            "kernels_GBps": round(total_bytes / sum(ex_seconds.values()) / 1e9, 1),
+            "graph_equals_eager": ex_same,
+            "per_launch": ex_detail,
+        },
+        "per_launch": detail,
     }
+    return result, copies
 
 
-TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "q8_decode_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q8_decode_traffic.json")
 
 
 def measured_traffic(route):
@@ -137,10 +369,72 @@ def measured_traffic(route):
     return record.get("traffic_bytes_per_launch")
 
 
-INT8_PEAK_TOPS = 5000.0
+def cpu_baseline(copies, seconds):
+    """Reference CPU path on copy 0 of the config-2 weights; same M values, seeded inputs."""
+    from oracle.cpu_path import CpuQuantizedLinear, cpu_threads, time_calls
+
+    threads = cpu_threads()
+    layers = []
+    for residents, (_, n, k) in zip(copies, PROJECTIONS):
+        codes, scales = (t.cpu() for t in residents[0].storage_tensors[:2])
+        layers.append((CpuQuantizedLinear(codes, scales, k), n, k))
+    gen = torch.Generator().manual_seed(7)
+    calls, step_bytes = [], 0
+    for m in TOKENS:
+        for layer, n, k in layers:
+            x = torch.randn(m, k, generator=gen).half()
+            calls.append(lambda layer=layer, x=x: layer.run(x))
+            step_bytes += launch_bytes(m, n, k)
+    reps, elapsed = time_calls(calls, seconds)
+    return {
+        "value": round(reps * step_bytes / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{reps} repetitions of the full config-2 step (4 projections x M in {list(TOKENS)}), "
+        f"FP32 weights materialised before timing, {elapsed:.1f} s; {cpu_description(threads)}",
+    }
 
 
-def prefill_a8(backend, device, steps, warmup):
+# ---------------------------------------------------------------- config 1
+
+
+def config1(backend, device, steps, warmup, copy_mb):
+    """one q8_g32_fp16 [4096 x 4096] projection at one token.
+
+    Weights N(0, 0.02) (copy 0 from seed 0), x fp16 N(0, 1) from seed 1. The
+    17.8 MB matrix fits the 256 MB Infinity Cache, so each graph rotates
+    >= `copy_mb` MB of independent copies (at least 2 x the copy count
+    launches per graph); auto and canonical routes are timed alike and their
+    outputs compared.
+    """
+    shape = (("w", 4096, 4096),)
+    copies = q8_copies(backend, device, shape, copy_mb, 0)[0]
+    x = torch.randn(1, 4096, generator=torch.Generator().manual_seed(1)).half().to(device)
+    reps = max(steps, 2 * len(copies))
+    b = launch_bytes(1, 4096, 4096)
+    out, result = {}, {"workload": "config1: q8_g32_fp16 [4096 x 4096], M=1", "weight_copies": len(copies),
+                       "launches_per_graph": reps, "bytes_per_launch": b}
+    for route in ("auto", "exact"):
+        plans = [r.prepare(tokens=1, route=route) for r in copies]
+        out[route] = torch.empty(1, 4096, dtype=torch.float16, device=device)
+        seconds, wall, same = graph_timing({route: rotated_group(plans, x, out[route], reps)}, reps, warmup, device)
+        avg = seconds[route] / reps
+        gbs = b / avg / 1e9
+        result[route] = {"route": plans[0].route, "us": round(avg * 1e6, 3), "GB/s": round(gbs, 1),
+                         "graph_equals_eager": same,
+                         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                      "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+        plans[0].run(x, out=out[route])
+    torch.cuda.synchronize(device)
+    result["parity_auto_vs_exact"] = compact(agreement(out["auto"], out["exact"]))
+    return result
+
+
+# ---------------------------------------------------------------- config 3
+
+
+def prefill_a8(backend, device, steps, warmup, cpu_seconds):
     """RMSNorm + 1-pass A8 at hidden 5120, int8 GEMMs at the config-2 shapes, M = 2048.
 
     x fp16 [2048, 5120] ~ N(0, 1) with 51 seeded channels (1%) scaled by 20;
@@ -149,7 +443,8 @@ def prefill_a8(backend, device, steps, warmup):
     activations with the plain A8 quantizer. Each stage runs `steps` times back
     to back between one pair of events; TOPS = 2*M*N*K / average time. The
     GEMMs run on the plan's auto route (matrix cores, natural group order);
-    the reference-order route is timed beside it.
+    the reference-order route is timed beside it and its outputs are the
+    parity reference.
     """
     from venturi_amd import prepare_q8_dp4a, prepare_rms_q8
 
@@ -163,36 +458,33 @@ def prefill_a8(backend, device, steps, warmup):
     norm = backend.upload_rmsnorm(gamma, dtype=torch.float16, device=device, epsilon=1e-6)
     rms_plan = prepare_rms_q8(norm, tokens=m, residual_compensation=False)
     stream = torch.cuda.current_stream(device)
-    results, total_ops, total_s, exact_s = {}, 0, 0.0, 0.0
-
-    def timed(fn, reps):
-        for _ in range(warmup):
-            fn()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(reps):
-            fn()
-        b.record(stream)
-        b.synchronize()
-        return a.elapsed_time(b) / 1e3 / reps
-
+    results, total_ops, total_s, exact_s, parity = {}, 0, 0.0, 0.0, {}
     ws_5120 = torch.empty(rms_plan.workspace_bytes, dtype=torch.uint8, device=device)
-    results["rms_a8_k5120"] = {"us": round(timed(lambda: rms_plan.run(x, workspace=ws_5120), steps) * 1e6, 2)}
-    for i, (name, n, k) in enumerate(PROJECTIONS):
+    results["rms_a8_k5120"] = {
+        "us": round(event_time(lambda: rms_plan.run(x, workspace=ws_5120), steps, warmup, stream) * 1e6, 2),
+        "bytes_per_token": 16000}
+    cpu_layers = []
+    for name, n, k in PROJECTIONS:
         packed = backend.quantize_q8(torch.randn(n, k, generator=gen, device=device) * 0.02)
         resident = backend.upload_linear(packed, dtype=torch.float16, device=device)
+        if cpu_seconds > 0:
+            cpu_layers.append((packed.codes.cpu(), packed.scales.cpu(), n, k))
         del packed
         plan = prepare_q8_dp4a(resident, tokens=m, residual_compensation=False)
         exact = prepare_q8_dp4a(resident, tokens=m, residual_compensation=False, route="exact")
         out = torch.empty(m, n, dtype=torch.float16, device=device)
+        ref = torch.empty_like(out)
         if k == 5120:
             ws = ws_5120
         else:
             ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
             xa = torch.randn(m, k, generator=gen, device=device).half()
-            results[f"a8_quantize_k{k}"] = {"us": round(timed(lambda: plan.quantize(xa, workspace=ws), steps) * 1e6, 2)}
-        t = timed(lambda: plan.project(out=out, workspace=ws), steps)
-        t_exact = timed(lambda: exact.project(out=out, workspace=ws), max(steps // 4, 2))
+            results[f"a8_quantize_k{k}"] = {
+                "us": round(event_time(lambda: plan.quantize(xa, workspace=ws), steps, warmup, stream) * 1e6, 2)}
+        t = event_time(lambda: plan.project(out=out, workspace=ws), steps, warmup, stream)
+        t_exact = event_time(lambda: exact.project(out=ref, workspace=ws), max(steps // 4, 2), 1, stream)
+        torch.cuda.synchronize(device)
+        parity[name] = compact(agreement(out, ref))
         ops = 2 * m * n * k
         total_ops += ops
         total_s += t
@@ -200,48 +492,62 @@ def prefill_a8(backend, device, steps, warmup):
         results[name] = {"us": round(t * 1e6, 1), "TOPS": round(ops / t / 1e12, 1),
                          "frac_int8_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4), "route": plan.route,
                          "exact_route_us": round(t_exact * 1e6, 1)}
-        del resident, plan, exact, out
+        del resident, plan, exact, out, ref
     tops = total_ops / total_s / 1e12
-    return {
+    result = {
         "workload": "config3: RMSNorm+A8 (1 pass) -> int8 GEMMs at the config-2 shapes, M=2048",
         "gemm_TOPS": round(tops, 1),
         "exact_route_gemm_TOPS": round(total_ops / exact_s / 1e12, 1),
-        "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                     "frac": round(tops / INT8_PEAK_TOPS, 4)},
+        "roofline": {"bound": "mfma", "kernel": "a8_gemm_fast", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS,
+                     "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4)},
+        "parity": {"against": "the reference-order route (venturi_q8_dp4a_run order, byte-identical to the oracle)",
+                   "summary": compact(merge_agreement(parity.values())), "per_projection": parity},
         "stages": results,
     }
+    if cpu_seconds > 0:
+        from oracle.cpu_path import CpuA8Linear, cpu_threads, time_calls
+
+        threads = cpu_threads()
+        sample = 128
+        cgen = torch.Generator().manual_seed(3)
+        calls, ops = [], 0
+        for codes, scales, n, k in cpu_layers:
+            layer = CpuA8Linear(codes, scales, k, passes=1)
+            xs = torch.randn(sample, k, generator=cgen).half()
+            calls.append(lambda layer=layer, xs=xs: layer.run(xs))
+            ops += 2 * sample * n * k
+        reps, elapsed = time_calls(calls, cpu_seconds)
+        result["cpu_baseline"] = {
+            "value": round(reps * ops / elapsed / 1e12, 4), "unit": "TOP/s", "cores": threads, "kind": "oracle",
+            "sample": f"{sample} of the 2048 tokens through the 4 projections ({reps} repetitions, {elapsed:.1f} s): "
+            f"FP32 restatement of quantize_reference (1 pass) plus the FP32 matmul of the represented values "
+            f"(the reference has no CPU int8 GEMM); {cpu_description(threads)}",
+        }
+    return result
 
 
-FP16_PEAK_TFLOPS = 2500.0
+# ---------------------------------------------------------------- A16 prefill
 
 
 def prefill_a16(backend, device, steps, warmup):
     """fp16-activation prefill GEMMs at the config-2 shapes, M = 2048 (the metric's
     "fp16 TOPS (M >= 256)" leg): W8A16 (q8_g32, venturi_q8_prefill_run) and W4A16
-    (q4_g64, venturi_q4_gemm_run), both on their plans' auto route.
+    (q4_g64, venturi_row_gemm_run), both on their plans' auto route.
 
     Weights N(0, 0.02) packed on the device; x fp16 N(0, 1). Each GEMM runs
     `steps` times back to back between one pair of events; TFLOP/s =
-    2*M*N*K / average time, against the 2.5 PFLOP/s dense fp16 peak.
+    2*M*N*K / average time, against the 2.5 PFLOP/s dense fp16 peak. Parity:
+    W8A16 against the canonical-order route (venturi_q8_head_run); W4A16
+    against the reference's own W4A16 path on this GPU (fp16(q*s) weights
+    decoded by venturi_row_dequant_rows, then torch's fp16 linear with fp32
+    accumulation, as the reference's dequant-then-F.linear path does).
     """
     m = 2048
     gen = torch.Generator(device=device).manual_seed(11)
     stream = torch.cuda.current_stream(device)
-
-    def timed(fn, reps):
-        for _ in range(warmup):
-            fn()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(reps):
-            fn()
-        b.record(stream)
-        b.synchronize()
-        return a.elapsed_time(b) / 1e3 / reps
-
     sections = {}
     for codec, quantize in (("w8a16", backend.quantize_q8), ("w4a16", backend.quantize_q4)):
-        stages, total_flops, total_s, route = {}, 0, 0.0, None
+        stages, total_flops, total_s, route, parity = {}, 0, 0.0, None, {}
         for name, n, k in PROJECTIONS:
             packed = quantize(torch.randn(n, k, generator=gen, device=device) * 0.02)
             resident = backend.upload_linear(packed, dtype=torch.float16, device=device)
@@ -250,24 +556,37 @@ def prefill_a16(backend, device, steps, warmup):
             route = plan.route
             x = torch.randn(m, k, generator=gen, device=device).half()
             out = torch.empty(m, n, dtype=torch.float16, device=device)
-            t = timed(lambda: plan.run(x, out=out), steps)
+            t = event_time(lambda: plan.run(x, out=out), steps, warmup, stream)
+            if codec == "w8a16":
+                ref = torch.empty_like(out)
+                resident.prepare(tokens=m, route="exact").run(x, out=ref)
+            else:
+                dense = torch.empty(n, k, dtype=torch.float16, device=device)
+                resident._payload.decode(out=dense)
+                ref = torch.nn.functional.linear(x, dense)
+                del dense
+            torch.cuda.synchronize(device)
+            parity[name] = compact(agreement(out, ref))
             flops = 2 * m * n * k
             total_flops += flops
             total_s += t
             stages[name] = {"us": round(t * 1e6, 1), "TFLOP/s": round(flops / t / 1e12, 1),
                             "frac_fp16_peak": round(flops / t / 1e12 / FP16_PEAK_TFLOPS, 4)}
-            del resident, plan, x, out
+            del resident, plan, x, out, ref
         tf = total_flops / total_s / 1e12
         sections[codec] = {"route": route, "TFLOP/s": round(tf, 1),
-                           "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": FP16_PEAK_TFLOPS,
-                                        "unit": "TFLOP/s", "frac": round(tf / FP16_PEAK_TFLOPS, 4)},
+                           "roofline": {"bound": "mfma", "kernel": "q8_prefill" if codec == "w8a16" else "row_prefill",
+                                        "achieved": round(tf, 1), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                        "frac": round(tf / FP16_PEAK_TFLOPS, 4)},
+                           "parity": {"against": "canonical-order route" if codec == "w8a16" else
+                                      "decoded fp16 weights + torch fp16 linear (the reference's W4A16 path)",
+                                      "summary": compact(merge_agreement(parity.values())),
+                                      "per_projection": parity},
                            "stages": stages}
     return {"workload": "fp16-activation prefill GEMMs at the config-2 shapes, M=2048", **sections}
 
 
-def q4_launch_bytes(m, n, k):
-    padded = (k + 127) // 128 * 128
-    return n * padded // 2 + n * (padded // 64) * 2 + m * k * 2 + m * n * 2
+# ---------------------------------------------------------------- Q4 / Q5 / Q6 decode
 
 
 def q4_decode(backend, device, steps, warmup, copy_mb):
@@ -295,76 +614,30 @@ def q4_decode(backend, device, steps, warmup, copy_mb):
     gen = torch.Generator(device=device).manual_seed(17)
     xs = {m: {k: torch.randn(m, k, generator=gen, device=device).half() for k in {p[2] for p in PROJECTIONS}}
           for m in TOKENS}
-    outs = {(m, n): torch.empty(m, n, dtype=torch.float16, device=device) for m in TOKENS for (_, n, _) in PROJECTIONS}
-    launches = [(mi, pi) for mi in range(len(TOKENS)) for pi in range(len(PROJECTIONS))]
-    plans = {(mi, pi): [r.prepare(tokens=TOKENS[mi]) for r in copies[pi]] for mi, pi in launches}
-    stream = torch.cuda.current_stream(device)
-
-    def run(mi, pi, reps):
-        m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
-        rotation = plans[(mi, pi)]
-        for s in range(reps):
-            rotation[s % len(rotation)].run(xs[m][k], out=outs[(m, n)])
-
-    for key in launches:
-        run(*key, warmup)
-    torch.cuda.synchronize(device)
-    graphs = {}
-    for key in launches:
-        graphs[key] = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graphs[key]):
-            run(*key, steps)
-    graph_equals_eager = True
-    for mi, pi in launches:
-        m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
-        ref = torch.empty_like(outs[(m, n)])
-        plans[(mi, pi)][(steps - 1) % len(plans[(mi, pi)])].run(xs[m][k], out=ref)
-        graphs[(mi, pi)].replay()
-        torch.cuda.synchronize(device)
-        graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
-    # As in the Q8 timing: the whole job as one graph for `GB/s`, the group
-    # graphs between events for the per-launch durations.
-    step_graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(step_graph):
-        for key in launches:
-            run(*key, steps)
-    step_graph.replay()
-    torch.cuda.synchronize(device)
-    last_writer = {(TOKENS[mi], PROJECTIONS[pi][1]): (mi, pi) for mi, pi in launches}
-    for mi, pi in last_writer.values():
-        m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
-        ref = torch.empty_like(outs[(m, n)])
-        plans[(mi, pi)][(steps - 1) % len(plans[(mi, pi)])].run(xs[m][k], out=ref)
-        torch.cuda.synchronize(device)
-        graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
-    events = {key: [torch.cuda.Event(enable_timing=True) for _ in range(2)] for key in launches}
-    torch.cuda.synchronize(device)
-    start = time.perf_counter()
-    step_graph.replay()
-    torch.cuda.synchronize(device)
-    wall = time.perf_counter() - start
-    for key in launches:
-        events[key][0].record(stream)
-        graphs[key].replay()
-        events[key][1].record(stream)
-    torch.cuda.synchronize(device)
-    detail, total_bytes, kernel_total = {}, 0, 0.0
-    for mi, pi in launches:
-        m, (name, n, k) = TOKENS[mi], PROJECTIONS[pi]
-        t = events[(mi, pi)][0].elapsed_time(events[(mi, pi)][1]) / 1e3
-        b = steps * q4_launch_bytes(m, n, k)
-        total_bytes += b
-        kernel_total += t
-        detail[f"{name}_m{m}"] = {"us": round(t / steps * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
-    achieved = total_bytes / kernel_total / 1e9
+    groups, route = {}, None
+    for m in TOKENS:
+        for pi, (name, n, k) in enumerate(PROJECTIONS):
+            plans = [r.prepare(tokens=m) for r in copies[pi]]
+            route = plans[0].route
+            groups[(m, name)] = rotated_group(plans, xs[m][k], torch.empty(m, n, dtype=torch.float16, device=device),
+                                              steps)
+    seconds, wall, same = graph_timing(groups, steps, warmup, device)
+    detail, total_bytes = {}, 0
+    for m in TOKENS:
+        for name, n, k in PROJECTIONS:
+            t = seconds[(m, name)]
+            b = steps * q4_launch_bytes(m, n, k)
+            total_bytes += b
+            detail[f"{name}_m{m}"] = {"us": round(t / steps * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+    achieved = total_bytes / sum(seconds.values()) / 1e9
     return {
         "workload": "config-2 projection set with q4_g64_fp16 weights (W4A16 contract), M in {1,4,8,16}",
-        "route": plans[(0, 0)][0].route,
+        "route": route,
         "GB/s": round(total_bytes / wall / 1e9, 1),
         "roofline": {"bound": "hbm", "kernel": "row_decode_gemm (fp16 MFMA, W4A16 contract)", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4)},
         "weight_copies": {p[0]: len(c) for p, c in zip(PROJECTIONS, copies)},
-        "graph_equals_eager": graph_equals_eager,
+        "graph_equals_eager": same,
         "per_launch": detail,
     }
 
@@ -389,14 +662,14 @@ def row_codec_decode(backend, device, steps, warmup, copy_mb, bits_list=(5, 6)):
     for bits in bits_list:
         hb = bits - 4
 
-        def launch_bytes_rc(m, n, k):
-            padded = (k + 127) // 128 * 128
+        def nbytes(m, n, k):
+            padded = padded_k(k)
             return n * padded // 2 + n * padded * hb // 8 + n * (padded // 64) * 2 + m * k * 2 + m * n * 2
 
         copies = []
         for name, n, k in PROJECTIONS:
-            padded = (k + 127) // 128 * 128
-            count = max(2, -(-int(copy_mb * 1e6) // launch_bytes_rc(0, n, k)))
+            padded = padded_k(k)
+            count = max(2, -(-int(copy_mb * 1e6) // nbytes(0, n, k)))
             planes = []
             for _ in range(count):
                 codes = torch.randint(0, 256, (n, padded // 2), dtype=torch.uint8, device=device, generator=gen)
@@ -407,69 +680,51 @@ def row_codec_decode(backend, device, steps, warmup, copy_mb, bits_list=(5, 6)):
             copies.append(planes)
         xs = {m: {k: torch.randn(m, k, generator=gen, device=device).half() for k in {p[2] for p in PROJECTIONS}}
               for m in TOKENS}
-        outs = {(m, pi): torch.empty(m, PROJECTIONS[pi][1], dtype=torch.float16, device=device)
-                for m in TOKENS for pi in range(len(PROJECTIONS))}
-        launches = [(mi, pi) for mi in range(len(TOKENS)) for pi in range(len(PROJECTIONS))]
-        slots = {}
-        for mi, pi in launches:
-            size = int(lib.venturi_q4_tiled_workspace_bytes(TOKENS[mi], PROJECTIONS[pi][1], PROJECTIONS[pi][2]))
-            if size:
-                slots[(mi, pi)] = torch.empty(size, dtype=torch.uint8, device=device)
-                backend._check(lib.venturi_q4_tiled_workspace_init(slots[(mi, pi)].data_ptr(), size,
-                                                                   stream.cuda_stream))
+        groups = {}
+        for m in TOKENS:
+            for pi, (name, n, k) in enumerate(PROJECTIONS):
+                size = int(lib.venturi_q4_tiled_workspace_bytes(m, n, k))
+                slot = None
+                if size:
+                    slot = torch.empty(size, dtype=torch.uint8, device=device)
+                    backend._check(lib.venturi_q4_tiled_workspace_init(slot.data_ptr(), size, stream.cuda_stream))
+                out = torch.empty(m, n, dtype=torch.float16, device=device)
 
-        def run(mi, pi, reps):
-            m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
-            padded = (k + 127) // 128 * 128
-            slot = slots.get((mi, pi))
-            launch_stream = torch.cuda.current_stream(device).cuda_stream  # the capture stream inside a graph
-            for r in range(reps):
-                codes, high, scales = copies[pi][r % len(copies[pi])]
-                backend._check(lib.venturi_row_tiled_run(
-                    xs[m][k].data_ptr(), codes.data_ptr(), high.data_ptr(), scales.data_ptr(),
-                    outs[(m, pi)].data_ptr(), m, n, k, padded, bits, 0, None if slot is None else slot.data_ptr(),
-                    0 if slot is None else slot.numel(), launch_stream))
+                def launch(r, out, m=m, n=n, k=k, pi=pi, slot=slot):
+                    codes, high, scales = copies[pi][r % len(copies[pi])]
+                    backend._check(lib.venturi_row_tiled_run(
+                        xs[m][k].data_ptr(), codes.data_ptr(), high.data_ptr(), scales.data_ptr(), out.data_ptr(),
+                        m, n, k, padded_k(k), bits, 0, None if slot is None else slot.data_ptr(),
+                        0 if slot is None else slot.numel(), torch.cuda.current_stream(device).cuda_stream))
 
-        for key in launches:
-            run(*key, warmup)
-        torch.cuda.synchronize(device)
-        graphs = {}
-        for key in launches:
-            graphs[key] = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graphs[key]):
-                run(*key, steps)
-        step_graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(step_graph):
-            for key in launches:
-                run(*key, steps)
-        step_graph.replay()
-        torch.cuda.synchronize(device)
-        start = time.perf_counter()
-        step_graph.replay()
-        torch.cuda.synchronize(device)
-        wall = time.perf_counter() - start
-        events = {key: [torch.cuda.Event(enable_timing=True) for _ in range(2)] for key in launches}
-        for key in launches:
-            events[key][0].record(stream)
-            graphs[key].replay()
-            events[key][1].record(stream)
-        torch.cuda.synchronize(device)
-        detail, total_bytes, kernel_total = {}, 0, 0.0
-        for mi, pi in launches:
-            m, (name, n, k) = TOKENS[mi], PROJECTIONS[pi]
-            t = events[(mi, pi)][0].elapsed_time(events[(mi, pi)][1]) / 1e3
-            b = steps * launch_bytes_rc(m, n, k)
-            total_bytes += b
-            kernel_total += t
-            detail[f"{name}_m{m}"] = {"us": round(t / steps * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
-        achieved = total_bytes / kernel_total / 1e9
+                def run(reps, launch=launch, out=out):
+                    for r in range(reps):
+                        launch(r, out)
+
+                def verify(launch=launch, out=out):
+                    ref = torch.empty_like(out)
+                    launch(steps - 1, ref)
+                    torch.cuda.synchronize(device)
+                    return torch.equal(ref.view(torch.int16), out.view(torch.int16))
+
+                groups[(m, name)] = (run, verify)
+        seconds, wall, same = graph_timing(groups, steps, warmup, device)
+        detail, total_bytes = {}, 0
+        for m in TOKENS:
+            for name, n, k in PROJECTIONS:
+                t = seconds[(m, name)]
+                b = steps * nbytes(m, n, k)
+                total_bytes += b
+                detail[f"{name}_m{m}"] = {"us": round(t / steps * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+        achieved = total_bytes / sum(seconds.values()) / 1e9
         result[f"q{bits}"] = {
             "GB/s": round(total_bytes / wall / 1e9, 1),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4)},
+            "graph_equals_eager": same,
             "per_launch": detail,
         }
-        del copies, graphs, step_graph
+        del copies, groups
     return result
 
 
@@ -483,7 +738,7 @@ def codecs(backend, device, steps, warmup):
     """
     lib = backend._native
     n, k = 34816, 5120
-    padded = (k + 127) // 128 * 128
+    padded = padded_k(k)
     gen = torch.Generator(device=device).manual_seed(29)
     w = (torch.randn(n, k, generator=gen, device=device) * 0.02).half()
     c8 = torch.empty(n, padded, dtype=torch.int8, device=device)
@@ -509,17 +764,30 @@ def codecs(backend, device, steps, warmup):
     }
     out = {"workload": "device row-codec pack/unpack at [34816 x 5120] (fp16 source), embedding of 4096 rows"}
     for name, (fn, nbytes) in calls.items():
-        for _ in range(warmup):
-            backend._check(fn())
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(steps):
-            backend._check(fn())
-        b.record(stream)
-        b.synchronize()
-        t = a.elapsed_time(b) / 1e3 / steps
+        t = event_time(lambda: backend._check(fn()), steps, warmup, stream)
         out[name] = {"us": round(t * 1e6, 1), "GB/s": round(nbytes / t / 1e9, 1),
                      "frac_hbm": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
+# ---------------------------------------------------------------- config 4
+
+
+def moe_reference(x, ids, scores, dense_gu, dense_dn):
+    """routed_experts (flash_next_moe.py:139-161) over fp16(q*s) expert weights on this GPU:
+    ascending experts, fp16 linear with fp32 accumulation, fp16 SiLU*up, fp16 score
+    multiply and index_add."""
+    out = torch.zeros_like(x)
+    inter = dense_gu[0].shape[0] // 2
+    for e in range(len(dense_gu)):
+        positions, tokens = torch.where((ids == e).T)
+        if tokens.numel() == 0:
+            continue
+        gu = torch.nn.functional.linear(x[tokens], dense_gu[e])
+        gate, up = gu[:, :inter], gu[:, inter:]
+        h = torch.nn.functional.silu(gate) * up
+        y = torch.nn.functional.linear(h, dense_dn[e])
+        out.index_add_(0, tokens, y * scores[tokens, positions, None])
     return out
 
 
@@ -533,13 +801,14 @@ def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
     from the 256 MB Infinity Cache. One step = routing + gate/up GEMM with
     SiLU*up + down GEMM with the score + ordered combine (four launches).
     Algorithmic bytes per step = expert planes + x + out + ids + scores;
-    FLOPs = 2 * pairs * (2I*H + H*I).
+    FLOPs = 2 * pairs * (2I*H + H*I). Parity against the reference's routed
+    expert loop run with torch on this GPU (fp16(q*s) weights, fp16 linear).
     """
     from venturi_amd.moe import MoEGeometry, Q4ExpertBank
 
     g = MoEGeometry(2048, 128, 8, 768)
     tokens = 512
-    banks, sample_planes = [], []
+    banks, sample_planes, dense_gu, dense_dn = [], [], [], []
     for copy in range(2):
         experts = []
         for e in range(g.num_experts):
@@ -548,8 +817,16 @@ def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
             dn = backend.quantize_q4(torch.randn(g.hidden_size, g.intermediate_size, generator=gen, device=device) * 0.02)
             experts.append((gu, dn))
         banks.append(Q4ExpertBank.upload(backend, g, experts, device=device))
-        if copy == 0:  # row-split planes of experts 0-15 for the CPU baseline
+        if copy == 0:
             sample_planes = [(gu.codes.cpu(), gu.scales.cpu(), dn.codes.cpu(), dn.scales.cpu()) for gu, dn in experts[:16]]
+            for gu, dn in experts:
+                for w, rows, cols, dest in ((gu, 2 * g.intermediate_size, g.hidden_size, dense_gu),
+                                            (dn, g.hidden_size, g.intermediate_size, dense_dn)):
+                    d = torch.empty(rows, cols, dtype=torch.float16, device=device)
+                    backend._check(backend._native.venturi_row_dequant_rows(
+                        w.codes.data_ptr(), None, w.scales.data_ptr(), d.data_ptr(), 0, rows, cols, w.padded_k, 4,
+                        torch.cuda.current_stream(device).cuda_stream))
+                    dest.append(d)
         del experts
     cpu_gen = torch.Generator().manual_seed(4)
     ids = torch.stack([torch.randperm(g.num_experts, generator=cpu_gen)[: g.top_k] for _ in range(tokens)])
@@ -560,16 +837,18 @@ def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
     workspace = torch.empty(plans[0].workspace_bytes, dtype=torch.uint8, device=device)
     out = torch.empty(tokens, g.hidden_size, dtype=torch.float16, device=device)
     stream = torch.cuda.current_stream(device)
-    for i in range(warmup):
-        plans[i % 2].run(xd, idsd, scoresd, out=out, workspace=workspace)
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    counter = [0]
+
+    def step():
+        plans[counter[0] % 2].run(xd, idsd, scoresd, out=out, workspace=workspace)
+        counter[0] += 1
+
+    step_s = event_time(step, steps, warmup, stream)
+    plans[0].run(xd, idsd, scoresd, out=out, workspace=workspace)
+    ref = moe_reference(xd, idsd, scoresd, dense_gu, dense_dn)
     torch.cuda.synchronize(device)
-    a.record(stream)
-    for i in range(steps):
-        plans[i % 2].run(xd, idsd, scoresd, out=out, workspace=workspace)
-    b.record(stream)
-    b.synchronize()
-    step_s = a.elapsed_time(b) / 1e3 / steps
+    parity = compact(agreement(out, ref))
+    del dense_gu, dense_dn, ref
     pairs = tokens * g.top_k
     nbytes = banks[0].storage_nbytes + 2 * tokens * g.hidden_size * 2 + pairs * (8 + 2)
     flops = 2 * pairs * (2 * g.intermediate_size * g.hidden_size + g.hidden_size * g.intermediate_size)
@@ -582,9 +861,11 @@ def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
         "tokens_per_s": round(tokens / step_s, 1),
         "bytes_per_step": nbytes,
         "flops_per_step": flops,
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": "q4_grouped", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "fp16_mfma_frac": round(flops / step_s / 1e12 / FP16_PEAK_TFLOPS, 4)},
+        "parity": {"against": "routed_experts loop with torch fp16 linear over fp16(q*s) weights on this GPU",
+                   **parity},
     }
     if cpu_seconds > 0:
         from oracle.cpu_path import CpuRoutedExperts, cpu_threads, q4_fp32_weight, time_calls
@@ -599,10 +880,14 @@ def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
         result["cpu_baseline"] = {
             "value": round(nbytes / full_s / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"experts 0-15 of 128 ({reps} repetitions, {elapsed:.1f} s), staged-fp32 cpu_expert path "
-            f"with pre-materialised fp32 weights, scaled x8 to the full step ({full_s * 1e3:.1f} ms per step)",
+            f"with pre-materialised fp32 weights, scaled x8 to the full step ({full_s * 1e3:.1f} ms per step); "
+            f"{cpu_description(threads)}",
         }
     del banks, plans
     return result
+
+
+# ---------------------------------------------------------------- config 5
 
 
 def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
@@ -630,8 +915,6 @@ def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
     inter = PROJECTIONS[2][1] // 2
     results = {}
     for b in batches:
-        # gate+up runs fused with SiLU*up (venturi_q8_tiled_swiglu_run: the bytes of
-        # the projection followed by venturi_silu_mul_run, one launch instead of two).
         plans = [[r.prepare_swiglu(tokens=b) if i == 2 else r.prepare(tokens=b) for i, r in enumerate(row)]
                  for row in matrices]
         gen = torch.Generator(device=device).manual_seed(b)
@@ -661,17 +944,7 @@ def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
         graph.replay()
         torch.cuda.synchronize(device)
         same = bool(torch.equal(h[layers % 2].view(torch.int16), eager.view(torch.int16)))
-        for _ in range(warmup):
-            graph.replay()
-        stream = torch.cuda.current_stream(device)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize(device)
-        e0.record(stream)
-        for _ in range(steps):
-            graph.replay()
-        e1.record(stream)
-        e1.synchronize()
-        step_s = e0.elapsed_time(e1) / 1e3 / steps
+        step_s = event_time(graph.replay, steps, warmup, torch.cuda.current_stream(device))
         step_bytes = layers * sum(launch_bytes(b, n, k) for _, n, k in PROJECTIONS)
         results[f"B{b}"] = {
             "ms_per_step": round(step_s * 1e3, 4),
@@ -690,183 +963,59 @@ def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
     }
 
 
+# ---------------------------------------------------------------- main
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, ROOT)
     from venturi_amd import create_backend
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     backend = create_backend("hip")
-    log("packing config-2 weight copies")
-    copies = build_copies(backend, device, args.copy_mb)
-    gen = torch.Generator(device=device).manual_seed(7)
-    xs = {m: {k: torch.randn(m, k, generator=gen, device=device).half() for k in {p[2] for p in PROJECTIONS}}
-          for m in TOKENS}
-    outs = {(m, n): torch.empty(m, n, dtype=torch.float16, device=device) for m in TOKENS for (_, n, _) in PROJECTIONS}
-    launches = [(mi, pi) for mi in range(len(TOKENS)) for pi in range(len(PROJECTIONS))]
-    plans = {(mi, pi): [r.prepare(tokens=TOKENS[mi], route=args.route) for r in copies[pi]] for mi, pi in launches}
-    routes = sorted({p[0].route for p in plans.values()})
-    step_bytes = sum(launch_bytes(TOKENS[mi], PROJECTIONS[pi][1], PROJECTIONS[pi][2]) for mi, pi in launches)
-    stream = torch.cuda.current_stream(device)
+    only = set(args.only.split(",")) if args.only else None
 
-    def run(mi, pi, reps, events=None):
-        m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
-        rotation = plans[(mi, pi)]
-        if events is not None:
-            events[0].record(stream)
-        for s in range(reps):
-            rotation[s % len(rotation)].run(xs[m][k], out=outs[(m, n)])
-        if events is not None:
-            events[1].record(stream)
+    def wanted(name, skip=False):
+        return (name in only) if only is not None else not skip
 
-    log("config-2 decode: warm-up, graph capture and timed region")
-    for mi, pi in launches:
-        run(mi, pi, args.warmup)
-    torch.cuda.synchronize(device)
-    # Each (projection, M) group of K rotated launches is captured once in a
-    # HIP graph, so the timed region measures the kernels rather than the
-    # Python launch path (a 10 us kernel is shorter than one host call).
-    graphs, graph_equals_eager = {}, None
-    if not args.eager:
-        for key in launches:
-            graphs[key] = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graphs[key]):
-                run(*key, args.steps)
-        for key in launches:
-            graphs[key].replay()
-        torch.cuda.synchronize(device)
-        graph_equals_eager = True
-        for mi, pi in launches:
-            m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
-            ref = torch.empty_like(outs[(m, n)])
-            plans[(mi, pi)][(args.steps - 1) % len(plans[(mi, pi)])].run(xs[m][k], out=ref)
-            graphs[(mi, pi)].replay()
-            torch.cuda.synchronize(device)
-            graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
-
-    # The whole job (K steps of the 16 launch groups) is also captured as one
-    # graph, as a decode step runs in production; its replay is the timed
-    # region of `value`. The per-group graphs, each between a pair of events,
-    # give the per-launch durations and the roofline.
-    step_graph = None
-    if not args.eager:
-        step_graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(step_graph):
-            for key in launches:
-                run(*key, args.steps)
-        step_graph.replay()
-        torch.cuda.synchronize(device)
-        # Output buffers are shared by projections of one shape (o_proj and down
-        # are both [M, 5120]): each holds its last writer's result.
-        last_writer = {(TOKENS[mi], PROJECTIONS[pi][1]): (mi, pi) for mi, pi in launches}
-        for mi, pi in last_writer.values():
-            m, (_, n, k) = TOKENS[mi], PROJECTIONS[pi]
-            ref = torch.empty_like(outs[(m, n)])
-            plans[(mi, pi)][(args.steps - 1) % len(plans[(mi, pi)])].run(xs[m][k], out=ref)
-            torch.cuda.synchronize(device)
-            graph_equals_eager &= bool(torch.equal(ref.view(torch.int16), outs[(m, n)].view(torch.int16)))
-
-    events = {key: [torch.cuda.Event(enable_timing=True) for _ in range(2)] for key in launches}
-    torch.cuda.synchronize(device)
-    if step_graph is not None:
-        start = time.perf_counter()
-        step_graph.replay()
-        torch.cuda.synchronize(device)
-        wall = time.perf_counter() - start
-    start = time.perf_counter()
-    for key in launches:
-        if args.eager:
-            run(*key, args.steps, events[key])
-        else:
-            events[key][0].record(stream)
-            graphs[key].replay()
-            events[key][1].record(stream)
-    torch.cuda.synchronize(device)
-    if step_graph is None:
-        wall = time.perf_counter() - start
-
-    kernel_s = {key: e[0].elapsed_time(e[1]) / 1e3 for key, e in events.items()}
-    total_bytes = args.steps * step_bytes
-    detail = {}
-    for mi, pi in launches:
-        m, (name, n, k) = TOKENS[mi], PROJECTIONS[pi]
-        avg = kernel_s[(mi, pi)] / args.steps
-        detail[f"{name}_m{m}"] = {"us": round(avg * 1e6, 2), "GB/s": round(launch_bytes(m, n, k) / avg / 1e9, 1),
-                                  "route": plans[(mi, pi)][0].route}
-    # Roofline of the dominant kernel (largest share of the timed kernel time):
-    # its algorithmic bytes over its own event-timed duration.
-    by_route = {}
-    for mi, pi in launches:
-        route = plans[(mi, pi)][0].route
-        b, t = by_route.get(route, (0, 0.0))
-        by_route[route] = (b + args.steps * launch_bytes(TOKENS[mi], PROJECTIONS[pi][1], PROJECTIONS[pi][2]),
-                           t + kernel_s[(mi, pi)])
-    dominant = max(by_route, key=lambda r: by_route[r][1])
-    achieved = by_route[dominant][0] / by_route[dominant][1] / 1e9
-    kernels = {"venturi-q8-exact": "q8_exact (canonical order)", "venturi-q8-mfma": "q8_tiled_lds / q8_tiled_decode (fp16 MFMA)"}
-    result = {
-        "metric": "Q8 quantlinear decode GB/s (M<=16), config-2 projection set",
-        "value": round(total_bytes / wall / 1e9, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(wall / args.steps * 1e3, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp32",
-        "data": "synthetic: weights N(0,0.02) packed to q8_g32_fp16 on device, activations N(0,1) fp16",
-        "config": {
-            "workload": "config2: Qwen-27B-class Q8 decode projection set, hidden 5120, M in {1,4,8,16}",
-            "projections": {p[0]: [p[1], p[2]] for p in PROJECTIONS},
-            "tokens": list(TOKENS),
-            "weight_copies": {p[0]: len(c) for p, c in zip(PROJECTIONS, copies)},
-            "routes": routes,
-            "bytes_per_step": step_bytes,
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": kernels.get(dominant, dominant),
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(args.route),
-        },
-        "all_kernels_GBps": round(total_bytes / sum(kernel_s.values()) / 1e9, 1),
-        "graph_equals_eager": graph_equals_eager,
-        "timing": ("eager launches" if args.eager else
-                   "value: one HIP graph of the whole job (K steps x 16 launch groups), wall clock of its replay; "
-                   "per_launch: one graph per group between HIP events"),
-        "per_launch": detail,
-    }
-    if not args.no_q4:
-        del plans, graphs
+    result, copies = config2(backend, device, args)
+    cpu_copies = None if args.no_cpu else [[r[0]] for r in copies]
+    del copies
+    torch.cuda.empty_cache()
+    if wanted("config1"):
+        log("config 1: 4096 x 4096 at one token")
+        result["config1"] = config1(backend, device, args.steps, args.warmup, args.copy_mb)
+    if wanted("q4", args.no_q4):
         log("Q4 W4A16 decode at the config-2 shapes")
         result["q4_decode"] = q4_decode(backend, device, args.steps, args.warmup, args.copy_mb)
+    if wanted("q56", args.no_q4):
         log("Q5/Q6 row-codec decode at the config-2 shapes")
         result["q56_decode"] = row_codec_decode(backend, device, args.steps, args.warmup, args.copy_mb)
-    log("row-codec pack/unpack on the device")
-    result["codecs"] = codecs(backend, device, max(args.steps // 2, 3), 2)
-    if not args.no_prefill:
+    torch.cuda.empty_cache()
+    if wanted("codecs"):
+        log("row-codec pack/unpack on the device")
+        result["codecs"] = codecs(backend, device, max(args.steps // 2, 3), 2)
+    if wanted("a8", args.no_prefill):
         log("config-3 A8 prefill")
-        result["prefill_a8"] = prefill_a8(backend, device, max(args.steps // 2, 3), 2)
+        result["prefill_a8"] = prefill_a8(backend, device, max(args.steps // 2, 3), 2, 0 if args.no_cpu else 6.0)
+    if wanted("a16", args.no_prefill):
         log("fp16-activation prefill GEMMs (W8A16, W4A16)")
         result["prefill_a16"] = prefill_a16(backend, device, max(args.steps // 4, 3), 1)
-    if not args.no_moe:
+    torch.cuda.empty_cache()
+    if wanted("moe", args.no_moe):
         log("config-4 routed-expert MoE")
         result["moe_w4a16"] = moe_w4a16(backend, device, max(args.steps, 10), 3, 0 if args.no_cpu else 4.0)
-    if not args.no_model:
+    torch.cuda.empty_cache()
+    if wanted("model", args.no_model):
         log("config-5 64-layer streaming decode")
         result["model_decode"] = model_decode(backend, device, max(args.steps // 4, 3), 2)
-    if not args.no_cpu:
+    if cpu_copies is not None:
         log("CPU baseline (reference CPU path)")
-        result["cpu_baseline"] = cpu_baseline(copies, xs, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(cpu_copies, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 

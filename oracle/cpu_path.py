@@ -77,3 +77,53 @@ class CpuRoutedExperts:
             y = torch.nn.functional.linear(h.float(), self.down[e]).to(torch.float16)
             out.index_add_(0, tokens, y * scores[tokens, positions, None])
         return out
+
+
+class CpuA8Linear:
+    """The A8 CPU leg, labelled "oracle": the reference has no CPU int8 GEMM.
+
+    Restates quantize_reference (tests/q8_dp4a_reference.py:6-28) in FP32 --
+    per 32-column group scale = max|r| / 127, codes = RNE(r * 127 / max|r|)
+    clamped to +-127, residual passes -- and projection_reference (:31-34) as
+    the FP32 matmul of the represented activations with the FP32 weight values
+    (materialised before timing).
+    """
+
+    def __init__(self, codes, scales, in_features, passes=1):
+        values = codes.to(torch.float32) * scales.to(torch.float32).repeat_interleave(32, -1)
+        self.weight = values[:, :in_features].contiguous()
+        self.passes = passes
+
+    def represented(self, x):
+        tokens, k = x.shape
+        groups = (k + 31) // 32
+        residual = torch.zeros(tokens, groups * 32, dtype=torch.float32)
+        residual[:, :k] = x.float()
+        residual = residual.reshape(tokens, groups, 32)
+        total = torch.zeros_like(residual)
+        for _ in range(self.passes):
+            maximum = residual.abs().amax(-1)
+            scale = maximum / 127
+            inverse = torch.where(maximum > 0, 127 / maximum, torch.zeros_like(maximum))
+            q = torch.round(residual * inverse[:, :, None]).clamp(-127, 127)
+            step = q * scale[:, :, None]
+            total += step
+            residual = residual - step
+        return total.reshape(tokens, -1)[:, :k]
+
+    def run(self, x):
+        return (self.represented(x) @ self.weight.T).to(torch.float16)
+
+
+def cpu_model():
+    """The host CPU's model name and logical core count, from /proc/cpuinfo."""
+    name, count = None, 0
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    count += 1
+                    name = name or line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return f"{name or 'unknown CPU'} ({count or os.cpu_count()} logical cores)"

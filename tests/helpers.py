@@ -24,3 +24,50 @@ def guarded_out(tokens, n, dtype, device, fill=47):
     """Output view with one sentinel element on each side."""
     guard = torch.full((tokens * n + 2,), fill, dtype=dtype, device=device)
     return guard, guard[1:-1].view(tokens, n)
+
+
+def ulp16(v):
+    """fp16 ulp at |v| (subnormal spacing below 2^-14)."""
+    v = np.abs(np.asarray(v, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(v, 2.0**-14)))
+    return 2.0 ** (e - 10)
+
+
+def agreement(got, ref):
+    """Raw agreement of fp16 outputs with reference-order fp16 values.
+
+    ``got`` and ``ref`` are float arrays (or fp16 bit patterns as uint16) of one
+    shape. Returns max-abs, the largest difference in fp16 ulps of the reference
+    value, the number of outputs that differ at all, the number above 2e-3, and
+    the relative L2 error.
+    """
+    def f64(a):
+        a = np.asarray(a)
+        return (a.view(np.float16) if a.dtype == np.uint16 else a).astype(np.float64)
+
+    g, r = f64(got), f64(ref)
+    diff = np.abs(g - r)
+    return {
+        "max_abs": float(diff.max(initial=0.0)),
+        "max_ulp": float((diff / ulp16(r)).max(initial=0.0)),
+        "max_over_tolerance": float((diff / np.maximum(2e-3, ulp16(r))).max(initial=0.0)),
+        "flips": int((diff > 0).sum()),
+        "over_2e-3": int((diff > 2e-3).sum()),
+        "rel_l2": float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30)),
+        "count": int(r.size),
+    }
+
+
+def assert_free_order(stats, flip_fraction=0.02, over_fraction=0.01):
+    """The tolerance of free-order (matrix-core) routes against the reference order.
+
+    Every output is within max(2e-3, one fp16 ulp of the reference value): the
+    2e-3 gate wherever |y| < 4, where an fp16 ulp is at most 1.95e-3; above 4
+    a single rounding flip is 3.9e-3, the one stated deviation from that gate.
+    rel-L2 <= 1e-3; at most `flip_fraction` of the outputs differ at all and
+    at most `over_fraction` by more than 2e-3.
+    """
+    assert stats["max_over_tolerance"] <= 1.0, stats
+    assert stats["rel_l2"] <= 1e-3, stats
+    assert stats["flips"] <= max(2, flip_fraction * stats["count"]), stats
+    assert stats["over_2e-3"] <= max(2, over_fraction * stats["count"]), stats

@@ -226,3 +226,62 @@ def test_row_tiled_decode_equals_row_major(backend, device, nbits, shape, tokens
     backend._check(lib.venturi_row_tiled_run(x.data_ptr(), tc.data_ptr(), th.data_ptr(), ts.data_ptr(), got.data_ptr(),
                                              tokens, n, k, padded, nbits, 0, None, 0, s))
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("nbits", [5, 6])
+@pytest.mark.parametrize("shape", [(16, 8192), (130, 8320), (37, 8200), (5120, 17408)])
+@pytest.mark.parametrize("tokens", [1, 3, 16])
+def test_row_tiled_decode_split_k(backend, device, nbits, shape, tokens):
+    # Q5/Q6 tiled decode where K is split over two workgroups (the exchange
+    # slots and the tiled high plane): the W*A16 contract bound against FP64,
+    # the same bytes on a second run, idle slots afterwards, and HIP-graph
+    # replays (eager work between them) equal to the eager result.
+    from venturi_amd.q5 import tile_row_codec
+
+    n, k = shape
+    print(f"case row-tiled-split bits={nbits} n={n} k={k} tokens={tokens}", flush=True)
+    packed, high, scales = _planes(n, k, nbits, 13 * nbits + n + tokens)
+    padded = packed.shape[1] * 2
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    size = lib.venturi_q4_tiled_workspace_bytes(tokens, n, k)
+    assert size == tokens * ((n + 15) // 16) * 64
+    slots = torch.empty(size, dtype=torch.uint8, device=device)
+    backend._check(lib.venturi_q4_tiled_workspace_init(slots.data_ptr(), size, s))
+    idle = slots.clone()
+    tc, th, ts = tile_row_codec(torch.from_numpy(packed).to(device), torch.from_numpy(high).to(device),
+                                torch.from_numpy(scales).to(device), nbits)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens * 5 + k)).half()
+    xd = x.to(device)
+
+    def run(out):
+        backend._check(lib.venturi_row_tiled_run(xd.data_ptr(), tc.data_ptr(), th.data_ptr(), ts.data_ptr(),
+                                                 out.data_ptr(), tokens, n, k, padded, nbits, 0, slots.data_ptr(),
+                                                 size, torch.cuda.current_stream(device).cuda_stream))
+
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    run(out)
+    again = torch.empty_like(out)
+    run(again)
+    torch.cuda.synchronize(device)
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    assert torch.equal(slots, idle)
+    replayed = torch.empty_like(out)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(replayed)
+    for i in range(3):
+        replayed.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        assert torch.equal(replayed.view(torch.int16), out.view(torch.int16)), f"replay {i}"
+        run(again)
+        torch.cuda.synchronize(device)
+        assert torch.equal(again.view(torch.int16), out.view(torch.int16))
+    assert torch.equal(slots, idle)
+    wd = oracle.row_decode(packed, high, scales, k, nbits).view(np.float16).astype(np.float64)
+    xf = x.float().numpy().astype(np.float64)
+    exact = xf @ wd.T
+    got = out.cpu().float().numpy().astype(np.float64)
+    bound = 0.5 * _ulp16(exact) + 2.0**-19 * (np.abs(xf) @ np.abs(wd).T)
+    assert (np.abs(got - exact) <= bound).all()

@@ -116,3 +116,28 @@ def test_device_pack_matches_from_dense(backend, device, dtype, shape):
         bad = src.clone().to(device)
         bad[0, 0] = float("nan")
         backend.quantize_q8(bad)
+
+
+@pytest.mark.parametrize("offset", [1, 2, 3, 4, 5, 8, 17])
+@pytest.mark.parametrize("shape,tokens", [((7, 65), 1), ((33, 300), 3), ((70, 1024), 5), ((5, 5120), 1)])
+def test_head_run_accepts_unaligned_codes(backend, device, offset, shape, tokens):
+    # venturi_q8_head_run takes any code pointer, as the reference's does
+    # (blocks.cu:935-948): a plane that starts `offset` bytes into a buffer (a
+    # row-offset view) gives the canonical bytes. The plane ends exactly at the
+    # end of its buffer, so no read may pass it.
+    n, k = shape
+    print(f"case q8-unaligned n={n} k={k} tokens={tokens} offset={offset}", flush=True)
+    codes, scales = random_q8(n, k, 31 * offset + n)
+    padded = codes.shape[1]
+    storage = torch.zeros(offset + n * padded, dtype=torch.int8, device=device)
+    plane = storage[offset:]
+    plane.copy_(codes.view(-1).to(device))
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(offset)).half()
+    ds = scales.to(device)
+    guard, out = guarded_out(tokens, n, torch.float16, device)
+    backend._check(backend._native.venturi_q8_head_run(x.to(device).data_ptr(), plane.data_ptr(), ds.data_ptr(),
+                                                       out.data_ptr(), tokens, n, k, padded, 0,
+                                                       torch.cuda.current_stream(device).cuda_stream))
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    np.testing.assert_array_equal(bits(out), oracle.q8_linear(bits(x), codes.numpy(), scales.numpy(), k))

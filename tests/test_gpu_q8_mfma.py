@@ -4,9 +4,11 @@ The MFMA route sums each 32-column group on the matrix core and applies the
 group scale in fp32, so it differs from the canonical order only by fp32
 association. Tolerances (written here, not relaxed silently):
   * vs FP64 exact: |y - exact| <= 0.5 ulp_fp16(exact) + 2^-19 * sum_k |x_k w_k|
-  * vs the canonical-order oracle: rel-L2 <= 1e-3, and every output within
-    max(2e-3, 1 fp16 ulp of the oracle value); the number of 1-ulp flips is
-    reported.
+  * vs the canonical-order oracle (helpers.assert_free_order): every output
+    within max(2e-3, 1 fp16 ulp of the oracle value), rel-L2 <= 1e-3, at most
+    2% of the outputs differing at all and at most 1% by more than 2e-3.
+    Above |y| = 4 a single flip is 3.9e-3: the one stated deviation from the
+    2e-3 gate.
 """
 
 import numpy as np
@@ -14,16 +16,10 @@ import pytest
 import torch
 
 import oracle
-from helpers import bits, random_q8
+from helpers import agreement, assert_free_order, bits, random_q8, ulp16
 from venturi_amd import Q8RowSplitWeight
 
 pytestmark = pytest.mark.gpu
-
-
-def ulp16(v):
-    v = np.abs(v)
-    e = np.floor(np.log2(np.maximum(v, 2.0**-14)))
-    return 2.0 ** (e - 10)
 
 
 def check(out, x, codes, scales, k):
@@ -33,11 +29,9 @@ def check(out, x, codes, scales, k):
     exact = xd @ w.T
     bound = 0.5 * ulp16(exact) + 2.0**-19 * (np.abs(xd) @ np.abs(w).T)
     assert (np.abs(got - exact) <= bound).all()
-    canon = oracle.q8_linear(bits(x), codes, scales, k).view(np.float16).astype(np.float64)
-    diff = np.abs(got - canon)
-    assert (diff <= np.maximum(2e-3, ulp16(canon))).all()
-    assert np.linalg.norm(got - canon) <= 1e-3 * max(np.linalg.norm(canon), 1e-12)
-    return int((diff > 0).sum())
+    stats = agreement(got, oracle.q8_linear(bits(x), codes, scales, k))
+    assert_free_order(stats)
+    return stats["flips"]
 
 
 @pytest.mark.parametrize("shape", [(1, 64), (7, 72), (33, 136), (16, 256), (257, 5120), (100, 1000), (16400, 136), (40, 16392)])
@@ -99,7 +93,7 @@ def test_prefill_config2_m2048_sampled_rows(backend, device, n, k):
 
 
 @pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
-@pytest.mark.parametrize("tokens", [4, 16, 32])
+@pytest.mark.parametrize("tokens", [1, 4, 8, 16, 32])
 def test_mfma_config2_sampled_rows(backend, device, n, k, tokens):
     gen = torch.Generator(device=device).manual_seed(n + k)
     w = torch.randn(n, k, generator=gen, device=device) * 0.02
@@ -221,3 +215,25 @@ def test_unsplit_shapes_own_no_slots(backend, device):
     assert resident.prepare(tokens=1, route="mfma").plan.slots is None
     assert resident.prepare(tokens=8, route="mfma").plan.slots is None
     assert resident.prepare(tokens=24, route="mfma").plan.slots is not None
+
+
+@pytest.mark.parametrize("shape", [(16, 64), (37, 200), (100, 1000), (300, 4104), (64, 17408)])
+@pytest.mark.parametrize("tokens", [1, 2, 5, 8, 11, 16])
+def test_row_major_mfma_decode(backend, device, shape, tokens):
+    # venturi_q8_gemm_run (the matrix-core decode over the row-major planes, an
+    # exported extension): the FP64 bound and the free-order tolerance against
+    # the canonical-order oracle, with k % 128 != 0 tails and output guards.
+    n, k = shape
+    print(f"case q8-gemm-run n={n} k={k} tokens={tokens}", flush=True)
+    codes, scales = random_q8(n, k, 4000 + n + tokens)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens + 7 * k)).half()
+    dc, ds = codes.to(device), scales.to(device)
+    guard = torch.full((tokens * n + 2,), 47, dtype=torch.float16, device=device)
+    out = guard[1:-1].view(tokens, n)
+    backend._check(backend._native.venturi_q8_gemm_run(x.to(device).data_ptr(), dc.data_ptr(), ds.data_ptr(),
+                                                       out.data_ptr(), tokens, n, k, codes.shape[1], 0,
+                                                       torch.cuda.current_stream(device).cuda_stream))
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    flips = check(out, x, codes.numpy(), scales.numpy(), k)
+    print(f"flips={flips} of {tokens * n}", flush=True)

@@ -1,26 +1,45 @@
-"""Prepared-operator contract, independent of any native library.
+"""Prepared-operator contract of the HIP backend, independent of the native library.
 
-Mirrors venturi.ops.backend (reference backend.py:16-237): the same
-``OperatorSupport``/``BackendCapabilities`` records and the ``LinearPlan`` /
-``LinearWeight`` / ``OperatorBackend`` protocols. ``create_backend`` builds
-this package's HIP backend for kind "hip" (or "cuda", the device type torch
-uses for HIP devices). There is no implicit CPU fallback: the reference's
-Torch reference backend is not part of this package.
+The public names, protocols and error texts are those of the reference's
+operator contract (src/venturi/ops/backend.py:16-237), so code written against
+it runs unchanged: ``OperatorSupport`` / ``BackendCapabilities`` records,
+``LinearPlan`` / ``LinearWeight`` / ``OperatorBackend`` protocols, the
+``Backend`` base and ``create_backend``.
+
+Here a capability set is compiled once into a frozen set of request keys
+(operation, device type, dtype, weight format, weight layout), so a support
+query is one set lookup. ``create_backend`` builds the gfx950 HIP backend for
+"hip" (or "cuda", the device type torch gives HIP devices); there is no CPU or
+torch fallback in this package.
 """
 
 from abc import ABC, abstractmethod
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Protocol, runtime_checkable
 
 import torch
+
+# Operations whose requests name a weight format; a request without one asks for dense weights.
+_WEIGHTED = frozenset(("linear", "embedding"))
 
 
 class UnsupportedOperationError(ValueError):
     """The selected backend has no declared implementation for a request."""
 
 
+def _fail(condition, error, message):
+    if condition:
+        raise error(message)
+
+
+def _nonempty_text(value):
+    return isinstance(value, str) and bool(value)
+
+
 @dataclass(frozen=True)
 class OperatorSupport:
+    """One declared (operation, devices, dtypes, weight format/layout) implementation."""
+
     operation: str
     device_types: frozenset
     dtypes: frozenset
@@ -29,49 +48,50 @@ class OperatorSupport:
     materializes_weights: bool = False
 
     def __post_init__(self):
-        object.__setattr__(self, "device_types", frozenset(self.device_types))
-        object.__setattr__(self, "dtypes", frozenset(self.dtypes))
-        if not isinstance(self.operation, str) or not self.operation or not self.device_types or not self.dtypes:
-            raise ValueError("Operator support requires an operation, devices and dtypes")
-        if any(not isinstance(d, str) or not d for d in self.device_types):
-            raise ValueError("Device types must be nonempty strings")
-        if any(not isinstance(d, torch.dtype) for d in self.dtypes):
-            raise TypeError("Capability dtypes must be torch.dtype values")
-        if self.weight_layout is not None and self.weight_format is None:
-            raise ValueError("A weight layout requires an explicit format")
-        for value in (self.weight_format, self.weight_layout):
-            if value is not None and (not isinstance(value, str) or not value):
-                raise ValueError("Weight format/layout must be nonempty strings")
-        if type(self.materializes_weights) is not bool:
-            raise TypeError("Weight materialization flag must be bool")
+        devices, dtypes = frozenset(self.device_types), frozenset(self.dtypes)
+        object.__setattr__(self, "device_types", devices)
+        object.__setattr__(self, "dtypes", dtypes)
+        _fail(not (_nonempty_text(self.operation) and devices and dtypes), ValueError,
+              "Operator support requires an operation, devices and dtypes")
+        _fail(not all(_nonempty_text(d) for d in devices), ValueError, "Device types must be nonempty strings")
+        _fail(not all(isinstance(d, torch.dtype) for d in dtypes), TypeError,
+              "Capability dtypes must be torch.dtype values")
+        _fail(self.weight_format is None and self.weight_layout is not None, ValueError,
+              "A weight layout requires an explicit format")
+        _fail(any(v is not None and not _nonempty_text(v) for v in (self.weight_format, self.weight_layout)),
+              ValueError, "Weight format/layout must be nonempty strings")
+        _fail(not isinstance(self.materializes_weights, bool), TypeError, "Weight materialization flag must be bool")
+
+    def keys(self):
+        """Every request key this declaration satisfies."""
+        return {(self.operation, d, t, self.weight_format, self.weight_layout)
+                for d in self.device_types for t in self.dtypes}
 
 
 @dataclass(frozen=True)
 class BackendCapabilities:
+    """Allocation-free implementation metadata: which requests a backend declares."""
+
     implementation: str
     operators: tuple
     reference: bool = False
     cuda_graphs: bool = False
+    _keys: frozenset = field(default=frozenset(), init=False, repr=False, compare=False)
 
     def __post_init__(self):
-        object.__setattr__(self, "operators", tuple(self.operators))
-        if not self.implementation or any(not isinstance(o, OperatorSupport) for o in self.operators):
-            raise ValueError("Capabilities require an implementation and typed operators")
-        if type(self.reference) is not bool or type(self.cuda_graphs) is not bool:
-            raise TypeError("Reference and graph capability flags must be bool")
+        operators = tuple(self.operators)
+        object.__setattr__(self, "operators", operators)
+        _fail(not self.implementation or not all(isinstance(o, OperatorSupport) for o in operators), ValueError,
+              "Capabilities require an implementation and typed operators")
+        _fail(not (isinstance(self.reference, bool) and isinstance(self.cuda_graphs, bool)), TypeError,
+              "Reference and graph capability flags must be bool")
+        object.__setattr__(self, "_keys", frozenset().union(*(o.keys() for o in operators)))
 
     def supports(self, operation, *, dtype, device, weight_format=None, weight_layout=None):
-        kind = torch.device(device).type  # metadata only; no device initialisation
-        if operation in ("linear", "embedding") and weight_format is None:
+        # torch.device only parses the name: no device is initialised here.
+        if weight_format is None and operation in _WEIGHTED:
             weight_format = "dense"
-        return any(
-            o.operation == operation
-            and kind in o.device_types
-            and dtype in o.dtypes
-            and weight_format == o.weight_format
-            and weight_layout == o.weight_layout
-            for o in self.operators
-        )
+        return (operation, torch.device(device).type, dtype, weight_format, weight_layout) in self._keys
 
     def require(self, operation, **request):
         if not self.supports(operation, **request):
@@ -128,7 +148,7 @@ class OperatorBackend(Protocol):
 
 
 class Backend(ABC):
-    """Optional base class for the public contract (backend.py:153-214)."""
+    """Optional base of concrete backends: capability checks on top of abstract upload/prepare."""
 
     @property
     @abstractmethod
@@ -138,13 +158,9 @@ class Backend(ABC):
         self.capabilities.require(operation, **request)
 
     def require_linear(self, weight, *, dtype, device):
-        self.require(
-            "linear",
-            dtype=dtype,
-            device=device,
-            weight_format=weight.format,
-            weight_layout=getattr(weight, "layout", None),
-        )
+        request = {"dtype": dtype, "device": device, "weight_format": weight.format,
+                   "weight_layout": getattr(weight, "layout", None)}
+        self.require("linear", **request)
 
     @abstractmethod
     def resolve_device(self, device) -> torch.device: ...
@@ -171,18 +187,19 @@ class Backend(ABC):
     def prepare_rmsnorm(self, weight, *, tokens, dtype, device, epsilon): ...
 
 
+_NATIVE_KINDS = ("hip", "cuda")
+
+
 def create_backend(kind, *, library=None, q4_backend=None) -> OperatorBackend:
-    """Explicit construction only: loads the native library, never builds or probes devices.
+    """Explicit construction: loads the native library; never builds, probes devices or falls back.
 
     ``library`` defaults to the in-tree build. ``q4_backend`` is accepted for
-    signature compatibility; Q4 is native to this backend and needs no plugin.
+    signature compatibility: Q4 runs in the same library and needs no plugin.
     """
-    if kind in ("hip", "cuda"):
-        from .blocks import HipBackend
+    if kind not in _NATIVE_KINDS:
+        detail = ("The CPU torch reference backend is not part of venturi_amd; select 'hip' explicitly"
+                  if kind == "torch" else f"Backend {kind!r} is not implemented; select 'hip' explicitly")
+        raise UnsupportedOperationError(detail)
+    from .blocks import HipBackend
 
-        return HipBackend(library)
-    if kind == "torch":
-        raise UnsupportedOperationError(
-            "The CPU torch reference backend is not part of venturi_amd; select 'hip' explicitly"
-        )
-    raise UnsupportedOperationError(f"Backend {kind!r} is not implemented; select 'hip' explicitly")
+    return HipBackend(library)

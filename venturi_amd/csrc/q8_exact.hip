@@ -98,12 +98,17 @@ struct Tile {
     unsigned short sb[U][RR];
 };
 
-template <class T, int TT, int RR, int U, bool VEC>
+// SHIFT: the code plane starts `shift` (1..3) bytes past a 4-byte boundary
+// (a row-offset view, which the reference accepts). `codes` then points at
+// that boundary and every code word is assembled from two aligned words with
+// v_alignbyte. The second word of a row's last code word holds the row's
+// last `shift` bytes, so no load leaves the plane's allocation.
+template <class T, int TT, int RR, int U, bool VEC, bool SHIFT>
 __global__ __launch_bounds__(kThreads) void q8_exact(const T* __restrict__ x,
                                                 const std::int8_t* __restrict__ codes,
                                                 const __half* __restrict__ scales,
                                                 T* __restrict__ out, int tokens, int n, int k,
-                                                int padded) {
+                                                int padded, int shift) {
     // [TT][tiles*U*64] groups of 4 activations: 16-bit words, or fp32 when TT == 1.
     extern __shared__ uint4 xstage[];
     uint2* xs = reinterpret_cast<uint2*>(xstage);
@@ -178,13 +183,20 @@ __global__ __launch_bounds__(kThreads) void q8_exact(const T* __restrict__ x,
                 const unsigned short* st = sp + c0 * 8 + (lane >> 3);
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    tile.cw[u][r] = wt[u * 64];
+                    if constexpr (SHIFT)
+                        tile.cw[u][r] = __builtin_amdgcn_alignbyte(wt[u * 64 + 1], wt[u * 64], shift);
+                    else
+                        tile.cw[u][r] = wt[u * 64];
                     tile.sb[u][r] = st[u * 8];
                 }
             } else {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    tile.cw[u][r] = wp[min((c0 + u) * 64 + lane, last_word)];
+                    const int word = min((c0 + u) * 64 + lane, last_word);
+                    if constexpr (SHIFT)
+                        tile.cw[u][r] = __builtin_amdgcn_alignbyte(wp[word + 1], wp[word], shift);
+                    else
+                        tile.cw[u][r] = wp[word];
                     tile.sb[u][r] = sp[min((c0 + u) * 8 + (lane >> 3), groups - 1)];
                 }
             }
@@ -265,22 +277,36 @@ void launch_tile(const void* x, const std::int8_t* codes, const __half* scales, 
     const std::size_t lds = exact_lds_bytes(TT, U, k);
     require(lds <= kMaxLds, "activation tile exceeds LDS");
     const bool vec = (k % 4 == 0) && aligned(x, 8);
-    auto kernel = vec ? q8_exact<T, TT, RR, U, true> : q8_exact<T, TT, RR, U, false>;
+    const int shift = static_cast<int>(reinterpret_cast<std::uintptr_t>(codes) & 3);
+    const void* kernels[4] = {
+        reinterpret_cast<const void*>(q8_exact<T, TT, RR, U, true, false>),
+        reinterpret_cast<const void*>(q8_exact<T, TT, RR, U, false, false>),
+        reinterpret_cast<const void*>(q8_exact<T, TT, RR, U, true, true>),
+        reinterpret_cast<const void*>(q8_exact<T, TT, RR, U, false, true>),
+    };
     if (lds > 64 * 1024) {
-        // Raise the dynamic-LDS limit of both variants once per process.
-        static const hipError_t raised = [] {
-            const hipError_t a = hipFuncSetAttribute(reinterpret_cast<const void*>(q8_exact<T, TT, RR, U, true>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     static_cast<int>(kMaxLds));
-            const hipError_t b = hipFuncSetAttribute(reinterpret_cast<const void*>(q8_exact<T, TT, RR, U, false>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     static_cast<int>(kMaxLds));
-            return a != hipSuccess ? a : b;
+        // Raise the dynamic-LDS limit of every variant once per process.
+        static const hipError_t raised = [&kernels] {
+            hipError_t status = hipSuccess;
+            for (const void* f : kernels) {
+                const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         static_cast<int>(kMaxLds));
+                if (status == hipSuccess) status = e;
+            }
+            return status;
         }();
         check(raised);
     }
-    kernel<<<grid, kThreads, lds, stream>>>(static_cast<const T*>(x), codes, scales, static_cast<T*>(out), tokens, n, k,
-                                       padded);
+    const T* xp = static_cast<const T*>(x);
+    T* op = static_cast<T*>(out);
+    const std::int8_t* base = codes - shift;  // 4-byte aligned
+    if (shift == 0) {
+        if (vec) q8_exact<T, TT, RR, U, true, false><<<grid, kThreads, lds, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
+        else q8_exact<T, TT, RR, U, false, false><<<grid, kThreads, lds, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
+    } else {
+        if (vec) q8_exact<T, TT, RR, U, true, true><<<grid, kThreads, lds, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
+        else q8_exact<T, TT, RR, U, false, true><<<grid, kThreads, lds, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
+    }
 }
 
 template <class T>
@@ -316,8 +342,7 @@ void validate_q8(const void* x, const void* codes, const void* scales, const voi
     require(tokens > 0 && n > 0 && k > 0, "Q8 geometry must be positive");
     require(padded == padded_k(k), "padded K must equal ceil(k/128)*128");
     require(static_cast<std::int64_t>(tokens) * n < INT32_MAX, "Q8 output count exceeds int32");
-    require(aligned(codes, 16), "Q8 codes require 16-byte alignment");
-    require(aligned(scales, 2) && aligned(x, 2) && aligned(out, 2), "Q8 operands must be 2-byte aligned");
+    require(aligned(scales, 2) && aligned(x, 2) && aligned(out, 2), "Q8 fp16/bf16 operands must be 2-byte aligned");
 }
 
 }  // namespace

@@ -74,13 +74,11 @@ void project(const VRCPlan& plan, const void* x, const void* codes, const void* 
         return;
     }
     if (plan.bits == 8) {
-        // Matrix cores where they apply (the reference's head kernel otherwise):
-        // decode tiles up to 16 tokens, prefill tiles above 32.
+        // Direct: the reference's head kernel (canonical bytes, as
+        // row_codec_dispatch.cuh:30-38 runs it) up to 32 tokens; above that the
+        // prefill GEMM on matrix cores where it applies (fp16, k % 8 == 0).
         const bool mfma = plan.dtype == kF16 && k % 8 == 0 && aligned(x, 16) && aligned(codes, 16);
-        if (mfma && tokens <= 16)
-            pass(venturi_q8_gemm_run(x, static_cast<const std::int8_t*>(codes), scales, out, tokens, n, k, padded,
-                                     plan.dtype, stream));
-        else if (mfma && tokens > 32)
+        if (mfma && tokens > 32)
             pass(venturi_q8_prefill_run(x, static_cast<const std::int8_t*>(codes), scales, out, tokens, n, k, padded,
                                         plan.dtype, stream));
         else
