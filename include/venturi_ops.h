@@ -143,6 +143,18 @@ int venturi_q8_tiled_workspace_init(void* workspace, size_t bytes, void* stream)
 int venturi_q8_tiled_run(const void* x, const void* codes, const void* scales, void* out, int tokens, int n, int k,
                          int padded, int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc):
+ * venturi_q8_tiled_run without the workspace arguments. The exchange slots of
+ * launches that split K live in a static 1 MiB device array held per GPU until
+ * the process ends (every split shape fits; larger needs are rejected with a
+ * message). The first call on a device fills the slots on `stream` and must
+ * run outside graph capture; every call leaves them idle. All calls on one GPU
+ * share the array, so calls that overlap in time on one GPU race. Allocates
+ * nothing. */
+int venturi_q8_tiled_run_noalloc(const void* x, const void* codes, const void* scales, void* out, int tokens, int n,
+                                 int k, int padded, int dtype, void* stream);
+
 /* Extension (no counterpart in the reference; the native runtime runs the
  * gate+up projection and then SwiGLU, blocks.cu:56-86): the fused gate+up
  * projection over paired tiled planes (16-row block b holds gate rows

@@ -43,6 +43,7 @@ SIGNATURES = {
     "venturi_q8_tiled_workspace_init": ([_P, _U64, _P], _I),
     "venturi_q8_tiled_run": ([_P] * 4 + [_I] * 5 + [_P, _U64, _P], _I),
     "venturi_q8_tiled_swiglu_run": ([_P] * 4 + [_I] * 5 + [_P, _U64, _P], _I),
+    "venturi_q8_tiled_run_noalloc": ([_P] * 4 + [_I] * 5 + [_P], _I),
     "venturi_q4_pack_run": ([_P] * 3 + [_I] * 4 + [_P], _I),
     "venturi_q4_abi": ([], _I),
     "venturi_q4_decode": ([_P] * 3 + [_I] * 3 + [_P], _I),
