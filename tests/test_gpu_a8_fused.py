@@ -143,7 +143,7 @@ def test_raw_invalid_descriptor_geometry(backend, device):
     x = torch.ones(2, 67, dtype=torch.float16, device=device)
     outs = [torch.empty(2, n, dtype=torch.float16, device=device) for n in (7, 33)]
     plan.run(x, outputs=outs, workspace=work)
-    desc = plan._arguments(x, outs, work)
+    desc = plan._descriptors(outs)
     stream = torch.cuda.current_stream(device).cuda_stream
     args = [work.data_ptr(), work.numel(), C.cast(desc, C.c_void_p), 2, 2, 67, 128, 2, stream]
     assert plan._run(*args) == 0

@@ -79,3 +79,48 @@ def test_reported_plan_binding():
         validate_reported_plan("q8_g32_fp16", "fp16", GFX950, [8, 32, 1, 0, 0, 0])
     with pytest.raises(ValueError):
         validate_reported_plan("q4_g64_fp16", "fp16", GFX950, [4, 64, 0, 0, 0, 0])
+
+
+def _spec(**changes):
+    from types import SimpleNamespace
+
+    base = dict(target="cuda:0", projection_profile="fp16", linear_implementation="auto", dtype=torch.float16,
+                weight_mode="resident", tensor_parallel_device=None, stage_range=None, dequant_resident=False)
+    base.update(changes)
+    return SimpleNamespace(**base)
+
+
+def _weights(*formats):
+    from types import SimpleNamespace
+
+    return SimpleNamespace(plan=SimpleNamespace(bindings=[SimpleNamespace(format=f) for f in formats]))
+
+
+def test_linear_contracts_on_gfx950(monkeypatch):
+    # quantization/linear.py:16-74 semantics with the gfx950 capability (9, 5).
+    from venturi_amd.quantization.linear import describe_linear_contracts, validate_linear_contracts
+
+    monkeypatch.setattr(torch.cuda, "get_device_capability", lambda target: GFX950)
+    validate_linear_contracts(_spec(), _weights("q8_g32_fp16", "q4_g64_fp16", "fp16"))
+    cases = [
+        (_spec(), ("q5_g64_fp16",), "not execution-qualified"),
+        (_spec(projection_profile="int8"), ("q8_g32_fp16",), "One-pass int8"),
+        (_spec(linear_implementation="fused"), ("q4_g64_fp16",), "Fused model execution"),
+        (_spec(dtype=torch.bfloat16), ("q4_g64_fp16",), "row-codec matrices require"),
+        (_spec(projection_profile="int8-residual"), ("q4_g64_fp16",), "Residual activation policy"),
+        (_spec(linear_implementation="dequant"), ("q8_g32_fp16",), "requires Q4/Q5/Q6 matrices"),
+        (_spec(linear_implementation="dequant", stage_range=(0, 4)), ("q8_g32_fp16",), "requires Q4/Q5/Q6"),
+        (_spec(dequant_resident=True), ("q4_g64_fp16", "q8_g32_fp16"), "FP16 shadow"),
+    ]
+    for spec, formats, message in cases:
+        with pytest.raises(ValueError, match=message):
+            validate_linear_contracts(spec, _weights(*formats))
+    monkeypatch.setattr(torch.cuda, "get_device_capability", lambda target: (9, 0))
+    with pytest.raises(ValueError, match="Unsupported QuantLinear architecture"):
+        validate_linear_contracts(_spec(), _weights("q8_g32_fp16"))
+    described = describe_linear_contracts(_weights("q4_g64_fp16", "q8_g32_fp16", "fp16"), "fp16")
+    assert described["q4_g64_fp16"]["weight_decode"] == "fp16-rounded-q-times-scale"
+    assert described["q8_g32_fp16"]["weight_decode"] == "fp32-scaled-integer-products"
+    assert set(described) == {"q4_g64_fp16", "q8_g32_fp16"}
+    fused = describe_linear_contracts(_weights("q4_g64_fp16"), "fp16", "fused")
+    assert fused["q4_g64_fp16"]["weight_decode"] == "fp32-scaled-integer-products"

@@ -1,12 +1,17 @@
-"""The Q4 linear plugin interface (reference ops/ada.py:20-204) over libventuri_ops.so.
+"""The Q4 linear plugin interface (the reference's ops/ada.py) over libventuri_ops.so.
 
-``AdaBackend`` keeps the reference plugin's objects and checks:
-``upload_linear`` copies the planes once, ``ResidentQ4Weight.prepare`` asks
-``venturi_q4_prepare`` for the native route (auto/generic -> 0) and
-``PreparedLinear.run`` calls ``venturi_q4_run``, the FP32-weight SIMT order of
-q4_linear.cu:21-56 (bit-identical here). Errors carry the plugin's own
-thread-local message (``venturi_ada_error``). Device qualification is gfx950
-instead of compute capability 8.9.
+Public objects and texts of the reference plugin: ``AdaBackend`` (ABI 2,
+``upload_linear``), ``ResidentQ4Weight.prepare(tokens=, dtype=, route=)`` and
+``PreparedLinear.run(x, out=)``. The plugin's entry points live in the same
+library as the blocks ABI: ``venturi_q4_prepare`` admits a native route (auto
+and generic map to route 0, the FP32-weight SIMT order of
+q4_linear.cu:21-56, bit-identical here) and ``venturi_q4_run`` executes it;
+failures carry the plugin's own thread-local message (``venturi_ada_error``).
+Device qualification is gfx950 instead of compute capability 8.9.
+
+A prepared plan keeps its launch arguments (weight pointers, geometry, dtype
+and route codes) as one tuple built at prepare time; ``run`` checks the two
+caller buffers against the plan and inserts their pointers.
 """
 
 from dataclasses import dataclass
@@ -17,6 +22,10 @@ import torch
 from . import native
 from .blocks import _overlaps, is_gfx950
 from .weights import Q4RowSplitWeight
+
+_MAX_TOKENS = 4 * 65535
+_ROUTE_CODES = {"auto": -1, "generic": 0}
+_DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 
 
 class AdaBackend:
@@ -34,40 +43,41 @@ class AdaBackend:
     def _error(self):
         return RuntimeError(self._native.venturi_ada_error().decode("utf-8", "replace"))
 
+    def _device(self, device):
+        """The concrete gfx950 device for `device`, outside graph capture."""
+        target = torch.device(device)
+        if target.type != "cuda":
+            raise ValueError("Ada execution requires an explicit GPU device")
+        with torch.cuda.device(target):
+            index = torch.cuda.current_device()
+            capturing = torch.cuda.is_current_stream_capturing()
+        if capturing:
+            raise RuntimeError("prepare_linear must run outside graph capture")
+        target = torch.device("cuda", index)
+        if not is_gfx950(target):
+            raise ValueError("This Q4 plugin build requires gfx950")
+        return target
+
     def upload_linear(self, weight, *, device="cuda:0"):
-        """Copy Q4 planes once; resident storage can bind multiple shapes/dtypes."""
+        """Copies the Q4 planes once; the resident storage serves plans of any shape and dtype."""
         if not isinstance(weight, Q4RowSplitWeight):
             raise TypeError("Venturi Ada currently supports Q4RowSplitWeight only")
         weight.validate()
         target = self._device(device)
         with torch.cuda.device(target):
-            codes = weight.codes.detach().to(target, copy=True)
-            scales = weight.scales.detach().to(target, copy=True)
-            if not bool(torch.isfinite(scales).all()):
+            planes = [t.detach().to(target, copy=True) for t in (weight.codes, weight.scales)]
+            if not bool(torch.isfinite(planes[1]).all()):
                 raise ValueError("scales must be finite")
-            owned = Q4RowSplitWeight(codes, scales, weight.in_features)
             torch.cuda.current_stream(target).synchronize()
-        return ResidentQ4Weight(self, owned)
-
-    def _device(self, device):
-        target = torch.device(device)
-        if target.type != "cuda":
-            raise ValueError("Ada execution requires an explicit GPU device")
-        with torch.cuda.device(target):
-            target = torch.device("cuda", torch.cuda.current_device())
-            if torch.cuda.is_current_stream_capturing():
-                raise RuntimeError("prepare_linear must run outside graph capture")
-            if not is_gfx950(target):
-                raise ValueError("This Q4 plugin build requires gfx950")
-        return target
+        return ResidentQ4Weight(self, Q4RowSplitWeight(*planes, weight.in_features))
 
 
-def _configuration(tokens, dtype, route):
-    if type(tokens) is not int or not 0 < tokens <= 4 * 65535:
+def _admit(tokens, dtype, route):
+    if type(tokens) is not int or not 0 < tokens <= _MAX_TOKENS:
         raise ValueError("tokens must be an integer in [1, 262140]")
-    if dtype not in (torch.float16, torch.bfloat16):
+    if dtype not in _DTYPE_CODES:
         raise ValueError("activations and output must be float16 or bfloat16")
-    if route not in ("auto", "generic"):
+    if route not in _ROUTE_CODES:
         raise ValueError("route must be auto or generic; tuned/mma were removed")
 
 
@@ -87,24 +97,22 @@ class ResidentQ4Weight:
         return sum(t.numel() * t.element_size() for t in self.storage_tensors)
 
     def prepare(self, *, tokens, dtype=torch.bfloat16, route="auto"):
-        _configuration(tokens, dtype, route)
-        target = self._backend._device(self._weight.codes.device)
+        _admit(tokens, dtype, route)
+        w, lib = self._weight, self._backend._native
+        target = self._backend._device(w.codes.device)
         with torch.cuda.device(target):
-            native_route = self._backend._native.venturi_q4_prepare(
-                self._weight.out_features,
-                self._weight.in_features,
-                tokens,
-                int(dtype == torch.bfloat16),
-                {"auto": -1, "generic": 0}[route],
-            )
-            if native_route < 0:
-                raise self._backend._error()
-        return PreparedLinear(self._backend, self._weight, tokens, dtype, native_route)
+            chosen = lib.venturi_q4_prepare(w.out_features, w.in_features, tokens, _DTYPE_CODES[dtype],
+                                            _ROUTE_CODES[route])
+        if chosen < 0:
+            raise self._backend._error()
+        launch = (w.codes.data_ptr(), w.scales.data_ptr(), w.out_features, w.in_features, w.padded_k, tokens,
+                  _DTYPE_CODES[dtype], chosen)
+        return PreparedLinear(self._backend, w, tokens, dtype, chosen, launch)
 
 
 @dataclass(frozen=True)
 class PreparedLinear:
-    """Fixed-shape Linear out[T, N] = x[T, K] @ W[N, K]^T, caller-owned output."""
+    """Fixed-shape out[T, N] = x[T, K] @ W[N, K]^T without bias; caller-owned output."""
 
     workspace_bytes = 0
 
@@ -113,6 +121,7 @@ class PreparedLinear:
     tokens: int
     dtype: torch.dtype
     _native_route: int
+    _launch: tuple = ()  # (codes, scales, n, k, padded, tokens, dtype code, route) for venturi_q4_run
 
     @property
     def device(self):
@@ -136,38 +145,28 @@ class PreparedLinear:
         """Explicit allocation helper; call before timing or graph capture."""
         return torch.empty((self.tokens, self.out_features), dtype=self.dtype, device=self.device)
 
+    def _check(self, name, tensor, features):
+        shape = (self.tokens, features)
+        if tensor.shape != shape or tensor.dtype != self.dtype or tensor.device != self.device:
+            raise ValueError(f"{name} must have shape {shape}, dtype {self.dtype}, device {self.device}")
+        if not tensor.is_contiguous():
+            raise ValueError(f"{name} must be contiguous; no implicit copy is performed")
+        if tensor.data_ptr() % 2:
+            raise ValueError(f"{name} requires 2-byte alignment")
+
     def run(self, x, *, out):
         if torch.is_grad_enabled() and (x.requires_grad or out.requires_grad):
             raise ValueError("Venturi Ada is inference-only; disable gradients")
         self._weight.validate()
-        for name, tensor, shape in (
-            ("x", x, (self.tokens, self.in_features)),
-            ("out", out, (self.tokens, self.out_features)),
-        ):
-            if tensor.shape != shape or tensor.dtype != self.dtype or tensor.device != self.device:
-                raise ValueError(f"{name} must have shape {shape}, dtype {self.dtype}, device {self.device}")
-            if not tensor.is_contiguous():
-                raise ValueError(f"{name} must be contiguous; no implicit copy is performed")
-            if tensor.data_ptr() % 2:
-                raise ValueError(f"{name} requires 2-byte alignment")
-        for operand in (x, self._weight.codes, self._weight.scales):
-            if _overlaps(out, operand):
-                raise ValueError("output must not alias input or weight storage")
+        self._check("x", x, self.in_features)
+        self._check("out", out, self.out_features)
+        if any(_overlaps(out, t) for t in (x, self._weight.codes, self._weight.scales)):
+            raise ValueError("output must not alias input or weight storage")
+        codes, scales, n, k, padded, tokens, dtype_code, route = self._launch
         with torch.cuda.device(self.device):
-            stream = torch.cuda.current_stream(self.device)
-            result = self._backend._native.venturi_q4_run(
-                x.data_ptr(),
-                self._weight.codes.data_ptr(),
-                self._weight.scales.data_ptr(),
-                out.data_ptr(),
-                self.out_features,
-                self.in_features,
-                self._weight.padded_k,
-                self.tokens,
-                int(self.dtype == torch.bfloat16),
-                self._native_route,
-                stream.cuda_stream,
-            )
-            if result < 0:
-                raise self._backend._error()
+            status = self._backend._native.venturi_q4_run(
+                x.data_ptr(), codes, scales, out.data_ptr(), n, k, padded, tokens, dtype_code, route,
+                torch.cuda.current_stream(self.device).cuda_stream)
+        if status < 0:
+            raise self._backend._error()
         return out

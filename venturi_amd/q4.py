@@ -11,10 +11,9 @@ from functools import cached_property
 from pathlib import Path
 
 import torch
-from torch.nn import functional as F
 
 from .blocks import _DTYPES, _no_overlap, _shape, _stream, _tensor
-from .weights import Q4RowSplitWeight
+from .weights import Q4RowSplitWeight, decode_k64_fp16, rtn_k64
 
 # Plan routes of a resident Q4 linear:
 #   mfma    W4A16 contract (fp16(q*scale) weights) on fp16 matrix cores, any tokens
@@ -54,40 +53,16 @@ def tile_q4(codes, scales):
 
 
 def quantize_q4_rtn(weight, *, max_elements=16 * 2**20):
-    """CPU round-to-nearest-even Q4 with the fp16 scale rounded before the codes."""
-    if (
-        not isinstance(weight, torch.Tensor)
-        or weight.device.type != "cpu"
-        or weight.ndim != 2
-        or weight.dtype not in (torch.float16, torch.bfloat16, torch.float32)
-        or min(weight.shape) < 1
-    ):
-        raise ValueError("Explicit nonempty CPU floating weight required")
-    if type(max_elements) is not int or max_elements <= 0 or weight.numel() > max_elements:
-        raise ValueError("Q4 quantization exceeds explicit element budget")
-    value = weight.float()
-    if not torch.isfinite(value).all():
-        raise ValueError("Finite source weights required")
-    rows, cols = weight.shape
-    padded = (cols + 127) // 128 * 128
-    blocks = F.pad(value, (0, padded - cols)).reshape(rows, padded // 64, 64)
-    scales = (blocks.abs().amax(-1) / 7).clamp_min(2**-24).half()
-    if not torch.isfinite(scales).all():
-        raise ValueError("Source scale overflows FP16")
-    codes = (blocks / scales.float().unsqueeze(-1)).round().clamp(-7, 7).to(torch.int8)
-    if not torch.isfinite((codes.float() * scales.float().unsqueeze(-1)).half()).all():
-        raise ValueError("Quantized weight overflows FP16 execution")
-    return Q4RowSplitWeight.from_codes(codes.reshape(rows, padded)[:, :cols], scales[:, : (cols + 63) // 64])
+    """CPU RTN for the model's Q4 experts (flash_next_q4.py:26-52): per K64 group the fp16
+    scale fp16(max(max|w| / 7, 2^-24)) is rounded first, then q = RNE(w / scale) in [-7, 7]
+    (the -8 code is never produced); returns a ``Q4RowSplitWeight``."""
+    codes, scales = rtn_k64(weight, levels=7, lowest=-7, tag="Q4", max_elements=max_elements)
+    return Q4RowSplitWeight.from_codes(codes, scales)
 
 
 def decode_q4_fp16(weight):
-    """fp16 matrix of fp16(q * scale) values (diagnostic; no retained cache)."""
-    weight.validate()
-    nibbles = torch.stack((weight.codes & 15, weight.codes >> 4), -1).reshape(weight.out_features, weight.padded_k)
-    nibbles = nibbles.to(torch.int16)
-    signed = torch.where(nibbles < 8, nibbles, nibbles - 16)
-    values = signed.float().reshape(weight.out_features, -1, 64) * weight.scales.float().unsqueeze(-1)
-    return values.reshape(weight.out_features, -1)[:, : weight.in_features].half()
+    """fp16 matrix of fp16(q * scale) values, the W4A16 weights (diagnostic; no retained cache)."""
+    return decode_k64_fp16(weight, 4)
 
 
 def _q4_planes(weight):

@@ -13,40 +13,18 @@ from dataclasses import dataclass
 from pathlib import Path
 
 import torch
-from torch.nn import functional as F
 
-from .weights import Q5RowSplitWeight
+from .weights import Q5RowSplitWeight, decode_k64_fp16, rtn_k64
 
 CODEC = "rtn_symmetric15_g64_fp16_row_split_k128_v1"
 
 
 def quantize_q5_rtn(weight, *, max_elements=16 * 2**20):
-    """CPU round-to-nearest-even Q5 with the fp16 scale rounded before the codes."""
-    if (
-        not isinstance(weight, torch.Tensor)
-        or weight.device.type != "cpu"
-        or weight.ndim != 2
-        or weight.dtype not in (torch.float16, torch.bfloat16, torch.float32)
-        or min(weight.shape) < 1
-    ):
-        raise ValueError("Explicit nonempty CPU floating weight required")
-    if type(max_elements) is not int or max_elements <= 0 or weight.numel() > max_elements:
-        raise ValueError("Q5 quantization exceeds explicit element budget")
-    value = weight.float()
-    if not torch.isfinite(value).all():
-        raise ValueError("Finite source weights required")
-    rows, cols = weight.shape
-    padded = (cols + 127) // 128 * 128
-    blocks = F.pad(value, (0, padded - cols)).reshape(rows, padded // 64, 64)
-    scales = (blocks.abs().amax(-1) / 15).clamp_min(2**-24).half()
-    if not torch.isfinite(scales).all():
-        raise ValueError("Source scale overflows FP16")
-    codes = (blocks / scales.float().unsqueeze(-1)).round().clamp(-16, 16).to(torch.int8)
-    # A +16 appears only where rounding the scale moved the group boundary.
-    codes = torch.where(codes == 16, torch.full_like(codes, 15), codes)
-    if not torch.isfinite((codes.float() * scales.float().unsqueeze(-1)).half()).all():
-        raise ValueError("Quantized weight overflows FP16 execution")
-    return Q5RowSplitWeight.from_codes(codes.reshape(rows, padded)[:, :cols], scales[:, : (cols + 63) // 64])
+    """CPU RTN for the experimental W5A16 codec (flash_next_q5.py:18-50): per K64 group the
+    fp16 scale fp16(max(max|w| / 15, 2^-24)) is rounded first, then q = RNE(w / scale) in
+    [-16, 15] (a +16 from the scale's rounding saturates to 15); returns a ``Q5RowSplitWeight``."""
+    codes, scales = rtn_k64(weight, levels=15, lowest=-16, tag="Q5", max_elements=max_elements)
+    return Q5RowSplitWeight.from_codes(codes, scales)
 
 
 def tile_row_codec(codes, high, scales, bits):
@@ -77,14 +55,8 @@ def tile_row_codec(codes, high, scales, bits):
 
 
 def decode_q5_fp16(weight):
-    """fp16 matrix of fp16(q * scale) values (diagnostic; no retained cache)."""
-    weight.validate()
-    low = torch.stack((weight.codes & 15, weight.codes >> 4), -1).reshape(weight.out_features, weight.padded_k)
-    bits = (weight.high.to(torch.int16).unsqueeze(-1) >> torch.arange(8, dtype=torch.int16)) & 1
-    unsigned = low.to(torch.int16) | (bits.reshape(weight.out_features, weight.padded_k) << 4)
-    signed = torch.where(unsigned < 16, unsigned, unsigned - 32)
-    values = signed.float().reshape(weight.out_features, -1, 64) * weight.scales.float().unsqueeze(-1)
-    return values.reshape(weight.out_features, -1)[:, : weight.in_features].half()
+    """fp16 matrix of fp16(q * scale) values, the W5A16 weights (diagnostic; no retained cache)."""
+    return decode_k64_fp16(weight, 5)
 
 
 @dataclass(frozen=True)

@@ -1,12 +1,17 @@
-"""Fused W8A8 projections: two or three Q8 matrices against one A8 activation pack.
+"""Fused W8A8 projections: two or three Q8 matrices of one K against one A8 activation pack.
 
-Mirrors venturi.ops.q8_fused (reference q8_fused.py:1-147): the plan quantizes
-the fp16 activations once into the caller-owned workspace (the A8 plan's
-layout and size) and projects every matrix with ``venturi_q8_fused_run``,
-which writes output i as [tokens][strides[i]]. Each output's bytes equal the
-reference-order A8 projection of that matrix (``venturi_q8_dp4a_run``).
-``packed=True`` skips the quantization step and reuses a workspace the caller
-filled before (for example with ``venturi_swiglu_q8_quantize``).
+Public surface of the reference's ops/q8_fused.py (``OutputDescriptor``,
+``PreparedQ8Fused.run(x, *, outputs, workspace, packed=False)``,
+``prepare_q8_fused(residents, *, tokens, residual_compensation,
+output_strides=None)``), with its argument checks and messages.
+
+A plan fixes every matrix's device pointers, row count and output stride at
+prepare time (``_matrices``); ``run`` checks the caller's buffers, quantizes
+the activations once into the workspace (the A8 plan's layout and size) unless
+``packed``, and issues one ``venturi_q8_fused_run`` launch over a descriptor
+array built from the fixed entries plus this call's output pointers. Output i
+is written as [tokens][strides[i]] and holds the bytes of the reference-order
+A8 projection of matrix i (``venturi_q8_dp4a_run``).
 """
 
 import ctypes as C
@@ -17,9 +22,11 @@ import torch
 from .blocks import ResidentLinear, _no_overlap, _stream, _tensor
 from .q8_dp4a import prepare_q8_dp4a
 
+_INT32_LIMIT = 2**31
+
 
 class OutputDescriptor(C.Structure):
-    """One matrix of a fused launch (the reference's VQFOutput, 32 bytes)."""
+    """One matrix of a fused launch: the C ABI's VQFOutput (32 bytes)."""
 
     _fields_ = [
         ("codes", C.c_void_p),
@@ -33,9 +40,10 @@ class OutputDescriptor(C.Structure):
 @dataclass(frozen=True)
 class PreparedQ8Fused:
     residents: tuple
-    base: object
+    base: object  # the A8 plan of the first matrix: tokens, passes, workspace size
     strides: tuple
     _run: object
+    _matrices: tuple = ()  # (codes pointer, scales pointer, rows, stride) per matrix
 
     @property
     def workspace_bytes(self):
@@ -45,82 +53,76 @@ class PreparedQ8Fused:
     def precision_profile(self):
         return self.base.precision_profile
 
-    def _arguments(self, x, outputs, workspace):
-        # Checks of q8_fused.py:40-72, in the same order.
-        p = self.base
-        r = self.residents[0]
-        if not isinstance(outputs, (list, tuple)) or len(outputs) != len(self.residents):
+    def _check_buffers(self, x, outputs, workspace):
+        lead = self.residents[0]
+        tokens = self.base.tokens
+        if not (isinstance(outputs, (list, tuple)) and len(outputs) == len(self.residents)):
             raise ValueError("one output per fused matrix required")
-        _tensor(x, (p.tokens, r.hidden_size), torch.float16, r.device, "x")
-        _tensor(workspace, (p.workspace_bytes,), torch.uint8, r.device, "workspace")
-        if workspace.data_ptr() % 16:
+        _tensor(x, (tokens, lead.hidden_size), torch.float16, lead.device, "x")
+        _tensor(workspace, (self.workspace_bytes,), torch.uint8, lead.device, "workspace")
+        if workspace.data_ptr() % 16 != 0:
             raise ValueError("DP4A workspace requires 16-byte alignment")
-        storage = tuple(t for resident in self.residents for t in resident.storage_tensors)
-        _no_overlap(workspace, (x,) + storage)
-        for i, (out, stride) in enumerate(zip(outputs, self.strides)):
-            _tensor(out, (p.tokens, stride), torch.float16, r.device, "out")
-            _no_overlap(out, (x, workspace) + storage + tuple(outputs[:i]))
-        return (OutputDescriptor * len(outputs))(
-            *[
-                OutputDescriptor(m._codes.data_ptr(), m._scales.data_ptr(), out.data_ptr(), m.vocab_size, stride)
-                for m, out, stride in zip(self.residents, outputs, self.strides)
-            ]
-        )
+        weights = sum((m.storage_tensors for m in self.residents), ())
+        _no_overlap(workspace, (x,) + weights)
+        earlier = ()
+        for out, stride in zip(outputs, self.strides):
+            _tensor(out, (tokens, stride), torch.float16, lead.device, "out")
+            _no_overlap(out, (x, workspace) + weights + earlier)
+            earlier += (out,)
+
+    def _descriptors(self, outputs):
+        table = (OutputDescriptor * len(outputs))()
+        for entry, (codes, scales, rows, stride), out in zip(table, self._matrices, outputs):
+            entry.codes, entry.scales, entry.out, entry.rows, entry.stride = codes, scales, out.data_ptr(), rows, stride
+        return table
 
     def run(self, x, *, outputs, workspace, packed=False):
         """packed=True is explicit caller-owned quantization reuse, not a pointer cache."""
-        if type(packed) is not bool:
+        if not isinstance(packed, bool):
             raise ValueError("packed must be boolean")
-        descriptors = self._arguments(x, outputs, workspace)
-        p = self.base
-        r = self.residents[0]
-        lib = r.backend._native
-        with torch.cuda.device(r.device):
-            stream = _stream(r.device)
+        self._check_buffers(x, outputs, workspace)
+        table = self._descriptors(outputs)
+        lead, a8 = self.residents[0], self.base
+        backend = lead.backend
+        with torch.cuda.device(lead.device):
+            stream = _stream(lead.device)
             if not packed:
-                r.backend._check(
-                    lib.venturi_q8_dp4a_quantize(
-                        x.data_ptr(), workspace.data_ptr(), p.workspace_bytes, p.tokens, r.hidden_size, p.passes,
-                        stream,
-                    )
-                )
-            r.backend._check(
-                self._run(
-                    workspace.data_ptr(),
-                    p.workspace_bytes,
-                    C.cast(descriptors, C.c_void_p),
-                    len(self.residents),
-                    p.tokens,
-                    r.hidden_size,
-                    r._codes.shape[1],
-                    p.passes,
-                    stream,
-                )
-            )
+                backend._check(backend._native.venturi_q8_dp4a_quantize(
+                    x.data_ptr(), workspace.data_ptr(), a8.workspace_bytes, a8.tokens, lead.hidden_size, a8.passes,
+                    stream))
+            backend._check(self._run(
+                workspace.data_ptr(), a8.workspace_bytes, C.cast(table, C.c_void_p), len(table), a8.tokens,
+                lead.hidden_size, lead._codes.shape[1], a8.passes, stream))
         return outputs
 
 
+def _fused_strides(values, tokens, output_strides):
+    strides = tuple(m.vocab_size for m in values) if output_strides is None else tuple(output_strides)
+
+    def valid(matrix, stride):
+        return (type(stride) is int and matrix.vocab_size <= stride < _INT32_LIMIT
+                and (tokens - 1) * stride + matrix.vocab_size < _INT32_LIMIT)
+
+    if len(strides) != len(values) or not all(valid(m, s) for m, s in zip(values, strides)):
+        raise ValueError("invalid fused output strides")
+    return strides
+
+
 def prepare_q8_fused(residents, *, tokens, residual_compensation, output_strides=None):
-    """Fused plan over two or three resident Q8 matrices of one K (q8_fused.py:108-147)."""
-    if not isinstance(residents, (tuple, list)) or len(residents) not in (2, 3):
+    """Fused plan over two or three resident Q8 matrices that share K, device and backend."""
+    if not (isinstance(residents, (tuple, list)) and 2 <= len(residents) <= 3):
         raise ValueError("fused projection requires two or three resident matrices")
     values = tuple(r._payload if isinstance(r, ResidentLinear) else r for r in residents)
-    plans = [
-        prepare_q8_dp4a(r, tokens=tokens, residual_compensation=residual_compensation, route="exact")
-        for r in values
-    ]
-    first = values[0]
-    if any(
-        r.device != first.device or r.hidden_size != first.hidden_size or r.backend is not first.backend
-        for r in values
-    ):
+    # Every matrix must admit its own A8 plan (shape and dtype checks); the
+    # first one's plan carries the shared token count, passes and workspace.
+    plans = [prepare_q8_dp4a(m, tokens=tokens, residual_compensation=residual_compensation, route="exact")
+             for m in values]
+    lead = values[0]
+    if not all(m.device == lead.device and m.hidden_size == lead.hidden_size and m.backend is lead.backend
+               for m in values):
         raise ValueError("fused matrices require the same device, backend and K")
-    if sum(r.vocab_size for r in values) >= 2**31 - 48:
+    if sum(m.vocab_size for m in values) >= _INT32_LIMIT - 48:
         raise ValueError("fused row sum exceeds int32")
-    strides = tuple(r.vocab_size for r in values) if output_strides is None else tuple(output_strides)
-    if len(strides) != len(values) or any(
-        type(s) is not int or s < r.vocab_size or s >= 2**31 or (tokens - 1) * s + r.vocab_size >= 2**31
-        for r, s in zip(values, strides)
-    ):
-        raise ValueError("invalid fused output strides")
-    return PreparedQ8Fused(values, plans[0], strides, first.backend._native.venturi_q8_fused_run)
+    strides = _fused_strides(values, tokens, output_strides)
+    matrices = tuple((m._codes.data_ptr(), m._scales.data_ptr(), m.vocab_size, s) for m, s in zip(values, strides))
+    return PreparedQ8Fused(values, plans[0], strides, lead.backend._native.venturi_q8_fused_run, matrices)
