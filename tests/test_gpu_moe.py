@@ -167,7 +167,7 @@ def test_moe_config4_and_determinism(backend, device):
     assert np.array_equal(bits(via_api), bits(out))
 
 
-def test_moe_invalid_ids_are_counted_not_used(backend, device):
+def test_moe_invalid_ids_give_nan_rows(backend, device):
     geometry = MoEGeometry(128, 8, 2, 64)
     bank, _, _ = build(backend, device, geometry, 3)
     x, ids, scores = routing(4, geometry, 5)
@@ -180,5 +180,14 @@ def test_moe_invalid_ids_are_counted_not_used(backend, device):
     views = plan.workspace_views(workspace)
     assert int(views["status"].item()) == 2
     assert int(views["seg"][-1].item()) == 6
+    # Tokens with an invalid id get NaN rows; the others equal a run without them.
+    rows = out.cpu()
+    assert bool(torch.isnan(rows[1]).all()) and bool(torch.isnan(rows[2]).all())
+    valid = torch.tensor([0, 3])
+    sub = bank.prepare(tokens=2)
+    sub_ws = torch.empty(sub.workspace_bytes, dtype=torch.uint8, device=device)
+    sub_out = torch.empty((2, 128), dtype=torch.float16, device=device)
+    sub.run(x[valid].to(device), ids[valid].to(device), scores[valid].to(device), out=sub_out, workspace=sub_ws)
+    assert np.array_equal(bits(sub_out), bits(rows[valid]))
     with pytest.raises(ValueError, match="real expert ids"):
         routed_experts(x.to(device), ids.to(device), scores.to(device), bank)

@@ -497,6 +497,8 @@ __global__ __launch_bounds__(1024) void moe_route(const std::int64_t* __restrict
 // owns 8 consecutive columns per 512-column step. The token's slots are
 // ordered by ascending expert id (stable: position order for repeated ids) and
 // added in that order from +0 with fp16 adds, as index_add_ does per expert.
+// A token with an expert id outside [0, experts) (the reference rejects such
+// routing) gets a NaN row, so the error shows without a host synchronisation.
 template <int K>
 __global__ __launch_bounds__(256) void moe_combine(const std::int64_t* __restrict__ ids,
                                                    const int* __restrict__ pair_slot, const __half* __restrict__ v,
@@ -549,6 +551,7 @@ __global__ __launch_bounds__(256) void moe_combine(const std::int64_t* __restric
         o.y = __builtin_bit_cast(std::uint32_t, acc[1]);
         o.z = __builtin_bit_cast(std::uint32_t, acc[2]);
         o.w = __builtin_bit_cast(std::uint32_t, acc[3]);
+        if (n < K) o = make_uint4(0x7e007e00u, 0x7e007e00u, 0x7e007e00u, 0x7e007e00u);  // fp16 quiet NaNs
         *reinterpret_cast<uint4*>(out + static_cast<std::int64_t>(token) * hidden + col) = o;
     }
 }
@@ -996,6 +999,24 @@ __global__ void fill_row_slots(unsigned long long* __restrict__ slots, std::size
         slots[i] = kRowSlotEmpty;
 }
 
+void fill_row_slot_buffer(unsigned long long* slots, std::size_t bytes, hipStream_t stream) {
+    const std::size_t count = bytes / 8;
+    if (count)
+        fill_row_slots<<<static_cast<unsigned>(std::min<std::size_t>((count + 255) / 256, 1024)), 256, 0, stream>>>(
+            slots, count);
+}
+
+// After a split decode's launch: a refused launch never ran and left the
+// slots idle; they are refilled anyway (best effort) before the error is
+// raised, so a caller never has to reason about their state.
+void settle_row_slots(unsigned long long* slots, std::size_t bytes, hipStream_t stream) {
+    const hipError_t launched = hipGetLastError();
+    if (launched != hipSuccess) {
+        if (slots) fill_row_slot_buffer(slots, bytes, stream);
+        check(launched);
+    }
+}
+
 template <int HB, int W, int RB, int NB, int STEPS, bool TILED, int KS = 1>
 void launch_row_decode(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
                        __half* out, int tokens, int n, int k, int padded, hipStream_t stream,
@@ -1213,11 +1234,7 @@ VT_EXPORT std::uint64_t venturi_q4_tiled_workspace_bytes(int tokens, int n, int 
 VT_EXPORT int venturi_q4_tiled_workspace_init(void* workspace, std::uint64_t bytes, void* stream) {
     return vt::guarded([&] {
         vt::require(workspace && vt::aligned(workspace, 8) && bytes % 8 == 0, "invalid Q4 slot buffer");
-        const std::size_t count = bytes / 8;
-        if (count)
-            vt::fill_row_slots<<<static_cast<unsigned>(std::min<std::size_t>((count + 255) / 256, 1024)), 256, 0,
-                                 static_cast<hipStream_t>(stream)>>>(static_cast<unsigned long long*>(workspace),
-                                                                     count);
+        vt::fill_row_slot_buffer(static_cast<unsigned long long*>(workspace), bytes, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -1238,10 +1255,11 @@ VT_EXPORT int venturi_q4_tiled_run(const void* x, const void* codes, const void*
         const std::uint64_t need = vt::row_decode_slot_bytes(tokens, n, padded);
         vt::require(workspace_bytes >= need && (need == 0 || (workspace && vt::aligned(workspace, 8))),
                     "the Q4 tiled decode needs its slot buffer (venturi_q4_tiled_workspace_bytes)");
+        auto* slots = need ? static_cast<unsigned long long*>(workspace) : nullptr;
         vt::row_decode_dispatch<0, true>(static_cast<const __half*>(x), static_cast<const std::uint8_t*>(codes), nullptr,
                                          static_cast<const __half*>(scales), static_cast<__half*>(out), tokens, n, k,
-                                         padded, static_cast<hipStream_t>(stream),
-                                         need ? static_cast<unsigned long long*>(workspace) : nullptr);
+                                         padded, static_cast<hipStream_t>(stream), slots);
+        vt::settle_row_slots(slots, need, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -1275,6 +1293,7 @@ VT_EXPORT int venturi_row_tiled_run(const void* x, const void* codes, const void
         if (bits == 4) vt::row_decode_dispatch<0, true>(xp, cp, nullptr, sp, op, tokens, n, k, padded, st, slots);
         else if (bits == 5) vt::row_decode_dispatch<1, true>(xp, cp, hp, sp, op, tokens, n, k, padded, st, slots);
         else vt::row_decode_dispatch<2, true>(xp, cp, hp, sp, op, tokens, n, k, padded, st, slots);
+        vt::settle_row_slots(slots, need, st);
     });
 }
 

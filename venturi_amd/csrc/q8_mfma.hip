@@ -692,6 +692,13 @@ void q8_tiled_launch(const void* x, const void* codes, const void* scales, void*
     auto* op = static_cast<__half*>(out);
     if (swiglu) tiled_dispatch<true>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else tiled_dispatch<false>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+    const hipError_t launched = hipGetLastError();
+    if (launched != hipSuccess) {
+        // A refused launch never ran, so the slots are still idle; refill them
+        // anyway (best effort) so that a caller never has to reason about it.
+        if (slots) q8_tiled_workspace_init(slots, need, stream);
+        check(launched);
+    }
 }
 
 void q8_mfma_launch(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n,

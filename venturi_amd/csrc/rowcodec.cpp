@@ -21,8 +21,10 @@ enum Path : int { kDirect = 0, kChunkedDense = 1, kQuantized = 2 };
 //    WxA8Residual -> Quantized (fp16 only), one or two activation passes;
 //  * q4/q5/q6_g64, fp16 only, WxA16: Auto or Dequant -> ChunkedDense (the
 //    W*A16 contract, fp16(q*scale) weights); FusedResearch -> Direct for q4
-//    (the research fused GEMV); q5 fused and q5 A8 are SM70 kernels the
-//    reference qualifies on that architecture only, so they are not admitted.
+//    (the research fused GEMV). The reference also admits q5 FusedResearch
+//    (venturi_q5_fused_run, on SM70 and SM89) and q5 A8 (SM70 only); this
+//    library builds neither research kernel, so both are refused with a
+//    message rather than routed elsewhere.
 VRCPlan admit(int bits, int group, int precision, int dtype, int implementation) {
     require(dtype == kF16 || dtype == kBF16, "row-codec plans take fp16 or bf16 activations");
     require(precision >= kWxA16 && precision <= kWxA8Residual, "unknown row-codec precision");

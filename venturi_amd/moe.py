@@ -187,6 +187,13 @@ class RoutedExpertsPlan:
         }
 
     def run(self, x, indices, scores, *, out, workspace):
+        """Routes, projects and combines on the device; no host synchronisation.
+
+        Expert ids outside [0, num_experts) are not checked on the host (that
+        would synchronise): each pair with such an id is counted in the
+        workspace's ``status`` word and skipped, and its token's output row is
+        NaN, so bad routing cannot pass for a valid result.
+        """
         b, g = self.bank, self.bank.geometry
         _tensor(x, (self.tokens, g.hidden_size), torch.float16, b.device, "x")
         _tensor(indices, (self.tokens, g.top_k), torch.int64, b.device, "indices")
