@@ -27,7 +27,8 @@ than 2e-3 off, rel-L2); `exact_route` times that canonical route on the same
 job; `cpu_baseline` times the reference's CPU path (torch FP32 GEMM over
 materialised weights) on a bounded sample of the same workload. Further
 sections of the same line carry their own roofline objects: `config1`
-(4096 x 4096 at one token, rotated copies), `q4_decode`
+(4096 x 4096 at one token, rotated copies), `vocab_head`
+(the 248 320 x 5120 Q8 head held once in the tiled layout), `q4_decode`
 (the metric's Q4 leg), `q56_decode`, `codecs`, `prefill_a8` (config 3),
 `prefill_a16` (W8A16 / W4A16 at M = 2048), `moe_w4a16` (config 4) and
 `model_decode` (config 5).
@@ -82,7 +83,7 @@ def parse():
     p.add_argument("--no-moe", action="store_true", help="skip the config-4 routed-expert MoE section")
     p.add_argument("--no-model", action="store_true", help="skip the config-5 64-layer decode section")
     p.add_argument("--only", default=None,
-                   help="comma-separated extra sections to run (config1,q4,q56,codecs,a8,a16,moe,model)")
+                   help="comma-separated extra sections to run (config1,head,q4,q56,codecs,a8,a16,moe,model)")
     p.add_argument("--eager", action="store_true",
                    help="time config-2 launches issued from Python instead of HIP-graph replays (for counter runs)")
     return p.parse_args()
@@ -887,6 +888,54 @@ def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
     return result
 
 
+# ---------------------------------------------------------------- vocabulary head
+
+
+def vocab_head(backend, device, steps, warmup, tokens_list=(1, 4, 16)):
+    """The Q8 vocabulary head at the model's shape: vocab 248 320 x hidden 5120
+    (1.35 GB of q8_g32_fp16 per token, larger than the Infinity Cache, so
+    back-to-back launches stream from HBM), held once in the tiled layout
+    (``residency="tiled"``) and run on the matrix-core decode route; `steps`
+    launches per token count in one HIP graph between events. Algorithmic
+    bytes per launch = N*Kp*(1+2/32) + M*K*2 + M*N*2. The canonical-order
+    route (row-major planes) is timed at one token beside it.
+    """
+    vocab, hidden = 248320, 5120
+    gen = torch.Generator(device=device).manual_seed(248320)
+    packed = backend.quantize_q8(torch.randn(vocab, hidden, generator=gen, device=device) * 0.02)
+    torch.cuda.empty_cache()
+    resident = backend.upload_linear(packed, dtype=torch.float16, device=device, residency="tiled")
+    result = {"workload": "Q8 vocabulary head 248320 x 5120 (tiled residency, one copy)",
+              "resident_bytes": resident.storage_nbytes}
+    xs = {m: torch.randn(m, hidden, generator=gen, device=device).half() for m in tokens_list}
+    detail, total_b, total_s = {}, 0, 0.0
+    for m in tokens_list:
+        plan = resident.prepare(tokens=m)
+        out = torch.empty(m, vocab, dtype=torch.float16, device=device)
+        seconds, _, same = graph_timing({m: rotated_group([plan], xs[m], out, steps)}, steps, warmup, device)
+        avg = seconds[m] / steps
+        b = launch_bytes(m, vocab, hidden)
+        total_b += b
+        total_s += avg
+        detail[f"m{m}"] = {"us": round(avg * 1e6, 2), "GB/s": round(b / avg / 1e9, 1), "graph_equals_eager": same}
+    del resident
+    torch.cuda.empty_cache()
+    full = backend.upload_linear(packed, dtype=torch.float16, device=device)
+    exact = full.prepare(tokens=1, route="exact")
+    out = torch.empty(1, vocab, dtype=torch.float16, device=device)
+    seconds, _, _ = graph_timing({"exact": rotated_group([exact], xs[1], out, steps)}, steps, warmup, device)
+    ex = seconds["exact"] / steps
+    detail["m1_exact_route"] = {"us": round(ex * 1e6, 2), "GB/s": round(launch_bytes(1, vocab, hidden) / ex / 1e9, 1)}
+    del full, packed
+    torch.cuda.empty_cache()
+    gbs = total_b / total_s / 1e9
+    result["roofline"] = {"bound": "hbm", "kernel": "q8_tiled_lds / q8_tiled_decode (fp16 MFMA)",
+                          "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    result["per_launch"] = detail
+    return result
+
+
 # ---------------------------------------------------------------- config 5
 
 
@@ -895,7 +944,8 @@ def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
 
     One step chains, per layer: h -> QKV; a seeded fp16 [B, 6144] -> o_proj;
     h -> gate+up fused with SiLU*up (the native runtime's SwiGLU arithmetic
-    in the projection's epilogue) -> down -> next h. The 256 launches of a
+    in the projection's epilogue) -> down -> next h. Each matrix is resident
+    once, in the tiled layout its decode kernel reads (no row-major copy). The 256 launches of a
     step are captured once in a HIP graph (checked bit-for-bit against an
     eager step) and replayed. Projection-only tokens/s = B / step time; GB/s counts the
     projections' algorithmic bytes (weights + activations + outputs).
@@ -907,7 +957,10 @@ def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
         for i, (name, n, k) in enumerate(PROJECTIONS):
             gen = torch.Generator(device=device).manual_seed(7_000_000 + 16 * layer + i)
             w = torch.randn(n, k, generator=gen, device=device) * 0.02
-            row.append(backend.upload_linear(backend.quantize_q8(w), dtype=torch.float16, device=device))
+            # One resident copy per matrix, in the layout its decode kernel reads.
+            residency = "tiled-paired" if name == "gate_up" else "tiled"
+            row.append(backend.upload_linear(backend.quantize_q8(w), dtype=torch.float16, device=device,
+                                             residency=residency))
             del w
         matrices.append(row)
     torch.cuda.synchronize(device)
@@ -989,6 +1042,9 @@ def main():
     if wanted("config1"):
         log("config 1: 4096 x 4096 at one token")
         result["config1"] = config1(backend, device, args.steps, args.warmup, args.copy_mb)
+    if wanted("head"):
+        log("vocabulary head 248320 x 5120")
+        result["vocab_head"] = vocab_head(backend, device, args.steps, args.warmup)
     if wanted("q4", args.no_q4):
         log("Q4 W4A16 decode at the config-2 shapes")
         result["q4_decode"] = q4_decode(backend, device, args.steps, args.warmup, args.copy_mb)

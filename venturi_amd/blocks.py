@@ -209,17 +209,22 @@ class HipBackend(Backend):
         torch.cuda.synchronize(self.resolve_device(device))
 
     # -- linear ------------------------------------------------------------
-    def upload_linear(self, weight, *, dtype, device):
+    def upload_linear(self, weight, *, dtype, device, residency="row-major"):
+        """Owned device copy of a weight. ``residency`` (an extension, Q8 only) keeps the
+        row-major planes ("row-major"), or only the matrix-core decode's tiled copy
+        ("tiled", or "tiled-paired" for a gate+up matrix run by ``prepare_swiglu``)."""
         if not isinstance(weight, (DenseWeight, Q4RowSplitWeight, Q8RowSplitWeight)):
             raise TypeError("Linear requires explicit DenseWeight, Q4RowSplitWeight or Q8RowSplitWeight")
         weight.validate()
         self.require_linear(weight, dtype=dtype, device=device)
         target = self.validate_device(dtype, device)
+        if residency != "row-major" and not isinstance(weight, Q8RowSplitWeight):
+            raise ValueError("tiled residency is defined for Q8 weights only")
         if isinstance(weight, Q8RowSplitWeight):
             from .vocabulary import Q8VocabularyWeights
 
             resident = Q8VocabularyWeights(weight.codes, weight.scales, weight.in_features).upload(
-                self, device=target, dtype=dtype
+                self, device=target, dtype=dtype, residency=residency
             )
         else:
             from .q4 import upload_q4

@@ -70,11 +70,12 @@ class PreparedQ8DP4A:
         if workspace.data_ptr() % 16:
             raise ValueError("A8 workspace requires 16-byte alignment")
         entry = self._native.venturi_q8_dp4a_run if self.kernel == "exact" else self._native.venturi_q8_a8_gemm_run
+        codes, scales = r.row_major_planes()
         with torch.cuda.device(r.device):
             r.backend._check(
                 entry(
-                    workspace.data_ptr(), self.workspace_bytes, r._codes.data_ptr(), r._scales.data_ptr(),
-                    out.data_ptr(), self.tokens, r.vocab_size, r.hidden_size, r._codes.shape[1], self.passes,
+                    workspace.data_ptr(), self.workspace_bytes, codes.data_ptr(), scales.data_ptr(),
+                    out.data_ptr(), self.tokens, r.vocab_size, r.hidden_size, r.padded_k, self.passes,
                     _stream(r.device),
                 )
             )
@@ -104,6 +105,7 @@ def prepare_q8_dp4a(resident, *, tokens, residual_compensation, route="auto"):
         resident = resident._payload
     if not isinstance(resident, ResidentQ8Vocabulary):
         raise ValueError("A8 requires resident native Q8 planes")
+    resident.row_major_planes()  # the A8 kernels read the row-major planes
     if type(residual_compensation) is not bool:
         raise ValueError("Explicit boolean residual_compensation required")
     _shape(tokens, resident.hidden_size)

@@ -92,7 +92,7 @@ class PreparedQ8Fused:
                     stream))
             backend._check(self._run(
                 workspace.data_ptr(), a8.workspace_bytes, C.cast(table, C.c_void_p), len(table), a8.tokens,
-                lead.hidden_size, lead._codes.shape[1], a8.passes, stream))
+                lead.hidden_size, lead.padded_k, a8.passes, stream))
         return outputs
 
 
@@ -124,5 +124,6 @@ def prepare_q8_fused(residents, *, tokens, residual_compensation, output_strides
     if sum(m.vocab_size for m in values) >= _INT32_LIMIT - 48:
         raise ValueError("fused row sum exceeds int32")
     strides = _fused_strides(values, tokens, output_strides)
-    matrices = tuple((m._codes.data_ptr(), m._scales.data_ptr(), m.vocab_size, s) for m, s in zip(values, strides))
+    planes = [m.row_major_planes() for m in values]
+    matrices = tuple((c.data_ptr(), sc.data_ptr(), m.vocab_size, s) for (c, sc), m, s in zip(planes, values, strides))
     return PreparedQ8Fused(values, plans[0], strides, lead.backend._native.venturi_q8_fused_run, matrices)

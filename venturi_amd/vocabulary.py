@@ -1,25 +1,30 @@
-"""Resident Q8 row-split planes: projection (output head) and embedding lookup.
+"""Resident Q8 row-split matrices: output projection (the vocabulary head) and embedding lookup.
 
-Mirrors venturi.ops.vocabulary (reference vocabulary.py:23-173). A resident
-Q8 matrix keeps its int8 codes and fp16 group scales on the device and is
-never expanded to dense weights. ``prepare(tokens=...)`` selects the kernel
-family once:
+Public names of the reference's ops/vocabulary.py (lines 23-173):
+``Q8VocabularyWeights(codes, scales, hidden_size)`` with ``validate`` and
+``upload``; ``ResidentQ8Vocabulary`` with ``prepare(tokens=)``,
+``prepare_embedding(ids)``, ``storage_tensors``; ``Q8OutputHead.run(x, out=)``
+and ``Q8Embedding.run(out=)``. The matrix is never expanded to dense weights.
 
-* ``exact``: the reference's canonical fp32 order (bytes identical to
-  ``venturi_q8_head_run`` on the reference's GPUs);
-* ``mfma``: fp16 matrix cores with per-group fp32 scaling (same values up to
-  fp32 association, see ``Q8OutputHead.route``). Up to 32 tokens (decode)
-  it reads a tiled copy of the planes (16-row blocks x 64-column chunks in
-  MFMA operand order, built once by the first such plan and kept with the
-  resident weight), so every wave streams contiguous 1 KB blocks; above 32
-  tokens (prefill) it runs ``venturi_q8_prefill_run`` on the row-major planes
-  (LDS-staged 256-token x 128-row tiles);
-* ``auto``: ``mfma`` whenever its conditions hold (FP16 activations,
-  K % 8 == 0), else ``exact``. The matrix-core kernels are faster at every
-  token count (the canonical order needs one fp32 FMA per token and weight
-  plus an exact weight conversion, and its lane-per-four-columns layout
-  issues 4-byte loads); callers that need the reference's bytes ask for
-  ``exact``.
+Kernel families, chosen once per plan (``prepare(tokens=, route=)``):
+
+* ``exact``: the reference's canonical fp32 order (``venturi_q8_head_run``,
+  the bytes of the reference's head kernel), row-major planes;
+* ``mfma``: fp16 matrix cores with per-group fp32 scaling (equal to the
+  canonical order up to fp32 association). Up to 32 tokens (decode) it reads
+  the tiled planes (16-row blocks x 64-column chunks in MFMA operand order),
+  so each wave streams contiguous 1 KB blocks; above 32 tokens (prefill) it
+  runs ``venturi_q8_prefill_run`` on the row-major planes;
+* ``auto``: ``mfma`` where its conditions hold (FP16 activations,
+  K % 8 == 0), else ``exact``.
+
+Residency (an upload option): ``"row-major"`` keeps the planes as the
+reference lays them out and builds a tiled copy the first time a decode plan
+needs it (both stay resident: 2.1 bytes per weight); ``"tiled"`` keeps only
+the tiled copy (1.06 bytes per weight) and admits decode plans of at most 32
+tokens on the matrix-core route; ``"tiled-paired"`` keeps only the paired
+copy of a gate+up matrix and admits ``prepare_swiglu``. The single-copy forms
+suit large matrices that only decode reads, such as a 248 320-row head.
 """
 
 from dataclasses import dataclass, field
@@ -31,11 +36,18 @@ from .blocks import _DTYPES, Q8_ROUTES, _no_overlap, _shape, _stream, _tensor
 
 EXACT_MAX_AUTO_TOKENS = 0
 MFMA_MAX_TOKENS = 32
+RESIDENCIES = ("row-major", "tiled", "tiled-paired")
 _TILE_LOCK = threading.Lock()
+_ROUTE_NAMES = {"exact": "venturi-q8-exact", "mfma": "venturi-q8-mfma", "prefill": "venturi-q8-mfma",
+                "swiglu": "venturi-q8-mfma-swiglu"}
+
+
+def _padded(k):
+    return (k + 127) // 128 * 128
 
 
 def tile_q8(codes, scales, paired=False):
-    """Tiled planes of the matrix-core route (read by ``venturi_q8_tiled_run``).
+    """Tiled planes of the matrix-core decode (read by ``venturi_q8_tiled_run``).
 
     Codes [row block][chunk][lane l = 16q + m][16 bytes]: row m of the block,
     columns 64c + 8q .. +8 (group 2c) then 64c + 32 + 8q .. +8 (group 2c + 1).
@@ -51,34 +63,34 @@ def tile_q8(codes, scales, paired=False):
             raise ValueError("a fused gate+up matrix needs an even row count")
         inter = n // 2
         blocks = (inter + 7) // 8
-        idx = torch.arange(blocks * 16, device=codes.device)
-        gate = (idx // 16) * 8 + idx % 8  # intermediate column of each slot
-        source = torch.where(idx % 16 < 8, gate, gate + inter)
-        valid = gate < inter
-        c = torch.zeros((blocks * 16, padded), dtype=torch.int8, device=codes.device)
-        s = torch.zeros((blocks * 16, padded // 32), dtype=torch.float16, device=codes.device)
-        c[valid] = codes[source[valid]]
-        s[valid] = scales[source[valid]]
+        slot = torch.arange(blocks * 16, device=codes.device)
+        column = (slot // 16) * 8 + slot % 8  # the intermediate column each slot serves
+        source = torch.where(slot % 16 < 8, column, column + inter)
+        keep = column < inter
     else:
         blocks = (n + 15) // 16
-        c = torch.zeros((blocks * 16, padded), dtype=torch.int8, device=codes.device)
-        s = torch.zeros((blocks * 16, padded // 32), dtype=torch.float16, device=codes.device)
-        c[:n] = codes
-        s[:n] = scales
-    tc = c.view(blocks, 16, chunks, 2, 4, 8).permute(0, 2, 4, 1, 3, 5).contiguous()
-    ts = s.view(blocks, 16, chunks, 2).permute(0, 2, 1, 3).contiguous()
-    return tc, ts
+        source = torch.arange(blocks * 16, device=codes.device)
+        keep = source < n
+    c = torch.zeros((blocks * 16, padded), dtype=torch.int8, device=codes.device)
+    s = torch.zeros((blocks * 16, padded // 32), dtype=torch.float16, device=codes.device)
+    c[keep] = codes[source[keep]]
+    s[keep] = scales[source[keep]]
+    tiled_codes = c.view(blocks, 16, chunks, 2, 4, 8).permute(0, 2, 4, 1, 3, 5).contiguous()
+    tiled_scales = s.view(blocks, 16, chunks, 2).permute(0, 2, 1, 3).contiguous()
+    return tiled_codes, tiled_scales
 
 
 def _ids(ids, vocab):
     if not isinstance(ids, (list, tuple)) or not ids:
         raise ValueError("Vocabulary IDs must be a nonempty list/tuple")
-    if len(ids) >= 2**31 or any(type(i) is not int or not 0 <= i < vocab for i in ids):
+    if len(ids) >= 2**31 or not all(type(i) is int and 0 <= i < vocab for i in ids):
         raise ValueError("Vocabulary ID/count is out of range")
 
 
 @dataclass(frozen=True)
 class Q8VocabularyWeights:
+    """Q8 planes of one matrix (CPU or device): codes int8 [N, Kp], scales fp16 [N, Kp/32]."""
+
     codes: torch.Tensor
     scales: torch.Tensor
     hidden_size: int
@@ -88,67 +100,100 @@ class Q8VocabularyWeights:
             raise ValueError("Q8 hidden size must be positive")
         if not isinstance(self.codes, torch.Tensor) or self.codes.ndim != 2:
             raise ValueError("Q8 codes require [vocab,padded_hidden]")
-        n, padded = self.codes.shape
-        _shape(n, self.hidden_size)
-        if padded != (self.hidden_size + 127) // 128 * 128:
+        rows, width = self.codes.shape
+        _shape(rows, self.hidden_size)
+        if width != _padded(self.hidden_size):
             raise ValueError("Q8 hidden padding must be a multiple of 128")
-        device = self.codes.device
-        _tensor(self.codes, (n, padded), torch.int8, device, "codes")
-        _tensor(self.scales, (n, padded // 32), torch.float16, device, "scales")
+        where = self.codes.device
+        _tensor(self.codes, (rows, width), torch.int8, where, "codes")
+        _tensor(self.scales, (rows, width // 32), torch.float16, where, "scales")
         if bool((self.codes == -128).any()):
             raise ValueError("Q8 code -128 is outside the artifact contract")
-        if not bool(torch.isfinite(self.scales).all()) or bool((self.scales < 0).any()):
+        if bool((self.scales < 0).any()) or not bool(torch.isfinite(self.scales).all()):
             raise ValueError("Q8 scales must be finite and nonnegative")
 
-    def upload(self, backend, *, device="cuda:0", dtype=torch.bfloat16):
-        """Copies the planes to the device once (a same-device source is copied too)."""
+    def upload(self, backend, *, device="cuda:0", dtype=torch.bfloat16, residency="row-major"):
+        """Copies the planes to the device once (a same-device source is copied too).
+
+        ``residency`` selects what stays resident (see the module docstring);
+        the single-copy forms are built from a transient device copy.
+        """
         self.validate()
         if dtype not in (torch.float16, torch.bfloat16):
             raise ValueError("Q8 vocabulary supports FP16/BF16 activations")
+        if residency not in RESIDENCIES:
+            raise ValueError(f"Q8 residency must be one of {RESIDENCIES}")
         target = backend.validate_device(dtype, device)
+        geometry = (self.codes.shape[0], self.codes.shape[1])
         with torch.cuda.device(target):
-            codes, scales = (t.detach().to(target, copy=True) for t in (self.codes, self.scales))
+            planes = tuple(t.detach().to(target, copy=True) for t in (self.codes, self.scales))
+            tiles = {}
+            if residency != "row-major":
+                if dtype != torch.float16 or self.hidden_size % 8:
+                    raise ValueError("tiled residency serves the matrix-core route: FP16 activations and K % 8 == 0")
+                paired = residency == "tiled-paired"
+                tiles[residency] = tile_q8(*planes, paired=paired)
+                planes = (None, None)
             torch.cuda.current_stream(target).synchronize()
-        return ResidentQ8Vocabulary(backend, codes, scales, self.hidden_size, dtype)
+        return ResidentQ8Vocabulary(backend, planes[0], planes[1], self.hidden_size, dtype, tiles, residency,
+                                    geometry, target)
 
 
 @dataclass(frozen=True)
 class ResidentQ8Vocabulary:
     backend: object
-    _codes: torch.Tensor
-    _scales: torch.Tensor
+    _codes: object  # int8 [N, Kp] on the device, or None when only tiled planes are resident
+    _scales: object
     hidden_size: int
     dtype: torch.dtype = torch.bfloat16
     _tiles: dict = field(default_factory=dict, compare=False, repr=False)
+    residency: str = "row-major"
+    _geometry: tuple = ()  # (rows, padded K)
+    _device: object = None
 
     @property
     def device(self):
-        return self._codes.device
-
-    def tiled_planes(self, paired=False):
-        """The matrix-core route's tiled copy of the planes (built on first use)."""
-        key = "mfma-paired" if paired else "mfma"
-        with _TILE_LOCK:
-            if key not in self._tiles:
-                with torch.cuda.device(self.device):
-                    self._tiles[key] = tile_q8(self._codes, self._scales, paired)
-                    torch.cuda.current_stream(self.device).synchronize()
-            return self._tiles[key]
+        return self._device if self._device is not None else self._codes.device
 
     @property
     def vocab_size(self):
-        return self._codes.shape[0]
+        return self._geometry[0] if self._geometry else self._codes.shape[0]
+
+    @property
+    def padded_k(self):
+        return self._geometry[1] if self._geometry else self._codes.shape[1]
 
     @property
     def storage_tensors(self):
-        return (self._codes, self._scales)
+        if self.residency == "row-major":
+            return (self._codes, self._scales)
+        return self._tiles[self.residency]
 
     @property
     def storage_nbytes(self):
         return sum(t.numel() * t.element_size() for t in self.storage_tensors)
 
+    def row_major_planes(self):
+        """(codes, scales) of the reference layout; residents without them refuse clearly."""
+        if self._codes is None:
+            raise ValueError(f"this Q8 resident keeps only tiled planes (residency={self.residency!r}); "
+                             "upload it with residency='row-major' for this kernel")
+        return self._codes, self._scales
+
+    def tiled_planes(self, paired=False):
+        """The tiled copy of the planes (built on first use for a row-major resident)."""
+        key = "tiled-paired" if paired else "tiled"
+        with _TILE_LOCK:
+            if key not in self._tiles:
+                codes, scales = self.row_major_planes()
+                with torch.cuda.device(self.device):
+                    self._tiles[key] = tile_q8(codes, scales, paired)
+                    torch.cuda.current_stream(self.device).synchronize()
+            return self._tiles[key]
+
     def prepare_embedding(self, ids):
         _ids(ids, self.vocab_size)
+        self.row_major_planes()
         self.backend.validate_device(self.dtype, self.device)
         indices = torch.tensor(ids, dtype=torch.int64, device=self.device)
         torch.cuda.current_stream(self.device).synchronize()
@@ -161,30 +206,18 @@ class ResidentQ8Vocabulary:
         if route not in Q8_ROUTES:
             raise ValueError(f"Q8 route must be one of {Q8_ROUTES}")
         self.backend.validate_device(self.dtype, self.device)
-        mfma_ok = self.dtype == torch.float16 and self.hidden_size % 8 == 0
+        matrix_cores = self.dtype == torch.float16 and self.hidden_size % 8 == 0
         if route == "auto":
-            route = "mfma" if mfma_ok and tokens > EXACT_MAX_AUTO_TOKENS else "exact"
-        if route == "mfma" and not mfma_ok:
+            route = "mfma" if matrix_cores and tokens > EXACT_MAX_AUTO_TOKENS else "exact"
+        if route == "mfma" and not matrix_cores:
             raise ValueError("The Q8 MFMA route takes FP16 activations and K % 8 == 0")
+        if self.residency == "tiled-paired" or (self.residency == "tiled" and (route == "exact" or tokens > MFMA_MAX_TOKENS)):
+            self.row_major_planes()  # raises: the plan needs planes this resident does not keep
         if route == "exact":
-            return Q8OutputHead(self, tokens, route)
+            return Q8OutputHead(self, tokens, "exact")
         if tokens > MFMA_MAX_TOKENS:
             return Q8OutputHead(self, tokens, "prefill")
-        return Q8OutputHead(self, tokens, route, self.tiled_planes(), self._slots(tokens, swiglu=False))
-
-    def _slots(self, tokens, *, swiglu):
-        """The plan's exchange slots for launches that split K (None when this shape does not split)."""
-        lib = self.backend._native
-        nbytes = lib.venturi_q8_tiled_workspace_bytes(tokens, self.vocab_size, int(swiglu))
-        if nbytes == 0:
-            self.backend._check(-1 if lib.venturi_blocks_error() else 0)
-            return None
-        with torch.cuda.device(self.device):
-            slots = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
-            self.backend._check(lib.venturi_q8_tiled_workspace_init(slots.data_ptr(), nbytes, _stream(self.device)))
-            torch.cuda.current_stream(self.device).synchronize()
-        return slots
-
+        return Q8OutputHead(self, tokens, "mfma", self.tiled_planes(), self._slots(tokens, swiglu=False))
 
     def prepare_swiglu(self, *, tokens):
         """Fused gate+up projection with SwiGLU (an extension; matrix cores only).
@@ -200,8 +233,23 @@ class ResidentQ8Vocabulary:
             raise ValueError(
                 f"The fused SwiGLU projection takes FP16 activations, K % 8 == 0 and at most {MFMA_MAX_TOKENS} tokens"
             )
+        if self.residency == "tiled":
+            self.row_major_planes()
         self.backend.validate_device(self.dtype, self.device)
         return Q8OutputHead(self, tokens, "swiglu", self.tiled_planes(paired=True), self._slots(tokens, swiglu=True))
+
+    def _slots(self, tokens, *, swiglu):
+        """The plan's exchange slots for launches that split K (None when this shape does not split)."""
+        lib = self.backend._native
+        nbytes = lib.venturi_q8_tiled_workspace_bytes(tokens, self.vocab_size, int(swiglu))
+        if nbytes == 0:
+            self.backend._check(-1 if lib.venturi_blocks_error() else 0)
+            return None
+        with torch.cuda.device(self.device):
+            slots = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            self.backend._check(lib.venturi_q8_tiled_workspace_init(slots.data_ptr(), nbytes, _stream(self.device)))
+            torch.cuda.current_stream(self.device).synchronize()
+        return slots
 
 
 @dataclass(frozen=True)
@@ -211,23 +259,13 @@ class Q8Embedding:
 
     def run(self, *, out):
         r = self.resident
+        codes, scales = r.row_major_planes()
         _tensor(out, (self._indices.numel(), r.hidden_size), r.dtype, r.device, "out")
-        _no_overlap(out, r.storage_tensors + (self._indices,))
+        _no_overlap(out, (codes, scales, self._indices))
         with torch.cuda.device(r.device):
-            r.backend._check(
-                r.backend._native.venturi_q8_embedding_run(
-                    r._codes.data_ptr(),
-                    r._scales.data_ptr(),
-                    self._indices.data_ptr(),
-                    out.data_ptr(),
-                    self._indices.numel(),
-                    r.vocab_size,
-                    r.hidden_size,
-                    r._codes.shape[1],
-                    _DTYPES[r.dtype],
-                    _stream(r.device),
-                )
-            )
+            r.backend._check(r.backend._native.venturi_q8_embedding_run(
+                codes.data_ptr(), scales.data_ptr(), self._indices.data_ptr(), out.data_ptr(), self._indices.numel(),
+                r.vocab_size, r.hidden_size, r.padded_k, _DTYPES[r.dtype], _stream(r.device)))
         return out
 
 
@@ -246,12 +284,7 @@ class Q8OutputHead:
 
     @property
     def route(self):
-        return {
-            "exact": "venturi-q8-exact",
-            "mfma": "venturi-q8-mfma",
-            "prefill": "venturi-q8-mfma",
-            "swiglu": "venturi-q8-mfma-swiglu",
-        }[self.kernel]
+        return _ROUTE_NAMES[self.kernel]
 
     @property
     def out_features(self):
@@ -260,37 +293,25 @@ class Q8OutputHead:
 
     @property
     def storage_tensors(self):
-        return self.resident.storage_tensors + tuple(self.tiles)
+        r = self.resident
+        kept = () if r._codes is None else (r._codes, r._scales)
+        return kept + tuple(self.tiles) + (() if self.slots is None else (self.slots,))
 
     def run(self, x, *, out):
         r = self.resident
         _tensor(x, (self.tokens, r.hidden_size), r.dtype, r.device, "x")
         _tensor(out, (self.tokens, self.out_features), r.dtype, r.device, "out")
-        slots = () if self.slots is None else (self.slots,)
-        _no_overlap(out, (x,) + self.storage_tensors + slots)
+        _no_overlap(out, (x,) + self.storage_tensors)
         lib = r.backend._native
-        if self.kernel == "exact":
-            entry, planes, tail = lib.venturi_q8_head_run, (r._codes, r._scales), ()
-        elif self.kernel == "prefill":
-            entry, planes, tail = lib.venturi_q8_prefill_run, (r._codes, r._scales), ()
+        if self.kernel in ("exact", "prefill"):
+            entry = lib.venturi_q8_head_run if self.kernel == "exact" else lib.venturi_q8_prefill_run
+            planes, tail = r.row_major_planes(), ()
         else:
             entry = lib.venturi_q8_tiled_swiglu_run if self.kernel == "swiglu" else lib.venturi_q8_tiled_run
             planes = self.tiles
             tail = (0, 0) if self.slots is None else (self.slots.data_ptr(), self.slots.numel())
         with torch.cuda.device(r.device):
-            r.backend._check(
-                entry(
-                    x.data_ptr(),
-                    planes[0].data_ptr(),
-                    planes[1].data_ptr(),
-                    out.data_ptr(),
-                    self.tokens,
-                    r.vocab_size,
-                    r.hidden_size,
-                    r._codes.shape[1],
-                    _DTYPES[r.dtype],
-                    *tail,
-                    _stream(r.device),
-                )
-            )
+            r.backend._check(entry(x.data_ptr(), planes[0].data_ptr(), planes[1].data_ptr(), out.data_ptr(),
+                                   self.tokens, r.vocab_size, r.hidden_size, r.padded_k, _DTYPES[r.dtype], *tail,
+                                   _stream(r.device)))
         return out
