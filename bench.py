@@ -83,7 +83,8 @@ def parse():
     p.add_argument("--no-moe", action="store_true", help="skip the config-4 routed-expert MoE section")
     p.add_argument("--no-model", action="store_true", help="skip the config-5 64-layer decode section")
     p.add_argument("--only", default=None,
-                   help="comma-separated extra sections to run (config1,head,q4,q56,codecs,a8,a16,moe,model)")
+                   help="comma-separated sections to run (config2,config1,head,q4,q56,codecs,a8,a16,moe,model); "
+                   "without config2 no headline metric is printed (for counter runs)")
     p.add_argument("--eager", action="store_true",
                    help="time config-2 launches issued from Python instead of HIP-graph replays (for counter runs)")
     return p.parse_args()
@@ -1035,9 +1036,12 @@ def main():
     def wanted(name, skip=False):
         return (name in only) if only is not None else not skip
 
-    result, copies = config2(backend, device, args)
-    cpu_copies = None if args.no_cpu else [[r[0]] for r in copies]
-    del copies
+    if only is None or "config2" in only:
+        result, copies = config2(backend, device, args)
+        cpu_copies = None if args.no_cpu else [[r[0]] for r in copies]
+        del copies
+    else:  # a section run (counter collection): no headline metric
+        result, cpu_copies = {"sections": sorted(only)}, None
     torch.cuda.empty_cache()
     if wanted("config1"):
         log("config 1: 4096 x 4096 at one token")

@@ -147,6 +147,21 @@ def test_row_gemm_contract_tolerances(backend, device, nbits, shape, tokens):
     # (up to 384, up to 1023 and from 1024 row blocks of 16).
     n, k = shape
     print(f"case row-gemm bits={nbits} n={n} k={k} tokens={tokens}", flush=True)
+    _row_gemm_contract(backend, device, nbits, n, k, tokens)
+
+
+@pytest.mark.parametrize("nbits", [4, 5, 6])
+@pytest.mark.parametrize("shape,tokens", [((16400, 264), 1000), ((14336, 136), 1024), ((14080, 136), 1024)])
+def test_row_prefill_tile_choice(backend, device, nbits, shape, tokens):
+    # Prefill launches pick 128 x 256 tiles when that grid has at least 448
+    # workgroups, else 256 x 64 tiles: 65 x 8 (ragged tokens) and 56 x 8 take
+    # the first, 55 x 8 the second; both hold the W*A16 contract.
+    n, k = shape
+    print(f"case row-prefill bits={nbits} n={n} k={k} tokens={tokens}", flush=True)
+    _row_gemm_contract(backend, device, nbits, n, k, tokens)
+
+
+def _row_gemm_contract(backend, device, nbits, n, k, tokens):
     packed, high, scales = _planes(n, k, nbits, 77 * nbits + n + tokens)
     padded = packed.shape[1] * 2
     x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens + k)).half()
