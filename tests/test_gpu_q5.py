@@ -151,11 +151,10 @@ def test_row_gemm_contract_tolerances(backend, device, nbits, shape, tokens):
 
 
 @pytest.mark.parametrize("nbits", [4, 5, 6])
-@pytest.mark.parametrize("shape,tokens", [((16400, 264), 1000), ((14336, 136), 1024), ((14080, 136), 1024)])
-def test_row_prefill_tile_choice(backend, device, nbits, shape, tokens):
-    # Prefill launches pick 128 x 256 tiles when that grid has at least 448
-    # workgroups, else 256 x 64 tiles: 65 x 8 (ragged tokens) and 56 x 8 take
-    # the first, 55 x 8 the second; both hold the W*A16 contract.
+@pytest.mark.parametrize("shape,tokens", [((16400, 264), 1000), ((14336, 136), 1024)])
+def test_row_prefill_large_grids(backend, device, nbits, shape, tokens):
+    # Prefill grids of about a thousand workgroups (129 x 8 and 112 x 8 tiles
+    # of 128 tokens x 128 rows), one of them with a ragged last token tile.
     n, k = shape
     print(f"case row-prefill bits={nbits} n={n} k={k} tokens={tokens}", flush=True)
     _row_gemm_contract(backend, device, nbits, n, k, tokens)

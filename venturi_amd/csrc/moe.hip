@@ -1117,21 +1117,10 @@ void row_gemm_launch(const void* x, const void* codes, const void* high, const v
     const auto* sp = static_cast<const __half*>(scales);
     auto* op = static_cast<__half*>(out);
     if (tokens >= kRowPrefillMinTokens) {
-        // Prefill tiles, 8 waves each, chosen by grid size (measured at the
-        // config-2 shapes, M = 2048): 128 tokens x 256 rows (64 x 64 per wave)
-        // where that grid has at least 448 workgroups (QKV, gate+up: +23% and
-        // +13% over 128 x 128), else 256 tokens x 64 rows (64 x 32 per wave;
-        // o_proj and down, whose 128 x 256 grid leaves CUs idle: +15%, +4%).
-        const long wide = static_cast<long>((n + 255) / 256) * ((tokens + 127) / 128);
-        if (wide >= 448) {
-            if (bits == 4) launch_row_prefill<0, 2, 4, 4, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
-            else if (bits == 5) launch_row_prefill<1, 2, 4, 4, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
-            else launch_row_prefill<2, 2, 4, 4, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
-        } else {
-            if (bits == 4) launch_row_prefill<0, 4, 2, 4, 2, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
-            else if (bits == 5) launch_row_prefill<1, 4, 2, 4, 2, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
-            else launch_row_prefill<2, 4, 2, 4, 2, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
-        }
+        // Prefill: 128-token tiles that read each weight once per tile.
+        if (bits == 4) launch_row_prefill<0, 4, 2, 2, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
+        else if (bits == 5) launch_row_prefill<1, 4, 2, 2, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
+        else launch_row_prefill<2, 4, 2, 2, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
         return;
     }
     if (bits == 4) row_decode_dispatch<0>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
