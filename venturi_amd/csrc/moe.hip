@@ -358,10 +358,24 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
                 __syncthreads();
             }
 
-            // D layout: lane holds row slot m of block b for tokens 16j + 4q + i.
+            // Epilogue through LDS: the staging buffers are free after the last
+            // chunk's barrier. The pass's output tile (tokens x the workgroup's
+            // 16 W RB rows, or its 8 W RB SwiGLU columns) is written there from
+            // the D layout (lane holds row slot m of block b for tokens
+            // 16j + 4q + i), then every token row leaves as 16-byte stores: 2-byte
+            // stores straight from the D layout leave 32-byte pieces of lines
+            // that other workgroups also write, which costs more than the GEMM's
+            // own weight stream. Row stride: 8 halves past the tile width, so the
+            // four token quads of a store land on distinct banks.
+            constexpr int kOutCols = EPI == kSwiGLU ? W * RB * 8 : W * RB * 16;
+            constexpr int kOutStride = kOutCols + 8;
+            static_assert(16 * NBMAX * kOutStride <= 2 * 16 * NBMAX * kXStride, "the output tile fits the staging buffers");
+            static_assert(W * RB % 8 == 0, "a workgroup covers whole SwiGLU column tiles");
+            __half* tile = reinterpret_cast<__half*>(&xl[0][0]);
+            const int first = part * W * RB;  // the workgroup's first row block
 #pragma unroll
             for (int r = 0; r < RB; ++r) {
-                const int blk = b0 + r;
+                const int slot_blk = b0 + r - first;
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -370,24 +384,34 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
                         const float v = acc[r][b][i];
                         if (EPI == kSwiGLU) {
                             const float other = __shfl_xor(v, 8, 64);  // lane m^8 holds the paired up/gate row
-                            const int col = (blk >> 3) * (kRows / 2) + 8 * (blk & 7) + (m & 7);
-                            if (m < 8 && t < live && blk < blocks && col < p.half_rows) {
+                            if (m < 8) {
                                 const float g = __half2float(from_f32<__half>(v));
                                 const float u = __half2float(from_f32<__half>(other));
                                 const float a = __half2float(from_f32<__half>(silu(g)));
-                                p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + col] =
-                                    from_f32<__half>(__fmul_rn(a, u));
+                                tile[t * kOutStride + 8 * slot_blk + m] = from_f32<__half>(__fmul_rn(a, u));
                             }
                         } else {
-                            const int row = 16 * blk + m;
-                            if (t < live && blk < blocks && row < p.n) {
-                                float y = __half2float(from_f32<__half>(v));
-                                if (EPI == kScore) y = __fmul_rn(y, __half2float(p.score[pass + t]));
-                                p.out[static_cast<std::int64_t>(pass + t) * p.out_stride + row] = from_f32<__half>(y);
-                            }
+                            float y = __half2float(from_f32<__half>(v));
+                            if (EPI == kScore) y = __fmul_rn(y, __half2float(p.score[pass + min(t, live - 1)]));
+                            tile[t * kOutStride + 16 * slot_blk + m] = from_f32<__half>(y);
                         }
                     }
                 }
+            }
+            __syncthreads();
+            // Rows t < live; columns of blocks past the last one, or past the
+            // matrix, are not stored (SwiGLU columns of block blk start at
+            // (blk >> 3) * 64 + 8 * (blk & 7); W * RB is a multiple of 8). The
+            // column limit is a multiple of 8 (hidden and intermediate sizes
+            // are), so a 16-byte unit is stored whole or not at all.
+            const int col0 = EPI == kSwiGLU ? (first >> 3) * (kRows / 2) : 16 * first;
+            const int limit = EPI == kSwiGLU ? p.half_rows : p.n;
+            constexpr int kUnits = kOutCols / 8;
+            for (int u = tid; u < live * kUnits; u += T) {
+                const int t = u / kUnits, c = 8 * (u % kUnits);
+                if (col0 + c < limit)
+                    *reinterpret_cast<uint4*>(p.out + static_cast<std::int64_t>(pass + t) * p.out_stride + col0 + c) =
+                        *reinterpret_cast<const uint4*>(tile + t * kOutStride + c);
             }
         };
         switch ((live + 15) >> 4) {
