@@ -152,6 +152,12 @@ def test_moe_stages(backend, device, geometry, tokens):
     run_and_check(backend, device, geometry, tokens, seed=tokens + geometry.hidden_size)
 
 
+def test_moe_routing_in_several_batches(backend, device):
+    # 1100 tokens x top-8 = 8800 pairs: the routing kernel takes them in three
+    # batches of 4096 (ranks of the later ones parked between its passes).
+    run_and_check(backend, device, MoEGeometry(64, 16, 8, 32), 1100, seed=21)
+
+
 def test_moe_repeated_expert_ids(backend, device):
     run_and_check(backend, device, MoEGeometry(128, 8, 4, 64), 30, seed=9, duplicates=True)
 

@@ -424,90 +424,99 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
     }
 }
 
-// Routing: one workgroup. Pair i = token * top_k + position. Pass 1 counts
-// pairs per expert (LDS atomics give each pair a rank in its expert), a scan
-// gives segment offsets, pass 2 places every pair at offset + rank. Each pass
-// handles kRouteBatch pairs per thread with all loads issued up front.
+// Routing: one workgroup of kRouteThreads. Pair i = token * top_k + position.
+// Pass 1 counts pairs per expert (LDS atomics give each pair a rank in its
+// expert); wave 0 turns the counts into segment offsets (each lane sums a run
+// of experts, then a shuffle scan across the wave), and pass 2 places every
+// pair at offset + rank. A batch is kRouteBatch pairs per thread, loaded up
+// front; the first batch keeps its ids, scores and ranks in registers, later
+// batches (more than kRouteThreads * kRouteBatch pairs) park their ranks in
+// pair_slot between the passes. Three barriers for one batch.
+constexpr int kRouteThreads = 512;
 constexpr int kRouteBatch = 8;
 
-__global__ __launch_bounds__(1024) void moe_route(const std::int64_t* __restrict__ ids,
-                                                  const __half* __restrict__ scores, int pairs, int top_k,
-                                                  int experts, int* __restrict__ seg, int* __restrict__ status,
-                                                  int* __restrict__ pair_slot, int* __restrict__ slot_token,
-                                                  __half* __restrict__ slot_score) {
+__global__ __launch_bounds__(kRouteThreads) void moe_route(const std::int64_t* __restrict__ ids,
+                                                           const __half* __restrict__ scores, int pairs, int top_k,
+                                                           int experts, int* __restrict__ seg,
+                                                           int* __restrict__ status, int* __restrict__ pair_slot,
+                                                           int* __restrict__ slot_token,
+                                                           __half* __restrict__ slot_score) {
+    constexpr int T = kRouteThreads, B = kRouteBatch;
     __shared__ int count[kMaxExperts];
-    __shared__ int scan[kMaxExperts];
+    __shared__ int base_of[kMaxExperts];
     __shared__ int invalid;
     const int tid = threadIdx.x;
-    for (int e = tid; e < experts; e += 1024) count[e] = 0;
+    // The first batch's ids and scores are requested before the counters are cleared.
+    std::int64_t first_e[B];
+    __half first_sc[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+        const int i = min(u * T + tid, pairs - 1);
+        first_e[u] = ids[i];
+        first_sc[u] = scores[i];
+    }
+    for (int e = tid; e < experts; e += T) count[e] = 0;
     if (tid == 0) invalid = 0;
     __syncthreads();
-    // Ranks of the first batch stay in registers; later batches (more than
-    // 1024 * kRouteBatch pairs) keep theirs in pair_slot between the passes.
-    int first_rank[kRouteBatch];
-    std::int64_t first_e[kRouteBatch];
-    __half first_sc[kRouteBatch];  // the first batch's scores, fetched with its ids
-    for (int base = 0; base < pairs; base += 1024 * kRouteBatch) {
-        std::int64_t e[kRouteBatch];
+    int first_rank[B];
+    for (int base = 0; base < pairs; base += T * B) {
+        std::int64_t e[B];
 #pragma unroll
-        for (int u = 0; u < kRouteBatch; ++u) e[u] = ids[min(base + u * 1024 + tid, pairs - 1)];
-        if (base == 0) {
+        for (int u = 0; u < B; ++u) e[u] = base == 0 ? first_e[u] : ids[min(base + u * T + tid, pairs - 1)];
 #pragma unroll
-            for (int u = 0; u < kRouteBatch; ++u) first_sc[u] = scores[min(u * 1024 + tid, pairs - 1)];
-        }
-#pragma unroll
-        for (int u = 0; u < kRouteBatch; ++u) {
-            const int i = base + u * 1024 + tid;
+        for (int u = 0; u < B; ++u) {
+            const int i = base + u * T + tid;
             int rank = -1;
             if (i < pairs) {
-                if (e[u] < 0 || e[u] >= experts) {
-                    atomicAdd(&invalid, 1);
-                } else {
-                    rank = atomicAdd(&count[e[u]], 1);
-                }
+                if (e[u] < 0 || e[u] >= experts) atomicAdd(&invalid, 1);
+                else rank = atomicAdd(&count[e[u]], 1);
                 if (base > 0) pair_slot[i] = rank;
             }
-            if (base == 0) {
-                first_rank[u] = rank;
-                first_e[u] = e[u];
-            }
+            if (base == 0) first_rank[u] = rank;
         }
     }
     __syncthreads();
-    // Inclusive Hillis-Steele scan over the expert counts (experts <= 1024).
-    for (int e = tid; e < experts; e += 1024) scan[e] = count[e];
-    __syncthreads();
-    for (int d = 1; d < experts; d <<= 1) {
-        int add = 0;
-        if (tid < experts && tid >= d) add = scan[tid - d];
-        __syncthreads();
-        if (tid < experts) scan[tid] += add;
-        __syncthreads();
-    }
-    for (int e = tid; e < experts; e += 1024) seg[e + 1] = scan[e];
-    if (tid == 0) {
-        seg[0] = 0;
-        *status = invalid;
-    }
-    for (int base = 0; base < pairs; base += 1024 * kRouteBatch) {
-        int rank[kRouteBatch];
-        std::int64_t e[kRouteBatch];
-        __half sc[kRouteBatch];
+    if (tid < 64) {
+        const int run = (experts + 63) / 64;
+        const int lo = min(tid * run, experts), hi = min(lo + run, experts);
+        int own = 0;
+        for (int e = lo; e < hi; ++e) own += count[e];
+        int inclusive = own;
 #pragma unroll
-        for (int u = 0; u < kRouteBatch; ++u) {
-            const int i = min(base + u * 1024 + tid, pairs - 1);
+        for (int d = 1; d < 64; d <<= 1) {
+            const int other = __shfl_up(inclusive, d, 64);
+            if (tid >= d) inclusive += other;
+        }
+        int offset = inclusive - own;
+        for (int e = lo; e < hi; ++e) {
+            base_of[e] = offset;
+            offset += count[e];
+            seg[e + 1] = offset;
+        }
+        if (tid == 0) {
+            seg[0] = 0;
+            *status = invalid;
+        }
+    }
+    __syncthreads();
+    for (int base = 0; base < pairs; base += T * B) {
+        int rank[B];
+        std::int64_t e[B];
+        __half sc[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int i = min(base + u * T + tid, pairs - 1);
             rank[u] = base == 0 ? first_rank[u] : pair_slot[i];
             e[u] = base == 0 ? first_e[u] : ids[i];
             sc[u] = base == 0 ? first_sc[u] : scores[i];
         }
 #pragma unroll
-        for (int u = 0; u < kRouteBatch; ++u) {
-            const int i = base + u * 1024 + tid;
+        for (int u = 0; u < B; ++u) {
+            const int i = base + u * T + tid;
             if (i < pairs) {
                 int slot = -1;
                 if (rank[u] >= 0) {
-                    const int ex = static_cast<int>(e[u]);
-                    slot = scan[ex] - count[ex] + rank[u];
+                    slot = base_of[e[u]] + rank[u];
                     slot_token[slot] = i / top_k;
                     slot_score[slot] = sc[u];
                 }
@@ -1178,8 +1187,8 @@ void moe_q4_launch_cfg(const void* x, const std::int64_t* ids, const void* score
     auto* v = reinterpret_cast<__half*>(ws + l.v);
     const int pairs = tokens * top_k;
 
-    moe_route<<<1, 1024, 0, stream>>>(ids, static_cast<const __half*>(scores), pairs, top_k, experts, seg, status,
-                                      pair_slot, slot_token, slot_score);
+    moe_route<<<1, kRouteThreads, 0, stream>>>(ids, static_cast<const __half*>(scores), pairs, top_k, experts, seg,
+                                               status, pair_slot, slot_token, slot_score);
 
     // Tiled planes: gate/up has ceil(inter/64) row tiles, down ceil(hidden/128);
     // chunks of 256 columns over the padded K.
