@@ -146,6 +146,7 @@ def run_and_check(backend, device, geometry, tokens, seed, duplicates=False):
         (MoEGeometry(136, 6, 3, 72), 37),
         (MoEGeometry(512, 8, 2, 200), 1),
         (MoEGeometry(384, 24, 8, 256), 300),
+        (MoEGeometry(128, 8, 2, 1032), 40),  # down K of five 256-column chunks, the last one ragged
     ],
 )
 def test_moe_stages(backend, device, geometry, tokens):
