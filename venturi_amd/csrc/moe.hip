@@ -205,9 +205,106 @@ struct Q4Tiled {
     const __half* score;        // per-slot fp16 factor (kScore)
     __half* out;                // out[slot][out_stride]
     int n, k, chunks, x_stride, out_stride, experts, row_tiles, half_rows;
+    // Routing inside the gate/up launch (the ROUTE instantiation): each
+    // workgroup ranks its expert's pairs itself; seg and gather are not read.
+    const std::int64_t* ids;  // [pairs] expert ids
+    const __half* scores;     // [pairs]
+    int* seg_out;             // [experts + 1], written by part 0 of each expert
+    int* status;              // invalid-id count, written by expert 0's part 0
+    int* pair_slot;           // [pairs] (-1 for invalid ids)
+    int* slot_token;          // [pairs]
+    __half* slot_score;       // [pairs]
+    int pairs, top_k;
 };
 
 constexpr int kTileCodes = 8 * 128;  // uint4 per (tile, chunk): 8 row blocks x 2 KB
+
+// Largest pair count routed inside the gate/up launch (pair indices kept as
+// 16-bit entries of a 16 KB LDS list); larger calls run moe_route first.
+constexpr int kRouteList = 8192;
+
+// In-kernel routing of one expert (all threads of the workgroup call it):
+// pairs are ranked in pair order, so the expert's pair indices land in
+// plist[0, count) and its slots are begin .. begin + count - 1, with begin the
+// number of valid pairs of lower expert ids (the segments of moe_route, which
+// ranks inside a segment by atomic order instead; every (token, expert)
+// product is independent of its place in the segment). Part 0 of the expert
+// writes the routing tables the down GEMM and the combine read. Returns
+// (begin, begin + count).
+template <int W>
+__device__ int2 route_expert(const Q4Tiled& p, int expert, bool writer, unsigned short* plist, int* rsum, int tid,
+                             int lane, int wave) {
+    constexpr int T = W * 64, PER = 8;
+    int ranked = 0, below = 0, invalid = 0;
+    for (int base = 0; base < p.pairs; base += T * PER) {
+        const int i0 = base + PER * tid;
+        std::int64_t e[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) e[u] = p.ids[min(i0 + u, p.pairs - 1)];
+        int mine = 0, lo = 0, bad = 0;
+        unsigned bits = 0;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            if (i0 + u >= p.pairs) break;
+            const bool ok = e[u] >= 0 && e[u] < p.experts;
+            bad += !ok;
+            lo += ok && e[u] < expert;
+            if (e[u] == expert) {
+                bits |= 1u << u;
+                ++mine;
+            }
+            if (!ok && writer && expert == 0) p.pair_slot[i0 + u] = -1;
+        }
+        int incl = mine;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int other = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += other;
+        }
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            lo += __shfl_xor(lo, d, 64);
+            bad += __shfl_xor(bad, d, 64);
+        }
+        if (lane == 63) rsum[wave] = incl;
+        if (lane == 0) {
+            rsum[W + wave] = lo;
+            rsum[2 * W + wave] = bad;
+        }
+        __syncthreads();
+        int before = 0, total = 0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const int c = rsum[w];
+            before += w < wave ? c : 0;
+            total += c;
+            below += rsum[W + w];
+            invalid += rsum[2 * W + w];
+        }
+        int rank = ranked + before + incl - mine;
+#pragma unroll
+        for (int u = 0; u < PER; ++u)
+            if ((bits >> u) & 1u) plist[rank++] = static_cast<unsigned short>(i0 + u);
+        ranked += total;
+        __syncthreads();  // rsum is reused by the next batch; plist is whole after the last
+    }
+    if (writer) {
+        if (tid == 0) {
+            p.seg_out[expert + 1] = below + ranked;
+            if (expert == 0) {
+                p.seg_out[0] = 0;
+                *p.status = invalid;
+            }
+        }
+        for (int r = tid; r < ranked; r += T) {
+            const int i = plist[r], slot = below + r;
+            p.pair_slot[i] = slot;
+            p.slot_token[slot] = i / p.top_k;
+            p.slot_score[slot] = p.scores[i];
+        }
+    }
+    return make_int2(below, below + ranked);
+}
 
 // Grouped expert GEMM over the tiled planes with a fraction of an expert per
 // workgroup: W = 8 waves, wave v owns RB consecutive 16-row blocks (global
@@ -219,10 +316,12 @@ constexpr int kTileCodes = 8 * 128;  // uint4 per (tile, chunk): 8 row blocks x 
 // half has been multiplied, so each wave keeps RB KB in flight. Each
 // activation fragment is read from LDS once per step and multiplied by all RB
 // blocks. Passes of up to 16 * NBMAX tokens.
-template <int EPI, int W, int RB, int NBMAX>
+template <int EPI, int W, int RB, int NBMAX, bool ROUTE>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void q4_grouped(Q4Tiled p, int parts,
                                                                                                 int blocks) {
     __shared__ __attribute__((aligned(16))) _Float16 xl[2][16 * NBMAX * kXStride];
+    __shared__ unsigned short plist[ROUTE ? kRouteList : 1];
+    __shared__ int rsum[ROUTE ? 3 * W : 1];
     constexpr int kPass = 16 * NBMAX;
 
     const int linear = blockIdx.x;
@@ -235,13 +334,19 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
         expert = linear / parts;
         part = linear % parts;
     }
-    const int seg_begin = p.seg[expert];
-    const int seg_end = p.seg[expert + 1];
-    if (seg_begin >= seg_end) return;
-
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int seg_begin, seg_end;
+    if constexpr (ROUTE) {
+        const int2 range = route_expert<W>(p, expert, part == 0, plist, rsum, tid, lane, wave);
+        seg_begin = range.x;
+        seg_end = range.y;
+    } else {
+        seg_begin = p.seg[expert];
+        seg_end = p.seg[expert + 1];
+    }
+    if (seg_begin >= seg_end) return;
     const int q = lane >> 4, m = lane & 15;
     constexpr int T = W * 64;
     const int b0 = (part * W + wave) * RB;  // this wave's first row block
@@ -269,7 +374,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
                 const int t = (tid + T * j) >> 5;
                 xlive[j] = t < live && t < 16 * NB;
                 const int slot = pass + min(t, live - 1);
-                const int row = p.gather ? p.gather[slot] : slot;
+                const int row = ROUTE ? plist[slot - seg_begin] / p.top_k : p.gather ? p.gather[slot] : slot;
                 xrow[j] = p.x + static_cast<std::int64_t>(row) * p.x_stride;
             }
             struct Half {
@@ -607,11 +712,11 @@ void combine_dispatch(int top_k, const std::int64_t* ids, const int* pair_slot, 
     }
 }
 
-template <int EPI, int W, int RB, int NBMAX>
+template <int EPI, int W, int RB, int NBMAX, bool ROUTE = false>
 void launch_q4_grouped(const Q4Tiled& p, hipStream_t stream) {
     const int blocks = p.row_tiles * 8;
     const int parts = (blocks + W * RB - 1) / (W * RB);
-    q4_grouped<EPI, W, RB, NBMAX><<<dim3(p.experts * parts), W * 64, 0, stream>>>(p, parts, blocks);
+    q4_grouped<EPI, W, RB, NBMAX, ROUTE><<<dim3(p.experts * parts), W * 64, 0, stream>>>(p, parts, blocks);
 }
 
 std::uint64_t align256(std::uint64_t v) { return (v + 255) / 256 * 256; }
@@ -1187,8 +1292,12 @@ void moe_q4_launch_cfg(const void* x, const std::int64_t* ids, const void* score
     auto* v = reinterpret_cast<__half*>(ws + l.v);
     const int pairs = tokens * top_k;
 
-    moe_route<<<1, kRouteThreads, 0, stream>>>(ids, static_cast<const __half*>(scores), pairs, top_k, experts, seg,
-                                               status, pair_slot, slot_token, slot_score);
+    // Up to kRouteList pairs the gate/up launch routes its experts itself (one
+    // launch fewer); larger calls rank all pairs in moe_route first.
+    const bool route_inside = pairs <= kRouteList;
+    if (!route_inside)
+        moe_route<<<1, kRouteThreads, 0, stream>>>(ids, static_cast<const __half*>(scores), pairs, top_k, experts,
+                                                   seg, status, pair_slot, slot_token, slot_score);
 
     // Tiled planes: gate/up has ceil(inter/64) row tiles, down ceil(hidden/128);
     // chunks of 256 columns over the padded K.
@@ -1211,7 +1320,17 @@ void moe_q4_launch_cfg(const void* x, const std::int64_t* ids, const void* score
     gu.out_stride = inter;
     gu.experts = experts;
     gu.half_rows = inter;
-    launch_q4_grouped<kSwiGLU, GW, GRB, NBMAX>(gu, stream);
+    gu.ids = ids;
+    gu.scores = static_cast<const __half*>(scores);
+    gu.seg_out = seg;
+    gu.status = status;
+    gu.pair_slot = pair_slot;
+    gu.slot_token = slot_token;
+    gu.slot_score = slot_score;
+    gu.pairs = pairs;
+    gu.top_k = top_k;
+    if (route_inside) launch_q4_grouped<kSwiGLU, GW, GRB, NBMAX, true>(gu, stream);
+    else launch_q4_grouped<kSwiGLU, GW, GRB, NBMAX>(gu, stream);
 
     Q4Tiled dn{};
     dn.x = h;
