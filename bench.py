@@ -801,7 +801,8 @@ def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
     randperm(128); scores = softmax of 8 seeded N(0, 1) logits (fp32 -> fp16).
     Two independent banks (2 x 321 MB) alternate so that no step is served
     from the 256 MB Infinity Cache. One step = routing + gate/up GEMM with
-    SiLU*up + down GEMM with the score + ordered combine (four launches).
+    SiLU*up + down GEMM with the score + ordered combine (three launches: the gate/up launch
+    routes its experts itself at this pair count).
     Algorithmic bytes per step = expert planes + x + out + ids + scores;
     FLOPs = 2 * pairs * (2I*H + H*I). Parity against the reference's routed
     expert loop run with torch on this GPU (fp16(q*s) weights, fp16 linear).

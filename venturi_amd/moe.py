@@ -1,10 +1,12 @@
 """Routed-expert Q4 W4A16 MoE on gfx950.
 
 Replaces the reference's per-expert host loop (flash_next_q4.py:204-224,
-flash_next_moe.py:139-161) with four launches of libventuri_ops.so and no host
-synchronisation: device routing, a grouped gate/up GEMM with SiLU*up fused in
-its epilogue, a grouped down GEMM with the routing score fused in its
-epilogue, and a per-token combine in ascending expert order.
+flash_next_moe.py:139-161) with three launches of libventuri_ops.so and no
+host synchronisation: a grouped gate/up GEMM that routes its experts itself
+(each workgroup ranks its expert's pairs) with SiLU*up fused in its epilogue,
+a grouped down GEMM with the routing score fused in its epilogue, and a
+per-token combine in ascending expert order. Above 8192 pairs routing is a
+launch of its own before the GEMMs.
 
 Semantics per token (the reference's operation graph, fp16 boundaries):
 ``h = fp16(fp16(silu(gate)) * up)``, ``v = fp16(fp16(h @ Wd^T) * score)``,
