@@ -281,7 +281,8 @@ uint64_t venturi_moe_q4_bytes(int tokens, int top_k, int experts, int hidden, in
  * both in the tiled layout built by moe.Q4ExpertBank.upload (128-row x
  * 256-column tiles, gate/up rows paired per wave, nibbles stored as q + 8);
  * out fp16 [tokens][hidden]; workspace 256-byte aligned. Ids outside
- * [0, experts) are skipped and counted in the workspace status word. */
+ * [0, experts) are skipped and counted in the workspace status word, and the
+ * tokens that carry one get rows of NaN (no host synchronisation). */
 int venturi_moe_q4_run(const void* x, const int64_t* ids, const void* scores, const void* gate_up_codes,
                        const void* gate_up_scales, const void* down_codes, const void* down_scales, void* out,
                        void* workspace, uint64_t workspace_bytes, int tokens, int top_k, int experts, int hidden,
