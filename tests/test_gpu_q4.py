@@ -281,7 +281,7 @@ def test_status_codes_and_plugin_errors(backend, device):
     assert "null" in backend._native.error()
 
 
-@pytest.mark.parametrize("k", [1, 63, 64, 65, 129, 2048, 4097])
+@pytest.mark.parametrize("k", [1, 63, 64, 65, 129, 136, 2048, 4097])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_device_q4_pack_equals_rtn(backend, device, k, dtype):
     """venturi_q4_pack_run == quantize_q4_rtn (flash_next_q4.py:26-52) byte for byte."""

@@ -88,6 +88,36 @@ def test_impulse_last_column_and_nonfinite(backend, device):
         assert not torch.isfinite(out[0]).any() or bool(torch.isnan(out[0]).all())
 
 
+@pytest.mark.parametrize("k", [65, 136, 5120])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_embedding_run_rows(backend, device, k, dtype, offset):
+    # venturi_q8_embedding_run through the C ABI: rows code * scale rounded once,
+    # ids outside [0, vocab) give zero rows (blocks.cu:293-304); the 16-byte path
+    # (k % 8 == 0, aligned output) and the element path (k = 65, or an output one
+    # element past an aligned address), 8-byte aligned codes and codes one byte off.
+    vocab = 37
+    codes, scales = random_q8(vocab, k, 40 + k)
+    planes = codes.to(device)
+    padded = planes.shape[1]
+    store = torch.zeros(vocab * padded + 8, dtype=torch.int8, device=device)
+    store[offset:offset + vocab * padded] = planes.reshape(-1)
+    dsc = scales.to(device)
+    ids = torch.tensor([3, 36, 0, -1, 37, 17, 3], dtype=torch.int64, device=device)
+    buf = torch.full((ids.numel() * k + 8,), 7.0, dtype=dtype, device=device)
+    out = buf[offset:offset + ids.numel() * k]
+    lib = backend._native
+    dt = 0 if dtype == torch.float16 else 1
+    s = torch.cuda.current_stream(device).cuda_stream
+    backend._check(lib.venturi_q8_embedding_run(store.data_ptr() + offset, dsc.data_ptr(), ids.data_ptr(),
+                                                out.data_ptr(), ids.numel(), vocab, k, padded, dt, s))
+    dense = (codes.float() * scales.float().repeat_interleave(32, -1))[:, :k]
+    want = torch.stack([dense[i] if 0 <= i < vocab else torch.zeros(k) for i in ids.tolist()]).to(dtype)
+    assert torch.equal(out.cpu().view(ids.numel(), k), want)
+    tail = buf.cpu()[offset + ids.numel() * k:]
+    assert (tail == 7.0).all() and (buf.cpu()[:offset] == 7.0).all()
+
+
 def test_embedding_matches_decode(backend, device):
     codes, scales = random_q8(31, 65, 18)
     weight = Q8RowSplitWeight(codes, scales, 65)
@@ -101,7 +131,7 @@ def test_embedding_matches_decode(backend, device):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("shape", [(11, 1), (11, 31), (7, 65), (5, 129), (64, 4096)])
+@pytest.mark.parametrize("shape", [(11, 1), (11, 31), (7, 65), (5, 129), (9, 136), (64, 4096)])
 def test_device_pack_matches_from_dense(backend, device, dtype, shape):
     gen = torch.Generator().manual_seed(38 + shape[1])
     src = (torch.randn(*shape, generator=gen) * 0.01).to(dtype)

@@ -18,9 +18,46 @@
 namespace vt {
 namespace {
 
+// Eight consecutive source values as fp32 from one 16-byte load (two for fp32).
+__device__ __forceinline__ void load8(const __half* p, float (&v)[8]) {
+    const uint4 w = *reinterpret_cast<const uint4*>(p);
+    const std::uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = half_lo(u[i]);
+        v[2 * i + 1] = half_hi(u[i]);
+    }
+}
+__device__ __forceinline__ void load8(const __hip_bfloat16* p, float (&v)[8]) {
+    const uint4 w = *reinterpret_cast<const uint4*>(p);
+    const std::uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16_lo(u[i]);
+        v[2 * i + 1] = bf16_hi(u[i]);
+    }
+}
+__device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+
+// The 8 columns col .. col + 7 of a source row, zero past k. With `vec` (k % 8
+// == 0 and a 16-byte aligned source) the 8 columns are all inside or all past
+// k and come from one vector load; otherwise element by element.
+template <class T>
+__device__ __forceinline__ void row8(const T* __restrict__ row, int col, int k, bool vec, float (&v)[8]) {
+    if (vec && col < k) {
+        load8(row + col, v);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = col + i < k ? to_f32(row[col + i]) : 0.0f;
+}
+
 template <class T>
 __global__ __launch_bounds__(256) void q8_pack(const T* __restrict__ src, std::int8_t* __restrict__ codes,
-                                               __half* __restrict__ scales, int n, int k, int padded) {
+                                               __half* __restrict__ scales, int n, int k, int padded, bool vec) {
     // 4 lanes per group, 8 consecutive columns per lane.
     const int groups = padded >> 5;
     const std::int64_t index = (static_cast<std::int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 2;
@@ -29,8 +66,7 @@ __global__ __launch_bounds__(256) void q8_pack(const T* __restrict__ src, std::i
     const std::int64_t row = index / groups;
     const int col = static_cast<int>(index % groups) * 32 + sub * 8;
     float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = col + i < k ? to_f32(src[row * k + col + i]) : 0.0f;
+    row8(src + row * k, col, k, vec, v);
     float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
@@ -52,7 +88,7 @@ __global__ __launch_bounds__(256) void q8_pack(const T* __restrict__ src, std::i
 
 template <class T>
 __global__ __launch_bounds__(256) void q4_pack(const T* __restrict__ src, std::uint8_t* __restrict__ codes,
-                                               __half* __restrict__ scales, int n, int k, int padded) {
+                                               __half* __restrict__ scales, int n, int k, int padded, bool vec) {
     // 8 lanes per 64-column group, 8 consecutive columns (4 code bytes) per lane.
     const int groups = padded >> 6;
     const std::int64_t index = (static_cast<std::int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 3;
@@ -62,8 +98,7 @@ __global__ __launch_bounds__(256) void q4_pack(const T* __restrict__ src, std::u
     const int group = static_cast<int>(index % groups);
     const int col = group * 64 + sub * 8;
     float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = col + i < k ? to_f32(src[row * k + col + i]) : 0.0f;
+    row8(src + row * k, col, k, vec, v);
     float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
@@ -102,12 +137,13 @@ extern "C" __attribute__((visibility("default"))) int venturi_q4_pack_run(const 
         auto* c = static_cast<std::uint8_t*>(codes);
         auto* sc = static_cast<__half*>(scales);
         const unsigned grid = static_cast<unsigned>(blocks);
+        const bool vec = k % 8 == 0 && vt::aligned(src, 16);
         if (dtype == vt::kF16)
-            vt::q4_pack<<<grid, 256, 0, s>>>(static_cast<const __half*>(src), c, sc, n, k, padded);
+            vt::q4_pack<<<grid, 256, 0, s>>>(static_cast<const __half*>(src), c, sc, n, k, padded, vec);
         else if (dtype == vt::kBF16)
-            vt::q4_pack<<<grid, 256, 0, s>>>(static_cast<const __hip_bfloat16*>(src), c, sc, n, k, padded);
+            vt::q4_pack<<<grid, 256, 0, s>>>(static_cast<const __hip_bfloat16*>(src), c, sc, n, k, padded, vec);
         else if (dtype == vt::kF32)
-            vt::q4_pack<<<grid, 256, 0, s>>>(static_cast<const float*>(src), c, sc, n, k, padded);
+            vt::q4_pack<<<grid, 256, 0, s>>>(static_cast<const float*>(src), c, sc, n, k, padded, vec);
         else
             throw vt::Invalid("unsupported source dtype");
     });
@@ -126,13 +162,14 @@ extern "C" __attribute__((visibility("default"))) int venturi_q8_pack_run(const 
         vt::require(blocks <= INT32_MAX, "Q8 pack grid too large");
         auto s = static_cast<hipStream_t>(stream);
         auto* sc = static_cast<__half*>(scales);
+        const bool vec = k % 8 == 0 && vt::aligned(src, 16);
+        const unsigned grid = static_cast<unsigned>(blocks);
         if (dtype == vt::kF16)
-            vt::q8_pack<<<static_cast<unsigned>(blocks), 256, 0, s>>>(static_cast<const __half*>(src), codes, sc, n, k, padded);
+            vt::q8_pack<<<grid, 256, 0, s>>>(static_cast<const __half*>(src), codes, sc, n, k, padded, vec);
         else if (dtype == vt::kBF16)
-            vt::q8_pack<<<static_cast<unsigned>(blocks), 256, 0, s>>>(static_cast<const __hip_bfloat16*>(src), codes, sc,
-                                                                      n, k, padded);
+            vt::q8_pack<<<grid, 256, 0, s>>>(static_cast<const __hip_bfloat16*>(src), codes, sc, n, k, padded, vec);
         else if (dtype == vt::kF32)
-            vt::q8_pack<<<static_cast<unsigned>(blocks), 256, 0, s>>>(static_cast<const float*>(src), codes, sc, n, k, padded);
+            vt::q8_pack<<<grid, 256, 0, s>>>(static_cast<const float*>(src), codes, sc, n, k, padded, vec);
         else
             throw vt::Invalid("unsupported source dtype");
     });

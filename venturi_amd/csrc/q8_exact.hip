@@ -320,19 +320,61 @@ void launch_exact(const void* x, const std::int8_t* codes, const __half* scales,
     else launch_tile<T, 4, 2, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
 }
 
-__global__ void q8_embedding(const std::int8_t* codes, const __half* scales, const std::int64_t* ids,
-                             void* out, int dtype, std::int64_t count, int vocab, int k, int padded) {
+// One thread per 8 columns of a token's row (one scale covers them: 8 divides
+// 32): one 8-byte code load (byte loads when the codes are not 8-byte
+// aligned), one scale, and one 16-byte store when the output row allows it
+// (k % 8 == 0 and a 16-byte aligned output), else 2-byte stores. grid.y runs
+// over tokens.
+template <class T>
+__global__ __launch_bounds__(256) void q8_embedding(const std::int8_t* __restrict__ codes,
+                                                    const __half* __restrict__ scales,
+                                                    const std::int64_t* __restrict__ ids, T* __restrict__ out,
+                                                    int tokens, int vocab, int k, int padded, bool codes8,
+                                                    bool out16) {
     // Reference: blocks.cu:293-304 (ids outside [0, vocab) read as zero rows).
-    for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
-         i += static_cast<std::int64_t>(gridDim.x) * blockDim.x) {
-        const std::int64_t row = ids[i / k];
-        const int col = static_cast<int>(i % k);
-        const float v = (row >= 0 && row < vocab)
-                            ? static_cast<float>(codes[row * padded + col]) *
-                                  __half2float(scales[row * (padded / 32) + col / 32])
-                            : 0.0f;
-        if (dtype == kF16) static_cast<__half*>(out)[i] = from_f32<__half>(v);
-        else static_cast<__hip_bfloat16*>(out)[i] = from_f32<__hip_bfloat16>(v);
+    const int col = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (col >= k) return;
+    for (int t = blockIdx.y; t < tokens; t += gridDim.y) {
+        const std::int64_t row = ids[t];
+        float v[8];
+        if (row >= 0 && row < vocab) {
+            const std::int8_t* c = codes + row * padded + col;  // col + 8 <= padded
+            std::uint32_t lo, hi;
+            if (codes8) {
+                const uint2 w = *reinterpret_cast<const uint2*>(c);
+                lo = w.x;
+                hi = w.y;
+            } else {
+                lo = hi = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    lo |= static_cast<std::uint32_t>(static_cast<std::uint8_t>(c[i])) << (8 * i);
+                    hi |= static_cast<std::uint32_t>(static_cast<std::uint8_t>(c[4 + i])) << (8 * i);
+                }
+            }
+            const float scale = __half2float(scales[row * (padded / 32) + col / 32]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = sbyte(lo, i) * scale;
+                v[4 + i] = sbyte(hi, i) * scale;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        }
+        T* o = out + static_cast<std::int64_t>(t) * k + col;
+        if (out16 && col + 8 <= k) {
+            std::uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const T a = from_f32<T>(v[2 * i]), b = from_f32<T>(v[2 * i + 1]);
+                w[i] = static_cast<std::uint32_t>(__builtin_bit_cast(unsigned short, a)) |
+                       (static_cast<std::uint32_t>(__builtin_bit_cast(unsigned short, b)) << 16);
+            }
+            *reinterpret_cast<uint4*>(o) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+            for (int i = 0; i < 8 && col + i < k; ++i) o[i] = from_f32<T>(v[i]);
+        }
     }
 }
 
@@ -380,10 +422,16 @@ __attribute__((visibility("default"))) int venturi_q8_embedding_run(const std::i
         vt::require(codes && scales && ids && out, "null Q8 embedding operand");
         vt::require(tokens > 0 && vocab > 0 && k > 0 && padded == vt::padded_k(k), "invalid Q8 embedding geometry");
         vt::require(dtype == vt::kF16 || dtype == vt::kBF16, "Q8 supports FP16/BF16 activations");
-        const std::int64_t count = static_cast<std::int64_t>(tokens) * k;
-        const int grid = static_cast<int>(std::min<std::int64_t>((count + 255) / 256, 65535));
-        vt::q8_embedding<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(codes, scales, ids, out, dtype,
-                                                                            count, vocab, k, padded);
+        const dim3 grid((k + 2047) / 2048, std::min(tokens, 65535));
+        const bool codes8 = vt::aligned(codes, 8);
+        const bool out16 = k % 8 == 0 && vt::aligned(out, 16);
+        auto s = static_cast<hipStream_t>(stream);
+        if (dtype == vt::kF16)
+            vt::q8_embedding<<<grid, 256, 0, s>>>(codes, scales, ids, static_cast<__half*>(out), tokens, vocab, k,
+                                                  padded, codes8, out16);
+        else
+            vt::q8_embedding<<<grid, 256, 0, s>>>(codes, scales, ids, static_cast<__hip_bfloat16*>(out), tokens,
+                                                  vocab, k, padded, codes8, out16);
     });
 }
 
