@@ -71,3 +71,37 @@ def assert_free_order(stats, flip_fraction=0.02, over_fraction=0.01):
     assert stats["rel_l2"] <= 1e-3, stats
     assert stats["flips"] <= max(2, flip_fraction * stats["count"]), stats
     assert stats["over_2e-3"] <= max(2, over_fraction * stats["count"]), stats
+
+
+def near_tie_matrix(levels, group, rows, groups, seed):
+    """fp32 [rows, groups * group] whose quotients x / scale sit on or within
+    three fp32 ulps of half-integers, for the RTN rule scale = fp16(max|x| /
+    levels), code = rint(fl32(x / scale)).
+
+    Each group holds max|x| = fl32(levels * d) for an fp16 scale d (normal or
+    subnormal, non-power-of-two mantissas), so the stored scale is d; the other
+    values are (t + 1/2) d moved by -3..3 ulps, so about 6 in 7 of them take the
+    packers' division fallback and the rest are exact ties. (With an fp16
+    scale and |t| < 128, t d is exact in fp32 and any other fp32 x has |x / d -
+    t| >= ulp(x) / d > ulp(t) / 2, so fl32(x / d) is a half-integer only when
+    x / d is one.)
+    """
+    rng = np.random.default_rng(seed)
+    out = np.zeros((rows, groups * group), np.float32)
+    for r in range(rows):
+        for g in range(groups):
+            while True:
+                tiny = rng.random() < 0.15
+                d = np.float16(rng.integers(1, 1024) * 2.0**-24) if tiny else np.float16(rng.uniform(2.0**-12, 4.0))
+                amax = np.float32(levels * float(d))
+                if d > 0 and np.float16(amax / np.float32(levels)) == d:
+                    break
+            vals = [amax * (1 if rng.random() < 0.5 else -1)]
+            for _ in range(group - 1):
+                t = rng.integers(-levels, levels) + 0.5
+                x = np.float32(t * float(d))
+                for _ in range(abs(step := int(rng.integers(-3, 4)))):
+                    x = np.nextafter(x, np.float32(np.sign(step) * np.inf))
+                vals.append(x)
+            out[r, g * group:(g + 1) * group] = np.array(vals, np.float32)[rng.permutation(group)]
+    return out

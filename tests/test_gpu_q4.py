@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import bits
+from helpers import bits, near_tie_matrix
 from venturi_amd import Q4RowSplitWeight
 
 pytestmark = pytest.mark.gpu
@@ -293,6 +293,22 @@ def test_device_q4_pack_equals_rtn(backend, device, k, dtype):
     w[0] = 0  # all-zero row: scale floor 2^-24, codes 0
     if k >= 6:
         w[1, :6] = torch.tensor([7.0, 0.5, 1.5, 2.5, -0.5, -1.5]).to(dtype)  # ties
+    ref = quantize_q4_rtn(w)
+    got = backend.quantize_q4(w.to(device))
+    assert torch.equal(got.codes.cpu(), ref.codes)
+    assert torch.equal(got.scales.cpu().view(torch.int16), ref.scales.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("trim", [0, 5])
+def test_device_q4_pack_near_ties(backend, device, dtype, trim):
+    # Quotients x / scale on and within three fp32 ulps of half-integers, under
+    # normal and subnormal fp16 scales: the packer's reciprocal estimate leaves
+    # these to the IEEE division, and the codes equal quantize_q4_rtn's.
+    from venturi_amd import quantize_q4_rtn
+
+    print(f"case q4-pack-ties {dtype} trim={trim}", flush=True)
+    w = torch.from_numpy(near_tie_matrix(7, 64, 64, 4, 29 + trim))[:, : 256 - trim].contiguous().to(dtype)
     ref = quantize_q4_rtn(w)
     got = backend.quantize_q4(w.to(device))
     assert torch.equal(got.codes.cpu(), ref.codes)

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import bits, guarded_out, random_q8
+from helpers import bits, guarded_out, near_tie_matrix, random_q8
 from venturi_amd import Q8RowSplitWeight
 
 pytestmark = pytest.mark.gpu
@@ -146,6 +146,20 @@ def test_device_pack_matches_from_dense(backend, device, dtype, shape):
         bad = src.clone().to(device)
         bad[0, 0] = float("nan")
         backend.quantize_q8(bad)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("trim", [0, 5])
+def test_device_pack_near_ties(backend, device, dtype, trim):
+    # Quotients x / scale on and within three fp32 ulps of half-integers, under
+    # normal and subnormal fp16 scales: the packer's reciprocal estimate leaves
+    # these to the IEEE division, and the codes equal from_dense's (ties to even).
+    print(f"case q8-pack-ties {dtype} trim={trim}", flush=True)
+    src = torch.from_numpy(near_tie_matrix(127, 32, 64, 4, 17 + trim))[:, : 128 - trim].contiguous().to(dtype)
+    got = backend.quantize_q8(src.to(device))
+    want = Q8RowSplitWeight.from_dense(src)
+    assert torch.equal(got.codes.cpu(), want.codes)
+    assert torch.equal(got.scales.cpu().view(torch.int16), want.scales.view(torch.int16))
 
 
 @pytest.mark.parametrize("offset", [1, 2, 3, 4, 5, 8, 17])

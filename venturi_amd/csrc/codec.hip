@@ -55,6 +55,33 @@ __device__ __forceinline__ void row8(const T* __restrict__ row, int col, int k, 
     for (int i = 0; i < 8; ++i) v[i] = col + i < k ? to_f32(row[col + i]) : 0.0f;
 }
 
+// q[i] = rint(fl32(v[i] / d)) for 0 < d (the reference's fp32 division, then
+// round half to even), without a division per value. r is the hardware
+// reciprocal (1 ulp) refined by one Newton-Raphson step, r' = r + r (1 - d r),
+// whose relative error is under 2^-24 + 2^-45 (the square of the reciprocal's
+// plus one rounding); y = v * r' is then within |v/d| (2^-23 + 2^-44) of v/d,
+// and fl32(v/d) within half an fp32 ulp of it. When every y lies farther than
+// `guard` from the half-integers, each fl32(v/d) rounds as y does; otherwise
+// the thread takes the IEEE division for all 8. Only quotients that the clamp
+// does not decide matter (|v/d| < 8 for Q4, < 128 for Q8), where |y - fl32(v/d)|
+// stays under 1.5 * 2^-20 and 1.25 * 2^-16: the guards of 2^-17 and 2^-14 leave
+// margins above 5x and 3x. A NaN estimate (non-finite source) takes the division.
+__device__ __forceinline__ void rint_quotients(const float (&v)[8], float d, float guard, float (&q)[8]) {
+    const float r0 = __builtin_amdgcn_rcpf(d);
+    const float r = fmaf(r0, fmaf(-d, r0, 1.0f), r0);
+    bool near = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float y = v[i] * r;
+        q[i] = rintf(y);
+        near |= !(fabsf(y - q[i]) < 0.5f - guard);
+    }
+    if (near) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = rintf(__fdiv_rn(v[i], d));
+    }
+}
+
 template <class T>
 __global__ __launch_bounds__(256) void q8_pack(const T* __restrict__ src, std::int8_t* __restrict__ codes,
                                                __half* __restrict__ scales, int n, int k, int padded, bool vec) {
@@ -74,11 +101,12 @@ __global__ __launch_bounds__(256) void q8_pack(const T* __restrict__ src, std::i
     mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
     const __half stored = from_f32<__half>(__fdiv_rn(mx, 127.0f));
     const float d = __half2float(stored);
+    float qf[8];
+    rint_quotients(v, d > 0.0f ? d : 1.0f, 0x1p-14f, qf);
     std::uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        int q = 0;
-        if (d > 0.0f) q = static_cast<int>(fminf(fmaxf(rintf(__fdiv_rn(v[i], d)), -127.0f), 127.0f));
+        const int q = d > 0.0f ? static_cast<int>(fminf(fmaxf(qf[i], -127.0f), 127.0f)) : 0;
         const std::uint32_t byte = static_cast<std::uint32_t>(q & 0xff) << (8 * (i & 3));
         if (i < 4) lo |= byte; else hi |= byte;
     }
@@ -108,10 +136,12 @@ __global__ __launch_bounds__(256) void q4_pack(const T* __restrict__ src, std::u
     const bool live = group * 64 < k;
     const __half stored = live ? from_f32<__half>(fmaxf(__fdiv_rn(mx, 7.0f), 0x1p-24f)) : __float2half(0.0f);
     const float d = __half2float(stored);
+    float qf[8];
+    rint_quotients(v, live ? d : 1.0f, 0x1p-17f, qf);
     std::uint32_t word = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int q = live ? static_cast<int>(fminf(fmaxf(rintf(__fdiv_rn(v[i], d)), -7.0f), 7.0f)) : 0;
+        const int q = live ? static_cast<int>(fminf(fmaxf(qf[i], -7.0f), 7.0f)) : 0;
         word |= static_cast<std::uint32_t>(q & 15) << (4 * i);
     }
     *reinterpret_cast<std::uint32_t*>(codes + row * (padded / 2) + col / 2) = word;
