@@ -623,8 +623,15 @@ template <int NB, bool SWIGLU>
 void launch_tiled_shape(const TiledShape& sh, const __half* xp, const uint4* cp, const std::uint32_t* sp, __half* op,
                         unsigned long long* slots, int tokens, int n, int k, int chunks, int blocks,
                         hipStream_t stream) {
+    // Two token blocks with three row blocks need about 154 VGPRs, so one
+    // 8-wave workgroup fits a CU (8 waves) where three 4-wave ones do (12
+    // waves): grids past 512 workgroups take the 4-wave shape (config-5 gate+up
+    // at 32 tokens, 726 workgroups: model step 7.40 -> 7.25 ms). With one
+    // token block the 8-wave shape stays faster.
     if (sh.rb == 2 && sh.ks == 1)
         launch_tiled<8, 2, NB, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+    else if (NB == 2 && sh.rb == 3 && sh.ks == 1 && (blocks + 2) / 3 > 512)
+        launch_tiled<4, 3, NB, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else if (sh.rb == 3 && sh.ks == 1)
         launch_tiled<8, 3, NB, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else if (sh.rb == 3 && sh.ks == 2)
