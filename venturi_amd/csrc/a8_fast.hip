@@ -236,8 +236,6 @@ __global__ __launch_bounds__(WM * WN * 64) void a8_gemm_fast(const std::int8_t* 
 #pragma unroll
             for (int s = 0; s < SB; ++s) {
                 const int g = (c + 1) * SB + s;  // next stage's group
-                constexpr int kSlotBase = 0;
-                (void)kSlotBase;
                 if (g < groups) {
                     store(st[(cs * SB + SB + s) % PF], g % (2 * SB));
                     if (g + PF < groups) load(g + PF, st[(cs * SB + SB + s) % PF]);
