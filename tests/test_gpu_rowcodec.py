@@ -135,3 +135,47 @@ def test_q4_fused_research_plan(backend, device):
     backend._check(backend._native.venturi_q4_fused_run(x.data_ptr(), dc.data_ptr(), ds.data_ptr(), want.data_ptr(),
                                                         tokens, n, k, 256, 0, s))
     assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("fmt", ["q8_g32_fp16", "q4_g64_fp16", "q5_g64_fp16"])
+def test_plan_over_planes_read_from_safetensors(backend, device, tmp_path, fmt):
+    # The stored schema (docs/qwen-safetensors.md:45-58) feeds the plan table as
+    # read: Q8 A16 up to 32 tokens gives the canonical bytes, Q4/Q5 at k % 8 != 0
+    # the exact GEMVs' bytes (flash_next_q4.cu:23-34, flash_next_q5.cu:26-38).
+    from safetensors.torch import save_file
+    from venturi_amd.planes import planes_of, read_planes
+    from venturi_amd.weights import Q4RowSplitWeight, Q5RowSplitWeight, Q8RowSplitWeight
+
+    n, tokens = 37, 5
+    k = 300 if fmt == "q8_g32_fp16" else 130
+    print(f"case planes {fmt} n={n} k={k} tokens={tokens}", flush=True)
+    gen = torch.Generator().manual_seed(len(fmt) + k)
+    if fmt == "q8_g32_fp16":
+        weight = Q8RowSplitWeight.from_dense((torch.randn(n, k, generator=gen) * 0.02).half())
+        plan, bits_ = prepare_row_codec(8, 32), 8
+    else:
+        lo = -8 if fmt == "q4_g64_fp16" else -16
+        codes = torch.randint(lo, -lo, (n, k), generator=gen)
+        scales = (torch.rand(n, -(-k // 64), generator=gen) * 0.01).half()
+        cls = Q4RowSplitWeight if fmt == "q4_g64_fp16" else Q5RowSplitWeight
+        weight = cls.from_codes(codes, scales)
+        bits_ = 4 if fmt == "q4_g64_fp16" else 5
+        plan = prepare_row_codec(bits_, 64)
+    path = tmp_path / "planes.safetensors"
+    save_file(planes_of("model.mlp.proj", weight), str(path))
+    planes = read_planes(path, "model.mlp.proj", fmt, (n, k))
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(3)).half()
+    dx = x.to(device)
+    dc, ds = planes.codes.to(device), planes.scales.to(device)
+    dh = planes.high.to(device) if planes.high is not None else None
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    s = torch.cuda.current_stream(device).cuda_stream
+    plan.project(dx.data_ptr(), dc.data_ptr(), dh.data_ptr() if dh is not None else None, ds.data_ptr(),
+                 out.data_ptr(), None, 0, tokens=tokens, n=n, k=k, padded=planes.padded_k, stream=s)
+    if bits_ == 8:
+        expected = oracle.q8_linear(bits(x), planes.codes.numpy(), planes.scales.numpy(), k)
+    elif bits_ == 4:
+        expected = oracle.q4_linear(bits(x), planes.codes.numpy(), planes.scales.numpy(), k)
+    else:
+        expected = oracle.q5_linear(bits(x), planes.codes.numpy(), planes.high.numpy(), planes.scales.numpy(), k)
+    np.testing.assert_array_equal(bits(out), expected)
