@@ -11,8 +11,10 @@
  *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream);
  *   - no entry point allocates device memory or synchronises; all buffers are
  *     caller-owned. Launches are graph-capturable.
- * Alignment: Q8 codes and A8 workspaces 16 bytes; fp16/bf16 operands 2 bytes
- * (the reference accepts unaligned Q8 codes; this library requires 16).
+ * Alignment: venturi_q8_head_run and venturi_q8_embedding_run take Q8 codes
+ * at any address, as the reference does (a row-offset view of a plane); the
+ * matrix-core Q8 entry points, the A8 projections and their workspaces need
+ * 16-byte codes and workspaces; fp16/bf16 operands 2 bytes.
  */
 #ifndef VENTURI_OPS_H
 #define VENTURI_OPS_H
