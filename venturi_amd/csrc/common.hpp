@@ -121,9 +121,16 @@ __device__ __forceinline__ float swiglu_value(float x, float y) {
     return __fmul_rn(__fmul_rn(x, sigmoid), y);
 }
 
-// Cross-lane read of `v` from lane (lane + delta) within a 64-lane wave.
-__device__ __forceinline__ float lane_down(float v, int delta) {
-    return __shfl_down(v, delta, 64);
+// v from lane (lane + N) of the same 16-lane row (DPP row_shl:N; lanes whose
+// source lies past the row read 0).
+template <int N>
+__device__ __forceinline__ float row_shl(float v) {
+    static_assert(N >= 1 && N <= 15, "DPP row shifts move 1..15 lanes");
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x100 + N, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
 // The reference's 256-thread reduction (cuda_common.cuh:38-51, block_sum)
@@ -133,18 +140,22 @@ __device__ __forceinline__ float lane_down(float v, int delta) {
 // t = 4*(lane%8) + v, i.e. lane offsets +4, +2, +1 and then register pairs
 // (+2, +1). The eight group sums are then reduced by the same tree run over
 // 32 lanes of which only 0..7 are nonzero: the +16 and +8 steps add exact
-// zeros, the +4/+2/+1 steps pair group sums (lane offsets 32, 16, 8 here).
-// The result is valid in lane 0.
+// zeros, the +4/+2/+1 steps pair group sums g + 4, then + 2, then + 1 (held
+// in lanes 8g). The lane offsets +4/+2/+1 stay inside a 16-lane row, so they
+// are DPP row shifts (the lanes that feed the group sums read only lanes of
+// their own group); the eight group sums are read into scalars and paired in
+// the tree's order. Every addition is the reference's, in its order, so the
+// bits are the same. Returns the same value in every lane; all lanes of the
+// wave must call it together.
 __device__ __forceinline__ float canonical_sum(float a0, float a1, float a2, float a3) {
-    a0 += lane_down(a0, 4); a1 += lane_down(a1, 4); a2 += lane_down(a2, 4); a3 += lane_down(a3, 4);
-    a0 += lane_down(a0, 2); a1 += lane_down(a1, 2); a2 += lane_down(a2, 2); a3 += lane_down(a3, 2);
-    a0 += lane_down(a0, 1); a1 += lane_down(a1, 1); a2 += lane_down(a2, 1); a3 += lane_down(a3, 1);
+    a0 += row_shl<4>(a0); a1 += row_shl<4>(a1); a2 += row_shl<4>(a2); a3 += row_shl<4>(a3);
+    a0 += row_shl<2>(a0); a1 += row_shl<2>(a1); a2 += row_shl<2>(a2); a3 += row_shl<2>(a3);
+    a0 += row_shl<1>(a0); a1 += row_shl<1>(a1); a2 += row_shl<1>(a2); a3 += row_shl<1>(a3);
     float p = (a0 + a2) + (a1 + a3);
     p = (p + 0.0f) + 0.0f;
-    p += lane_down(p, 32);
-    p += lane_down(p, 16);
-    p += lane_down(p, 8);
-    return p;
+    const float g04 = lane_value(p, 0) + lane_value(p, 32), g26 = lane_value(p, 16) + lane_value(p, 48);
+    const float g15 = lane_value(p, 8) + lane_value(p, 40), g37 = lane_value(p, 24) + lane_value(p, 56);
+    return (g04 + g26) + (g15 + g37);
 }
 
 // 32-lane shfl_down 16/8/4/2/1 tree (one reference warp per half-wave);
