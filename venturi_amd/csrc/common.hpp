@@ -159,13 +159,16 @@ __device__ __forceinline__ float canonical_sum(float a0, float a1, float a2, flo
 }
 
 // 32-lane shfl_down 16/8/4/2/1 tree (one reference warp per half-wave);
-// valid in lanes 0 and 32.
+// valid in lanes 0 and 32. The +16 step crosses a 16-lane row (one LDS
+// permute); the +8/+4/+2/+1 steps that lanes 0 and 32 depend on read only
+// lanes of their own row, so they are DPP row shifts. Same additions, same
+// order. All lanes of the wave must call it together.
 __device__ __forceinline__ float warp32_sum(float v) {
     v += __shfl_down(v, 16, 32);
-    v += __shfl_down(v, 8, 32);
-    v += __shfl_down(v, 4, 32);
-    v += __shfl_down(v, 2, 32);
-    v += __shfl_down(v, 1, 32);
+    v += row_shl<8>(v);
+    v += row_shl<4>(v);
+    v += row_shl<2>(v);
+    v += row_shl<1>(v);
     return v;
 }
 
