@@ -29,7 +29,8 @@ materialised weights) on a bounded sample of the same workload. Further
 sections of the same line carry their own roofline objects: `config1`
 (4096 x 4096 at one token, rotated copies), `vocab_head`
 (the 248 320 x 5120 Q8 head held once in the tiled layout), `q4_decode`
-(the metric's Q4 leg), `q56_decode`, `codecs`, `prefill_a8` (config 3),
+(the metric's Q4 leg), `q56_decode`, `codecs`, `a8_decode` (the A8 path at
+1 and 8 tokens, one and two passes), `prefill_a8` (config 3),
 `prefill_a16` (W8A16 / W4A16 at M = 2048), `moe_w4a16` (config 4) and
 `model_decode` (config 5).
 """
@@ -83,7 +84,7 @@ def parse():
     p.add_argument("--no-moe", action="store_true", help="skip the config-4 routed-expert MoE section")
     p.add_argument("--no-model", action="store_true", help="skip the config-5 64-layer decode section")
     p.add_argument("--only", default=None,
-                   help="comma-separated sections to run (config2,config1,head,q4,q56,codecs,a8,a16,moe,model); "
+                   help="comma-separated sections to run (config2,config1,head,q4,q56,codecs,a8dec,a8,a16,moe,model); "
                    "without config2 no headline metric is printed (for counter runs)")
     p.add_argument("--eager", action="store_true",
                    help="time config-2 launches issued from Python instead of HIP-graph replays (for counter runs)")
@@ -532,6 +533,64 @@ def prefill_a8(backend, device, steps, warmup, cpu_seconds):
             f"(the reference has no CPU int8 GEMM); {cpu_description(threads)}",
         }
     return result
+
+
+def a8_decode(backend, device, steps, warmup, copy_mb, tokens_list=(1, 8)):
+    """The A8 path at decode token counts (the reference's V100 benchmark case,
+    benchmarks/v100-q8-dp4a/summary.md:101-110): the config-2 projection set,
+    M in {1, 8}, one pass and two (the residual profile). Each launch quantizes
+    the fp16 activations into the plan's workspace and runs the W8A8 projection
+    (route auto: the reference-order kernel below 64 tokens), rotating >=
+    `copy_mb` MB of weight copies in one HIP graph per group, as the Q8 decode.
+    Algorithmic bytes per launch = N*Kp*(1 + 2/32) weights + M*K*2 activations +
+    2 * M*ceil(K/32)*36*passes workspace (written, read) + M*N*2 outputs.
+    """
+    from venturi_amd import prepare_q8_dp4a
+
+    copies = q8_copies(backend, device, PROJECTIONS, copy_mb, 9000)
+    gen = torch.Generator(device=device).manual_seed(23)
+    xs = {m: {k: torch.randn(m, k, generator=gen, device=device).half() for k in {p[2] for p in PROJECTIONS}}
+          for m in tokens_list}
+    groups, nbytes, route = {}, {}, None
+    for passes in (1, 2):
+        for m in tokens_list:
+            for pi, (name, n, k) in enumerate(PROJECTIONS):
+                plans = [prepare_q8_dp4a(r, tokens=m, residual_compensation=passes == 2) for r in copies[pi]]
+                route = plans[0].route
+                ws = torch.empty(plans[0].workspace_bytes, dtype=torch.uint8, device=device)
+                out = torch.empty(m, n, dtype=torch.float16, device=device)
+                x = xs[m][k]
+
+                def run(reps, plans=plans, x=x, out=out, ws=ws):
+                    for r in range(reps):
+                        plans[r % len(plans)].run(x, out=out, workspace=ws)
+
+                def verify(plans=plans, x=x, out=out, ws=ws):
+                    ref = torch.empty_like(out)
+                    plans[(steps - 1) % len(plans)].run(x, out=ref, workspace=ws)
+                    torch.cuda.synchronize(out.device)
+                    return torch.equal(ref.view(torch.int16), out.view(torch.int16))
+
+                key = (passes, m, name)
+                groups[key] = (run, verify)
+                nbytes[key] = launch_bytes(m, n, k) + 2 * m * -(-k // 32) * 36 * passes
+    seconds, wall, same = graph_timing(groups, steps, warmup, device)
+    detail, total = {}, 0
+    for (passes, m, name), t in seconds.items():
+        b = steps * nbytes[(passes, m, name)]
+        total += b
+        detail[f"{name}_m{m}_p{passes}"] = {"us": round(t / steps * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+    achieved = total / sum(seconds.values()) / 1e9
+    return {
+        "workload": "A8 decode: config-2 projection set, M in {1, 8}, 1 and 2 passes (quantize + W8A8 projection)",
+        "route": route,
+        "GB/s": round(total / wall / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": "a8 quantize + reference-order W8A8 projection",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4)},
+        "graph_equals_eager": same,
+        "per_launch": detail,
+    }
 
 
 # ---------------------------------------------------------------- A16 prefill
@@ -1066,6 +1125,10 @@ def main():
     if wanted("codecs"):
         log("row-codec pack/unpack on the device")
         result["codecs"] = codecs(backend, device, max(args.steps // 2, 3), 2)
+    if wanted("a8dec", args.no_prefill):
+        log("A8 decode at the config-2 shapes")
+        result["a8_decode"] = a8_decode(backend, device, args.steps, args.warmup, args.copy_mb)
+    torch.cuda.empty_cache()
     if wanted("a8", args.no_prefill):
         log("config-3 A8 prefill")
         result["prefill_a8"] = prefill_a8(backend, device, max(args.steps // 2, 3), 2, 0 if args.no_cpu else 6.0)
