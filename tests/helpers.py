@@ -80,8 +80,9 @@ def near_tie_matrix(levels, group, rows, groups, seed):
 
     Each group holds max|x| = fl32(levels * d) for an fp16 scale d (normal or
     subnormal, non-power-of-two mantissas), so the stored scale is d; the other
-    values are (t + 1/2) d moved by -3..3 ulps, so about 6 in 7 of them take the
-    packers' division fallback and the rest are exact ties. (With an fp16
+    values are (t + 1/2) d moved by -3..3 ulps (one in seven an exact tie), so
+    nearly all of them lie inside the packers' guard band around half-integers
+    and take the IEEE division. (With an fp16
     scale and |t| < 128, t d is exact in fp32 and any other fp32 x has |x / d -
     t| >= ulp(x) / d > ulp(t) / 2, so fl32(x / d) is a half-integer only when
     x / d is one.)
