@@ -599,7 +599,10 @@ def a8_decode(backend, device, steps, warmup, copy_mb, tokens_list=(1, 8)):
 def prefill_a16(backend, device, steps, warmup):
     """fp16-activation prefill GEMMs at the config-2 shapes, M = 2048 (the metric's
     "fp16 TOPS (M >= 256)" leg): W8A16 (q8_g32, venturi_q8_prefill_run) and W4A16
-    (q4_g64, venturi_row_gemm_run), both on their plans' auto route.
+    (q4_g64), both on their plans' auto route. W4A16's auto route at 2048 tokens
+    is the dense one (venturi_row_dense_run: fp16 shadow chunks + hipBLASLt, the
+    reference's ChunkedDense form); the fused matrix-core kernel
+    (venturi_q4_gemm_run) is timed beside it as `fused_mfma_us`.
 
     Weights N(0, 0.02) packed on the device; x fp16 N(0, 1). Each GEMM runs
     `steps` times back to back between one pair of events; TFLOP/s =
@@ -623,7 +626,14 @@ def prefill_a16(backend, device, steps, warmup):
             route = plan.route
             x = torch.randn(m, k, generator=gen, device=device).half()
             out = torch.empty(m, n, dtype=torch.float16, device=device)
-            t = event_time(lambda: plan.run(x, out=out), steps, warmup, stream)
+            ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device) if plan.workspace_bytes else None
+            kw = {} if ws is None else {"workspace": ws}
+            t = event_time(lambda: plan.run(x, out=out, **kw), steps, warmup, stream)
+            fused_us = None
+            if route == "venturi-q4-dense":  # the hand-written fused kernel on the same weights, for comparison
+                fused = resident.prepare(tokens=m, route="mfma")
+                fused_us = round(event_time(lambda: fused.run(x, out=out), steps, warmup, stream) * 1e6, 1)
+                plan.run(x, out=out, **kw)
             if codec == "w8a16":
                 ref = torch.empty_like(out)
                 resident.prepare(tokens=m, route="exact").run(x, out=ref)
@@ -639,10 +649,13 @@ def prefill_a16(backend, device, steps, warmup):
             total_s += t
             stages[name] = {"us": round(t * 1e6, 1), "TFLOP/s": round(flops / t / 1e12, 1),
                             "frac_fp16_peak": round(flops / t / 1e12 / FP16_PEAK_TFLOPS, 4)}
-            del resident, plan, x, out, ref
+            if fused_us is not None:
+                stages[name]["fused_mfma_us"] = fused_us
+            del resident, plan, x, out, ref, ws
         tf = total_flops / total_s / 1e12
         sections[codec] = {"route": route, "TFLOP/s": round(tf, 1),
-                           "roofline": {"bound": "mfma", "kernel": "q8_prefill" if codec == "w8a16" else "row_prefill",
+                           "roofline": {"bound": "mfma", "kernel": "q8_prefill" if codec == "w8a16" else
+                                        "row_decode + hipBLASLt GEMM" if route == "venturi-q4-dense" else "row_prefill",
                                         "achieved": round(tf, 1), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                         "frac": round(tf / FP16_PEAK_TFLOPS, 4)},
                            "parity": {"against": "canonical-order route" if codec == "w8a16" else
@@ -1134,7 +1147,7 @@ def main():
         result["prefill_a8"] = prefill_a8(backend, device, max(args.steps // 2, 3), 2, 0 if args.no_cpu else 6.0)
     if wanted("a16", args.no_prefill):
         log("fp16-activation prefill GEMMs (W8A16, W4A16)")
-        result["prefill_a16"] = prefill_a16(backend, device, max(args.steps // 4, 3), 1)
+        result["prefill_a16"] = prefill_a16(backend, device, max(args.steps // 2, 3), 2)
     torch.cuda.empty_cache()
     if wanted("moe", args.no_moe):
         log("config-4 routed-expert MoE")

@@ -9,8 +9,9 @@
  *   - `padded` must equal ceil(k/128)*128; Q8 codes are int8 [n][padded],
  *     Q8 scales fp16 [n][padded/32];
  *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream);
- *   - no entry point allocates device memory or synchronises; all buffers are
- *     caller-owned. Launches are graph-capturable.
+ *   - no entry point allocates device memory or synchronises (except the first
+ *     call of venturi_row_dense_run per device and shape, which sets up
+ *     hipBLASLt); all buffers are caller-owned. Launches are graph-capturable.
  * Alignment: venturi_q8_head_run and venturi_q8_embedding_run take Q8 codes
  * at any address, as the reference does (a row-offset view of a plane); the
  * matrix-core Q8 entry points, the A8 projections and their workspaces need
@@ -273,6 +274,22 @@ int venturi_row_tiled_run(const void* x, const void* codes, const void* high, co
 int venturi_row_gemm_run(const void* x, const void* codes, const void* high, const void* scales, void* out, int tokens,
                          int n, int k, int padded, int bits, int dtype, void* stream);
 
+/* The reference's ChunkedDense W*A16 projection for q4/q5/q6_g64 (admitted by
+ * row_codec_dispatch.cuh:41-48, run by row_dense_project,
+ * qwen_runtime.cuh:348-364): chunks of rows are decoded to fp16(q*scale) into
+ * the workspace and multiplied by one hipBLASLt GEMM each (fp16 operands, fp32
+ * accumulation), written straight into out's columns. fp16 activations only;
+ * k % 8 == 0, n % 8 == 0; x and out 16-byte aligned, workspace 256-byte
+ * aligned. venturi_row_dense_workspace_bytes gives the workspace of the
+ * preferred chunking (0 on invalid geometry); a smaller one (at least 32 MiB
+ * plus 16 rows of the shadow) runs in smaller chunks. The first call per
+ * (device, shape) creates hipBLASLt state (it allocates: not under graph
+ * capture); later calls allocate nothing. */
+uint64_t venturi_row_dense_workspace_bytes(int tokens, int n, int k);
+int venturi_row_dense_run(const void* x, const void* codes, const void* high, const void* scales, void* out,
+                          int tokens, int n, int k, int padded, int bits, int dtype, void* workspace,
+                          uint64_t workspace_bytes, void* stream);
+
 /* Extension: workspace bytes of venturi_moe_q4_run (0 on invalid geometry). */
 uint64_t venturi_moe_q4_bytes(int tokens, int top_k, int experts, int hidden, int inter);
 
@@ -319,8 +336,11 @@ typedef struct VRCPlan {
 int venturi_rowcodec_prepare(int bits, int group, int precision, int dtype, int implementation, VRCPlan* plan);
 
 /* Workspace of venturi_rowcodec_project for `tokens` rows of K = k: the A8
- * activation pack for quantized plans (venturi_q8_dp4a_bytes), 0 otherwise
- * (and 0 with a message for an invalid plan). */
+ * activation pack for quantized plans (venturi_q8_dp4a_bytes); for fp16
+ * ChunkedDense plans at 1024 tokens or more, the dense route's fixed buffer
+ * (224 MiB: hipBLASLt's 32 MiB and the fp16 shadow, see venturi_row_dense_run;
+ * with less, those plans run the fused matrix-core GEMM); 0 otherwise (and 0
+ * with a message for an invalid plan). */
 uint64_t venturi_rowcodec_workspace_bytes(const VRCPlan* plan, int tokens, int k);
 
 /* One matrix of Model::project: out [tokens][n] = x [tokens][k] times the

@@ -1,0 +1,202 @@
+"""The dense W*A16 route (venturi_row_dense_run), the reference's ChunkedDense
+projection (row_codec_dispatch.cuh:41-48, qwen_runtime.cuh:348-364): rows are
+decoded to the contract's fp16(q*scale) weights in the workspace and multiplied
+by hipBLASLt with fp32 accumulation. Outputs are checked against the FP64
+product of the oracle's decoded weights (half an fp16 ulp plus 2^-19 of the
+absolute product, the bound every W*A16 route here meets) and, at the
+config-2 gate+up shape, against the fp32 product of the same weights within
+max(2e-3, 1 fp16 ulp); chunked and whole runs, the Q4 plan's auto route and
+the native plan table are covered, and every run is repeated for determinism.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import agreement, assert_free_order, ulp16
+from venturi_amd.q4 import DENSE_TOKENS
+from venturi_amd.rowcodec import prepare_row_codec
+from venturi_amd.weights import Q4RowSplitWeight
+
+pytestmark = pytest.mark.gpu
+
+BLAS_BYTES = 32 * 2**20
+
+
+def _planes(n, k, nbits, seed):
+    padded = (k + 127) // 128 * 128
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(-(1 << (nbits - 1)), 1 << (nbits - 1), size=(n, padded))
+    codes[:, k:] = 0
+    scales = (rng.random((n, padded // 64)) * 0.02).astype(np.float16)
+    return oracle.pack_row_codec(codes, scales, nbits)
+
+
+def _bound_check(got, x, packed, high, scales, k, nbits, rows=None, tokens=None):
+    """FP64 contract bound on the (tokens x rows) sample of the output."""
+    rows = np.arange(packed.shape[0]) if rows is None else rows
+    tokens = np.arange(x.shape[0]) if tokens is None else tokens
+    wd = oracle.row_decode(packed[rows], high[rows], scales[rows], k, nbits).view(np.float16).astype(np.float64)
+    xd = x[tokens].float().numpy().astype(np.float64)
+    exact = xd @ wd.T
+    sample = got[np.ix_(tokens, rows)].astype(np.float64)
+    bound = 0.5 * ulp16(exact) + 2.0**-19 * (np.abs(xd) @ np.abs(wd).T)
+    assert (np.abs(sample - exact) <= bound).all()
+    return wd, xd
+
+
+def _device_planes(packed, high, scales, nbits, device):
+    dc = torch.from_numpy(packed).to(device)
+    dh = torch.from_numpy(high if nbits > 4 else np.zeros((1, 16), np.uint8)).to(device)
+    ds = torch.from_numpy(scales).to(device)
+    return dc, dh, ds
+
+
+def _run(lib, backend, x, dc, dh, ds, out, tokens, n, k, padded, nbits, ws, size, s):
+    backend._check(lib.venturi_row_dense_run(x.data_ptr(), dc.data_ptr(), dh.data_ptr(), ds.data_ptr(), out.data_ptr(),
+                                             tokens, n, k, padded, nbits, 0, ws.data_ptr(), size, s))
+
+
+@pytest.mark.parametrize("nbits", [4, 5, 6])
+@pytest.mark.parametrize("shape,tokens", [((200, 264), 37), ((64, 512), 1), ((1032, 136), 300), ((256, 5120), 1024)])
+@pytest.mark.parametrize("chunk", [None, 48])
+def test_dense_contract(backend, device, nbits, shape, tokens, chunk):
+    # chunk None: the preferred workspace (these matrices decode whole); 48: a
+    # workspace of 48 shadow rows, so the rows run in 48-row chunks and the
+    # last one is ragged.
+    n, k = shape
+    print(f"case dense bits={nbits} n={n} k={k} tokens={tokens} chunk={chunk}", flush=True)
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    packed, high, scales = _planes(n, k, nbits, 31 * nbits + n + tokens)
+    padded = packed.shape[1] * 2
+    dc, dh, ds = _device_planes(packed, high, scales, nbits, device)
+    size = int(lib.venturi_row_dense_workspace_bytes(tokens, n, k))
+    assert size == BLAS_BYTES + 2 * n * k
+    if chunk is not None:
+        size = BLAS_BYTES + 2 * k * chunk
+    ws = torch.empty(size, dtype=torch.uint8, device=device)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens + k)).half()
+    xd = x.to(device)
+    guard = torch.full((tokens * n + 16,), 47, dtype=torch.float16, device=device)
+    out = guard[8:-8].view(tokens, n)  # 16-byte aligned interior
+    _run(lib, backend, xd, dc, dh, ds, out, tokens, n, k, padded, nbits, ws, size, s)
+    again = torch.empty_like(out)
+    _run(lib, backend, xd, dc, dh, ds, again, tokens, n, k, padded, nbits, ws, size, s)
+    g = guard.cpu()
+    assert (g[:8] == 47).all() and (g[-8:] == 47).all()
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    _bound_check(out.cpu().float().numpy(), x, packed, high, scales, k, nbits)
+
+
+def test_q4_plan_auto_route_is_dense(backend, device):
+    n, k, tokens = 256, 512, DENSE_TOKENS
+    print(f"case dense-plan n={n} k={k} tokens={tokens}", flush=True)
+    packed, high, scales = _planes(n, k, 4, 5)
+    w = Q4RowSplitWeight(torch.from_numpy(packed), torch.from_numpy(scales), k)
+    resident = backend.upload_linear(w, dtype=torch.float16, device=device)
+    assert resident.prepare(tokens=tokens - 1).route == "venturi-q4-mfma"
+    plan = resident.prepare(tokens=tokens)
+    assert plan.route == "venturi-q4-dense"
+    assert plan.workspace_bytes == BLAS_BYTES + 2 * n * k
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(3)).half()
+    xd = x.to(device)
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    with pytest.raises(TypeError):  # a dense plan needs its workspace, as the reference's dense plans do
+        plan.run(xd, out=out)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    plan.run(xd, out=out, workspace=ws)
+    got = out.cpu().float().numpy()
+    wd, xf = _bound_check(got, x, packed, high, scales, k, 4)
+    ref = (xf.astype(np.float32) @ wd.astype(np.float32).T).astype(np.float16).astype(np.float64)
+    diff = np.abs(got - ref)
+    assert (diff <= np.maximum(2e-3, ulp16(ref))).all()
+    # The fused matrix-core route on the same plan is the same contract.
+    fused = torch.empty_like(out)
+    resident.prepare(tokens=tokens, route="mfma").run(xd, out=fused)
+    _bound_check(fused.cpu().float().numpy(), x, packed, high, scales, k, 4)
+
+
+def test_dense_at_config2_gate_up(backend, device):
+    # The timed prefill shape: 34 816 x 5120 at 2048 tokens decodes in four
+    # 8192-row chunks and a 2048-row tail (the 340 MiB shadow is cut into
+    # 80 MiB pieces). Sampled rows (every chunk edge among them) and tokens
+    # against FP64 and fp32.
+    n, k, tokens = 34816, 5120, 2048
+    print(f"case dense-gate-up n={n} k={k} tokens={tokens}", flush=True)
+    lib = backend._native
+    assert lib.venturi_row_dense_workspace_bytes(tokens, n, k) == BLAS_BYTES + 2 * 8192 * k
+    packed, high, scales = _planes(n, k, 4, 77)
+    w = Q4RowSplitWeight(torch.from_numpy(packed), torch.from_numpy(scales), k)
+    plan = backend.upload_linear(w, dtype=torch.float16, device=device).prepare(tokens=tokens)
+    assert plan.route == "venturi-q4-dense"
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(8)).half()
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    plan.run(x.to(device), out=out, workspace=ws)
+    got = out.cpu().float().numpy()
+    rng = np.random.default_rng(1)
+    edges = np.array([0, 8191, 8192, 16383, 16384, 24575, 24576, 32767, 32768, n - 1])
+    rows = np.unique(np.concatenate([edges, rng.choice(n, 120, replace=False)]))
+    toks = np.unique(np.concatenate([[0, tokens - 1], rng.choice(tokens, 62, replace=False)]))
+    wd, xf = _bound_check(got, x, packed, high, scales, k, 4, rows, toks)
+    ref = (xf.astype(np.float32) @ wd.astype(np.float32).T).astype(np.float16).astype(np.float64)
+    stats = agreement(got[np.ix_(toks, rows)], ref)
+    print(f"max_abs={stats['max_abs']:.3g} max_ulp={stats['max_ulp']:.2f} flips={stats['flips']} of {ref.size}",
+          flush=True)
+    assert_free_order(stats)
+
+
+def test_plan_table_runs_the_dense_route(backend, device):
+    # At 1024 tokens a ChunkedDense plan given its workspace runs the dense
+    # route (the bits of venturi_row_dense_run with that workspace); without a
+    # workspace it runs the fused matrix-core GEMM (the bits of venturi_row_gemm_run).
+    n, k, tokens, nbits = 136, 384, 1024, 5
+    print(f"case dense-rowcodec n={n} k={k} tokens={tokens}", flush=True)
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    packed, high, scales = _planes(n, k, nbits, 12)
+    padded = packed.shape[1] * 2
+    dc, dh, ds = _device_planes(packed, high, scales, nbits, device)
+    plan = prepare_row_codec(nbits, 64, precision="wxa16", dtype=0, implementation="auto")
+    size = plan.workspace_bytes(tokens=tokens, k=k)
+    assert size == (32 + 192) * 2**20
+    ws = torch.empty(size, dtype=torch.uint8, device=device)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(4)).half().to(device)
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    plan.project(x.data_ptr(), dc.data_ptr(), dh.data_ptr(), ds.data_ptr(), out.data_ptr(), ws.data_ptr(), size,
+                 tokens=tokens, n=n, k=k, padded=padded, stream=s)
+    want = torch.empty_like(out)
+    _run(lib, backend, x, dc, dh, ds, want, tokens, n, k, padded, nbits, ws, size, s)
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    plan.project(x.data_ptr(), dc.data_ptr(), dh.data_ptr(), ds.data_ptr(), out.data_ptr(), None, 0, tokens=tokens,
+                 n=n, k=k, padded=padded, stream=s)
+    backend._check(lib.venturi_row_gemm_run(x.data_ptr(), dc.data_ptr(), dh.data_ptr(), ds.data_ptr(), want.data_ptr(),
+                                            tokens, n, k, padded, nbits, 0, s))
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
+def test_dense_rejects_bad_arguments(backend, device):
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    n, k, tokens = 16, 128, 4
+    x = torch.zeros(tokens, k, dtype=torch.float16, device=device)
+    c = torch.zeros(n, k // 2, dtype=torch.uint8, device=device)
+    sc = torch.zeros(n, 2, dtype=torch.float16, device=device)
+    o = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    size = int(lib.venturi_row_dense_workspace_bytes(tokens, n, k))
+    ws = torch.empty(size + 256, dtype=torch.uint8, device=device)
+    args = (x.data_ptr(), c.data_ptr(), None, sc.data_ptr(), o.data_ptr())
+    assert lib.venturi_row_dense_run(*args, tokens, n, k, k, 4, 1, ws.data_ptr(), size, s) == -1
+    assert "fp16" in lib.error()
+    assert lib.venturi_row_dense_run(*args, tokens, n, 124, 128, 4, 0, ws.data_ptr(), size, s) == -1
+    assert "k % 8" in lib.error()
+    assert lib.venturi_row_dense_run(*args, tokens, n, k, k, 4, 0, ws.data_ptr(), BLAS_BYTES, s) == -1
+    assert "16-row chunk" in lib.error()
+    assert lib.venturi_row_dense_run(*args, tokens, n, k, k, 4, 0, ws.data_ptr() + 16, size, s) == -1
+    assert "256-byte" in lib.error()
+    assert lib.venturi_row_dense_run(*args, tokens, n, k, k, 7, 0, ws.data_ptr(), size, s) == -1
+    assert lib.venturi_row_dense_run(x.data_ptr(), c.data_ptr(), None, sc.data_ptr(), None, tokens, n, k, k, 4, 0,
+                                     ws.data_ptr(), size, s) == -1
+    torch.cuda.synchronize(device)

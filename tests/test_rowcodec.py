@@ -25,6 +25,11 @@ def test_admitted_plans(bits, group, precision, dtype, impl, path, passes):
     assert plan.path == path and plan.passes == passes
     assert (plan.raw.bits, plan.raw.group, plan.raw.dtype) == (bits, group, dtype)
     want = 2048 * 160 * 36 * passes if passes else 0
+    if path == "chunked-dense":
+        # fp16 ChunkedDense plans from 1024 tokens: the dense route's fixed buffer
+        # (hipBLASLt's 32 MiB and 192 MiB of fp16 shadow); below that, none.
+        want = (32 + 192) * 2**20
+        assert plan.workspace_bytes(tokens=1023, k=5120) == 0
     assert plan.workspace_bytes(tokens=2048, k=5120) == want
 
 
@@ -59,3 +64,21 @@ def test_forged_plans_fail_before_the_device():
     assert lib.venturi_rowcodec_project(C.byref(direct.raw), *([None] * 6), 0, 1, 1, 64, 128, 1, None) == -1
     assert "packed" in lib.error()
     assert lib.venturi_rowcodec_project(None, *([None] * 6), 0, 1, 1, 64, 128, 0, None) == -1
+
+
+def test_dense_workspace_policy():
+    # venturi_row_dense_workspace_bytes (host only): hipBLASLt's 32 MiB plus the
+    # fp16 shadow of one chunk; shadows up to 192 MiB decode whole, larger ones
+    # in chunks of whole 1024-row blocks within 80 MiB (at least one block).
+    from venturi_amd import native
+
+    lib = native.load()
+    blas = 32 * 2**20
+    assert lib.venturi_row_dense_workspace_bytes(2048, 5120, 17408) == blas + 2 * 5120 * 17408  # 170 MiB: whole
+    assert lib.venturi_row_dense_workspace_bytes(2048, 34816, 5120) == blas + 2 * 8192 * 5120  # 4 + a 2048-row tail
+    assert lib.venturi_row_dense_workspace_bytes(1, 248320, 5120) == blas + 2 * 8192 * 5120
+    assert lib.venturi_row_dense_workspace_bytes(4096, 65536, 16384) == blas + 2 * 2048 * 16384
+    assert lib.venturi_row_dense_workspace_bytes(8, 16384, 65536) == blas + 2 * 1024 * 65536  # one block at least
+    assert lib.venturi_row_dense_workspace_bytes(0, 8, 8) == 0
+    assert lib.venturi_row_dense_workspace_bytes(4, 8, 12) == 0 and "k % 8" in lib.error()
+    assert lib.venturi_row_dense_workspace_bytes(4, 12, 8) == 0

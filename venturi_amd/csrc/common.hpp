@@ -3,7 +3,8 @@
 // Every exported entry point follows one contract: validate geometry and
 // pointers on the host, launch on the caller's stream, return 0 on success or
 // -1 with a per-thread message readable through venturi_blocks_error().
-// Nothing here allocates device memory or synchronises.
+// Nothing here allocates device memory or synchronises (the dense route's
+// one-time hipBLASLt set-up per device and shape aside).
 #pragma once
 
 #include <hip/hip_runtime.h>

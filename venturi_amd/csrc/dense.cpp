@@ -1,0 +1,164 @@
+// The dense W*A16 projection: the reference's ChunkedDense path
+// (row_codec_dispatch.cuh:41-48 admits it for q4/q5/q6_g64; Model::project
+// runs it as row_dense_project, qwen_runtime.cuh:348-364) for gfx950.
+//
+// For each chunk of weight rows: decode the rows to the contract's fp16
+// weights fp16(q * scale) (row_decode_launch, the kernel of
+// venturi_row_dequant_rows) into a shadow inside the caller's workspace, then
+// one hipBLASLt GEMM (fp16 operands, fp32 accumulation, fp16 output) writes
+// the chunk's columns of out in place (ldd = n), where the reference GEMMs
+// into a staging chunk and copies it over with cudaMemcpy2DAsync.
+//
+// Chunking: a matrix whose fp16 shadow is at most 192 MiB is decoded whole
+// (one GEMM keeps the whole grid of output tiles). Larger matrices run in
+// chunks of whole 1024-row blocks within 80 MiB (8192 rows at K = 5120): the
+// GEMM re-reads its weight chunk once per row of token tiles, and a chunk of
+// that size stays in the 256 MB Infinity Cache between those reads. Measured
+// on config-2 gate+up (34816 x 5120) at 2048 tokens: 702 us whole, 598 us in
+// 8192-row chunks, 614 in 7168; 8704- and 17408-row chunks took 760 and
+// 884 us (hipBLASLt's kernels for those row counts launch fewer workgroups
+// than the chip has CUs). A smaller workspace gives smaller chunks
+// (multiples of 16 rows).
+//
+// hipBLASLt state: one handle per device and one (descriptor, layouts,
+// algorithm) entry per (device, tokens, rows, k, n), made on first use under
+// a mutex and kept for the life of the process. That first call allocates
+// the handle's own resources, so it must not run under graph capture; later
+// calls make no allocation and are capturable.
+#include "common.hpp"
+
+#include "../../include/venturi_ops.h"
+
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+namespace vt {
+
+void row_decode_launch(const void* codes, const void* high, const void* scales, const std::int64_t* ids, void* out,
+                       int row_begin, int rows, int k, int padded, int bits, hipStream_t stream);
+
+namespace {
+
+constexpr std::uint64_t kBlasBytes = 32ull << 20;    // hipBLASLt's share, at the start of the workspace
+constexpr std::uint64_t kWholeBytes = 192ull << 20;  // shadows up to this size are decoded whole
+constexpr std::uint64_t kChunkBytes = 80ull << 20;   // else chunks of 1024-row blocks within this size
+
+void blas(hipblasStatus_t status, const char* what) {
+    if (status != HIPBLAS_STATUS_SUCCESS)
+        throw std::runtime_error(std::string("hipBLASLt ") + what + " failed (status " + std::to_string(status) + ")");
+}
+
+int policy_rows(int n, int k) {
+    if (2ull * n * k <= kWholeBytes) return n;
+    const std::uint64_t blocks = std::max<std::uint64_t>(1, kChunkBytes / (2048ull * k));
+    return static_cast<int>(std::min<std::uint64_t>(n, blocks * 1024));
+}
+
+void check_geometry(int tokens, int n, int k) {
+    require(tokens > 0 && n > 0 && k > 0, "invalid dense projection geometry");
+    require(k % 8 == 0 && n % 8 == 0, "the dense route needs k % 8 == 0 and n % 8 == 0");
+}
+
+struct Gemm {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+};
+
+struct DeviceBlas {
+    hipblasLtHandle_t handle = nullptr;
+    std::map<std::tuple<int, int, int, int>, Gemm> gemms;
+};
+
+std::mutex blas_mutex;
+
+// D (rows x tokens, column-major, ldd = n) = A^T B: A is the shadow chunk
+// (k x rows column-major, i.e. [rows][k] row-major), B is x (k x tokens
+// column-major, i.e. [tokens][k] row-major); D is out[t][begin + j].
+std::pair<hipblasLtHandle_t, const Gemm*> gemm_for(int tokens, int rows, int k, int n) {
+    int device = 0;
+    check(hipGetDevice(&device));
+    std::lock_guard<std::mutex> lock(blas_mutex);
+    static std::map<int, DeviceBlas> devices;
+    DeviceBlas& dev = devices[device];
+    if (!dev.handle) blas(hipblasLtCreate(&dev.handle), "handle creation");
+    const auto key = std::make_tuple(tokens, rows, k, n);
+    auto found = dev.gemms.find(key);
+    if (found != dev.gemms.end()) return {dev.handle, &found->second};
+
+    Gemm g;
+    blas(hipblasLtMatmulDescCreate(&g.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F), "descriptor creation");
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    blas(hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)), "transpose A");
+    blas(hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)), "transpose B");
+    blas(hipblasLtMatrixLayoutCreate(&g.a, HIP_R_16F, k, rows, k), "layout A");
+    blas(hipblasLtMatrixLayoutCreate(&g.b, HIP_R_16F, k, tokens, k), "layout B");
+    blas(hipblasLtMatrixLayoutCreate(&g.d, HIP_R_16F, rows, tokens, n), "layout D");
+    hipblasLtMatmulPreference_t pref = nullptr;
+    blas(hipblasLtMatmulPreferenceCreate(&pref), "preference creation");
+    const std::uint64_t limit = kBlasBytes;
+    blas(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &limit, sizeof(limit)),
+         "workspace preference");
+    hipblasLtMatmulHeuristicResult_t result{};
+    int count = 0;
+    const hipblasStatus_t found_algo =
+        hipblasLtMatmulAlgoGetHeuristic(dev.handle, g.desc, g.a, g.b, g.d, g.d, pref, 1, &result, &count);
+    hipblasLtMatmulPreferenceDestroy(pref);
+    blas(found_algo, "algorithm search");
+    require(count > 0 && result.state == HIPBLAS_STATUS_SUCCESS, "hipBLASLt has no algorithm for this dense GEMM");
+    g.algo = result.algo;
+    auto placed = dev.gemms.emplace(key, g).first;
+    return {dev.handle, &placed->second};
+}
+
+void dense_run(const void* x, const void* codes, const void* high, const void* scales, void* out, int tokens, int n,
+               int k, int padded, int bits, int dtype, void* workspace, std::uint64_t bytes, hipStream_t stream) {
+    require(dtype == kF16, "the dense W*A16 route takes fp16 activations");
+    require(bits >= 4 && bits <= 6, "row codecs are 4, 5 or 6 bits");
+    check_geometry(tokens, n, k);
+    require(x && out && workspace, "null dense projection operand");
+    require(aligned(x, 16) && aligned(out, 16) && aligned(workspace, 256),
+            "the dense route needs 16-byte x and out and a 256-byte aligned workspace");
+    const std::uint64_t shadow_bytes = bytes > kBlasBytes ? bytes - kBlasBytes : 0;
+    int rows = policy_rows(n, k);
+    if (shadow_bytes / (2ull * k) < static_cast<std::uint64_t>(rows))
+        rows = static_cast<int>(shadow_bytes / (2ull * k)) / 16 * 16;
+    require(rows > 0, "the workspace holds no 16-row chunk of the fp16 shadow (see venturi_row_dense_workspace_bytes)");
+    auto* shadow = static_cast<unsigned char*>(workspace) + kBlasBytes;
+    const float alpha = 1.0f, beta = 0.0f;
+    for (int begin = 0; begin < n; begin += rows) {
+        const int r = std::min(rows, n - begin);
+        row_decode_launch(codes, high, scales, nullptr, shadow, begin, r, k, padded, bits, stream);
+        const auto [handle, g] = gemm_for(tokens, r, k, n);
+        __half* d = static_cast<__half*>(out) + begin;
+        blas(hipblasLtMatmul(handle, g->desc, &alpha, shadow, g->a, x, g->b, &beta, d, g->d, d, g->d, &g->algo,
+                             workspace, kBlasBytes, stream),
+             "GEMM launch");
+    }
+}
+
+}  // namespace
+}  // namespace vt
+
+#define VT_EXPORT extern "C" __attribute__((visibility("default")))
+
+VT_EXPORT uint64_t venturi_row_dense_workspace_bytes(int tokens, int n, int k) {
+    std::uint64_t bytes = 0;
+    vt::host_guarded([&] {
+        vt::check_geometry(tokens, n, k);
+        bytes = vt::kBlasBytes + 2ull * vt::policy_rows(n, k) * k;
+    });
+    return bytes;
+}
+
+VT_EXPORT int venturi_row_dense_run(const void* x, const void* codes, const void* high, const void* scales, void* out,
+                                    int tokens, int n, int k, int padded, int bits, int dtype, void* workspace,
+                                    uint64_t workspace_bytes, void* stream) {
+    return vt::guarded([&] {
+        vt::dense_run(x, codes, high, scales, out, tokens, n, k, padded, bits, dtype, workspace, workspace_bytes,
+                      static_cast<hipStream_t>(stream));
+    });
+}

@@ -15,6 +15,15 @@ enum Precision : int { kWxA16 = 0, kWxA8 = 1, kWxA8Residual = 2 };
 enum Implementation : int { kAuto = 0, kDequant = 1, kFusedResearch = 2 };
 enum Path : int { kDirect = 0, kChunkedDense = 1, kQuantized = 2 };
 
+// ChunkedDense plans from this many tokens run the decoded-shadow GEMM
+// (venturi_row_dense_run) when the caller's workspace holds it. Its workspace
+// is one fixed buffer, as the reference runtime's dequant buffer is: the
+// 32 MiB hipBLASLt share plus 192 MiB of shadow, which holds any matrix the
+// dense route decodes whole and every chunk it cuts larger ones into.
+constexpr int kDenseTokens = 1024;
+constexpr std::uint64_t kDenseMinBytes = 32ull << 20;
+constexpr std::uint64_t kDenseBytes = kDenseMinBytes + (192ull << 20);
+
 // rowcodec::prepare's table with the architecture gate replaced by gfx950
 // (the only target of this library):
 //  * q8_g32: Auto only; WxA16 -> Direct (fp16 or bf16); WxA8 and
@@ -92,8 +101,16 @@ void project(const VRCPlan& plan, const void* x, const void* codes, const void* 
         pass(venturi_q4_fused_run(x, codes, scales, out, tokens, n, k, padded, plan.dtype, stream));
         return;
     }
-    // ChunkedDense: the W*A16 contract. Matrix cores when k % 8 == 0; else the
-    // reference-order expert GEMVs (same fp16(q*scale) weights) up to 64 tokens.
+    // ChunkedDense: the W*A16 contract. From kDenseTokens tokens the reference's
+    // own form (fp16 shadow chunks in the workspace + hipBLASLt) when the
+    // geometry and the workspace allow it; else the fused matrix-core GEMM when
+    // k % 8 == 0; else the reference-order expert GEMVs up to 64 tokens.
+    if (tokens >= kDenseTokens && plan.dtype == kF16 && k % 8 == 0 && n % 8 == 0 && aligned(x, 16) &&
+        aligned(out, 16) && workspace && aligned(workspace, 256) && available >= kDenseMinBytes + 32ull * k) {
+        pass(venturi_row_dense_run(x, codes, high, scales, out, tokens, n, k, padded, plan.bits, plan.dtype, workspace,
+                                   available, stream));
+        return;
+    }
     if (k % 8 == 0 && aligned(x, 16)) {
         pass(venturi_row_gemm_run(x, codes, high, scales, out, tokens, n, k, padded, plan.bits, plan.dtype, stream));
         return;
@@ -126,6 +143,9 @@ VT_EXPORT uint64_t venturi_rowcodec_workspace_bytes(const VRCPlan* plan, int tok
         if (plan->path == vt::kQuantized) {
             bytes = venturi_q8_dp4a_bytes(tokens, k, plan->passes);
             vt::require(bytes > 0, "invalid A8 geometry");
+        } else if (plan->path == vt::kChunkedDense && plan->dtype == vt::kF16 && tokens >= vt::kDenseTokens) {
+            vt::require(k > 0, "invalid row-codec geometry");
+            bytes = vt::kDenseBytes;
         }
     });
     return bytes;

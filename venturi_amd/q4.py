@@ -20,10 +20,17 @@ from .weights import Q4RowSplitWeight, decode_k64_fp16, rtn_k64
 #           (below DECODE_TILED_TOKENS over the resident's tiled decode copy);
 #   generic the plugin order of q4_linear.cu:21-56 (FP32 weights), fp16/bf16;
 #   exact   the expert order of flash_next_q4.cu:23-34 (fp16 weights), fp16, <= 64 tokens;
-#   fused   the research order of q4_fused.cuh:10-89 (FP32 weights), fp16.
-# auto: mfma for fp16 activations, generic for bf16.
-Q4_ROUTES = ("auto", "mfma", "generic", "exact", "fused")
+#   fused   the research order of q4_fused.cuh:10-89 (FP32 weights), fp16;
+#   dense   the reference's ChunkedDense path (qwen_runtime.cuh:348-364): rows
+#           decoded to fp16(q*scale) in the caller's workspace, then hipBLASLt
+#           (fp32 accumulation), fp16, k % 8 == 0 and n % 8 == 0.
+# auto: for fp16 activations dense from DENSE_TOKENS tokens (where the library
+# GEMM outruns the fused matrix-core kernel despite decoding the weights:
+# config-2 shapes at 1024 tokens 0.95-1.44x, at 2048 1.36-1.62x), else mfma;
+# generic for bf16.
+Q4_ROUTES = ("auto", "mfma", "generic", "exact", "fused", "dense")
 DECODE_TILED_TOKENS = 32
+DENSE_TOKENS = 1024
 
 
 def tile_q4(codes, scales):
@@ -108,9 +115,15 @@ class ResidentQ4Linear:
             raise ValueError("Q4 output count must fit int32")
         if route not in Q4_ROUTES:
             raise ValueError(f"Q4 route must be one of {Q4_ROUTES}")
-        if route == "auto":
-            route = "mfma" if self.dtype == torch.float16 and self.in_features % 8 == 0 else "generic"
         fp16 = self.dtype == torch.float16
+        dense_ok = fp16 and self.in_features % 8 == 0 and self.out_features % 8 == 0
+        if route == "auto":
+            if dense_ok and tokens >= DENSE_TOKENS:
+                route = "dense"
+            else:
+                route = "mfma" if fp16 and self.in_features % 8 == 0 else "generic"
+        if route == "dense" and not dense_ok:
+            raise ValueError("The dense Q4 route takes FP16 activations, K % 8 == 0 and N % 8 == 0")
         if route == "mfma" and not (fp16 and self.in_features % 8 == 0):
             raise ValueError("The Q4 matrix-core route takes FP16 activations and K % 8 == 0")
         if route == "exact" and not (fp16 and tokens <= 64):
@@ -135,7 +148,13 @@ class ResidentQ4Linear:
                                                                               _stream(self.device)))
             # The copy and the slots were written on this stream; a plan may run on another.
             torch.cuda.current_stream(self.device).synchronize()
-        return Q4LinearPlan(self, tokens, route, slots)
+        workspace = 0
+        if route == "dense":
+            workspace = int(self.backend._native.venturi_row_dense_workspace_bytes(
+                tokens, self.out_features, self.in_features))
+            if workspace == 0:
+                raise ValueError(self.backend._native.error())
+        return Q4LinearPlan(self, tokens, route, slots, workspace)
 
     def decode(self, *, out, row=0):
         """fp16 rows fp16(q * scale) of [row, row + len(out)) into ``out`` (blocks.cu:1077-1086)."""
@@ -163,7 +182,7 @@ class Q4LinearPlan:
     tokens: int
     kernel: str
     slots: object = None  # exchange slots of a decode that splits K (plan-owned)
-    workspace_bytes = 0
+    workspace_bytes: int = 0  # the dense route's caller-owned shadow and hipBLASLt workspace
 
     @property
     def route(self):
@@ -191,16 +210,26 @@ class Q4LinearPlan:
         return r.storage_tensors + (r.tiled if self.kernel == "mfma" and self.tokens < DECODE_TILED_TOKENS else ())
 
     def run(self, x, *, out, workspace=None):
-        if workspace is not None:
-            raise ValueError("Q4 Linear uses no workspace")
         r = self.resident
+        if self.kernel != "dense" and workspace is not None:
+            raise ValueError("Q4 Linear uses no workspace")
         _tensor(x, (self.tokens, r.in_features), r.dtype, r.device, "x")
         _tensor(out, (self.tokens, r.out_features), r.dtype, r.device, "out")
         _no_overlap(out, (x,) + self.storage_tensors)
+        if self.kernel == "dense":
+            _tensor(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
+            if workspace.data_ptr() % 256 or x.data_ptr() % 16 or out.data_ptr() % 16:
+                raise ValueError("the dense Q4 route needs a 256-byte aligned workspace and 16-byte aligned x and out")
+            _no_overlap(workspace, (x, out) + self.storage_tensors)
         w, lib, stream = r.weight, r.backend._native, _stream(r.device)
         args = (x.data_ptr(), w.codes.data_ptr(), w.scales.data_ptr(), out.data_ptr())
         with torch.cuda.device(r.device):
-            if self.kernel == "mfma" and self.tokens < DECODE_TILED_TOKENS:
+            if self.kernel == "dense":
+                status = lib.venturi_row_dense_run(
+                    *args[:2], None, *args[2:], self.tokens, w.out_features, w.in_features, w.padded_k, 4,
+                    _DTYPES[r.dtype], workspace.data_ptr(), self.workspace_bytes, stream
+                )
+            elif self.kernel == "mfma" and self.tokens < DECODE_TILED_TOKENS:
                 tc, ts = r.tiled
                 slots = self.slots
                 status = lib.venturi_q4_tiled_run(
