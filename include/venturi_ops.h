@@ -290,6 +290,22 @@ int venturi_row_dense_run(const void* x, const void* codes, const void* high, co
                           int tokens, int n, int k, int padded, int bits, int dtype, void* workspace,
                           uint64_t workspace_bytes, void* stream);
 
+/* Extension: the Q8 A16 projection in the same dense form, for prefill. The
+ * contract scales each exact group dot, so each weight row is decoded to the
+ * exact two-term fp16 form q*s = hi + lo (hi = fp16(q*s)), x is doubled to
+ * [x | x] and one hipBLASLt GEMM over 2k columns sums the exact products in
+ * fp32: outputs agree with venturi_q8_head_run to fp32 association, like the
+ * matrix-core routes. Scales must be below 516 (rows with larger ones give NaN
+ * outputs); fp16 activations, 1..65535 tokens, k % 8 == 0, n % 8 == 0; x and
+ * out 16-byte aligned, codes 8-byte, workspace 256-byte aligned; workspace of
+ * venturi_q8_dense_workspace_bytes (hipBLASLt's 32 MiB, the doubled x, and the
+ * shadow of up to 8192 rows; a smaller one runs smaller chunks). First call
+ * per (device, shape) as for venturi_row_dense_run. No counterpart in the
+ * reference (its Q8 prefill runs the head kernel). */
+uint64_t venturi_q8_dense_workspace_bytes(int tokens, int n, int k);
+int venturi_q8_dense_run(const void* x, const int8_t* codes, const void* scales, void* out, int tokens, int n, int k,
+                         int padded, int dtype, void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Extension: workspace bytes of venturi_moe_q4_run (0 on invalid geometry). */
 uint64_t venturi_moe_q4_bytes(int tokens, int top_k, int experts, int hidden, int inter);
 

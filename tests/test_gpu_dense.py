@@ -200,3 +200,193 @@ def test_dense_rejects_bad_arguments(backend, device):
     assert lib.venturi_row_dense_run(x.data_ptr(), c.data_ptr(), None, sc.data_ptr(), None, tokens, n, k, k, 4, 0,
                                      ws.data_ptr(), size, s) == -1
     torch.cuda.synchronize(device)
+
+
+# ---------------------------------------------------------------------------
+# The Q8 dense route (venturi_q8_dense_run): rows decoded to the exact two-term
+# fp16 form q*s = hi + lo, x doubled, one GEMM over 2k. Held to the matrix-core
+# routes' contract: the FP64 bound on the exact products q*s and, against the
+# canonical-order oracle, helpers.assert_free_order.
+
+from helpers import bits, random_q8  # noqa: E402
+from venturi_amd import Q8RowSplitWeight  # noqa: E402
+from venturi_amd.vocabulary import DENSE_TOKENS as Q8_DENSE_TOKENS  # noqa: E402
+
+
+def _q8_check(got, x, codes, scales, k):
+    w = oracle.q8_unpack(codes, scales, k)  # q*s exactly, FP64
+    xd = x.float().numpy().astype(np.float64)
+    exact = xd @ w.T
+    g = got.astype(np.float64)
+    bound = 0.5 * ulp16(exact) + 2.0**-19 * (np.abs(xd) @ np.abs(w).T)
+    assert (np.abs(g - exact) <= bound).all()
+    stats = agreement(g, oracle.q8_linear(bits(x), codes, scales, k))
+    assert_free_order(stats)
+    return stats
+
+
+def _q8_run(lib, backend, x, dc, ds, out, tokens, n, k, ws, size, s):
+    backend._check(lib.venturi_q8_dense_run(x.data_ptr(), dc.data_ptr(), ds.data_ptr(), out.data_ptr(), tokens, n, k,
+                                            dc.shape[1], 0, ws.data_ptr(), size, s))
+
+
+@pytest.mark.parametrize("shape,tokens", [((200, 264), 37), ((64, 512), 1), ((1032, 136), 300), ((8200, 128), 40)])
+@pytest.mark.parametrize("chunk", [None, 48])
+def test_q8_dense_contract(backend, device, shape, tokens, chunk):
+    # (8200, 128) runs an 8192-row chunk and an 8-row one; chunk 48 forces
+    # 48-row chunks through a smaller workspace.
+    n, k = shape
+    print(f"case q8-dense n={n} k={k} tokens={tokens} chunk={chunk}", flush=True)
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    codes, scales = random_q8(n, k, 401 + n + tokens)
+    dc, ds = codes.to(device), scales.to(device)
+    size = int(lib.venturi_q8_dense_workspace_bytes(tokens, n, k))
+    x2 = (4 * tokens * k + 255) // 256 * 256
+    assert size == BLAS_BYTES + x2 + 4 * min(n, 8192) * k
+    if chunk is not None:
+        size = BLAS_BYTES + x2 + 4 * k * chunk
+    ws = torch.empty(size, dtype=torch.uint8, device=device)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(tokens + 2 * k)).half()
+    xd = x.to(device)
+    guard = torch.full((tokens * n + 16,), 47, dtype=torch.float16, device=device)
+    out = guard[8:-8].view(tokens, n)
+    _q8_run(lib, backend, xd, dc, ds, out, tokens, n, k, ws, size, s)
+    again = torch.empty_like(out)
+    _q8_run(lib, backend, xd, dc, ds, again, tokens, n, k, ws, size, s)
+    g = guard.cpu()
+    assert (g[:8] == 47).all() and (g[-8:] == 47).all()
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    stats = _q8_check(out.cpu().float().numpy(), x, codes.numpy(), scales.numpy(), k)
+    print(f"flips={stats['flips']} of {stats['count']}", flush=True)
+
+
+def test_q8_dense_two_term_form_is_exact_at_extreme_scales(backend, device):
+    # Subnormal, tiny, ordinary and large (just below 516) scales with the
+    # extreme codes: hi + lo must be q*s exactly, so a single-code row times a
+    # power-of-two activation returns q*s rounded once to fp16.
+    n, k, tokens = 64, 128, 8
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    picks = [2.0**-24, 3 * 2.0**-24, 2.0**-15 + 2.0**-24, 1.0009765625 * 2.0**-10, 0.0123, 1.0, 33.97, 515.5]
+    scales = torch.tensor(picks * (n * 4 // len(picks)), dtype=torch.float16).view(n, 4)
+    codes = torch.zeros(n, 128, dtype=torch.int8)
+    rng = np.random.default_rng(3)
+    codes[:, :k] = torch.from_numpy(rng.choice([-127, -126, -1, 1, 5, 77, 126, 127], size=(n, k)).astype(np.int8))
+    dc, ds = codes.to(device), scales.to(device)
+    size = int(lib.venturi_q8_dense_workspace_bytes(tokens, n, k))
+    ws = torch.empty(size, dtype=torch.uint8, device=device)
+    # Token t selects column 3t (x = 1 there, 0 elsewhere): out[t][j] = fp16(q[j][3t] * s[j][group]).
+    x = torch.zeros(tokens, k, dtype=torch.float16)
+    for t in range(tokens):
+        x[t, 3 * t] = 1.0
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    _q8_run(lib, backend, x.to(device), dc, ds, out, tokens, n, k, ws, size, s)
+    want = np.empty((tokens, n), np.float16)
+    for t in range(tokens):
+        c = 3 * t
+        want[t] = (codes[:, c].numpy().astype(np.float64) * scales[:, c // 32].numpy().astype(np.float64)).astype(np.float16)
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), want.view(np.uint16))
+    # A full random row mix at the same scales meets the contract bound (x is
+    # scaled by 2^-10 so that the large-scale rows stay inside the fp16 range).
+    codes2, _ = random_q8(n, k, 9)
+    dc2 = codes2.to(device)
+    xr = (torch.randn(tokens, k, generator=torch.Generator().manual_seed(1)) * 2.0**-10).half()
+    _q8_run(lib, backend, xr.to(device), dc2, ds, out, tokens, n, k, ws, size, s)
+    w = oracle.q8_unpack(codes2.numpy(), scales.numpy(), k)
+    xd = xr.float().numpy().astype(np.float64)
+    exact = xd @ w.T
+    assert np.abs(exact).max() < 60000
+    bound = 0.5 * ulp16(exact) + 2.0**-19 * (np.abs(xd) @ np.abs(w).T)
+    assert (np.abs(out.cpu().float().numpy().astype(np.float64) - exact) <= bound).all()
+
+
+def test_q8_dense_scale_limit(backend, device):
+    # A scale of 516 or more puts 127 * s past the fp16 range: the route is
+    # refused by the plan (auto stays on the fused GEMM), and the C entry turns
+    # that row's outputs into NaN instead of a finite wrong value.
+    n, k, tokens = 16, 64, Q8_DENSE_TOKENS
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    codes, scales = random_q8(n, k, 5)
+    codes[3, :] = 127
+    scales[3, :] = 600.0
+    resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, k), dtype=torch.float16, device=device)
+    assert resident.prepare(tokens=tokens).route == "venturi-q8-mfma"
+    with pytest.raises(ValueError, match="516"):
+        resident.prepare(tokens=tokens, route="dense")
+    dc, ds = codes.to(device), scales.to(device)
+    size = int(lib.venturi_q8_dense_workspace_bytes(tokens, n, k))
+    ws = torch.empty(size, dtype=torch.uint8, device=device)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(2)).half().to(device)
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    _q8_run(lib, backend, x, dc, ds, out, tokens, n, k, ws, size, s)
+    o = out.cpu().float()
+    assert torch.isnan(o[:, 3]).all()
+    assert torch.isfinite(torch.cat([o[:, :3], o[:, 4:]], 1)).all()
+
+
+def test_q8_plan_auto_route_is_dense(backend, device):
+    n, k = 136, 256
+    codes, scales = random_q8(n, k, 8)
+    resident = backend.upload_linear(Q8RowSplitWeight(codes, scales, k), dtype=torch.float16, device=device)
+    assert resident.prepare(tokens=Q8_DENSE_TOKENS - 1).plan.kernel == "prefill"
+    plan = resident.prepare(tokens=Q8_DENSE_TOKENS)
+    assert plan.route == "venturi-q8-dense" and plan.workspace_bytes > 0
+    x = torch.randn(Q8_DENSE_TOKENS, k, generator=torch.Generator().manual_seed(6)).half()
+    out = torch.empty(Q8_DENSE_TOKENS, n, dtype=torch.float16, device=device)
+    with pytest.raises(TypeError):
+        plan.run(x.to(device), out=out)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    plan.run(x.to(device), out=out, workspace=ws)
+    _q8_check(out.cpu().float().numpy(), x, codes.numpy(), scales.numpy(), k)
+    bf = backend.upload_linear(Q8RowSplitWeight(codes, scales, k), dtype=torch.bfloat16, device=device)
+    assert bf.prepare(tokens=Q8_DENSE_TOKENS).route == "venturi-q8-exact"
+
+
+@pytest.mark.parametrize("n,k", [(34816, 5120), (5120, 17408)])
+def test_q8_dense_config2_m2048_sampled_rows(backend, device, n, k):
+    # The timed prefill shapes: gate+up in four 8192-row chunks and a 2048-row
+    # tail, down whole. Sampled rows (chunk edges among them), every token.
+    print(f"case q8-dense-config2 n={n} k={k}", flush=True)
+    gen = torch.Generator(device=device).manual_seed(n + k + 3)
+    w = torch.randn(n, k, generator=gen, device=device) * 0.02
+    packed = backend.quantize_q8(w)
+    del w
+    tokens = 2048
+    plan = backend.upload_linear(packed, dtype=torch.float16, device=device).prepare(tokens=tokens)
+    assert plan.route == "venturi-q8-dense"
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(7)).half()
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    plan.run(x.to(device), out=out, workspace=ws)
+    edges = [r for r in (0, 8191, 8192, 16383, 16384, 32767, 32768, n - 1) if r < n]
+    rows = np.unique(np.concatenate([edges, np.random.default_rng(n).choice(n, 24, replace=False)]))
+    codes, scales = packed.codes.cpu().numpy()[rows], packed.scales.cpu().numpy()[rows]
+    stats = _q8_check(out[:, torch.from_numpy(rows).to(device)].cpu().float().numpy(), x, codes, scales, k)
+    print(f"q8-dense config2 n={n} k={k}: max_abs={stats['max_abs']:.3g} flips={stats['flips']} of {stats['count']}",
+          flush=True)
+
+
+def test_q8_dense_rejects_bad_arguments(backend, device):
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    n, k, tokens = 16, 128, 4
+    x = torch.zeros(tokens, k, dtype=torch.float16, device=device)
+    c = torch.zeros(n, k, dtype=torch.int8, device=device)
+    sc = torch.zeros(n, k // 32, dtype=torch.float16, device=device)
+    o = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    size = int(lib.venturi_q8_dense_workspace_bytes(tokens, n, k))
+    ws = torch.empty(size + 256, dtype=torch.uint8, device=device)
+    args = (x.data_ptr(), c.data_ptr(), sc.data_ptr(), o.data_ptr())
+    assert lib.venturi_q8_dense_run(*args, tokens, n, k, k, 1, ws.data_ptr(), size, s) == -1
+    assert "fp16" in lib.error()
+    assert lib.venturi_q8_dense_run(*args, tokens, n, k, 256, 0, ws.data_ptr(), size, s) == -1
+    assert lib.venturi_q8_dense_run(*args, tokens, 12, k, k, 0, ws.data_ptr(), size, s) == -1
+    assert "n % 8" in lib.error()
+    assert lib.venturi_q8_dense_run(*args, tokens, n, k, k, 0, ws.data_ptr(), BLAS_BYTES, s) == -1
+    assert "16-row chunk" in lib.error()
+    assert lib.venturi_q8_dense_run(*args, tokens, n, k, k, 0, ws.data_ptr() + 16, size, s) == -1
+    assert "256-byte" in lib.error()
+    assert lib.venturi_q8_dense_workspace_bytes(70000, n, k) == 0
+    torch.cuda.synchronize(device)

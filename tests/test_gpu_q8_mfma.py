@@ -82,7 +82,8 @@ def test_prefill_config2_m2048_sampled_rows(backend, device, n, k):
     del w
     tokens = 2048
     x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(5)).half()
-    plan = backend.upload_linear(packed, dtype=torch.float16, device=device).prepare(tokens=tokens)
+    # The fused matrix-core GEMM (auto takes the dense route at this size; it is tested in test_gpu_dense.py).
+    plan = backend.upload_linear(packed, dtype=torch.float16, device=device).prepare(tokens=tokens, route="mfma")
     assert plan.plan.kernel == "prefill"
     out = torch.empty(tokens, n, dtype=torch.float16, device=device)
     plan.run(x.to(device), out=out)
@@ -125,6 +126,7 @@ def test_mfma_route_admission(backend, device):
     assert resident.prepare(tokens=33).route == "venturi-q8-mfma"  # prefill GEMM above 32 tokens
     assert resident.prepare(tokens=33).plan.kernel == "prefill"
     assert resident.prepare(tokens=4096).plan.slots is None
+    assert resident.prepare(tokens=4096).route == "venturi-q8-dense"  # prefill from 2048 tokens
     bf = backend.upload_linear(Q8RowSplitWeight(codes, scales, 64), dtype=torch.bfloat16, device=device)
     assert bf.prepare(tokens=8).route == "venturi-q8-exact"
 

@@ -20,7 +20,7 @@ from .weights import DenseWeight, Q4RowSplitWeight, Q8RowSplitWeight
 
 _DTYPES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
-Q8_ROUTES = ("auto", "exact", "mfma")
+Q8_ROUTES = ("auto", "exact", "mfma", "dense")
 
 
 def _shape(tokens, features):
@@ -342,7 +342,10 @@ class _Q8Linear:
     """LinearPlan adapter over a Q8 output-head plan (blocks.py:735-768)."""
 
     plan: object
-    workspace_bytes = 0
+
+    @property
+    def workspace_bytes(self):
+        return self.plan.workspace_bytes
 
     @property
     def route(self):
@@ -373,9 +376,9 @@ class _Q8Linear:
         return self.plan.storage_tensors
 
     def run(self, x, *, out, workspace=None):
-        if workspace is not None:
+        if workspace is not None and self.plan.workspace_bytes == 0:
             raise ValueError("Direct Q8 Linear uses no workspace")
-        return self.plan.run(x, out=out)
+        return self.plan.run(x, out=out, workspace=workspace)
 
 
 @dataclass(frozen=True)

@@ -1,4 +1,4 @@
-// The dense W*A16 projection: the reference's ChunkedDense path
+// Dense projections through hipBLASLt. W*A16 (q4/q5/q6): the reference's ChunkedDense path
 // (row_codec_dispatch.cuh:41-48 admits it for q4/q5/q6_g64; Model::project
 // runs it as row_dense_project, qwen_runtime.cuh:348-364) for gfx950.
 //
@@ -39,6 +39,9 @@ namespace vt {
 
 void row_decode_launch(const void* codes, const void* high, const void* scales, const std::int64_t* ids, void* out,
                        int row_begin, int rows, int k, int padded, int bits, hipStream_t stream);
+void q8_split_launch(const std::int8_t* codes, const __half* scales, void* shadow, int row0, int rows, int k,
+                     int padded, hipStream_t stream);
+void q8_dup_launch(const void* x, void* x2, int tokens, int k, hipStream_t stream);
 
 namespace {
 
@@ -140,10 +143,70 @@ void dense_run(const void* x, const void* codes, const void* high, const void* s
     }
 }
 
+// The Q8 form: the W8A16 contract scales each exact group dot, so the
+// decoded weights must be q*s exactly; the shadow holds each row as its two
+// fp16 terms [hi | lo] (q8_split) and the activations are doubled to [x | x],
+// so one GEMM over 2k columns sums x*hi + x*lo, every product exact, in fp32.
+// Chunks: whole matrices up to 8192 rows, else 8192-row chunks (config-2
+// gate+up, K = 2 x 5120: 1024 us in 8192-row chunks against 1149-1294 in
+// 4096- to 6144-row ones and 1170 whole; down, K = 2 x 17408, is faster whole).
+constexpr int kQ8ChunkRows = 8192;
+
+std::uint64_t q8_x2_bytes(int tokens, int k) { return (4ull * tokens * k + 255) / 256 * 256; }
+
+void q8_dense_run(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n, int k,
+                  int padded, int dtype, void* workspace, std::uint64_t bytes, hipStream_t stream) {
+    require(dtype == kF16, "the dense Q8 route takes fp16 activations");
+    check_geometry(tokens, n, k);
+    require(tokens <= 65535, "the dense Q8 route takes at most 65535 tokens");
+    require(x && codes && scales && out && workspace, "null dense projection operand");
+    require(padded == padded_k(k), "invalid Q8 geometry");
+    require(aligned(x, 16) && aligned(out, 16) && aligned(workspace, 256) && aligned(codes, 8),
+            "the dense route needs 16-byte x and out, 8-byte codes and a 256-byte aligned workspace");
+    const std::uint64_t x2 = q8_x2_bytes(tokens, k);
+    const std::uint64_t shadow_bytes = bytes > kBlasBytes + x2 ? bytes - kBlasBytes - x2 : 0;
+    int rows = std::min(n, kQ8ChunkRows);
+    if (shadow_bytes / (4ull * k) < static_cast<std::uint64_t>(rows))
+        rows = static_cast<int>(shadow_bytes / (4ull * k)) / 16 * 16;
+    require(rows > 0, "the workspace holds no 16-row chunk of the fp16 shadow (see venturi_q8_dense_workspace_bytes)");
+    auto* xd = static_cast<unsigned char*>(workspace) + kBlasBytes;
+    auto* shadow = xd + x2;
+    q8_dup_launch(x, xd, tokens, k, stream);
+    const float alpha = 1.0f, beta = 0.0f;
+    for (int begin = 0; begin < n; begin += rows) {
+        const int r = std::min(rows, n - begin);
+        q8_split_launch(codes, scales, shadow, begin, r, k, padded, stream);
+        const auto [handle, g] = gemm_for(tokens, r, 2 * k, n);
+        __half* d = static_cast<__half*>(out) + begin;
+        blas(hipblasLtMatmul(handle, g->desc, &alpha, shadow, g->a, xd, g->b, &beta, d, g->d, d, g->d, &g->algo,
+                             workspace, kBlasBytes, stream),
+             "GEMM launch");
+    }
+}
+
 }  // namespace
 }  // namespace vt
 
 #define VT_EXPORT extern "C" __attribute__((visibility("default")))
+
+VT_EXPORT uint64_t venturi_q8_dense_workspace_bytes(int tokens, int n, int k) {
+    std::uint64_t bytes = 0;
+    vt::host_guarded([&] {
+        vt::check_geometry(tokens, n, k);
+        vt::require(tokens <= 65535, "the dense Q8 route takes at most 65535 tokens");
+        bytes = vt::kBlasBytes + vt::q8_x2_bytes(tokens, k) + 4ull * std::min(n, vt::kQ8ChunkRows) * k;
+    });
+    return bytes;
+}
+
+VT_EXPORT int venturi_q8_dense_run(const void* x, const int8_t* codes, const void* scales, void* out, int tokens,
+                                   int n, int k, int padded, int dtype, void* workspace, uint64_t workspace_bytes,
+                                   void* stream) {
+    return vt::guarded([&] {
+        vt::q8_dense_run(x, codes, static_cast<const __half*>(scales), out, tokens, n, k, padded, dtype, workspace,
+                         workspace_bytes, static_cast<hipStream_t>(stream));
+    });
+}
 
 VT_EXPORT uint64_t venturi_row_dense_workspace_bytes(int tokens, int n, int k) {
     std::uint64_t bytes = 0;

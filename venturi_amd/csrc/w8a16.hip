@@ -236,7 +236,66 @@ void launch_prefill(const __half* x, const std::int8_t* codes, const __half* sca
                                                                         padded, groups);
 }
 
+// The exact two-term fp16 form of Q8 weights, for the dense route: row j of
+// the shadow holds hi = fp16(q*s) in columns [0, k) and lo = q*s - hi in
+// [k, 2k). q*s is exact in fp32 (an 8-bit integer times an 11-bit
+// significand), hi is its RNE fp16 rounding, and the difference is a multiple
+// of the scale's ulp smaller than half an ulp of hi, at most 8 significant
+// bits, which fp16 (with its subnormals) holds exactly; so hi + lo == q*s for
+// every scale below 516. At 516 and above 127*s rounds past 65504: hi becomes
+// inf and lo -inf, and every output that row touches is NaN, never a finite
+// wrong value. Thread: 8 columns of one row (k % 8 == 0).
+__global__ __launch_bounds__(256) void q8_split(const std::int8_t* __restrict__ codes, const __half* __restrict__ scales,
+                                                __half* __restrict__ shadow, int row0, int k, int padded) {
+    const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (c >= k) return;
+    const std::int64_t row = row0 + static_cast<std::int64_t>(blockIdx.y);
+    const uint2 w = *reinterpret_cast<const uint2*>(codes + row * padded + c);
+    const float s = __half2float(scales[row * (padded / 32) + c / 32]);
+    const std::uint32_t words[2] = {w.x, w.y};
+    std::uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        float v[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            v[j] = static_cast<float>(static_cast<std::int8_t>(words[(i + j) / 4] >> (8 * ((i + j) % 4)))) * s;
+        const __half h0 = __float2half_rn(v[0]), h1 = __float2half_rn(v[1]);
+        const __half l0 = __float2half_rn(v[0] - __half2float(h0)), l1 = __float2half_rn(v[1] - __half2float(h1));
+        hi[i / 2] = static_cast<std::uint32_t>(__half_as_ushort(h0)) | static_cast<std::uint32_t>(__half_as_ushort(h1)) << 16;
+        lo[i / 2] = static_cast<std::uint32_t>(__half_as_ushort(l0)) | static_cast<std::uint32_t>(__half_as_ushort(l1)) << 16;
+    }
+    __half* dst = shadow + static_cast<std::int64_t>(blockIdx.y) * 2 * k + c;
+    *reinterpret_cast<uint4*>(dst) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    *reinterpret_cast<uint4*>(dst + k) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+}
+
+// x [tokens][k] -> x2 [tokens][2k] = [x | x] (the activations of the dense
+// route's doubled K). Thread: 8 halves (k % 8 == 0).
+__global__ __launch_bounds__(256) void q8_dup_rows(const __half* __restrict__ x, __half* __restrict__ x2, int k) {
+    const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (c >= k) return;
+    const std::int64_t t = blockIdx.y;
+    const uint4 v = *reinterpret_cast<const uint4*>(x + t * k + c);
+    *reinterpret_cast<uint4*>(x2 + t * 2 * k + c) = v;
+    *reinterpret_cast<uint4*>(x2 + t * 2 * k + k + c) = v;
+}
+
 }  // namespace
+
+void q8_split_launch(const std::int8_t* codes, const __half* scales, void* shadow, int row0, int rows, int k,
+                     int padded, hipStream_t stream) {
+    require(k % 8 == 0 && rows > 0 && rows <= 65535 && padded == padded_k(k), "invalid Q8 split geometry");
+    require(aligned(codes, 8) && aligned(scales, 2) && aligned(shadow, 16), "misaligned Q8 split operand");
+    q8_split<<<dim3((k / 8 + 255) / 256, rows), 256, 0, stream>>>(codes, scales, static_cast<__half*>(shadow), row0, k,
+                                                                 padded);
+}
+
+void q8_dup_launch(const void* x, void* x2, int tokens, int k, hipStream_t stream) {
+    require(k % 8 == 0 && tokens > 0 && tokens <= 65535, "invalid activation geometry for the dense Q8 route");
+    q8_dup_rows<<<dim3((k / 8 + 255) / 256, tokens), 256, 0, stream>>>(static_cast<const __half*>(x),
+                                                                       static_cast<__half*>(x2), k);
+}
 
 void q8_prefill_launch(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n,
                        int k, int padded, int dtype, hipStream_t stream) {

@@ -66,6 +66,8 @@ SIGNATURES = {
     "venturi_row_gemm_run": ([_P] * 5 + [_I] * 6 + [_P], _I),
     "venturi_row_dense_workspace_bytes": ([_I] * 3, _U64),
     "venturi_row_dense_run": ([_P] * 5 + [_I] * 6 + [_P, _U64, _P], _I),
+    "venturi_q8_dense_workspace_bytes": ([_I] * 3, _U64),
+    "venturi_q8_dense_run": ([_P] * 4 + [_I] * 5 + [_P, _U64, _P], _I),
     "venturi_rowcodec_prepare": ([_I] * 5 + [_P], _I),
     "venturi_rowcodec_workspace_bytes": ([_P, _I, _I], _U64),
     "venturi_rowcodec_project": ([_P] * 7 + [_U64] + [_I] * 5 + [_P], _I),

@@ -15,8 +15,15 @@ Kernel families, chosen once per plan (``prepare(tokens=, route=)``):
   the tiled planes (16-row blocks x 64-column chunks in MFMA operand order),
   so each wave streams contiguous 1 KB blocks; above 32 tokens (prefill) it
   runs ``venturi_q8_prefill_run`` on the row-major planes;
-* ``auto``: ``mfma`` where its conditions hold (FP16 activations,
-  K % 8 == 0), else ``exact``.
+* ``dense``: for prefill, each chunk of rows decoded to the exact two-term
+  fp16 form of its weights (q*s = hi + lo, ``venturi_q8_dense_run``) and
+  multiplied by hipBLASLt over the doubled K (every product exact, fp32
+  sums: equal to the canonical order up to fp32 association); FP16, K and N
+  multiples of 8, row-major planes, every scale below 516; the plan takes a
+  caller-owned workspace of ``workspace_bytes``;
+* ``auto``: ``dense`` from DENSE_TOKENS tokens where its conditions hold,
+  else ``mfma`` where its conditions hold (FP16 activations, K % 8 == 0),
+  else ``exact``.
 
 Residency (an upload option): ``"row-major"`` keeps the planes as the
 reference lays them out and builds a tiled copy the first time a decode plan
@@ -36,10 +43,15 @@ from .blocks import _DTYPES, Q8_ROUTES, _no_overlap, _shape, _stream, _tensor
 
 EXACT_MAX_AUTO_TOKENS = 0
 MFMA_MAX_TOKENS = 32
+# The dense route decodes and writes 4 bytes per weight before its GEMM, so it
+# pays only at large token counts: config-2 shapes against the fused GEMM at
+# 1024 tokens 0.87-1.28x (gate+up and down slower), at 2048 1.13-1.21x.
+DENSE_TOKENS = 2048
+DENSE_MAX_SCALE = 516.0  # 127 * 516 rounds past the fp16 range
 RESIDENCIES = ("row-major", "tiled", "tiled-paired")
 _TILE_LOCK = threading.Lock()
 _ROUTE_NAMES = {"exact": "venturi-q8-exact", "mfma": "venturi-q8-mfma", "prefill": "venturi-q8-mfma",
-                "swiglu": "venturi-q8-mfma-swiglu"}
+                "swiglu": "venturi-q8-mfma-swiglu", "dense": "venturi-q8-dense"}
 
 
 def _padded(k):
@@ -150,6 +162,7 @@ class ResidentQ8Vocabulary:
     residency: str = "row-major"
     _geometry: tuple = ()  # (rows, padded K)
     _device: object = None
+    _facts: dict = field(default_factory=dict, compare=False, repr=False)  # cached plane properties
 
     @property
     def device(self):
@@ -180,6 +193,17 @@ class ResidentQ8Vocabulary:
                              "upload it with residency='row-major' for this kernel")
         return self._codes, self._scales
 
+    def dense_admissible(self):
+        """Whether the dense route's two-term form is exact for these planes
+        (row-major planes kept, every scale below DENSE_MAX_SCALE); computed once."""
+        if self._codes is None:
+            return False
+        with _TILE_LOCK:
+            if "dense" not in self._facts:
+                with torch.cuda.device(self.device):
+                    self._facts["dense"] = bool((self._scales.float().abs() < DENSE_MAX_SCALE).all())
+            return self._facts["dense"]
+
     def tiled_planes(self, paired=False):
         """The tiled copy of the planes (built on first use for a row-major resident)."""
         key = "tiled-paired" if paired else "tiled"
@@ -207,10 +231,25 @@ class ResidentQ8Vocabulary:
             raise ValueError(f"Q8 route must be one of {Q8_ROUTES}")
         self.backend.validate_device(self.dtype, self.device)
         matrix_cores = self.dtype == torch.float16 and self.hidden_size % 8 == 0
+        dense_shape = matrix_cores and self.vocab_size % 8 == 0 and tokens <= 65535
         if route == "auto":
-            route = "mfma" if matrix_cores and tokens > EXACT_MAX_AUTO_TOKENS else "exact"
+            if dense_shape and tokens >= DENSE_TOKENS and self.dense_admissible():
+                route = "dense"
+            else:
+                route = "mfma" if matrix_cores and tokens > EXACT_MAX_AUTO_TOKENS else "exact"
         if route == "mfma" and not matrix_cores:
             raise ValueError("The Q8 MFMA route takes FP16 activations and K % 8 == 0")
+        if route == "dense":
+            if not dense_shape:
+                raise ValueError("The dense Q8 route takes FP16 activations, K and N multiples of 8, <= 65535 tokens")
+            self.row_major_planes()
+            if not self.dense_admissible():
+                raise ValueError(f"The dense Q8 route needs every scale below {DENSE_MAX_SCALE}")
+            lib = self.backend._native
+            size = int(lib.venturi_q8_dense_workspace_bytes(tokens, self.vocab_size, self.hidden_size))
+            if size == 0:
+                raise ValueError(lib.error())
+            return Q8OutputHead(self, tokens, "dense", workspace_bytes=size)
         if self.residency == "tiled-paired" or (self.residency == "tiled" and (route == "exact" or tokens > MFMA_MAX_TOKENS)):
             self.row_major_planes()  # raises: the plan needs planes this resident does not keep
         if route == "exact":
@@ -280,7 +319,7 @@ class Q8OutputHead:
     kernel: str = "exact"
     tiles: tuple = ()
     slots: object = None
-    workspace_bytes = 0
+    workspace_bytes: int = 0  # the dense route's caller-owned workspace
 
     @property
     def route(self):
@@ -297,12 +336,26 @@ class Q8OutputHead:
         kept = () if r._codes is None else (r._codes, r._scales)
         return kept + tuple(self.tiles) + (() if self.slots is None else (self.slots,))
 
-    def run(self, x, *, out):
+    def run(self, x, *, out, workspace=None):
         r = self.resident
+        if self.kernel != "dense" and workspace is not None:
+            raise ValueError("This Q8 plan uses no workspace")
         _tensor(x, (self.tokens, r.hidden_size), r.dtype, r.device, "x")
         _tensor(out, (self.tokens, self.out_features), r.dtype, r.device, "out")
         _no_overlap(out, (x,) + self.storage_tensors)
         lib = r.backend._native
+        if self.kernel == "dense":
+            _tensor(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
+            if workspace.data_ptr() % 256 or x.data_ptr() % 16 or out.data_ptr() % 16:
+                raise ValueError("the dense Q8 route needs a 256-byte aligned workspace and 16-byte aligned x and out")
+            _no_overlap(workspace, (x, out) + self.storage_tensors)
+            codes, scales = r.row_major_planes()
+            with torch.cuda.device(r.device):
+                r.backend._check(lib.venturi_q8_dense_run(
+                    x.data_ptr(), codes.data_ptr(), scales.data_ptr(), out.data_ptr(), self.tokens, r.vocab_size,
+                    r.hidden_size, r.padded_k, _DTYPES[r.dtype], workspace.data_ptr(), self.workspace_bytes,
+                    _stream(r.device)))
+            return out
         if self.kernel in ("exact", "prefill"):
             entry = lib.venturi_q8_head_run if self.kernel == "exact" else lib.venturi_q8_prefill_run
             planes, tail = r.row_major_planes(), ()
