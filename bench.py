@@ -599,10 +599,12 @@ def a8_decode(backend, device, steps, warmup, copy_mb, tokens_list=(1, 8)):
 def prefill_a16(backend, device, steps, warmup):
     """fp16-activation prefill GEMMs at the config-2 shapes, M = 2048 (the metric's
     "fp16 TOPS (M >= 256)" leg): W8A16 (q8_g32, venturi_q8_prefill_run) and W4A16
-    (q4_g64), both on their plans' auto route. W4A16's auto route at 2048 tokens
-    is the dense one (venturi_row_dense_run: fp16 shadow chunks + hipBLASLt, the
-    reference's ChunkedDense form); the fused matrix-core kernel
-    (venturi_q4_gemm_run) is timed beside it as `fused_mfma_us`.
+    (q4_g64), both on their plans' auto route, which at 2048 tokens is the dense
+    one: W4A16 through venturi_row_dense_run (fp16 shadow chunks + hipBLASLt, the
+    reference's ChunkedDense form), W8A16 through venturi_q8_dense_run (exact
+    two-term fp16 weights over a doubled K). TFLOP/s counts 2*M*N*K either way;
+    the fused matrix-core kernel on the same weights is timed beside it as
+    `fused_mfma_us`.
 
     Weights N(0, 0.02) packed on the device; x fp16 N(0, 1). Each GEMM runs
     `steps` times back to back between one pair of events; TFLOP/s =
@@ -630,7 +632,7 @@ def prefill_a16(backend, device, steps, warmup):
             kw = {} if ws is None else {"workspace": ws}
             t = event_time(lambda: plan.run(x, out=out, **kw), steps, warmup, stream)
             fused_us = None
-            if route == "venturi-q4-dense":  # the hand-written fused kernel on the same weights, for comparison
+            if route in ("venturi-q4-dense", "venturi-q8-dense"):  # the fused kernel on the same weights, for comparison
                 fused = resident.prepare(tokens=m, route="mfma")
                 fused_us = round(event_time(lambda: fused.run(x, out=out), steps, warmup, stream) * 1e6, 1)
                 plan.run(x, out=out, **kw)
@@ -654,8 +656,9 @@ def prefill_a16(backend, device, steps, warmup):
             del resident, plan, x, out, ref, ws
         tf = total_flops / total_s / 1e12
         sections[codec] = {"route": route, "TFLOP/s": round(tf, 1),
-                           "roofline": {"bound": "mfma", "kernel": "q8_prefill" if codec == "w8a16" else
-                                        "row_decode + hipBLASLt GEMM" if route == "venturi-q4-dense" else "row_prefill",
+                           "roofline": {"bound": "mfma", "kernel": {"venturi-q4-dense": "row_decode + hipBLASLt GEMM",
+                                                                    "venturi-q8-dense": "q8_split + hipBLASLt GEMM (2K)"}.get(
+                                            route, "q8_prefill" if codec == "w8a16" else "row_prefill"),
                                         "achieved": round(tf, 1), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                         "frac": round(tf / FP16_PEAK_TFLOPS, 4)},
                            "parity": {"against": "canonical-order route" if codec == "w8a16" else
