@@ -10,8 +10,9 @@
  *     Q8 scales fp16 [n][padded/32];
  *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream);
  *   - no entry point allocates device memory or synchronises (except the first
- *     call of venturi_row_dense_run per device and shape, which sets up
- *     hipBLASLt); all buffers are caller-owned. Launches are graph-capturable.
+ *     call of the hipBLASLt-backed entry points, venturi_dense_run and the
+ *     *_dense_run projections, per device and shape); all buffers are
+ *     caller-owned. Launches are graph-capturable.
  * Alignment: venturi_q8_head_run and venturi_q8_embedding_run take Q8 codes
  * at any address, as the reference does (a row-offset view of a plane); the
  * matrix-core Q8 entry points, the A8 projections and their workspaces need
@@ -289,6 +290,18 @@ uint64_t venturi_row_dense_workspace_bytes(int tokens, int n, int k);
 int venturi_row_dense_run(const void* x, const void* codes, const void* high, const void* scales, void* out,
                           int tokens, int n, int k, int padded, int bits, int dtype, void* workspace,
                           uint64_t workspace_bytes, void* stream);
+
+/* The dense bridge of the reference's native runtime (ChunkedDense chunks and
+ * dequant-resident shadows): out[t][n] = x[t][k] * w[n][k]^T, dtype of the
+ * plan 0 fp16 / 1 bf16 / 2 fp32, fp32 arithmetic, workspace (non-null) used as
+ * the GEMM's scratch. create returns NULL with a message for another dtype.
+ * hipBLASLt in place of cuBLAS; the first run per (device, shape, dtype,
+ * workspace size) creates its algorithm (allocates: not under graph capture).
+ * Replaces ops_api.h:21-24 / blocks.cu:674-713. */
+void* venturi_dense_create(int dtype);
+void venturi_dense_destroy(void* plan);
+int venturi_dense_run(void* plan, const void* x, const void* w, void* out, int tokens, int n, int k, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 /* Extension: the Q8 A16 projection in the same dense form, for prefill. The
  * contract scales each exact group dot, so each weight row is decoded to the

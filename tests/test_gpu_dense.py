@@ -390,3 +390,49 @@ def test_q8_dense_rejects_bad_arguments(backend, device):
     assert "256-byte" in lib.error()
     assert lib.venturi_q8_dense_workspace_bytes(70000, n, k) == 0
     torch.cuda.synchronize(device)
+
+
+# ---------------------------------------------------------------------------
+# The dense bridge (venturi_dense_run, blocks.cu:674-713) on hipBLASLt.
+
+_TORCH = {0: torch.float16, 1: torch.bfloat16, 2: torch.float32}
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+@pytest.mark.parametrize("tokens,n,k", [(1, 64, 8), (37, 136, 1000), (300, 64, 5120), (2048, 1024, 512)])
+def test_dense_bridge(backend, device, dtype, tokens, n, k):
+    # out = x w^T in the plan's dtype with fp32 arithmetic: within half an ulp
+    # of the output type plus 2^-19 (2^-17 for fp32 data) of the absolute
+    # product of FP64, and the same bits on a second run.
+    print(f"case dense-bridge dtype={dtype} tokens={tokens} n={n} k={k}", flush=True)
+    lib = backend._native
+    s = torch.cuda.current_stream(device).cuda_stream
+    t = _TORCH[dtype]
+    gen = torch.Generator().manual_seed(tokens + n + k + dtype)
+    x = torch.randn(tokens, k, generator=gen).to(t)
+    w = (torch.randn(n, k, generator=gen) * 0.05).to(t)
+    plan = lib.venturi_dense_create(dtype)
+    assert plan
+    try:
+        ws = torch.empty(4 * 2**20, dtype=torch.uint8, device=device)
+        xd, wd = x.to(device), w.to(device)
+        out = torch.empty(tokens, n, dtype=t, device=device)
+        again = torch.empty_like(out)
+        for o in (out, again):
+            backend._check(lib.venturi_dense_run(plan, xd.data_ptr(), wd.data_ptr(), o.data_ptr(), tokens, n, k,
+                                                 ws.data_ptr(), ws.numel(), s))
+        assert torch.equal(out.view(torch.uint8), again.view(torch.uint8))
+        x64, w64 = x.double().numpy(), w.double().numpy()
+        exact = x64 @ w64.T
+        mag = np.abs(x64) @ np.abs(w64).T
+        half_ulp = {0: 0.5 * ulp16(exact), 1: 2.0 ** (np.floor(np.log2(np.maximum(np.abs(exact), 2.0**-126))) - 8),
+                    2: np.abs(exact) * 2.0**-24}[dtype]
+        bound = half_ulp + (2.0**-17 if dtype == 2 else 2.0**-19) * mag
+        got = out.cpu().double().numpy()
+        assert (np.abs(got - exact) <= bound).all()
+        assert lib.venturi_dense_run(plan, xd.data_ptr(), wd.data_ptr(), out.data_ptr(), tokens, n, k, None, 0, s) == -1
+        assert "null Linear operand" in lib.error()
+        assert lib.venturi_dense_run(plan, xd.data_ptr(), wd.data_ptr(), out.data_ptr(), tokens, n, 0,
+                                     ws.data_ptr(), ws.numel(), s) == -1
+    finally:
+        lib.venturi_dense_destroy(plan)

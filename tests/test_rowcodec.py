@@ -82,3 +82,18 @@ def test_dense_workspace_policy():
     assert lib.venturi_row_dense_workspace_bytes(0, 8, 8) == 0
     assert lib.venturi_row_dense_workspace_bytes(4, 8, 12) == 0 and "k % 8" in lib.error()
     assert lib.venturi_row_dense_workspace_bytes(4, 12, 8) == 0
+
+
+def test_dense_bridge_create_and_destroy():
+    # venturi_dense_create (blocks.cu:674-689): a plan for dtype 0/1/2, NULL with
+    # the reference's message for another; destroy accepts NULL.
+    from venturi_amd import native
+
+    lib = native.load()
+    for dtype in (0, 1, 2):
+        plan = lib.venturi_dense_create(dtype)
+        assert plan
+        lib.venturi_dense_destroy(plan)
+    assert not lib.venturi_dense_create(3)
+    assert "unsupported scalar type" in lib.error()
+    lib.venturi_dense_destroy(None)

@@ -73,22 +73,29 @@ struct Gemm {
 
 struct DeviceBlas {
     hipblasLtHandle_t handle = nullptr;
-    std::map<std::tuple<int, int, int, int>, Gemm> gemms;
+    std::map<std::tuple<int, int, int, int, int, std::uint64_t>, Gemm> gemms;
 };
+
+hipDataType blas_type(int dtype) {
+    require(dtype == kF16 || dtype == kBF16 || dtype == kF32, "unsupported scalar type");
+    return dtype == kF16 ? HIP_R_16F : dtype == kBF16 ? HIP_R_16BF : HIP_R_32F;
+}
 
 std::mutex blas_mutex;
 
 // D (rows x tokens, column-major, ldd = n) = A^T B: A is the shadow chunk
 // (k x rows column-major, i.e. [rows][k] row-major), B is x (k x tokens
 // column-major, i.e. [tokens][k] row-major); D is out[t][begin + j].
-std::pair<hipblasLtHandle_t, const Gemm*> gemm_for(int tokens, int rows, int k, int n) {
+std::pair<hipblasLtHandle_t, const Gemm*> gemm_for(int tokens, int rows, int k, int n, int dtype = kF16,
+                                                   std::uint64_t limit = kBlasBytes) {
     int device = 0;
     check(hipGetDevice(&device));
+    const hipDataType type = blas_type(dtype);
     std::lock_guard<std::mutex> lock(blas_mutex);
     static std::map<int, DeviceBlas> devices;
     DeviceBlas& dev = devices[device];
     if (!dev.handle) blas(hipblasLtCreate(&dev.handle), "handle creation");
-    const auto key = std::make_tuple(tokens, rows, k, n);
+    const auto key = std::make_tuple(dtype, tokens, rows, k, n, limit);
     auto found = dev.gemms.find(key);
     if (found != dev.gemms.end()) return {dev.handle, &found->second};
 
@@ -97,12 +104,11 @@ std::pair<hipblasLtHandle_t, const Gemm*> gemm_for(int tokens, int rows, int k, 
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
     blas(hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)), "transpose A");
     blas(hipblasLtMatmulDescSetAttribute(g.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)), "transpose B");
-    blas(hipblasLtMatrixLayoutCreate(&g.a, HIP_R_16F, k, rows, k), "layout A");
-    blas(hipblasLtMatrixLayoutCreate(&g.b, HIP_R_16F, k, tokens, k), "layout B");
-    blas(hipblasLtMatrixLayoutCreate(&g.d, HIP_R_16F, rows, tokens, n), "layout D");
+    blas(hipblasLtMatrixLayoutCreate(&g.a, type, k, rows, k), "layout A");
+    blas(hipblasLtMatrixLayoutCreate(&g.b, type, k, tokens, k), "layout B");
+    blas(hipblasLtMatrixLayoutCreate(&g.d, type, rows, tokens, n), "layout D");
     hipblasLtMatmulPreference_t pref = nullptr;
     blas(hipblasLtMatmulPreferenceCreate(&pref), "preference creation");
-    const std::uint64_t limit = kBlasBytes;
     blas(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &limit, sizeof(limit)),
          "workspace preference");
     hipblasLtMatmulHeuristicResult_t result{};
@@ -184,10 +190,50 @@ void q8_dense_run(const void* x, const std::int8_t* codes, const __half* scales,
     }
 }
 
+// The reference's dense bridge (venturi_dense_create/run/destroy,
+// blocks.cu:674-713): out[t][n] = x[t][k] w[n][k]^T in the plan's dtype
+// (0 fp16, 1 bf16, 2 fp32) with fp32 arithmetic, the caller's buffer as the
+// GEMM workspace. hipBLASLt in cuBLAS's place; the plan holds only its dtype
+// (the per-device handle and per-shape algorithms are shared, see gemm_for).
+struct DenseLinear {
+    int dtype;
+};
+
+void dense_linear_run(const DenseLinear* p, const void* x, const void* w, void* out, int tokens, int n, int k,
+                      void* workspace, std::uint64_t bytes, hipStream_t stream) {
+    require(p && x && w && out && workspace, "null Linear operand");
+    require(tokens > 0 && n > 0, "invalid shape");
+    require(k > 0, "invalid K");
+    const auto [handle, g] = gemm_for(tokens, n, k, n, p->dtype, bytes);
+    const float alpha = 1.0f, beta = 0.0f;
+    blas(hipblasLtMatmul(handle, g->desc, &alpha, w, g->a, x, g->b, &beta, out, g->d, out, g->d, &g->algo, workspace,
+                         bytes, stream),
+         "GEMM launch");
+}
+
 }  // namespace
 }  // namespace vt
 
 #define VT_EXPORT extern "C" __attribute__((visibility("default")))
+
+VT_EXPORT void* venturi_dense_create(int dtype) {
+    vt::DenseLinear* plan = nullptr;
+    vt::host_guarded([&] {
+        (void)vt::blas_type(dtype);
+        plan = new vt::DenseLinear{dtype};
+    });
+    return plan;
+}
+
+VT_EXPORT void venturi_dense_destroy(void* opaque) { delete static_cast<vt::DenseLinear*>(opaque); }
+
+VT_EXPORT int venturi_dense_run(void* opaque, const void* x, const void* w, void* out, int tokens, int n, int k,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+    return vt::guarded([&] {
+        vt::dense_linear_run(static_cast<const vt::DenseLinear*>(opaque), x, w, out, tokens, n, k, workspace,
+                             workspace_bytes, static_cast<hipStream_t>(stream));
+    });
+}
 
 VT_EXPORT uint64_t venturi_q8_dense_workspace_bytes(int tokens, int n, int k) {
     std::uint64_t bytes = 0;

@@ -67,6 +67,9 @@ SIGNATURES = {
     "venturi_row_dense_workspace_bytes": ([_I] * 3, _U64),
     "venturi_row_dense_run": ([_P] * 5 + [_I] * 6 + [_P, _U64, _P], _I),
     "venturi_q8_dense_workspace_bytes": ([_I] * 3, _U64),
+    "venturi_dense_create": ([_I], _P),
+    "venturi_dense_destroy": ([_P], None),
+    "venturi_dense_run": ([_P] * 4 + [_I] * 3 + [_P, C.c_size_t, _P], _I),
     "venturi_q8_dense_run": ([_P] * 4 + [_I] * 5 + [_P, _U64, _P], _I),
     "venturi_rowcodec_prepare": ([_I] * 5 + [_P], _I),
     "venturi_rowcodec_workspace_bytes": ([_P, _I, _I], _U64),
