@@ -294,7 +294,9 @@ int venturi_row_dense_run(const void* x, const void* codes, const void* high, co
 /* The dense bridge of the reference's native runtime (ChunkedDense chunks and
  * dequant-resident shadows): out[t][n] = x[t][k] * w[n][k]^T, dtype of the
  * plan 0 fp16 / 1 bf16 / 2 fp32, fp32 arithmetic, workspace (non-null) used as
- * the GEMM's scratch. create returns NULL with a message for another dtype.
+ * the GEMM's scratch; x, w, out and workspace 16-byte aligned (the reference's
+ * cuBLAS bridge takes any address; its runtime passes allocations). create
+ * returns NULL with a message for another dtype.
  * hipBLASLt in place of cuBLAS; the first run per (device, shape, dtype,
  * workspace size) creates its algorithm (allocates: not under graph capture).
  * Replaces ops_api.h:21-24 / blocks.cu:674-713. */

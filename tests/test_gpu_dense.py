@@ -434,5 +434,8 @@ def test_dense_bridge(backend, device, dtype, tokens, n, k):
         assert "null Linear operand" in lib.error()
         assert lib.venturi_dense_run(plan, xd.data_ptr(), wd.data_ptr(), out.data_ptr(), tokens, n, 0,
                                      ws.data_ptr(), ws.numel(), s) == -1
+        assert lib.venturi_dense_run(plan, xd.data_ptr() + 2, wd.data_ptr(), out.data_ptr(), tokens, n, k,
+                                     ws.data_ptr(), ws.numel(), s) == -1
+        assert "16-byte" in lib.error()
     finally:
         lib.venturi_dense_destroy(plan)

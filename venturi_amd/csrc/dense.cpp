@@ -204,6 +204,10 @@ void dense_linear_run(const DenseLinear* p, const void* x, const void* w, void* 
     require(p && x && w && out && workspace, "null Linear operand");
     require(tokens > 0 && n > 0, "invalid shape");
     require(k > 0, "invalid K");
+    // hipBLASLt's kernels read operands in 16-byte vectors; the runtime's own
+    // buffers (allocations and whole-row offsets of them) meet this.
+    require(aligned(x, 16) && aligned(w, 16) && aligned(out, 16) && aligned(workspace, 16),
+            "the dense bridge needs 16-byte aligned x, w, out and workspace");
     const auto [handle, g] = gemm_for(tokens, n, k, n, p->dtype, bytes);
     const float alpha = 1.0f, beta = 0.0f;
     blas(hipblasLtMatmul(handle, g->desc, &alpha, w, g->a, x, g->b, &beta, out, g->d, out, g->d, &g->algo, workspace,
