@@ -439,3 +439,34 @@ def test_dense_bridge(backend, device, dtype, tokens, n, k):
         assert "16-byte" in lib.error()
     finally:
         lib.venturi_dense_destroy(plan)
+
+
+def test_dense_chunks_under_graph_capture(backend, device):
+    # A chunked run (decode, GEMM, decode, ...) captured in a HIP graph after an
+    # eager run has created the hipBLASLt state: three replays give the eager bits.
+    n, k, tokens, nbits = 200, 264, 37, 4
+    lib = backend._native
+    packed, high, scales = _planes(n, k, nbits, 17)
+    padded = packed.shape[1] * 2
+    dc, dh, ds = _device_planes(packed, high, scales, nbits, device)
+    size = BLAS_BYTES + 2 * k * 48  # 48-row chunks: five
+    ws = torch.empty(size, dtype=torch.uint8, device=device)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(5)).half().to(device)
+    want = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    out = torch.empty_like(want)
+
+    def run(o):
+        _run(lib, backend, x, dc, dh, ds, o, tokens, n, k, padded, nbits, ws, size,
+             torch.cuda.current_stream(device).cuda_stream)
+
+    run(want)
+    torch.cuda.synchronize(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(out)
+    for _ in range(3):
+        out.fill_(7.0)
+        torch.cuda.synchronize(device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
