@@ -17,11 +17,11 @@
 // Tiling: a workgroup of WM x WN waves computes (WM*TI*16) tokens x
 // (WN*TJ*16) rows; each wave computes TI x TJ MFMA tiles of 16 x 16. Groups
 // are staged one at a time in two LDS buffers: the group's codes (converted
-// to fp16 once per workgroup) and scales. Global loads run PF groups ahead
-// in registers, so their latency is covered by PF compute stages; one
-// barrier per group. LDS rows are 32 halves (four 16-byte units) with the
-// units of row t XOR-swizzled by (t >> 1) & 3, so the 16-byte fragment reads
-// of 16 consecutive rows fall on distinct banks.
+// to fp16 once per workgroup) and scales. Global loads run two groups ahead
+// in registers; one barrier per group. LDS rows are 32 halves (four 16-byte
+// units) with the units of row t XOR-swizzled by (t >> 1) & 3, so the
+// 16-byte fragment reads of 16 consecutive rows fall on distinct banks. The
+// output tile leaves through LDS as 16-byte row units.
 #include "common.hpp"
 
 #include <algorithm>
@@ -77,7 +77,18 @@ struct FastStage {
     unsigned short ws;
 };
 
-template <int P, int WM, int WN, int TI, int TJ, int PF, int SB>
+template <int P, int WM, int WN, int TI, int TJ>
+struct FastLds {
+    using G = FastGeom<P, WM, WN, TI, TJ>;
+    static constexpr int kA = P * G::kTM * 4;   // 16-byte units of one activation buffer
+    static constexpr int kB = G::kTN * 4;       // 16-byte units of one weight buffer
+    static constexpr int kStage = 2 * (kA + kB) * 16 + 2 * (P * G::kTM + G::kTN) * 4;
+    static constexpr int kPitch = G::kTN + 8;   // halves per token row of the output tile
+    static constexpr int kOut = G::kTM * kPitch * 2;
+    static constexpr int kBytes = kStage > kOut ? kStage : kOut;
+};
+
+template <int P, int WM, int WN, int TI, int TJ>
 __global__ __launch_bounds__(WM * WN * 64) void a8_gemm_fast(const std::int8_t* __restrict__ acodes,
                                                             const float* __restrict__ ascales,
                                                             const std::int8_t* __restrict__ wcodes,
@@ -85,12 +96,14 @@ __global__ __launch_bounds__(WM * WN * 64) void a8_gemm_fast(const std::int8_t* 
                                                             __half* __restrict__ out, int tokens, int n, int padded,
                                                             int groups) {
     using G = FastGeom<P, WM, WN, TI, TJ>;
+    using L = FastLds<P, WM, WN, TI, TJ>;
     using Stage = FastStage<P, WM, WN, TI, TJ>;
     constexpr int TM = G::kTM, TN = G::kTN, T = G::kThreads;
-    __shared__ __attribute__((aligned(16))) uint4 a_lds[2 * SB][P * TM * 4];
-    __shared__ __attribute__((aligned(16))) uint4 b_lds[2 * SB][TN * 4];
-    __shared__ __attribute__((aligned(16))) float as_lds[2 * SB][P * TM];
-    __shared__ __attribute__((aligned(16))) float ws_lds[2 * SB][TN];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[L::kBytes];
+    auto* a_lds = reinterpret_cast<uint4(*)[L::kA]>(lds);
+    auto* b_lds = reinterpret_cast<uint4(*)[L::kB]>(lds + 2 * L::kA * 16);
+    auto* as_lds = reinterpret_cast<float(*)[P * TM]>(lds + 2 * (L::kA + L::kB) * 16);
+    auto* ws_lds = reinterpret_cast<float(*)[TN]>(lds + 2 * (L::kA + L::kB) * 16 + 2 * P * TM * 4);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -124,6 +137,8 @@ __global__ __launch_bounds__(WM * WN * 64) void a8_gemm_fast(const std::int8_t* 
         ascales + s_pass * count + static_cast<std::int64_t>(min(t0 + sid % TM, tokens - 1)) * groups;
     const __half* ws_src = wscales + static_cast<std::int64_t>(min(n0 + sid % TN, n - 1)) * (padded / 32);
 
+    // Group g's operands into registers (g is clamped by the caller, so a load
+    // past the last group re-reads it and is never consumed).
     auto load = [&](int g, Stage& s) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < G::kAPer; ++u)
@@ -166,106 +181,136 @@ __global__ __launch_bounds__(WM * WN * 64) void a8_gemm_fast(const std::int8_t* 
 #pragma unroll
         for (int j = 0; j < TJ; ++j) y[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](int buf) __attribute__((always_inline)) {
-        const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    struct Frag {
+        half8 fa[P][TI];
         half8 fb[TJ];
+        float4 asv[P][TI];
         float wsv[TJ];
+    };
+    auto read = [&](int buf, Frag& f) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
             const int row = wn * TJ * 16 + j * 16 + r;
-            fb[j] = __builtin_bit_cast(half8, b_lds[buf][row * 4 + (q ^ swz(row))]);
-            wsv[j] = ws_lds[buf][row];
+            f.fb[j] = __builtin_bit_cast(half8, b_lds[buf][row * 4 + (q ^ swz(row))]);
+            f.wsv[j] = ws_lds[buf][row];
         }
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
             const int tok = wm * TI * 16 + i * 16 + r;
-            half8 fa[P];
-            float4 asv[P];
 #pragma unroll
             for (int p = 0; p < P; ++p) {
-                fa[p] = __builtin_bit_cast(half8, a_lds[buf][(p * TM + tok) * 4 + (q ^ swz(tok))]);
-                asv[p] = *reinterpret_cast<const float4*>(&as_lds[buf][p * TM + wm * TI * 16 + i * 16 + 4 * q]);
-            }
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                if constexpr (P == 1) {
-                    const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[0], fb[j], zero, 0, 0, 0);
-                    const float a4[4] = {asv[0].x, asv[0].y, asv[0].z, asv[0].w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) y[i][j][e] = fmaf(d[e], wsv[j] * a4[e], y[i][j][e]);
-                } else {
-                    const float4v d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[0], fb[j], zero, 0, 0, 0);
-                    const float4v d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[1], fb[j], zero, 0, 0, 0);
-                    const float a0[4] = {asv[0].x, asv[0].y, asv[0].z, asv[0].w};
-                    const float a1[4] = {asv[1].x, asv[1].y, asv[1].z, asv[1].w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float t = fmaf(d1[e], a1[e], d0[e] * a0[e]);
-                        y[i][j][e] = fmaf(t, wsv[j], y[i][j][e]);
-                    }
-                }
+                f.fa[p][i] = __builtin_bit_cast(half8, a_lds[buf][(p * TM + tok) * 4 + (q ^ swz(tok))]);
+                f.asv[p][i] = *reinterpret_cast<const float4*>(&as_lds[buf][p * TM + wm * TI * 16 + i * 16 + 4 * q]);
             }
         }
     };
-
-    // Pipeline: groups are staged SB at a time. The operands of group g are
-    // loaded PF groups earlier, written to LDS slot g % (2 SB) during the
-    // compute of the previous stage, and consumed after the barrier that ends
-    // that stage (one barrier per SB groups).
-    static_assert(PF % SB == 0, "prefetch depth is a whole number of stages");
-    Stage st[PF];
+    // One group: each tile's MFMA is followed by the scaling of an earlier
+    // tile, so one wave's matrix-core work runs under its own VALU epilogue
+    // (the schedule below pins that interleave: the epilogue may not be
+    // gathered after the group's barrier, where both waves of a SIMD would
+    // run their VALU work at once).
+    constexpr int kEpi = P == 1 ? 8 : 12;  // VALU instructions per tile
+    auto math = [&](const Frag& f) __attribute__((always_inline)) {
+        const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < PF; ++s) load(min(s, groups - 1), st[s]);
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int s = 0; s < SB; ++s) {
-        store(st[s], s);
-        if (s + PF < groups) load(s + PF, st[s]);
-    }
-    __syncthreads();
-    const int stages = (groups + SB - 1) / SB;
-    for (int c0 = 0; c0 < stages; c0 += PF / SB) {
+            for (int j = 0; j < TJ; ++j) {
+                if constexpr (P == 1) {
+                    const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.fa[0][i], f.fb[j], zero, 0, 0, 0);
+                    const float a4[4] = {f.asv[0][i].x, f.asv[0][i].y, f.asv[0][i].z, f.asv[0][i].w};
 #pragma unroll
-        for (int cs = 0; cs < PF / SB; ++cs) {
-            const int c = c0 + cs;
-            if (c >= stages) break;
+                    for (int e = 0; e < 4; ++e) y[i][j][e] = fmaf(d[e], f.wsv[j] * a4[e], y[i][j][e]);
+                } else {
+                    const float4v d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.fa[0][i], f.fb[j], zero, 0, 0, 0);
+                    const float4v d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.fa[1][i], f.fb[j], zero, 0, 0, 0);
+                    const float a0[4] = {f.asv[0][i].x, f.asv[0][i].y, f.asv[0][i].z, f.asv[0][i].w};
+                    const float a1[4] = {f.asv[1][i].x, f.asv[1][i].y, f.asv[1][i].z, f.asv[1][i].w};
 #pragma unroll
-            for (int s = 0; s < SB; ++s) {
-                const int g = c * SB + s;
-                if (g < groups) compute(g % (2 * SB));
-            }
-#pragma unroll
-            for (int s = 0; s < SB; ++s) {
-                const int g = (c + 1) * SB + s;  // next stage's group
-                if (g < groups) {
-                    store(st[(cs * SB + SB + s) % PF], g % (2 * SB));
-                    if (g + PF < groups) load(g + PF, st[(cs * SB + SB + s) % PF]);
+                    for (int e = 0; e < 4; ++e) {
+                        const float t = fmaf(d1[e], a1[e], d0[e] * a0[e]);
+                        y[i][j][e] = fmaf(t, f.wsv[j], y[i][j][e]);
+                    }
                 }
             }
-            __syncthreads();
+#pragma unroll
+        for (int t = 0; t < TI * TJ; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, P, 0);     // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, kEpi, 0);  // VALU
         }
+    };
+
+    // Pipeline over groups, two LDS buffers and two register stages: while
+    // group g is multiplied out of buffer g % 2, group g + 1 (loaded two
+    // groups earlier) is converted into the other buffer and group g + 3 is
+    // requested; one barrier per group. The body of a step has no branches
+    // on g, so the scheduler sees the fragment reads, the conversion and the
+    // interleaved MFMA / VALU work as one region.
+    Stage st0, st1;
+    load(0, st0);
+    load(min(1, groups - 1), st1);
+    store(st0, 0);
+    load(min(2, groups - 1), st0);
+    __syncthreads();
+    int g = 0;
+    for (; g + 1 < groups; g += 2) {
+        Frag f;
+        read(0, f);
+        store(st1, 1);
+        load(min(g + 3, groups - 1), st1);
+        math(f);
+        __syncthreads();
+        read(1, f);
+        store(st0, 0);
+        load(min(g + 4, groups - 1), st0);
+        math(f);
+        __syncthreads();
+    }
+    if (g < groups) {
+        Frag f;
+        read(0, f);
+        math(f);
+        __syncthreads();
     }
 
+    // Output tile: fp16 through LDS (token rows of TN halves, padded by 8 so
+    // the four token quads of a wave's 2-byte writes fall on distinct banks),
+    // then 16-byte row units to HBM.
+    auto* o_lds = reinterpret_cast<__half*>(lds);
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            const int row = n0 + wn * TJ * 16 + j * 16 + r;
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = t0 + wm * TI * 16 + i * 16 + 4 * q + e;
-                if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(y[i][j][e]);
-            }
+            for (int e = 0; e < 4; ++e)
+                o_lds[(wm * TI * 16 + i * 16 + 4 * q + e) * L::kPitch + wn * TJ * 16 + j * 16 + r] =
+                    from_f32<__half>(y[i][j][e]);
+    __syncthreads();
+    const bool vec = (n % 8) == 0 && (reinterpret_cast<std::uintptr_t>(out) & 15) == 0;
+    constexpr int kUnits = TM * TN / 8;
+#pragma unroll
+    for (int u = tid; u < kUnits; u += T) {
+        const int tok = u / (TN / 8), c = (u % (TN / 8)) * 8;
+        const int t = t0 + tok, col = n0 + c;
+        if (t >= tokens || col >= n) continue;
+        const __half* src = o_lds + tok * L::kPitch + c;
+        __half* dst = out + static_cast<std::int64_t>(t) * n + col;
+        if (vec) {
+            *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+        } else {
+            for (int e = 0; e < 8 && col + e < n; ++e) dst[e] = src[e];
         }
+    }
 }
 
-template <int P, int WM, int WN, int TI, int TJ, int PF, int SB = 1>
+template <int P, int WM, int WN, int TI, int TJ>
 void launch_fast(const std::int8_t* acodes, const float* ascales, const std::int8_t* codes, const __half* scales,
                  __half* out, int tokens, int n, int padded, int groups, hipStream_t stream) {
     using G = FastGeom<P, WM, WN, TI, TJ>;
     const dim3 grid((n + G::kTN - 1) / G::kTN, (tokens + G::kTM - 1) / G::kTM);
     require(grid.y <= 65535, "token tiles exceed the launch grid");
-    a8_gemm_fast<P, WM, WN, TI, TJ, PF, SB><<<grid, G::kThreads, 0, stream>>>(acodes, ascales, codes, scales, out, tokens,
-                                                                          n, padded, groups);
+    a8_gemm_fast<P, WM, WN, TI, TJ><<<grid, G::kThreads, 0, stream>>>(acodes, ascales, codes, scales, out, tokens, n,
+                                                                     padded, groups);
 }
 
 }  // namespace
@@ -278,9 +323,9 @@ void a8_fast_launch(const void* workspace, const std::int8_t* codes, const __hal
     const auto* ascales = reinterpret_cast<const float*>(acodes + count * 32 * passes);
     auto* y = static_cast<__half*>(out);
     if (passes == 1)
-        launch_fast<1, 4, 2, 4, 4, 2>(acodes, ascales, codes, scales, y, tokens, n, padded, groups, stream);
+        launch_fast<1, 4, 2, 4, 4>(acodes, ascales, codes, scales, y, tokens, n, padded, groups, stream);
     else
-        launch_fast<2, 4, 2, 2, 4, 2>(acodes, ascales, codes, scales, y, tokens, n, padded, groups, stream);
+        launch_fast<2, 4, 2, 2, 4>(acodes, ascales, codes, scales, y, tokens, n, padded, groups, stream);
 }
 
 }  // namespace vt

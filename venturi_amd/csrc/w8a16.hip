@@ -80,9 +80,13 @@ __global__ __launch_bounds__(WM * WN * 64) void q8_prefill(const __half* __restr
     using G = PrefillGeom<WM, WN, TI, TJ, GS>;
     using Stage = PrefillStage<WM, WN, TI, TJ, GS>;
     constexpr int TM = G::kTM, TN = G::kTN, T = G::kThreads, U = G::kU;
-    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][TM * U];
-    __shared__ __attribute__((aligned(16))) uint4 b_lds[2][TN * U];
-    __shared__ __attribute__((aligned(16))) float ws_lds[2][GS][TN];
+    constexpr int kStageBytes = 2 * (TM + TN) * U * 16 + 2 * GS * TN * 4;
+    constexpr int kPitch = TN + 8;  // halves per token row of the output tile
+    constexpr int kBytes = kStageBytes > TM * kPitch * 2 ? kStageBytes : TM * kPitch * 2;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kBytes];
+    auto* a_lds = reinterpret_cast<uint4(*)[TM * U]>(lds);
+    auto* b_lds = reinterpret_cast<uint4(*)[TN * U]>(lds + 2 * TM * U * 16);
+    auto* ws_lds = reinterpret_cast<float(*)[GS][TN]>(lds + 2 * (TM + TN) * U * 16);
     const int stages = (groups + GS - 1) / GS;
 
     const int tid = threadIdx.x;
@@ -164,65 +168,118 @@ __global__ __launch_bounds__(WM * WN * 64) void q8_prefill(const __half* __restr
 #pragma unroll
         for (int j = 0; j < TJ; ++j) y[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](int buf) __attribute__((always_inline)) {
-        const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    // A stage's fragments, read from LDS before the next stage is converted
+    // into the other buffer, so the conversion covers the read latency.
+    struct Frag {
+        half8 fa[GS][TI];
+        half8 fb[GS][TJ];
+        float wsv[GS][TJ];
+    };
+    auto read = [&](int buf, Frag& f) __attribute__((always_inline)) {
 #pragma unroll
-        for (int gg = 0; gg < GS; ++gg) {  // groups in natural order
-            half8 fb[TJ];
-            float wsv[TJ];
+        for (int gg = 0; gg < GS; ++gg) {
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
                 const int row = wn * TJ * 16 + j * 16 + r;
-                fb[j] = __builtin_bit_cast(half8, b_lds[buf][row * U + ((4 * gg + q) ^ swizzle<U>(row))]);
-                wsv[j] = ws_lds[buf][gg][row];
+                f.fb[gg][j] = __builtin_bit_cast(half8, b_lds[buf][row * U + ((4 * gg + q) ^ swizzle<U>(row))]);
+                f.wsv[gg][j] = ws_lds[buf][gg][row];
             }
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
                 const int tok = wm * TI * 16 + i * 16 + r;
-                const half8 fa = __builtin_bit_cast(half8, a_lds[buf][tok * U + ((4 * gg + q) ^ swizzle<U>(tok))]);
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) {
-                    const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa, fb[j], zero, 0, 0, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) y[i][j][e] = fmaf(d[e], wsv[j], y[i][j][e]);
-                }
+                f.fa[gg][i] = __builtin_bit_cast(half8, a_lds[buf][tok * U + ((4 * gg + q) ^ swizzle<U>(tok))]);
             }
         }
     };
+    // Groups in natural order; each tile's MFMA is followed by the scaling of
+    // an earlier tile (the schedule below pins the interleave, so the matrix
+    // cores run under the wave's own VALU work instead of the epilogue being
+    // gathered after the stage's barrier).
+    auto math = [&](const Frag& f) __attribute__((always_inline)) {
+        const float4v zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int gg = 0; gg < GS; ++gg)
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) {
+                    const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.fa[gg][i], f.fb[gg][j], zero, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) y[i][j][e] = fmaf(d[e], f.wsv[gg][j], y[i][j][e]);
+                }
+#pragma unroll
+        for (int t = 0; t < GS * TI * TJ; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+        }
+    };
 
-    // Stage s is loaded PF stages ahead, written to LDS buffer s % 2 during
-    // the compute of stage s - 1, and consumed after the barrier that ends it.
+    // Stage s is loaded PF stages ahead into register stage s % PF, converted
+    // into LDS buffer s % 2 while stage s - 1 is multiplied out, and consumed
+    // after the barrier that ends that step. Full rounds of PF steps have no
+    // branch on the stage index (loads and stores past the last stage are
+    // clamped and never consumed); the last partial round is guarded.
+    static_assert(PF % 2 == 0, "the buffer parity of a step is fixed within a round");
     Stage st[PF];
 #pragma unroll
     for (int s = 0; s < PF; ++s) load(min(s, stages - 1), st[s]);
     store(st[0], 0, 0);
-    if (PF < stages) load(PF, st[0]);
+    load(min(PF, stages - 1), st[0]);
     __syncthreads();
-    for (int g0 = 0; g0 < stages; g0 += PF) {
+    int g0 = 0;
+    for (; g0 + PF <= stages; g0 += PF) {
 #pragma unroll
         for (int s = 0; s < PF; ++s) {
-            const int g = g0 + s;
-            if (g >= stages) break;
-            compute(g & 1);
-            if (g + 1 < stages) {
-                store(st[(s + 1) % PF], g + 1, (g + 1) & 1);
-                if (g + 1 + PF < stages) load(g + 1 + PF, st[(s + 1) % PF]);
-            }
+            Frag f;
+            read(s & 1, f);
+            const int nxt = min(g0 + s + 1, stages - 1);
+            store(st[(s + 1) % PF], nxt, (s + 1) & 1);
+            load(min(g0 + s + 1 + PF, stages - 1), st[(s + 1) % PF]);
+            math(f);
             __syncthreads();
         }
     }
+    if (g0 < stages) {
+#pragma unroll
+        for (int s = 0; s < PF; ++s) {
+            if (g0 + s < stages) {
+                Frag f;
+                read(s & 1, f);
+                store(st[(s + 1) % PF], min(g0 + s + 1, stages - 1), (s + 1) & 1);
+                math(f);
+                __syncthreads();
+            }
+        }
+    }
 
+    // Output tile: fp16 through LDS (token rows padded by 8 halves so the four
+    // token quads of a wave's 2-byte writes fall on distinct banks), then
+    // 16-byte row units to HBM.
+    auto* o_lds = reinterpret_cast<__half*>(lds);
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            const int row = n0 + wn * TJ * 16 + j * 16 + r;
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = t0 + wm * TI * 16 + i * 16 + 4 * q + e;
-                if (t < tokens && row < n) out[static_cast<std::int64_t>(t) * n + row] = from_f32<__half>(y[i][j][e]);
-            }
+            for (int e = 0; e < 4; ++e)
+                o_lds[(wm * TI * 16 + i * 16 + 4 * q + e) * kPitch + wn * TJ * 16 + j * 16 + r] =
+                    from_f32<__half>(y[i][j][e]);
+    __syncthreads();
+    const bool vec = (n % 8) == 0 && (reinterpret_cast<std::uintptr_t>(out) & 15) == 0;
+    constexpr int kUnits = TM * TN / 8;
+#pragma unroll
+    for (int u = tid; u < kUnits; u += T) {
+        const int tok = u / (TN / 8), c = (u % (TN / 8)) * 8;
+        const int t = t0 + tok, col = n0 + c;
+        if (t >= tokens || col >= n) continue;
+        const __half* src = o_lds + tok * kPitch + c;
+        __half* dst = out + static_cast<std::int64_t>(t) * n + col;
+        if (vec) {
+            *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+        } else {
+            for (int e = 0; e < 8 && col + e < n; ++e) dst[e] = src[e];
         }
+    }
 }
 
 template <int WM, int WN, int TI, int TJ, int PF, int GS = 1>
@@ -316,7 +373,7 @@ void q8_prefill_launch(const void* x, const std::int8_t* codes, const __half* sc
     if (big_grid < 384)
         launch_prefill<2, 4, 4, 2, 2, 2>(xp, codes, scales, op, tokens, n, k, padded, stream);
     else
-        launch_prefill<4, 2, 4, 4, 4, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
+        launch_prefill<4, 2, 4, 4, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
 }
 
 }  // namespace vt
