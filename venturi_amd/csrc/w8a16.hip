@@ -15,7 +15,8 @@
 // and weight rows (32 GS codes converted to fp16 once per workgroup) plus the
 // weight scales. Global loads run PF stages ahead in registers; one barrier
 // per stage. LDS rows are 4 GS 16-byte units XOR-swizzled by (row >> 1) so
-// that 16 consecutive rows' fragment reads fall on distinct banks.
+// that 16 consecutive rows' fragment reads fall on distinct banks. The output
+// tile leaves through LDS as 16-byte row units.
 #include "common.hpp"
 
 namespace vt {
