@@ -22,8 +22,13 @@ import numpy as np
 
 
 def silu_fp16(gate):
+    """F.silu on fp16 (flash_next_q4.py:222): fp16(g / (1 + e^-g)) evaluated in fp32.
+
+    Pinned against FP64 over every finite fp16 input (tests/test_silu_oracle.py).
+    """
     g = np.asarray(gate, dtype=np.float16).astype(np.float32)
-    return (g / (np.float32(1.0) + np.exp(-g))).astype(np.float16)
+    with np.errstate(over="ignore"):  # e^-g overflows to inf for g < -88.7: g / inf = -0, as in fp32
+        return (g / (np.float32(1.0) + np.exp(-g))).astype(np.float16)
 
 
 def fp16_mul(a, b):
