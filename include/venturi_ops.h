@@ -381,6 +381,48 @@ int venturi_rowcodec_project(const VRCPlan* plan, const void* x, const void* cod
                              const void* scales, void* out, void* workspace, uint64_t available, int tokens, int n,
                              int k, int padded, int packed, void* stream);
 
+/* ---- Reference exports outside the quantized-linear path. The reference's
+ * Python backend binds each of these when it is constructed
+ * (blocks.py:336-427), so they are exported with the reference's signatures;
+ * every call returns -1 with the message "<name>: not built for gfx950
+ * (outside the quantized-linear path)", makes no HIP call and writes nothing. ---- */
+
+/* ops_api.h:46-47 */
+int venturi_greedy_run(const void* logits, int64_t* out, void* workspace, size_t workspace_bytes, int rows,
+                       int vocab, int dtype, void* stream);
+/* ops_api.h:30-31 */
+int venturi_fp32_linear_run(const void* x, const float* w, void* out, int tokens, int n, int k, int dtype,
+                            void* stream);
+/* ops_api.h:95-96 */
+int venturi_rope_run(const void* x, const float* cos, const float* sin, void* out, int tokens, int heads, int d,
+                     int r, int interleaved, int dtype, void* stream);
+/* ops_api.h:87-90 */
+int venturi_qwen_qk_run(const void* qg, const void* key, const float* qgamma, const float* kgamma, const float* cos,
+                        const float* sin, void* qout, void* kout, int tokens, int hq, int hkv, int d, int r,
+                        int dtype, float epsilon, void* stream);
+/* ops_api.h:85-86 */
+int venturi_qwen_gate_run(const void* x, const void* qg, void* out, int tokens, int heads, int d, int dtype,
+                          void* stream);
+/* ops_api.h:13-15 */
+int venturi_attention_run(const void* q, const void* k, const void* v, void* out, int tokens, int kv_tokens, int hq,
+                          int hkv, int d, int dtype, float scale, void* stream);
+/* ops_api.h:28-29 */
+int venturi_embedding_run(const void* weight, const int64_t* ids, void* out, int tokens, int vocab, int hidden,
+                          int dtype, void* stream);
+/* ops_api.h:42-44 */
+int venturi_gdn_run(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                    const float* state, void* out, float* state_out, int tokens, int hqk, int hv, int dk, int dv,
+                    int normalize, int packed, int dtype, float scale, void* stream);
+/* ops_api.h:19-20 */
+int venturi_conv_run(const void* x, const void* w, const void* history, void* out, void* history_out, int tokens,
+                     int channels, int kernel, int dtype, int fp32_weight, void* stream);
+/* ops_api.h:34-35 */
+int venturi_gates_run(const void* a, const void* b, const float* rate, const float* bias, float* g, float* beta,
+                      int tokens, int heads, int dtype, int round_beta, void* stream);
+/* ops_api.h:32-33 */
+int venturi_gated_rms_run(const void* x, const void* z, const void* w, void* out, int tokens, int heads,
+                          int features, int dtype, int fp32_weight, float epsilon, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -399,12 +399,17 @@ _TORCH = {0: torch.float16, 1: torch.bfloat16, 2: torch.float32}
 
 
 @pytest.mark.parametrize("dtype", [0, 1, 2])
-@pytest.mark.parametrize("tokens,n,k", [(1, 64, 8), (37, 136, 1000), (300, 64, 5120), (2048, 1024, 512)])
-def test_dense_bridge(backend, device, dtype, tokens, n, k):
+@pytest.mark.parametrize("tokens,n,k,ws_mib", [
+    (1, 64, 8, 4), (37, 136, 1000, 4), (300, 64, 5120, 4), (2048, 1024, 512, 4),
+    # odd K (the reference bridge takes any k > 0) and a workspace above the
+    # 32 MiB share, where the heuristic may pick split-K kernels
+    (37, 136, 1001, 64), (5, 24, 13, 64), (2048, 1024, 512, 64), (300, 64, 5120, 64),
+])
+def test_dense_bridge(backend, device, dtype, tokens, n, k, ws_mib):
     # out = x w^T in the plan's dtype with fp32 arithmetic: within half an ulp
     # of the output type plus 2^-19 (2^-17 for fp32 data) of the absolute
     # product of FP64, and the same bits on a second run.
-    print(f"case dense-bridge dtype={dtype} tokens={tokens} n={n} k={k}", flush=True)
+    print(f"case dense-bridge dtype={dtype} tokens={tokens} n={n} k={k} workspace={ws_mib} MiB", flush=True)
     lib = backend._native
     s = torch.cuda.current_stream(device).cuda_stream
     t = _TORCH[dtype]
@@ -414,7 +419,7 @@ def test_dense_bridge(backend, device, dtype, tokens, n, k):
     plan = lib.venturi_dense_create(dtype)
     assert plan
     try:
-        ws = torch.empty(4 * 2**20, dtype=torch.uint8, device=device)
+        ws = torch.empty(ws_mib * 2**20, dtype=torch.uint8, device=device)
         xd, wd = x.to(device), w.to(device)
         out = torch.empty(tokens, n, dtype=t, device=device)
         again = torch.empty_like(out)

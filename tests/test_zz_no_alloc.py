@@ -45,6 +45,38 @@ def _case(handle, fn, device, n, k, tokens, seed):
     assert bool((slots.view(torch.int64) == SLOT_IDLE).all())
 
 
+def test_first_call_on_a_side_stream_then_another_stream(lib, device):
+    # Collected first in this file, so in a fresh process this is the call that
+    # fills the static slots: on a side stream. The next call runs on the
+    # current stream, ordered after the side stream's work by an event only
+    # (no host synchronisation), and must find idle slots.
+    handle, fn = lib
+    n, k, tokens = 5120, 6144, 4
+    codes, scales = random_q8(n, k, 73)
+    tc, ts = tile_q8(codes.to(device), scales.to(device))
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(73)).half().to(device)
+    main = torch.cuda.current_stream(device)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(main)
+    first = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    with torch.cuda.stream(side):
+        handle.check(fn(x.data_ptr(), tc.data_ptr(), ts.data_ptr(), first.data_ptr(), tokens, n, k, k, 0,
+                        side.cuda_stream))
+    main.wait_stream(side)
+    second = torch.empty_like(first)
+    handle.check(fn(x.data_ptr(), tc.data_ptr(), ts.data_ptr(), second.data_ptr(), tokens, n, k, k, 0,
+                    main.cuda_stream))
+    size = handle.venturi_q8_tiled_workspace_bytes(tokens, n, 0)
+    slots = torch.empty(size, dtype=torch.uint8, device=device)
+    handle.check(handle.venturi_q8_tiled_workspace_init(slots.data_ptr(), size, main.cuda_stream))
+    want = torch.empty_like(first)
+    handle.check(handle.venturi_q8_tiled_run(x.data_ptr(), tc.data_ptr(), ts.data_ptr(), want.data_ptr(), tokens, n,
+                                             k, k, 0, slots.data_ptr(), size, main.cuda_stream))
+    torch.cuda.synchronize(device)
+    assert torch.equal(first.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(second.view(torch.int16), want.view(torch.int16))
+
+
 def test_noalloc_equals_workspace_entry_point(lib, device):
     handle, fn = lib
     _case(handle, fn, device, 5120, 6144, 4, 71)  # split K, 320 row blocks

@@ -20,7 +20,8 @@ from pathlib import Path
 import torch
 
 from . import native
-from .blocks import _overlaps, is_gfx950
+from .blocks import is_gfx950
+from .operands import overlapping
 from .weights import Q4RowSplitWeight
 
 _MAX_TOKENS = 4 * 65535
@@ -160,7 +161,7 @@ class PreparedLinear:
         self._weight.validate()
         self._check("x", x, self.in_features)
         self._check("out", out, self.out_features)
-        if any(_overlaps(out, t) for t in (x, self._weight.codes, self._weight.scales)):
+        if any(overlapping(out, t) for t in (x, self._weight.codes, self._weight.scales)):
             raise ValueError("output must not alias input or weight storage")
         codes, scales, n, k, padded, tokens, dtype_code, route = self._launch
         with torch.cuda.device(self.device):

@@ -8,69 +8,16 @@ synchronisation or implicit cast, so they can be captured in HIP graphs.
 Every kernel is called through the C ABI of libventuri_ops.so.
 """
 
-import ctypes
 from dataclasses import dataclass
-import math
 
 import torch
 
 from . import native
 from .backend import Backend, BackendCapabilities, OperatorSupport, UnsupportedOperationError
+from .operands import DTYPE_CODES, admit, disjoint, epsilon as admit_epsilon, extents, stream_of
 from .weights import DenseWeight, Q4RowSplitWeight, Q8RowSplitWeight
 
-_DTYPES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
-
 Q8_ROUTES = ("auto", "exact", "mfma", "dense")
-
-
-def _shape(tokens, features):
-    if any(type(v) is not int or not 0 < v < 2**31 for v in (tokens, features)):
-        raise ValueError("tokens and features must be positive int32 values")
-    return (tokens, features)
-
-
-def _tensor(tensor, shape, dtype, device, name):
-    if not isinstance(tensor, torch.Tensor):
-        raise TypeError(f"{name} must be a tensor")
-    if tensor.shape != shape or tensor.dtype != dtype or tensor.device != device:
-        raise ValueError(f"{name} requires shape {shape}, dtype {dtype}, device {device}")
-    if not tensor.is_contiguous():
-        raise ValueError(f"{name} must be contiguous; no implicit copy")
-    if torch.is_grad_enabled() and tensor.requires_grad:
-        raise ValueError("Prepared operators are inference-only")
-
-
-def _overlaps(a, b):
-    """Byte-interval overlap of two contiguous tensors on one device."""
-    return a.device == b.device and max(a.data_ptr(), b.data_ptr()) < min(
-        a.data_ptr() + a.numel() * a.element_size(), b.data_ptr() + b.numel() * b.element_size()
-    )
-
-
-def _no_overlap(out, operands, *, allow_inplace=False):
-    for operand in operands:
-        if _overlaps(out, operand) and not (
-            allow_inplace
-            and out.data_ptr() == operand.data_ptr()
-            and out.shape == operand.shape
-            and out.dtype == operand.dtype
-        ):
-            raise ValueError("output/workspace must not alias operand storage")
-
-
-def _epsilon(value):
-    if (
-        type(value) not in (float, int)
-        or not math.isfinite(value)
-        or not torch.finfo(torch.float32).tiny <= value <= torch.finfo(torch.float32).max
-        or ctypes.c_float(value).value == 0
-    ):
-        raise ValueError("epsilon must be finite, positive, and a normal FP32 value")
-    return float(value)
-
-
-def _stream(device):
-    return torch.cuda.current_stream(device).cuda_stream
 
 
 @dataclass(frozen=True)
@@ -97,7 +44,7 @@ class ResidentLinear:
         raise UnsupportedOperationError("Embedding lookup is defined for Q8 weights only")
 
     def prepare(self, *, tokens, route="auto"):
-        _shape(tokens, self.in_features)
+        extents(tokens, self.in_features)
         self._backend.validate_device(self.dtype, self.device)
         return self._backend.bind_linear(self, tokens=tokens, route=route)
 
@@ -107,7 +54,7 @@ class ResidentLinear:
         output is [tokens, inter]."""
         from .vocabulary import ResidentQ8Vocabulary
 
-        _shape(tokens, self.in_features)
+        extents(tokens, self.in_features)
         if not isinstance(self._payload, ResidentQ8Vocabulary):
             raise UnsupportedOperationError("The fused SwiGLU projection is defined for Q8 weights only")
         return _Q8Linear(self._payload.prepare_swiglu(tokens=tokens))
@@ -139,7 +86,7 @@ class ResidentRMSNorm:
         return self._weight.numel()
 
     def prepare(self, *, tokens):
-        _shape(tokens, self.features)
+        extents(tokens, self.features)
         self._backend.validate_device(self.dtype, self.device)
         return self._backend.bind_rmsnorm(self, tokens=tokens)
 
@@ -147,8 +94,11 @@ class ResidentRMSNorm:
 def _capabilities():
     devices = frozenset(("cuda",))
     quant = frozenset((torch.float16, torch.bfloat16))
+    floating = frozenset((torch.float16, torch.bfloat16, torch.float32))
     operators = [
-        OperatorSupport("rmsnorm", devices, frozenset((torch.float16, torch.bfloat16, torch.float32))),
+        OperatorSupport("rmsnorm", devices, floating),
+        OperatorSupport("swiglu", devices, floating),
+        OperatorSupport("add", devices, floating),
         OperatorSupport("linear", devices, quant, "q8_g32_fp16", "row_split_k128_v1"),
         OperatorSupport("embedding", devices, quant, "q8_g32_fp16", "row_split_k128_v1"),
         OperatorSupport("linear", devices, quant, "q4_g64_fp16", "row_split_k128_v1"),
@@ -181,29 +131,42 @@ class HipBackend(Backend):
         return self._native.check(status)
 
     def validate_device(self, dtype, device):
-        if dtype not in _DTYPES:
+        if dtype not in DTYPE_CODES:
             raise ValueError("Native blocks require FP16, BF16 or FP32")
         return self.resolve_device(device)
 
     def resolve_device(self, device):
-        target = torch.device(device)
-        if target.type != "cuda":
+        """The concrete gfx950 device a request names; refused during graph capture."""
+        requested = torch.device(device)
+        if requested.type != "cuda":
             raise ValueError("HipBackend requires an explicit GPU device")
-        with torch.cuda.device(target):
-            target = torch.device("cuda", torch.cuda.current_device())
-            if torch.cuda.is_current_stream_capturing():
-                raise RuntimeError("Preparation must run outside graph capture")
-            if not is_gfx950(target):
-                raise ValueError("libventuri_ops.so is built for gfx950 (MI355X) only")
+        with torch.cuda.device(requested):
+            index = torch.cuda.current_device()
+            capturing = torch.cuda.is_current_stream_capturing()
+        if capturing:
+            raise RuntimeError("Preparation must run outside graph capture")
+        target = torch.device("cuda", index)
+        if not is_gfx950(target):
+            raise ValueError("libventuri_ops.so is built for gfx950 (MI355X) only")
         return target
 
     def empty(self, shape, *, dtype, device):
-        if not isinstance(shape, (list, tuple)) or any(type(d) is not int or not 0 <= d < 2**31 for d in shape):
+        """Uninitialised device tensor for caller-owned buffers (outputs, workspaces)."""
+        valid_shape = isinstance(shape, (list, tuple)) and all(type(d) is int and 0 <= d < 2**31 for d in shape)
+        if not valid_shape:
             raise ValueError("Allocation shape must contain nonnegative int32 extents")
         if not isinstance(dtype, torch.dtype):
             raise TypeError("Allocation requires an explicit torch.dtype")
-        target = self.validate_device(dtype, device) if dtype.is_floating_point else self.resolve_device(device)
-        return torch.empty(tuple(shape), dtype=dtype, device=target)
+        # Floating buffers must be a dtype the kernels take; byte and index buffers only a device.
+        check = self.validate_device if dtype.is_floating_point else lambda _, d: self.resolve_device(d)
+        return torch.empty(tuple(shape), dtype=dtype, device=check(dtype, device))
+
+    def _launch(self, entry, device, *operands):
+        """Calls one C entry point on `device`'s current stream: tensors pass as data pointers,
+        every other operand as it is; a -1 return raises the library's message."""
+        arguments = [v.data_ptr() if isinstance(v, torch.Tensor) else v for v in operands]
+        with torch.cuda.device(device):
+            self._check(getattr(self._native, entry)(*arguments, stream_of(device)))
 
     def synchronize(self, device):
         torch.cuda.synchronize(self.resolve_device(device))
@@ -248,7 +211,7 @@ class HipBackend(Backend):
             raise ValueError("Device Q8 packing supports fp16/bf16/fp32 sources")
         target = self.resolve_device(source.device)
         n, k = source.shape
-        _shape(n, k)
+        extents(n, k)
         padded = (k + 127) // 128 * 128
         with torch.cuda.device(target):
             if not bool(torch.isfinite(source).all()):
@@ -259,8 +222,8 @@ class HipBackend(Backend):
             scales = torch.empty(n, padded // 32, dtype=torch.float16, device=target)
             self._check(
                 self._native.venturi_q8_pack_run(
-                    source.data_ptr(), codes.data_ptr(), scales.data_ptr(), n, k, padded, _DTYPES[source.dtype],
-                    _stream(target),
+                    source.data_ptr(), codes.data_ptr(), scales.data_ptr(), n, k, padded, DTYPE_CODES[source.dtype],
+                    stream_of(target),
                 )
             )
         return Q8RowSplitWeight(codes, scales, k)
@@ -280,7 +243,7 @@ class HipBackend(Backend):
             raise ValueError("Device Q4 packing supports fp16/bf16/fp32 sources")
         target = self.resolve_device(source.device)
         n, k = source.shape
-        _shape(n, k)
+        extents(n, k)
         padded = (k + 127) // 128 * 128
         with torch.cuda.device(target):
             if not bool(torch.isfinite(source).all()):
@@ -292,14 +255,14 @@ class HipBackend(Backend):
             scales = torch.empty(n, padded // 64, dtype=torch.float16, device=target)
             self._check(
                 self._native.venturi_q4_pack_run(
-                    source.data_ptr(), codes.data_ptr(), scales.data_ptr(), n, k, padded, _DTYPES[source.dtype],
-                    _stream(target),
+                    source.data_ptr(), codes.data_ptr(), scales.data_ptr(), n, k, padded, DTYPE_CODES[source.dtype],
+                    stream_of(target),
                 )
             )
         return Q4RowSplitWeight(codes, scales, k)
 
     def bind_linear(self, resident, *, tokens, route="auto"):
-        _shape(tokens, 1)
+        extents(tokens, 1)
         if resident._backend is not self:
             raise ValueError("Resident weight belongs to a different backend instance")
         from .vocabulary import ResidentQ8Vocabulary
@@ -309,32 +272,48 @@ class HipBackend(Backend):
         return resident._payload.prepare(tokens=tokens, route=route)
 
     def prepare_linear(self, weight, *, tokens, dtype, device):
-        _shape(tokens, 1)
+        extents(tokens, 1)
         return self.upload_linear(weight, dtype=dtype, device=device).prepare(tokens=tokens)
 
-    # -- rmsnorm -----------------------------------------------------------
+    # -- rmsnorm and the elementwise blocks of the gated MLP ---------------
     def upload_rmsnorm(self, weight, *, dtype, device, epsilon):
-        if not isinstance(weight, torch.Tensor) or weight.ndim != 1 or not weight.is_floating_point():
+        """Owned fp32 copy of a norm vector (the kernel reads gamma in fp32 for every dtype)."""
+        is_vector = isinstance(weight, torch.Tensor) and weight.ndim == 1 and weight.is_floating_point()
+        if not is_vector:
             raise ValueError("RMSNorm weight must be a floating-point vector")
-        _shape(1, weight.numel())
-        epsilon = _epsilon(epsilon)
+        extents(1, weight.numel())
+        eps = admit_epsilon(epsilon)
         target = self.validate_device(dtype, device)
         with torch.cuda.device(target):
-            owned = weight.detach().to(device=target, dtype=torch.float32, copy=True).contiguous()
-            if not bool(torch.isfinite(owned).all()):
-                raise ValueError("RMSNorm weight must be finite in FP32")
-            torch.cuda.current_stream(target).synchronize()
-        return ResidentRMSNorm(self, owned, dtype, epsilon)
+            gamma = torch.empty(weight.numel(), dtype=torch.float32, device=target)
+            gamma.copy_(weight.detach())
+            finite = bool(torch.isfinite(gamma).all())  # synchronises: the copy is complete
+        if not finite:
+            raise ValueError("RMSNorm weight must be finite in FP32")
+        return ResidentRMSNorm(self, gamma, dtype, eps)
 
-    def bind_rmsnorm(self, resident, *, tokens):
-        _shape(tokens, 1)
+    def _owned_by_me(self, resident):
         if resident._backend is not self:
             raise ValueError("Resident weight belongs to a different backend instance")
+
+    def bind_rmsnorm(self, resident, *, tokens):
+        extents(tokens, 1)
+        self._owned_by_me(resident)
         return _RMSNorm(self, resident._weight, tokens, resident.dtype, resident.epsilon)
 
     def prepare_rmsnorm(self, weight, *, tokens, dtype, device, epsilon):
-        _shape(tokens, 1)
+        extents(tokens, 1)
         return self.upload_rmsnorm(weight, dtype=dtype, device=device, epsilon=epsilon).prepare(tokens=tokens)
+
+    def prepare_swiglu(self, *, tokens, features, dtype, device):
+        """Plan of out = cast((a * sigmoid(a)) * b) over [tokens, features] (blocks.py:565-572)."""
+        shape = extents(tokens, features)
+        return _Pointwise(self, shape, dtype, self.validate_device(dtype, device), "venturi_swiglu_run")
+
+    def prepare_add(self, *, tokens, features, dtype, device):
+        """Plan of out = cast(a + b) over [tokens, features] (blocks.py:574-581)."""
+        shape = extents(tokens, features)
+        return _Pointwise(self, shape, dtype, self.validate_device(dtype, device), "venturi_add_run")
 
 
 @dataclass(frozen=True)
@@ -383,7 +362,7 @@ class _Q8Linear:
 
 @dataclass(frozen=True)
 class _RMSNorm:
-    """RMSNorm plan (blocks.py:789-823); statistics in the reference's reduction order."""
+    """RMSNorm plan (blocks.py:789-823): statistics in the reference's reduction order."""
 
     _backend: HipBackend
     _weight: torch.Tensor
@@ -406,20 +385,36 @@ class _RMSNorm:
 
     def run(self, x, *, out):
         shape = (self.tokens, self.features)
-        _tensor(x, shape, self.dtype, self.device, "x")
-        _tensor(out, shape, self.dtype, self.device, "out")
-        _no_overlap(out, (x, self._weight))
-        with torch.cuda.device(self.device):
-            self._backend._check(
-                self._backend._native.venturi_rms_run(
-                    x.data_ptr(),
-                    self._weight.data_ptr(),
-                    out.data_ptr(),
-                    self.tokens,
-                    self.features,
-                    _DTYPES[self.dtype],
-                    self.epsilon,
-                    _stream(self.device),
-                )
-            )
+        for name, tensor in (("x", x), ("out", out)):
+            admit(tensor, shape, self.dtype, self.device, name)
+        disjoint(out, (x, self._weight))
+        self._backend._launch("venturi_rms_run", self.device, x, self._weight, out, self.tokens, self.features,
+                              DTYPE_CODES[self.dtype], self.epsilon)
+        return out
+
+
+@dataclass(frozen=True)
+class _Pointwise:
+    """Elementwise plan over three [tokens, features] tensors of one dtype (blocks.py:848-876).
+
+    ``out`` may be ``a`` or ``b`` itself (the gated MLP writes SwiGLU over its
+    gate buffer), never a partial overlap.
+    """
+
+    _backend: HipBackend
+    shape: tuple
+    dtype: torch.dtype
+    device: torch.device
+    entry: str
+    workspace_bytes = 0
+
+    @property
+    def swiglu(self):
+        return self.entry == "venturi_swiglu_run"
+
+    def run(self, a, b, *, out):
+        for name, tensor in (("a", a), ("b", b), ("out", out)):
+            admit(tensor, self.shape, self.dtype, self.device, name)
+        disjoint(out, (a, b), allow_inplace=True)
+        self._backend._launch(self.entry, self.device, a, b, out, a.numel(), DTYPE_CODES[self.dtype])
         return out

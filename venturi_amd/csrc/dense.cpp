@@ -21,10 +21,13 @@
 // (multiples of 16 rows).
 //
 // hipBLASLt state: one handle per device and one (descriptor, layouts,
-// algorithm) entry per (device, tokens, rows, k, n), made on first use under
-// a mutex and kept for the life of the process. That first call allocates
-// the handle's own resources, so it must not run under graph capture; later
-// calls make no allocation and are capturable.
+// algorithm) entry per (device, dtype, tokens, rows, k, n, workspace share),
+// made on first use under a mutex and kept for the life of the process (the
+// bridge's share is bucketed to 17 sizes, so the cache stays bounded by the
+// shapes a process runs). That first call per key allocates the handle's
+// resources and queries the heuristic, so it must not run under graph
+// capture; later calls with the same key make no allocation and are
+// capturable.
 #include "common.hpp"
 
 #include "../../include/venturi_ops.h"
@@ -199,6 +202,18 @@ struct DenseLinear {
     int dtype;
 };
 
+// The workspace share handed to hipBLASLt for a caller's buffer of `bytes`:
+// at most 32 MiB, rounded down to a power of two (0 below 1 KiB). The
+// per-shape algorithm cache is keyed on it, so callers that size their buffer
+// differently share a few entries (at most 16 per shape) instead of adding
+// one, and one heuristic query, per distinct size.
+std::uint64_t workspace_bucket(std::uint64_t bytes) {
+    if (bytes < 1024) return 0;
+    std::uint64_t bucket = 1024;
+    while (bucket * 2 <= std::min<std::uint64_t>(bytes, kBlasBytes)) bucket *= 2;
+    return bucket;
+}
+
 void dense_linear_run(const DenseLinear* p, const void* x, const void* w, void* out, int tokens, int n, int k,
                       void* workspace, std::uint64_t bytes, hipStream_t stream) {
     require(p && x && w && out && workspace, "null Linear operand");
@@ -208,10 +223,11 @@ void dense_linear_run(const DenseLinear* p, const void* x, const void* w, void* 
     // buffers (allocations and whole-row offsets of them) meet this.
     require(aligned(x, 16) && aligned(w, 16) && aligned(out, 16) && aligned(workspace, 16),
             "the dense bridge needs 16-byte aligned x, w, out and workspace");
-    const auto [handle, g] = gemm_for(tokens, n, k, n, p->dtype, bytes);
+    const std::uint64_t share = workspace_bucket(bytes);
+    const auto [handle, g] = gemm_for(tokens, n, k, n, p->dtype, share);
     const float alpha = 1.0f, beta = 0.0f;
     blas(hipblasLtMatmul(handle, g->desc, &alpha, w, g->a, x, g->b, &beta, out, g->d, out, g->d, &g->algo, workspace,
-                         bytes, stream),
+                         share, stream),
          "GEMM launch");
 }
 

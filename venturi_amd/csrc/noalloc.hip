@@ -9,8 +9,11 @@
 // its own copy until the process ends. The slots must start idle (the
 // signalling-NaN pattern of the tiled kernels, not zero): the first call on a
 // device fills them with a kernel on the caller's stream, outside graph
-// capture, and every projection leaves them idle again. All calls on one GPU
-// share the array, so calls that overlap in time on one GPU race.
+// capture, and waits for that fill (so later calls on any stream find idle
+// slots); every projection leaves them idle again. All calls on one GPU share
+// the array, so calls that overlap in time on one GPU race, and a race can
+// leave slots non-idle for every later call on that GPU: nothing re-arms the
+// array, so recovery from an overlapping call is a new process.
 #include "common.hpp"
 
 #include <mutex>
@@ -51,6 +54,9 @@ void* device_scratch(hipStream_t stream) {
         check(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)));
         q8_tiled_workspace_init(address, kScratchBytes, stream);
         check(hipGetLastError());
+        // Finish the fill before any call on another stream can reach the slots:
+        // the split-K exchange reads every non-idle word as a partner's partial.
+        check(hipStreamSynchronize(stream));
         scratch_address[device] = address;
     }
     return scratch_address[device];

@@ -20,7 +20,7 @@ from dataclasses import dataclass
 
 import torch
 
-from .blocks import _no_overlap, _stream, _tensor
+from .operands import admit, disjoint, stream_of
 from .weights import Q4RowSplitWeight
 
 
@@ -197,16 +197,16 @@ class RoutedExpertsPlan:
         NaN, so bad routing cannot pass for a valid result.
         """
         b, g = self.bank, self.bank.geometry
-        _tensor(x, (self.tokens, g.hidden_size), torch.float16, b.device, "x")
-        _tensor(indices, (self.tokens, g.top_k), torch.int64, b.device, "indices")
-        _tensor(scores, (self.tokens, g.top_k), torch.float16, b.device, "scores")
-        _tensor(out, (self.tokens, g.hidden_size), torch.float16, b.device, "out")
+        admit(x, (self.tokens, g.hidden_size), torch.float16, b.device, "x")
+        admit(indices, (self.tokens, g.top_k), torch.int64, b.device, "indices")
+        admit(scores, (self.tokens, g.top_k), torch.float16, b.device, "scores")
+        admit(out, (self.tokens, g.hidden_size), torch.float16, b.device, "out")
         if not isinstance(workspace, torch.Tensor) or workspace.device != b.device or not workspace.is_contiguous():
             raise ValueError("workspace must be a contiguous tensor on the bank's device")
         if workspace.numel() * workspace.element_size() < self.workspace_bytes or workspace.data_ptr() % 256:
             raise ValueError(f"workspace requires {self.workspace_bytes} bytes at 256-byte alignment")
-        _no_overlap(out, (x, indices, scores, workspace) + b.storage_tensors)
-        _no_overlap(workspace, (x, indices, scores) + b.storage_tensors)
+        disjoint(out, (x, indices, scores, workspace) + b.storage_tensors)
+        disjoint(workspace, (x, indices, scores) + b.storage_tensors)
         with torch.cuda.device(b.device):
             b.backend._check(
                 b.backend._native.venturi_moe_q4_run(
@@ -215,7 +215,7 @@ class RoutedExpertsPlan:
                     b.down_codes.data_ptr(), b.down_scales.data_ptr(),
                     out.data_ptr(), workspace.data_ptr(), self.workspace_bytes,
                     self.tokens, g.top_k, g.num_experts, g.hidden_size, g.intermediate_size,
-                    _stream(b.device),
+                    stream_of(b.device),
                 )
             )
         return out

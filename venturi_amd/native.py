@@ -79,6 +79,19 @@ SIGNATURES = {
     "venturi_silu_mul_run": ([_P] * 2 + [_I] * 3 + [_P], _I),
     "venturi_swiglu_run": ([_P] * 3 + [C.c_int64, _I, _P], _I),
     "venturi_add_run": ([_P] * 3 + [C.c_int64, _I, _P], _I),
+    # Reference exports outside the quantized-linear path: present so a binding
+    # of the reference's whole table loads; each call returns -1 with a message.
+    "venturi_greedy_run": ([_P] * 3 + [C.c_size_t] + [_I] * 3 + [_P], _I),
+    "venturi_fp32_linear_run": ([_P] * 3 + [_I] * 4 + [_P], _I),
+    "venturi_rope_run": ([_P] * 4 + [_I] * 6 + [_P], _I),
+    "venturi_qwen_qk_run": ([_P] * 8 + [_I] * 6 + [_F, _P], _I),
+    "venturi_qwen_gate_run": ([_P] * 3 + [_I] * 4 + [_P], _I),
+    "venturi_attention_run": ([_P] * 4 + [_I] * 6 + [_F, _P], _I),
+    "venturi_embedding_run": ([_P] * 3 + [_I] * 4 + [_P], _I),
+    "venturi_gdn_run": ([_P] * 8 + [_I] * 8 + [_F, _P], _I),
+    "venturi_conv_run": ([_P] * 5 + [_I] * 5 + [_P], _I),
+    "venturi_gates_run": ([_P] * 6 + [_I] * 4 + [_P], _I),
+    "venturi_gated_rms_run": ([_P] * 4 + [_I] * 5 + [_F, _P], _I),
 }
 
 _lock = threading.Lock()

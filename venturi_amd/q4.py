@@ -8,11 +8,11 @@ W4A16 weight value fp16(q * scale).
 
 from dataclasses import dataclass
 from functools import cached_property
-from pathlib import Path
 
 import torch
 
-from .blocks import _DTYPES, _no_overlap, _shape, _stream, _tensor
+from .operands import DTYPE_CODES, admit, disjoint, extents, stream_of
+from .plugin import CodecEntry, RowCodecOperator
 from .weights import Q4RowSplitWeight, decode_k64_fp16, rtn_k64
 
 # Plan routes of a resident Q4 linear:
@@ -110,7 +110,7 @@ class ResidentQ4Linear:
         return self.weight.out_features
 
     def prepare(self, *, tokens, route="auto"):
-        _shape(tokens, self.out_features)
+        extents(tokens, self.out_features)
         if tokens * self.out_features >= 2**31:
             raise ValueError("Q4 output count must fit int32")
         if route not in Q4_ROUTES:
@@ -145,7 +145,7 @@ class ResidentQ4Linear:
                 slots = torch.empty(size, dtype=torch.uint8, device=self.device)
                 with torch.cuda.device(self.device):
                     self.backend._check(lib.venturi_q4_tiled_workspace_init(slots.data_ptr(), size,
-                                                                              _stream(self.device)))
+                                                                              stream_of(self.device)))
             # The copy and the slots were written on this stream; a plan may run on another.
             torch.cuda.current_stream(self.device).synchronize()
         workspace = 0
@@ -161,14 +161,14 @@ class ResidentQ4Linear:
         rows = out.shape[0] if isinstance(out, torch.Tensor) and out.ndim == 2 else -1
         if type(row) is not int or row < 0 or rows <= 0 or row + rows > self.out_features:
             raise ValueError("Q4 decode rows must lie inside the matrix")
-        _tensor(out, (rows, self.in_features), torch.float16, self.device, "out")
-        _no_overlap(out, self.storage_tensors)
+        admit(out, (rows, self.in_features), torch.float16, self.device, "out")
+        disjoint(out, self.storage_tensors)
         w = self.weight
         with torch.cuda.device(self.device):
             self.backend._check(
                 self.backend._native.venturi_row_dequant_rows(
                     w.codes.data_ptr(), None, w.scales.data_ptr(), out.data_ptr(), row, rows, w.in_features,
-                    w.padded_k, 4, _stream(self.device),
+                    w.padded_k, 4, stream_of(self.device),
                 )
             )
         return out
@@ -213,37 +213,37 @@ class Q4LinearPlan:
         r = self.resident
         if self.kernel != "dense" and workspace is not None:
             raise ValueError("Q4 Linear uses no workspace")
-        _tensor(x, (self.tokens, r.in_features), r.dtype, r.device, "x")
-        _tensor(out, (self.tokens, r.out_features), r.dtype, r.device, "out")
-        _no_overlap(out, (x,) + self.storage_tensors)
+        admit(x, (self.tokens, r.in_features), r.dtype, r.device, "x")
+        admit(out, (self.tokens, r.out_features), r.dtype, r.device, "out")
+        disjoint(out, (x,) + self.storage_tensors)
         if self.kernel == "dense":
-            _tensor(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
+            admit(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
             if workspace.data_ptr() % 256 or x.data_ptr() % 16 or out.data_ptr() % 16:
                 raise ValueError("the dense Q4 route needs a 256-byte aligned workspace and 16-byte aligned x and out")
-            _no_overlap(workspace, (x, out) + self.storage_tensors)
-        w, lib, stream = r.weight, r.backend._native, _stream(r.device)
+            disjoint(workspace, (x, out) + self.storage_tensors)
+        w, lib, stream = r.weight, r.backend._native, stream_of(r.device)
         args = (x.data_ptr(), w.codes.data_ptr(), w.scales.data_ptr(), out.data_ptr())
         with torch.cuda.device(r.device):
             if self.kernel == "dense":
                 status = lib.venturi_row_dense_run(
                     *args[:2], None, *args[2:], self.tokens, w.out_features, w.in_features, w.padded_k, 4,
-                    _DTYPES[r.dtype], workspace.data_ptr(), self.workspace_bytes, stream
+                    DTYPE_CODES[r.dtype], workspace.data_ptr(), self.workspace_bytes, stream
                 )
             elif self.kernel == "mfma" and self.tokens < DECODE_TILED_TOKENS:
                 tc, ts = r.tiled
                 slots = self.slots
                 status = lib.venturi_q4_tiled_run(
                     x.data_ptr(), tc.data_ptr(), ts.data_ptr(), out.data_ptr(), self.tokens, w.out_features,
-                    w.in_features, w.padded_k, _DTYPES[r.dtype], None if slots is None else slots.data_ptr(),
+                    w.in_features, w.padded_k, DTYPE_CODES[r.dtype], None if slots is None else slots.data_ptr(),
                     0 if slots is None else slots.numel(), stream
                 )
             elif self.kernel == "mfma":
                 status = lib.venturi_q4_gemm_run(
-                    *args, self.tokens, w.out_features, w.in_features, w.padded_k, _DTYPES[r.dtype], stream
+                    *args, self.tokens, w.out_features, w.in_features, w.padded_k, DTYPE_CODES[r.dtype], stream
                 )
             elif self.kernel == "generic":
                 status = lib.venturi_q4_run(
-                    *args, w.out_features, w.in_features, w.padded_k, self.tokens, _DTYPES[r.dtype], 0, stream
+                    *args, w.out_features, w.in_features, w.padded_k, self.tokens, DTYPE_CODES[r.dtype], 0, stream
                 )
                 if status < 0:
                     raise RuntimeError(lib.venturi_ada_error().decode("utf-8", "replace"))
@@ -274,7 +274,7 @@ def upload_q4(backend, weight, *, device, dtype):
 
 
 # ---------------------------------------------------------------------------
-# The reference's stand-alone Q4 operator objects, over the same library.
+# The reference's stand-alone Q4 operator object, over the same library.
 
 
 @dataclass(frozen=True)
@@ -283,7 +283,7 @@ class PreparedQ4:
     ready: object
 
 
-class NativeQ4:
+class NativeQ4(RowCodecOperator):
     """Expert Q4 operators of ABI 1 (reference ops/flash_next_q4.py:17-89).
 
     ``linear`` is the expert GEMV order (fp16(q*scale) weights, lane-strided
@@ -291,87 +291,6 @@ class NativeQ4:
     matrix. Device qualification is gfx950 instead of SM70.
     """
 
-    def __init__(self, library=None, *, max_output_bytes=64 * 2**20):
-        from . import native
-
-        if type(max_output_bytes) is not int or max_output_bytes <= 0:
-            raise ValueError("Positive explicit output budget required")
-        self.max_output_bytes = max_output_bytes
-        self.lib = native.load(library)
-        self.library = Path(self.lib.path)
-        if self.lib.venturi_q4_abi() != 1:
-            raise ValueError("Unsupported Q4 operator ABI")
-
-    def prepare(self, weight, *, device):
-        from .blocks import is_gfx950
-
-        if not isinstance(weight, Q4RowSplitWeight) or weight.codes.device.type != "cpu":
-            raise ValueError("Explicit CPU Q4 descriptor required for preparation")
-        weight.validate()
-        if (
-            not torch.isfinite(weight.scales).all()
-            or (weight.scales < 0).any()
-            or weight.out_features * weight.in_features * 2 > self.max_output_bytes
-        ):
-            raise ValueError("Finite nonnegative Q4 scales and bounded matrix required")
-        device = torch.device(device)
-        if device.type != "cuda":
-            raise ValueError("Explicit GPU device required")
-        with torch.cuda.device(device):
-            if not is_gfx950(device):
-                raise ValueError("This operator is qualified only for gfx950")
-            result = Q4RowSplitWeight(weight.codes.to(device), weight.scales.to(device), weight.in_features)
-            ready = torch.cuda.Event()
-            ready.record(torch.cuda.current_stream(device))
-        return PreparedQ4(result, ready)
-
-    def _lease(self, prepared):
-        if not isinstance(prepared, PreparedQ4) or prepared.weight.codes.device.type != "cuda":
-            raise ValueError("Explicit prepared GPU Q4 weight required")
-        w = prepared.weight
-        w.validate()
-        stream = torch.cuda.current_stream(w.codes.device)
-        stream.wait_event(prepared.ready)
-        w.codes.record_stream(stream)
-        w.scales.record_stream(stream)
-        return w, stream
-
-    def decode(self, prepared):
-        with torch.cuda.device(prepared.weight.codes.device):
-            w, stream = self._lease(prepared)
-            if w.out_features * w.in_features * 2 > self.max_output_bytes:
-                raise ValueError("Q4 decode exceeds output budget")
-            out = torch.empty((w.out_features, w.in_features), device=w.codes.device, dtype=torch.float16)
-            status = self.lib.venturi_q4_decode(
-                w.codes.data_ptr(), w.scales.data_ptr(), out.data_ptr(), w.out_features, w.in_features, w.padded_k,
-                stream.cuda_stream,
-            )
-            if status:
-                raise RuntimeError(f"Q4 decode HIP launch failed: {status}")
-            return out
-
-    def linear(self, x, prepared):
-        if not isinstance(prepared, PreparedQ4):
-            raise ValueError("Explicit prepared GPU Q4 weight required")
-        w = prepared.weight
-        if (
-            x.ndim != 2
-            or not 1 <= len(x) <= 64
-            or x.shape[1] != w.in_features
-            or x.dtype != torch.float16
-            or x.device != w.codes.device
-            or not x.is_contiguous()
-        ):
-            raise ValueError("Bounded contiguous FP16 GPU input required")
-        if len(x) * w.out_features * 2 > self.max_output_bytes:
-            raise ValueError("Q4 linear exceeds output budget")
-        with torch.cuda.device(x.device):
-            w, stream = self._lease(prepared)
-            out = torch.empty((len(x), w.out_features), device=x.device, dtype=x.dtype)
-            status = self.lib.venturi_q4_linear(
-                x.data_ptr(), w.codes.data_ptr(), w.scales.data_ptr(), out.data_ptr(), len(x), w.out_features,
-                w.in_features, w.padded_k, stream.cuda_stream,
-            )
-            if status:
-                raise RuntimeError(f"Q4 GEMV HIP launch failed: {status}")
-            return out
+    entry = CodecEntry("Q4", Q4RowSplitWeight, ("codes", "scales"), "venturi_q4_abi", "venturi_q4_decode",
+                       "venturi_q4_linear")
+    prepared = PreparedQ4

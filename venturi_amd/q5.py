@@ -10,10 +10,10 @@ qualification instead of SM70.
 """
 
 from dataclasses import dataclass
-from pathlib import Path
 
 import torch
 
+from .plugin import CodecEntry, RowCodecOperator
 from .weights import Q5RowSplitWeight, decode_k64_fp16, rtn_k64
 
 CODEC = "rtn_symmetric15_g64_fp16_row_split_k128_v1"
@@ -65,7 +65,7 @@ class PreparedQ5:
     ready: object
 
 
-class NativeQ5:
+class NativeQ5(RowCodecOperator):
     """W5A16 operators of Q5 ABI 1 (reference ops/flash_next_q5.py:17-89).
 
     ``linear`` is the reference GEMV order (fp16(q*scale) weights,
@@ -73,89 +73,6 @@ class NativeQ5:
     the fp16 matrix.
     """
 
-    def __init__(self, library=None, *, max_output_bytes=64 * 2**20):
-        from . import native
-
-        if type(max_output_bytes) is not int or max_output_bytes <= 0:
-            raise ValueError("Positive explicit output budget required")
-        self.max_output_bytes = max_output_bytes
-        self.lib = native.load(library)
-        self.library = Path(self.lib.path)
-        if self.lib.venturi_q5_abi() != 1:
-            raise ValueError("Unsupported Q5 operator ABI")
-
-    def prepare(self, weight, *, device):
-        from .blocks import is_gfx950
-
-        if not isinstance(weight, Q5RowSplitWeight) or weight.codes.device.type != "cpu":
-            raise ValueError("Explicit CPU Q5 descriptor required for preparation")
-        weight.validate()
-        if (
-            not torch.isfinite(weight.scales).all()
-            or (weight.scales < 0).any()
-            or weight.out_features * weight.in_features * 2 > self.max_output_bytes
-        ):
-            raise ValueError("Finite nonnegative Q5 scales and bounded matrix required")
-        device = torch.device(device)
-        if device.type != "cuda":
-            raise ValueError("Explicit GPU device required")
-        with torch.cuda.device(device):
-            if not is_gfx950(device):
-                raise ValueError("This operator is qualified only for gfx950")
-            result = Q5RowSplitWeight(
-                weight.codes.to(device), weight.high.to(device), weight.scales.to(device), weight.in_features
-            )
-            ready = torch.cuda.Event()
-            ready.record(torch.cuda.current_stream(device))
-        return PreparedQ5(result, ready)
-
-    def _lease(self, prepared):
-        if not isinstance(prepared, PreparedQ5) or prepared.weight.codes.device.type != "cuda":
-            raise ValueError("Explicit prepared GPU Q5 weight required")
-        w = prepared.weight
-        w.validate()
-        stream = torch.cuda.current_stream(w.codes.device)
-        stream.wait_event(prepared.ready)
-        for plane in (w.codes, w.high, w.scales):
-            plane.record_stream(stream)
-        return w, stream
-
-    def decode(self, prepared):
-        with torch.cuda.device(prepared.weight.codes.device):
-            w, stream = self._lease(prepared)
-            if w.out_features * w.in_features * 2 > self.max_output_bytes:
-                raise ValueError("Q5 decode exceeds output budget")
-            out = torch.empty((w.out_features, w.in_features), device=w.codes.device, dtype=torch.float16)
-            status = self.lib.venturi_q5_decode(
-                w.codes.data_ptr(), w.high.data_ptr(), w.scales.data_ptr(), out.data_ptr(), w.out_features,
-                w.in_features, w.padded_k, stream.cuda_stream,
-            )
-            if status:
-                raise RuntimeError(f"Q5 decode HIP launch failed: {status}")
-            return out
-
-    def linear(self, x, prepared):
-        if not isinstance(prepared, PreparedQ5):
-            raise ValueError("Explicit prepared GPU Q5 weight required")
-        w = prepared.weight
-        if (
-            x.ndim != 2
-            or not 1 <= len(x) <= 64
-            or x.shape[1] != w.in_features
-            or x.dtype != torch.float16
-            or x.device != w.codes.device
-            or not x.is_contiguous()
-        ):
-            raise ValueError("Bounded contiguous FP16 GPU input required")
-        if len(x) * w.out_features * 2 > self.max_output_bytes:
-            raise ValueError("Q5 linear exceeds output budget")
-        with torch.cuda.device(x.device):
-            w, stream = self._lease(prepared)
-            out = torch.empty((len(x), w.out_features), device=x.device, dtype=x.dtype)
-            status = self.lib.venturi_q5_linear(
-                x.data_ptr(), w.codes.data_ptr(), w.high.data_ptr(), w.scales.data_ptr(), out.data_ptr(), len(x),
-                w.out_features, w.in_features, w.padded_k, stream.cuda_stream,
-            )
-            if status:
-                raise RuntimeError(f"Q5 GEMV HIP launch failed: {status}")
-            return out
+    entry = CodecEntry("Q5", Q5RowSplitWeight, ("codes", "high", "scales"), "venturi_q5_abi", "venturi_q5_decode",
+                       "venturi_q5_linear")
+    prepared = PreparedQ5

@@ -20,7 +20,8 @@ from dataclasses import dataclass
 
 import torch
 
-from .blocks import ResidentLinear, _no_overlap, _shape, _stream, _tensor
+from .blocks import ResidentLinear
+from .operands import admit, disjoint, extents, stream_of
 from .vocabulary import ResidentQ8Vocabulary
 
 A8_ROUTES = ("auto", "exact", "mfma")
@@ -47,16 +48,16 @@ class PreparedQ8DP4A:
     def quantize(self, x, *, workspace):
         """Only the activation quantization step (fills ``workspace``)."""
         r = self.resident
-        _tensor(x, (self.tokens, r.hidden_size), torch.float16, r.device, "x")
-        _tensor(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
-        _no_overlap(workspace, (x,) + r.storage_tensors)
+        admit(x, (self.tokens, r.hidden_size), torch.float16, r.device, "x")
+        admit(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
+        disjoint(workspace, (x,) + r.storage_tensors)
         if workspace.data_ptr() % 16:
             raise ValueError("A8 workspace requires 16-byte alignment")
         with torch.cuda.device(r.device):
             r.backend._check(
                 self._native.venturi_q8_dp4a_quantize(
                     x.data_ptr(), workspace.data_ptr(), self.workspace_bytes, self.tokens, r.hidden_size,
-                    self.passes, _stream(r.device),
+                    self.passes, stream_of(r.device),
                 )
             )
         return workspace
@@ -64,9 +65,9 @@ class PreparedQ8DP4A:
     def project(self, *, out, workspace):
         """Only the int8 projection of an already filled workspace."""
         r = self.resident
-        _tensor(out, (self.tokens, r.vocab_size), torch.float16, r.device, "out")
-        _tensor(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
-        _no_overlap(out, (workspace,) + r.storage_tensors)
+        admit(out, (self.tokens, r.vocab_size), torch.float16, r.device, "out")
+        admit(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
+        disjoint(out, (workspace,) + r.storage_tensors)
         if workspace.data_ptr() % 16:
             raise ValueError("A8 workspace requires 16-byte alignment")
         entry = self._native.venturi_q8_dp4a_run if self.kernel == "exact" else self._native.venturi_q8_a8_gemm_run
@@ -76,18 +77,18 @@ class PreparedQ8DP4A:
                 entry(
                     workspace.data_ptr(), self.workspace_bytes, codes.data_ptr(), scales.data_ptr(),
                     out.data_ptr(), self.tokens, r.vocab_size, r.hidden_size, r.padded_k, self.passes,
-                    _stream(r.device),
+                    stream_of(r.device),
                 )
             )
         return out
 
     def run(self, x, *, out, workspace):
         r = self.resident
-        _tensor(x, (self.tokens, r.hidden_size), torch.float16, r.device, "x")
-        _tensor(out, (self.tokens, r.vocab_size), torch.float16, r.device, "out")
-        _tensor(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
-        _no_overlap(out, (x, workspace) + r.storage_tensors)
-        _no_overlap(workspace, (x,) + r.storage_tensors)
+        admit(x, (self.tokens, r.hidden_size), torch.float16, r.device, "x")
+        admit(out, (self.tokens, r.vocab_size), torch.float16, r.device, "out")
+        admit(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
+        disjoint(out, (x, workspace) + r.storage_tensors)
+        disjoint(workspace, (x,) + r.storage_tensors)
         if workspace.data_ptr() % 16:
             raise ValueError("A8 workspace requires 16-byte alignment")
         self.quantize(x, workspace=workspace)
@@ -108,7 +109,7 @@ def prepare_q8_dp4a(resident, *, tokens, residual_compensation, route="auto"):
     resident.row_major_planes()  # the A8 kernels read the row-major planes
     if type(residual_compensation) is not bool:
         raise ValueError("Explicit boolean residual_compensation required")
-    _shape(tokens, resident.hidden_size)
+    extents(tokens, resident.hidden_size)
     if resident.dtype != torch.float16 or resident.device.type != "cuda":
         raise ValueError("A8 profile requires GPU FP16 input/output")
     resident.backend.validate_device(resident.dtype, resident.device)

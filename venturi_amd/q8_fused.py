@@ -19,7 +19,8 @@ from dataclasses import dataclass
 
 import torch
 
-from .blocks import ResidentLinear, _no_overlap, _stream, _tensor
+from .blocks import ResidentLinear
+from .operands import admit, disjoint, stream_of
 from .q8_dp4a import prepare_q8_dp4a
 
 _INT32_LIMIT = 2**31
@@ -58,16 +59,16 @@ class PreparedQ8Fused:
         tokens = self.base.tokens
         if not (isinstance(outputs, (list, tuple)) and len(outputs) == len(self.residents)):
             raise ValueError("one output per fused matrix required")
-        _tensor(x, (tokens, lead.hidden_size), torch.float16, lead.device, "x")
-        _tensor(workspace, (self.workspace_bytes,), torch.uint8, lead.device, "workspace")
+        admit(x, (tokens, lead.hidden_size), torch.float16, lead.device, "x")
+        admit(workspace, (self.workspace_bytes,), torch.uint8, lead.device, "workspace")
         if workspace.data_ptr() % 16 != 0:
             raise ValueError("DP4A workspace requires 16-byte alignment")
         weights = sum((m.storage_tensors for m in self.residents), ())
-        _no_overlap(workspace, (x,) + weights)
+        disjoint(workspace, (x,) + weights)
         earlier = ()
         for out, stride in zip(outputs, self.strides):
-            _tensor(out, (tokens, stride), torch.float16, lead.device, "out")
-            _no_overlap(out, (x, workspace) + weights + earlier)
+            admit(out, (tokens, stride), torch.float16, lead.device, "out")
+            disjoint(out, (x, workspace) + weights + earlier)
             earlier += (out,)
 
     def _descriptors(self, outputs):
@@ -85,7 +86,7 @@ class PreparedQ8Fused:
         lead, a8 = self.residents[0], self.base
         backend = lead.backend
         with torch.cuda.device(lead.device):
-            stream = _stream(lead.device)
+            stream = stream_of(lead.device)
             if not packed:
                 backend._check(backend._native.venturi_q8_dp4a_quantize(
                     x.data_ptr(), workspace.data_ptr(), a8.workspace_bytes, a8.tokens, lead.hidden_size, a8.passes,

@@ -11,7 +11,8 @@ from dataclasses import dataclass
 
 import torch
 
-from .blocks import ResidentRMSNorm, _no_overlap, _shape, _stream, _tensor
+from .blocks import ResidentRMSNorm
+from .operands import admit, disjoint, extents, stream_of
 
 
 @dataclass(frozen=True)
@@ -24,12 +25,12 @@ class PreparedRMSQ8:
     def run(self, x, *, workspace, intermediate=None):
         n = self.norm
         k = n.features
-        _tensor(x, (self.tokens, k), torch.float16, n.device, "x")
-        _tensor(workspace, (self.workspace_bytes,), torch.uint8, n.device, "workspace")
-        _no_overlap(workspace, (x, n._weight))
+        admit(x, (self.tokens, k), torch.float16, n.device, "x")
+        admit(workspace, (self.workspace_bytes,), torch.uint8, n.device, "workspace")
+        disjoint(workspace, (x, n._weight))
         if intermediate is not None:
-            _tensor(intermediate, (self.tokens, k), torch.float16, n.device, "intermediate")
-            _no_overlap(intermediate, (x, n._weight, workspace))
+            admit(intermediate, (self.tokens, k), torch.float16, n.device, "intermediate")
+            disjoint(intermediate, (x, n._weight, workspace))
         if workspace.data_ptr() % 16:
             raise ValueError("A8 workspace requires 16-byte alignment")
         lib = n._backend._native
@@ -38,7 +39,7 @@ class PreparedRMSQ8:
                 lib.venturi_rms_q8_quantize_passes(
                     x.data_ptr(), n._weight.data_ptr(), workspace.data_ptr(), self.workspace_bytes, self.tokens, k,
                     n.epsilon, self.passes, intermediate.data_ptr() if intermediate is not None else None,
-                    _stream(n.device),
+                    stream_of(n.device),
                 )
             )
         return workspace
@@ -52,7 +53,7 @@ def prepare_rms_q8(norm, *, tokens, residual_compensation):
         raise ValueError("Explicit boolean residual_compensation required")
     if norm.dtype != torch.float16:
         raise ValueError("RMS/A8 requires FP16 activations")
-    _shape(tokens, norm.features)
+    extents(tokens, norm.features)
     norm._backend.validate_device(norm.dtype, norm.device)
     passes = 2 if residual_compensation else 1
     size = norm._backend._native.venturi_q8_dp4a_bytes(tokens, norm.features, passes)

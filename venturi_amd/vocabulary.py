@@ -39,7 +39,8 @@ import threading
 
 import torch
 
-from .blocks import _DTYPES, Q8_ROUTES, _no_overlap, _shape, _stream, _tensor
+from .blocks import Q8_ROUTES
+from .operands import DTYPE_CODES, admit, disjoint, extents, stream_of
 
 EXACT_MAX_AUTO_TOKENS = 0
 MFMA_MAX_TOKENS = 32
@@ -113,12 +114,12 @@ class Q8VocabularyWeights:
         if not isinstance(self.codes, torch.Tensor) or self.codes.ndim != 2:
             raise ValueError("Q8 codes require [vocab,padded_hidden]")
         rows, width = self.codes.shape
-        _shape(rows, self.hidden_size)
+        extents(rows, self.hidden_size)
         if width != _padded(self.hidden_size):
             raise ValueError("Q8 hidden padding must be a multiple of 128")
         where = self.codes.device
-        _tensor(self.codes, (rows, width), torch.int8, where, "codes")
-        _tensor(self.scales, (rows, width // 32), torch.float16, where, "scales")
+        admit(self.codes, (rows, width), torch.int8, where, "codes")
+        admit(self.scales, (rows, width // 32), torch.float16, where, "scales")
         if bool((self.codes == -128).any()):
             raise ValueError("Q8 code -128 is outside the artifact contract")
         if bool((self.scales < 0).any()) or not bool(torch.isfinite(self.scales).all()):
@@ -224,7 +225,7 @@ class ResidentQ8Vocabulary:
         return Q8Embedding(self, indices)
 
     def prepare(self, *, tokens, route="auto"):
-        _shape(tokens, self.vocab_size)
+        extents(tokens, self.vocab_size)
         if tokens * self.vocab_size >= 2**31:
             raise ValueError("Q8 head row count must fit int32")
         if route not in Q8_ROUTES:
@@ -265,7 +266,7 @@ class ResidentQ8Vocabulary:
         plan writes out [tokens, inter] = fp16(swiglu(fp16(gate), fp16(up))), the
         bytes of the ``mfma`` projection followed by ``venturi_silu_mul_run``.
         """
-        _shape(tokens, self.vocab_size)
+        extents(tokens, self.vocab_size)
         if self.vocab_size % 2:
             raise ValueError("a fused gate+up matrix needs an even row count")
         if not (self.dtype == torch.float16 and self.hidden_size % 8 == 0 and tokens <= MFMA_MAX_TOKENS):
@@ -286,7 +287,7 @@ class ResidentQ8Vocabulary:
             return None
         with torch.cuda.device(self.device):
             slots = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
-            self.backend._check(lib.venturi_q8_tiled_workspace_init(slots.data_ptr(), nbytes, _stream(self.device)))
+            self.backend._check(lib.venturi_q8_tiled_workspace_init(slots.data_ptr(), nbytes, stream_of(self.device)))
             torch.cuda.current_stream(self.device).synchronize()
         return slots
 
@@ -299,12 +300,12 @@ class Q8Embedding:
     def run(self, *, out):
         r = self.resident
         codes, scales = r.row_major_planes()
-        _tensor(out, (self._indices.numel(), r.hidden_size), r.dtype, r.device, "out")
-        _no_overlap(out, (codes, scales, self._indices))
+        admit(out, (self._indices.numel(), r.hidden_size), r.dtype, r.device, "out")
+        disjoint(out, (codes, scales, self._indices))
         with torch.cuda.device(r.device):
             r.backend._check(r.backend._native.venturi_q8_embedding_run(
                 codes.data_ptr(), scales.data_ptr(), self._indices.data_ptr(), out.data_ptr(), self._indices.numel(),
-                r.vocab_size, r.hidden_size, r.padded_k, _DTYPES[r.dtype], _stream(r.device)))
+                r.vocab_size, r.hidden_size, r.padded_k, DTYPE_CODES[r.dtype], stream_of(r.device)))
         return out
 
 
@@ -340,21 +341,21 @@ class Q8OutputHead:
         r = self.resident
         if self.kernel != "dense" and workspace is not None:
             raise ValueError("This Q8 plan uses no workspace")
-        _tensor(x, (self.tokens, r.hidden_size), r.dtype, r.device, "x")
-        _tensor(out, (self.tokens, self.out_features), r.dtype, r.device, "out")
-        _no_overlap(out, (x,) + self.storage_tensors)
+        admit(x, (self.tokens, r.hidden_size), r.dtype, r.device, "x")
+        admit(out, (self.tokens, self.out_features), r.dtype, r.device, "out")
+        disjoint(out, (x,) + self.storage_tensors)
         lib = r.backend._native
         if self.kernel == "dense":
-            _tensor(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
+            admit(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
             if workspace.data_ptr() % 256 or x.data_ptr() % 16 or out.data_ptr() % 16:
                 raise ValueError("the dense Q8 route needs a 256-byte aligned workspace and 16-byte aligned x and out")
-            _no_overlap(workspace, (x, out) + self.storage_tensors)
+            disjoint(workspace, (x, out) + self.storage_tensors)
             codes, scales = r.row_major_planes()
             with torch.cuda.device(r.device):
                 r.backend._check(lib.venturi_q8_dense_run(
                     x.data_ptr(), codes.data_ptr(), scales.data_ptr(), out.data_ptr(), self.tokens, r.vocab_size,
-                    r.hidden_size, r.padded_k, _DTYPES[r.dtype], workspace.data_ptr(), self.workspace_bytes,
-                    _stream(r.device)))
+                    r.hidden_size, r.padded_k, DTYPE_CODES[r.dtype], workspace.data_ptr(), self.workspace_bytes,
+                    stream_of(r.device)))
             return out
         if self.kernel in ("exact", "prefill"):
             entry = lib.venturi_q8_head_run if self.kernel == "exact" else lib.venturi_q8_prefill_run
@@ -365,6 +366,6 @@ class Q8OutputHead:
             tail = (0, 0) if self.slots is None else (self.slots.data_ptr(), self.slots.numel())
         with torch.cuda.device(r.device):
             r.backend._check(entry(x.data_ptr(), planes[0].data_ptr(), planes[1].data_ptr(), out.data_ptr(),
-                                   self.tokens, r.vocab_size, r.hidden_size, r.padded_k, _DTYPES[r.dtype], *tail,
-                                   _stream(r.device)))
+                                   self.tokens, r.vocab_size, r.hidden_size, r.padded_k, DTYPE_CODES[r.dtype], *tail,
+                                   stream_of(r.device)))
         return out
