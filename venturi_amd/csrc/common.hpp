@@ -102,6 +102,21 @@ __device__ __forceinline__ float half_hi(std::uint32_t w) {
 __device__ __forceinline__ float bf16_lo(std::uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(std::uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Weight-stream loads. Decode kernels read every weight byte once per launch,
+// so the loads carry the non-temporal hint (global_load ... nt): on MI355X a
+// streaming read with it measured 5-9% faster at 33-189 MB than the default
+// policy (189 MB: 30.3 -> 27.8 us; 94 MB: 16.0 -> 14.7 us), the lines not
+// competing with activations and outputs for L2.
+__device__ __forceinline__ uint4 stream_load(const uint4* p) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ std::uint32_t stream_load(const std::uint32_t* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ unsigned short stream_load(const unsigned short* p) {
+    return __builtin_nontemporal_load(p);
+}
+
 // Sign-extending byte extraction from a packed int8x4 word.
 __device__ __forceinline__ float sbyte(std::uint32_t w, int i) {
     return static_cast<float>(static_cast<std::int8_t>(w >> (8 * i)));

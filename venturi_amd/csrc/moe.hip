@@ -389,8 +389,8 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
 #pragma unroll
                 for (int r = 0; r < RB; ++r) {
                     const std::int64_t u = unit[r] + static_cast<std::int64_t>(c) * 8;
-                    st.w[r] = wbase[u * 128 + 64 * h];
-                    if (h == 0) st.s[r] = __half_as_ushort(sbase[u * 64]);
+                    st.w[r] = stream_load(wbase + u * 128 + 64 * h);
+                    if (h == 0) st.s[r] = stream_load(reinterpret_cast<const unsigned short*>(sbase + u * 64));
                 }
             };
             auto load_x = [&](int c, XStage& x) {
@@ -994,8 +994,8 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
             const int c = min(c0 + i * STEPS + st, c1 - 1);
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
-                t.w[st][b] = *reinterpret_cast<const uint4*>(cp[b] + (TILED ? 1024 : 64) * c);
-                t.s[st][b] = sp[b][TILED ? 16 * c : c];
+                t.w[st][b] = stream_load(reinterpret_cast<const uint4*>(cp[b] + (TILED ? 1024 : 64) * c));
+                t.s[st][b] = stream_load(sp[b] + (TILED ? 16 * c : c));
                 if constexpr (HB > 0) {
 #pragma unroll
                     for (int h = 0; h < HB; ++h)

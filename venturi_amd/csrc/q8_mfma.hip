@@ -316,8 +316,8 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_decode(const __half* __restri
             const int ch = min(c0 + i * STEPS + s, c1 - 1);
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
-                t.w[s][b] = wsrc[b][static_cast<std::int64_t>(ch) * 64];
-                t.sc[s][b] = ssrc[b][static_cast<std::int64_t>(ch) * 16];
+                t.w[s][b] = stream_load(wsrc[b] + static_cast<std::int64_t>(ch) * 64);
+                t.sc[s][b] = stream_load(ssrc[b] + static_cast<std::int64_t>(ch) * 16);
             }
         }
 #pragma unroll
@@ -467,8 +467,8 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_lds(const __half* __restrict_
             const int ch = min(c0 + i * STEPS + s, c1 - 1);
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
-                t.w[s][b] = wsrc[b][static_cast<std::int64_t>(ch) * 64];
-                t.sc[s][b] = ssrc[b][static_cast<std::int64_t>(ch) * 16];
+                t.w[s][b] = stream_load(wsrc[b] + static_cast<std::int64_t>(ch) * 64);
+                t.sc[s][b] = stream_load(ssrc[b] + static_cast<std::int64_t>(ch) * 16);
             }
         }
     };
