@@ -1106,26 +1106,35 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
             // second adds (two fp32 terms: the result does not depend on the
             // arrival order), stores and returns the slot to idle. Only the slot is
             // shared, so no fence is needed, and every call leaves the slots idle.
+            // All four exchanges of a lane are issued before any result is used
+            // (one atomic round trip, not four in sequence).
             const int blocks = (n + 15) / 16;
+            float partner[4];
+            unsigned long long old[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) partner[e] = __shfl_xor(sum[e], 8, 64);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float mine = sum[e];
-                const float partner = __shfl_xor(mine, 8, 64);
                 const int t = 16 * tb + 4 * q + e;
+                old[e] = kRowSlotEmpty;
                 if (r < 8 && t < tokens && blk < blocks) {
                     unsigned long long* slot = slots + (static_cast<std::int64_t>(t) * blocks + blk) * 8 + r;
                     const unsigned long long packed =
-                        (static_cast<unsigned long long>(__float_as_uint(partner)) << 32) | __float_as_uint(mine);
-                    const unsigned long long old =
-                        __hip_atomic_exchange(slot, packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (old != kRowSlotEmpty) {
-                        __hip_atomic_store(slot, kRowSlotEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        const float lo = mine + __uint_as_float(static_cast<std::uint32_t>(old));
-                        const float hi = partner + __uint_as_float(static_cast<std::uint32_t>(old >> 32));
-                        __half* o = out + static_cast<std::int64_t>(t) * n;
-                        if (row < n) o[row] = from_f32<__half>(lo);
-                        if (row + 8 < n) o[row + 8] = from_f32<__half>(hi);
-                    }
+                        (static_cast<unsigned long long>(__float_as_uint(partner[e])) << 32) | __float_as_uint(sum[e]);
+                    old[e] = __hip_atomic_exchange(slot, packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = 16 * tb + 4 * q + e;
+                if (r < 8 && t < tokens && blk < blocks && old[e] != kRowSlotEmpty) {
+                    unsigned long long* slot = slots + (static_cast<std::int64_t>(t) * blocks + blk) * 8 + r;
+                    __hip_atomic_store(slot, kRowSlotEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const float lo = sum[e] + __uint_as_float(static_cast<std::uint32_t>(old[e]));
+                    const float hi = partner[e] + __uint_as_float(static_cast<std::uint32_t>(old[e] >> 32));
+                    __half* o = out + static_cast<std::int64_t>(t) * n;
+                    if (row < n) o[row] = from_f32<__half>(lo);
+                    if (row + 8 < n) o[row + 8] = from_f32<__half>(hi);
                 }
             }
         }

@@ -229,23 +229,32 @@ __device__ __forceinline__ void finish_tile(__half* __restrict__ out, unsigned l
         for (int j = 0; j < 4; ++j) store_tile_value<SWIGLU>(out, sum[j], t0 + 4 * q + j, blk, r, tokens, n);
     } else {
         static_assert(KS == 2, "K is split in two at most");
+        // All four exchanges of a lane are issued before any result is used, so
+        // the wave waits for one atomic round trip instead of four in sequence.
+        float partner[4];
+        unsigned long long old[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) partner[j] = __shfl_xor(sum[j], 8, 64);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float mine = sum[j];
-            const float partner = __shfl_xor(mine, 8, 64);
             const int t = t0 + 4 * q + j;
+            old[j] = kSlotEmpty;
             if (r < 8 && t < tokens) {
                 unsigned long long* slot = slots + (static_cast<std::int64_t>(t) * blocks + blk) * 8 + r;
                 const unsigned long long packed =
-                    (static_cast<unsigned long long>(__float_as_uint(partner)) << 32) | __float_as_uint(mine);
-                const unsigned long long old =
-                    __hip_atomic_exchange(slot, packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (old != kSlotEmpty) {
-                    __hip_atomic_store(slot, kSlotEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    const float lo = mine + __uint_as_float(static_cast<std::uint32_t>(old));
-                    const float hi = partner + __uint_as_float(static_cast<std::uint32_t>(old >> 32));
-                    store_row_pair<SWIGLU>(out, lo, hi, t, blk, r, n);
-                }
+                    (static_cast<unsigned long long>(__float_as_uint(partner[j])) << 32) | __float_as_uint(sum[j]);
+                old[j] = __hip_atomic_exchange(slot, packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = t0 + 4 * q + j;
+            if (r < 8 && t < tokens && old[j] != kSlotEmpty) {
+                unsigned long long* slot = slots + (static_cast<std::int64_t>(t) * blocks + blk) * 8 + r;
+                __hip_atomic_store(slot, kSlotEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const float lo = sum[j] + __uint_as_float(static_cast<std::uint32_t>(old[j]));
+                const float hi = partner[j] + __uint_as_float(static_cast<std::uint32_t>(old[j] >> 32));
+                store_row_pair<SWIGLU>(out, lo, hi, t, blk, r, n);
             }
         }
     }
@@ -320,28 +329,17 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_decode(const __half* __restri
                 t.sc[s][b] = stream_load(ssrc[b] + static_cast<std::int64_t>(ch) * 16);
             }
         }
+        // Activation fragments, branch-free so that the wait counts stay exact:
+        // read at clamped in-bounds columns (lanes of absent tokens read the last
+        // token's row and feed only output rows never stored); the multiply
+        // zeroes columns at or past k.
 #pragma unroll
         for (int s = 0; s < STEPS; ++s) {
             const int col = min(c0 + i * STEPS + s, c1 - 1) * 64;
-            if (col + 64 <= k) {
-                // Inside k every lane loads unmasked: lanes of absent tokens read
-                // the last token's row and feed only output rows never stored.
 #pragma unroll
-                for (int tb = 0; tb < NB; ++tb) {
-                    t.xa[s][tb] = *reinterpret_cast<const uint4*>(xrow[tb] + col);
-                    t.xb[s][tb] = *reinterpret_cast<const uint4*>(xrow[tb] + col + 32);
-                }
-            } else {
-#pragma unroll
-                for (int tb = 0; tb < NB; ++tb) {
-                    uint4 a = make_uint4(0u, 0u, 0u, 0u), bq = make_uint4(0u, 0u, 0u, 0u);
-                    if (live[tb]) {
-                        a = *reinterpret_cast<const uint4*>(xrow[tb] + min(col, k - 8 - 8 * q));
-                        bq = *reinterpret_cast<const uint4*>(xrow[tb] + min(col + 32, k - 8 - 8 * q));
-                    }
-                    t.xa[s][tb] = a;
-                    t.xb[s][tb] = bq;
-                }
+            for (int tb = 0; tb < NB; ++tb) {
+                t.xa[s][tb] = *reinterpret_cast<const uint4*>(xrow[tb] + min(col, k - 8 - 8 * q));
+                t.xb[s][tb] = *reinterpret_cast<const uint4*>(xrow[tb] + min(col + 32, k - 8 - 8 * q));
             }
         }
     };
@@ -391,16 +389,35 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_decode(const __half* __restri
         }
     };
 
+    // Two batches in flight. Batches 0 and 1 are requested up front (with one
+    // batch, the second request re-reads its last chunk and is never used), and
+    // in the steady state each multiply is followed by the request that reuses
+    // its registers, so every multiply waits only for its own batch while the
+    // other is in flight. The loop's loads are unconditional and its entry and
+    // back edge leave the same requests outstanding: a conditional request, or
+    // a loop entered with fewer requests in flight, makes the compiler's wait
+    // counts assume the worst and drain the prefetch. The scheduling barriers
+    // keep the compiler from sinking a request below the next multiply.
     if (batches > 0) {
         TiledBatch<RB, NB, STEPS> ta, tb2;
         fetch(0, ta);
-        for (int i = 0; i < batches; i += 2) {
-            if (i + 1 < batches) fetch(i + 1, tb2);
+        fetch(1, tb2);
+        int i = 0;
+        for (; i + 3 < batches; i += 2) {
             consume(i, ta);
-            if (i + 1 >= batches) break;
-            if (i + 2 < batches) fetch(i + 2, ta);
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(i + 2, ta);
+            __builtin_amdgcn_sched_barrier(0);
             consume(i + 1, tb2);
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(i + 3, tb2);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        // One to three batches left: i, i + 1, i + 2.
+        consume(i, ta);
+        if (i + 2 < batches) fetch(i + 2, ta);
+        if (i + 1 < batches) consume(i + 1, tb2);
+        if (i + 2 < batches) consume(i + 2, ta);
     }
 #pragma unroll
     for (int b = 0; b < RB; ++b)
@@ -472,9 +489,13 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_lds(const __half* __restrict_
             }
         }
     };
-    // The first weight batch is in flight while the activations are staged.
+    // The first two weight batches are in flight while the activations are
+    // staged (with one batch, the second request re-reads its last chunk).
     LdsBatch<RB, STEPS> ta, tb2;
-    if (batches > 0) fetch(0, ta);
+    if (batches > 0) {
+        fetch(0, ta);
+        fetch(1, tb2);
+    }
 
     // Staged row t holds columns [64 k0, 64 k1) of the workgroup's K range.
     const int units = (range.k1 - range.k0) * 8;  // 16-byte units per staged row
@@ -527,14 +548,24 @@ __global__ __launch_bounds__(W * 64) void q8_tiled_lds(const __half* __restrict_
             }
         }
     };
+    // Two batches in flight, pipelined as in q8_tiled_decode; batches 0 and 1
+    // were requested before the staging.
     if (batches > 0) {
-        for (int i = 0; i < batches; i += 2) {
-            if (i + 1 < batches) fetch(i + 1, tb2);
+        int i = 0;
+        for (; i + 3 < batches; i += 2) {
             consume(i, ta);
-            if (i + 1 >= batches) break;
-            if (i + 2 < batches) fetch(i + 2, ta);
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(i + 2, ta);
+            __builtin_amdgcn_sched_barrier(0);
             consume(i + 1, tb2);
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(i + 3, tb2);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        consume(i, ta);
+        if (i + 2 < batches) fetch(i + 2, ta);
+        if (i + 1 < batches) consume(i + 1, tb2);
+        if (i + 2 < batches) consume(i + 2, ta);
     }
     __syncthreads();  // every wave is done with the staged activations
     float4v* partial = reinterpret_cast<float4v*>(lds);  // [W][RB][64]
@@ -583,7 +614,9 @@ void launch_tiled(const __half* x, const uint4* codes, const std::uint32_t* scal
 //
 // One token: activations staged in LDS; 16 waves over one row block (four
 // chunks per batch) up to 256 blocks, over two row blocks below 1024 blocks,
-// else 8 waves over three. More tokens: register fragments, 8
+// else 8 waves over three (one chunk per batch: with two, the two batches in
+// flight hold 12 KB per wave and gate+up at one token measured 32.0 against
+// 29.9 us). More tokens: register fragments, 8
 // waves, one batch of chunks in flight behind the current one, and the
 // (row blocks, K halves) shape of the candidates below whose grid is largest
 // without passing 256 workgroups; ties go to the unsplit shape up to 16 tokens
@@ -649,7 +682,7 @@ void tiled_dispatch(const __half* xp, const uint4* cp, const std::uint32_t* sp, 
     else if (sh.lds && sh.rb == 2)
         launch_tiled_lds<16, 2, 1, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else if (sh.lds)
-        launch_tiled_lds<8, 3, 2, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+        launch_tiled_lds<8, 3, 1, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else if (tokens <= 16)
         launch_tiled_shape<1, SWIGLU>(sh, xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else
