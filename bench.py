@@ -540,7 +540,7 @@ def a8_decode(backend, device, steps, warmup, copy_mb, tokens_list=(1, 8)):
     benchmarks/v100-q8-dp4a/summary.md:101-110): the config-2 projection set,
     M in {1, 8}, one pass and two (the residual profile). Each launch quantizes
     the fp16 activations into the plan's workspace and runs the W8A8 projection
-    (route auto: the reference-order kernel below 64 tokens), rotating >=
+    (route auto: the int8 matrix-core decode kernel up to 32 tokens), rotating >=
     `copy_mb` MB of weight copies in one HIP graph per group, as the Q8 decode.
     Algorithmic bytes per launch = N*Kp*(1 + 2/32) weights + M*K*2 activations +
     2 * M*ceil(K/32)*36*passes workspace (written, read) + M*N*2 outputs.
@@ -585,7 +585,9 @@ def a8_decode(backend, device, steps, warmup, copy_mb, tokens_list=(1, 8)):
         "workload": "A8 decode: config-2 projection set, M in {1, 8}, 1 and 2 passes (quantize + W8A8 projection)",
         "route": route,
         "GB/s": round(total / wall / 1e9, 1),
-        "roofline": {"bound": "hbm", "kernel": "a8 quantize + reference-order W8A8 projection",
+        "roofline": {"bound": "hbm", "kernel": "a8 quantize + " + (
+                         "int8 matrix-core W8A8 decode projection (a8_tiled_decode)" if route == "venturi-q8-a8-mfma"
+                         else "reference-order W8A8 projection"),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4)},
         "graph_equals_eager": same,

@@ -66,6 +66,16 @@ int venturi_q8_dp4a_run(const void* workspace, uint64_t available, const int8_t*
 int venturi_q8_a8_gemm_run(const void* workspace, uint64_t available, const int8_t* codes, const void* scales,
                            void* out, int tokens, int n, int k, int padded, int passes, void* stream);
 
+/* Extension (no counterpart in the reference): the same W8A8 projection at
+ * 1..32 tokens on int8 matrix cores (v_mfma_i32_16x16x32_i8: one exact int32
+ * group dot per 32-column group) over the tiled Q8 planes that
+ * venturi_q8_tiled_run reads (codes [block][chunk][lane][16 B], scales
+ * [block][chunk][row][2]); the scaled group terms summed in natural order, so
+ * outputs match the reference to fp32 association. Same workspace as
+ * venturi_q8_dp4a_run; workspace and planes 16-byte aligned. */
+int venturi_q8_a8_tiled_run(const void* workspace, uint64_t available, const void* codes, const void* scales,
+                            void* out, int tokens, int n, int k, int padded, int passes, void* stream);
+
 /* One matrix of a fused projection: resident Q8 planes, its fp16 output
  * [tokens][stride] (rows n, stride >= n). 32 bytes, as ops_api.h:8-9. */
 typedef struct VQFOutput {

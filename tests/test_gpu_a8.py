@@ -30,7 +30,7 @@ def test_quantizer_and_projection_bytes(backend, device, passes, tokens, shape):
     n, k = shape
     print(f"case a8 n={n} k={k} tokens={tokens} passes={passes}", flush=True)
     codes, scales, x, resident = _setup(backend, device, n, k, tokens)
-    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=passes == 2)
+    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=passes == 2, route="exact")
     workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
     guard, out = guarded_out(tokens, n, torch.float16, device)
     plan.run(x.to(device), out=out, workspace=workspace)

@@ -10,10 +10,13 @@ fp16 activations into a caller-owned workspace (``workspace_bytes`` bytes,
   shuffle-tree order (SIMT below 64 tokens, matrix cores above), so the fp16
   outputs are byte-identical to the reference's;
 * ``mfma``: matrix cores with the scaled group terms summed in natural order
-  (one accumulator per output, large tiles), equal to the reference up to
-  fp32 association;
-* ``auto``: ``mfma`` from 64 tokens (prefill), ``exact`` below (decode, where
-  the projection streams the weights and the order costs nothing).
+  (one accumulator per output), equal to the reference up to fp32
+  association: up to 32 tokens the int8 decode kernel over the resident's
+  tiled planes (``venturi_q8_a8_tiled_run``, the layout of the A16 decode
+  route, built once per resident), above that the prefill GEMM's large tiles;
+* ``auto``: ``mfma`` up to 32 tokens and from 64 (decode and prefill),
+  ``exact`` between (the SIMT kernel streams the weights there, and the
+  prefill GEMM's 256-token tiles would mostly hold padding).
 """
 
 from dataclasses import dataclass
@@ -26,6 +29,7 @@ from .vocabulary import ResidentQ8Vocabulary
 
 A8_ROUTES = ("auto", "exact", "mfma")
 A8_MFMA_MIN_AUTO_TOKENS = 64
+A8_TILED_MAX_TOKENS = 32  # the int8 decode kernel's limit (two token blocks of 16)
 
 
 @dataclass(frozen=True)
@@ -70,8 +74,12 @@ class PreparedQ8DP4A:
         disjoint(out, (workspace,) + r.storage_tensors)
         if workspace.data_ptr() % 16:
             raise ValueError("A8 workspace requires 16-byte alignment")
-        entry = self._native.venturi_q8_dp4a_run if self.kernel == "exact" else self._native.venturi_q8_a8_gemm_run
-        codes, scales = r.row_major_planes()
+        if self.kernel == "tiled":
+            entry = self._native.venturi_q8_a8_tiled_run
+            codes, scales = r.tiled_planes()
+        else:
+            entry = self._native.venturi_q8_dp4a_run if self.kernel == "exact" else self._native.venturi_q8_a8_gemm_run
+            codes, scales = r.row_major_planes()
         with torch.cuda.device(r.device):
             r.backend._check(
                 entry(
@@ -121,5 +129,9 @@ def prepare_q8_dp4a(resident, *, tokens, residual_compensation, route="auto"):
     if not size:
         resident.backend._check(-1)
     if route == "auto":
-        route = "mfma" if tokens >= A8_MFMA_MIN_AUTO_TOKENS else "exact"
-    return PreparedQ8DP4A(resident, tokens, passes, size, native, route)
+        route = "mfma" if tokens >= A8_MFMA_MIN_AUTO_TOKENS or tokens <= A8_TILED_MAX_TOKENS else "exact"
+    kernel = route
+    if route == "mfma" and tokens <= A8_TILED_MAX_TOKENS:
+        kernel = "tiled"
+        resident.tiled_planes()  # built once per resident, outside any capture
+    return PreparedQ8DP4A(resident, tokens, passes, size, native, kernel)
