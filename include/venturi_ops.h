@@ -76,6 +76,17 @@ int venturi_q8_a8_gemm_run(const void* workspace, uint64_t available, const int8
 int venturi_q8_a8_tiled_run(const void* workspace, uint64_t available, const void* codes, const void* scales,
                             void* out, int tokens, int n, int k, int padded, int passes, void* stream);
 
+/* Extension (no counterpart in the reference): venturi_q8_dp4a_quantize
+ * (q8_dp4a.cuh:15-45) of fp16 x [tokens][k] into the workspace followed by
+ * venturi_q8_a8_tiled_run, as one launch when tokens <= 16, k % 8 == 0, x is
+ * 16-byte aligned and the quantized activations fit 64 KB of LDS (each
+ * workgroup quantizes them itself), else as the two launches. Either way the
+ * workspace ends holding the quantizer's bytes and out the bytes of the two
+ * calls. */
+int venturi_q8_a8_tiled_linear_run(const void* x, void* workspace, uint64_t available, const void* codes,
+                                   const void* scales, void* out, int tokens, int n, int k, int padded, int passes,
+                                   void* stream);
+
 /* One matrix of a fused projection: resident Q8 planes, its fp16 output
  * [tokens][stride] (rows n, stride >= n). 32 bytes, as ops_api.h:8-9. */
 typedef struct VQFOutput {

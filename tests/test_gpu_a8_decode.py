@@ -10,7 +10,10 @@
   reference-order oracle (check_a8_tolerance), for one and two passes, odd
   shapes (k not a multiple of 64 or 128, n not a multiple of 16), one and
   two token blocks, and the config-2 shapes on sampled rows.
-* The plan picks the kernel: auto and mfma take it up to 32 tokens.
+* The plan picks the kernel: auto and mfma take it up to 32 tokens; run()
+  quantizes inside the projection kernel where the activations fit (up to 16
+  tokens, k % 8 == 0, x 16-byte aligned, 64 KB of LDS) and equals the separate
+  quantize + project steps byte for byte, fused or not.
 """
 
 import numpy as np
@@ -48,6 +51,55 @@ def test_tiled_a8_tolerance(backend, device, passes, tokens, shape):
     again = torch.empty_like(out)
     plan.run(x.to(device), out=again, workspace=workspace)
     assert torch.equal(again.view(torch.int16), out.view(torch.int16))  # deterministic
+    # run() quantizes inside the projection where the activations fit; the two
+    # separate steps give the same workspace and output bytes.
+    split_ws = torch.full_like(workspace, 0x5A)
+    split = torch.empty_like(out)
+    plan.quantize(x.to(device), workspace=split_ws)
+    plan.project(out=split, workspace=split_ws)
+    assert torch.equal(split_ws, workspace)
+    assert torch.equal(split.view(torch.int16), out.view(torch.int16))
+
+
+@pytest.mark.parametrize("tokens", [1, 5, 16])
+def test_tiled_a8_unaligned_input(backend, device, tokens):
+    # x at a 2-byte offset takes the two-launch form: same bytes as the fused one.
+    n, k = 100, 1024
+    codes, scales, x, resident = _setup(backend, device, n, k, tokens)
+    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=False)
+    base = torch.empty(tokens * k + 8, dtype=torch.float16, device=device)
+    shifted = base[1 : 1 + tokens * k].view(tokens, k)
+    shifted.copy_(x.to(device))
+    aligned = x.to(device)
+    assert shifted.data_ptr() % 16 and aligned.data_ptr() % 16 == 0
+    outs, spaces = [], []
+    for source in (aligned, shifted):
+        ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+        out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+        plan.run(source, out=out, workspace=ws)
+        outs.append(out)
+        spaces.append(ws)
+    assert torch.equal(spaces[0], spaces[1])
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    q, d = oracle.a8_quantize(bits(x), 1)
+    np.testing.assert_array_equal(spaces[0].cpu().numpy(), oracle.a8_workspace(q, d))
+    check_a8_tolerance(bits(outs[0]), q, d, codes.numpy(), scales.numpy(), k,
+                       oracle.a8_linear(q, d, codes.numpy(), scales.numpy(), k))
+
+
+def test_tiled_a8_nonfinite(backend, device):
+    # A group with a non-finite value: zero codes, NaN scale, NaN outputs for that token only.
+    n, k, tokens = 48, 256, 3
+    _, _, x, resident = _setup(backend, device, n, k, tokens)
+    x[1, 40] = float("inf")
+    plan = prepare_q8_dp4a(resident, tokens=tokens, residual_compensation=True)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    plan.run(x.to(device), out=out, workspace=ws)
+    q, d = oracle.a8_quantize(bits(x), 2)
+    np.testing.assert_array_equal(ws.cpu().numpy(), oracle.a8_workspace(q, d))
+    o = out.cpu()
+    assert torch.isnan(o[1]).all() and torch.isfinite(o[0]).all() and torch.isfinite(o[2]).all()
 
 
 @pytest.mark.parametrize("tokens", [1, 5, 16, 32])

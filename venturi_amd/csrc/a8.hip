@@ -5,7 +5,7 @@
 // Workspace layout (q8_dp4a.cuh:7-13, 72-76): with G = ceil(k/32) groups and
 // count = tokens*G, int8 codes [pass][token][group][32] are followed directly
 // by fp32 scales [pass][token][group]; total count*36*passes bytes.
-#include "common.hpp"
+#include "a8_group.hpp"
 
 namespace vt {
 
@@ -27,54 +27,6 @@ std::uint64_t a8_bytes(int tokens, int k, int passes) {
 }
 
 namespace {
-
-// Quantization of one 32-value group (q8_dp4a.cuh:15-34). GL adjacent lanes
-// hold NV values each (NV*GL == 32). The group max is order independent; the
-// scale and inverse are IEEE f32 divisions, the code is the RNE f32 product
-// rounded half-to-even and clamped to +-127, and the residual update is one
-// fused multiply-add, exactly as the reference. A group with any non-finite
-// input stores zero codes and a NaN scale for every pass.
-template <int NV, int GL>
-__device__ __forceinline__ void quantize_group(float (&r)[NV], bool bad_local, int passes,
-                                               std::int8_t* codes_out, float* scale_out,
-                                               std::int64_t code_pass_stride,
-                                               std::int64_t scale_pass_stride, bool leader) {
-    static_assert(NV * GL == 32, "a group is 32 values");
-    int bad = bad_local ? 1 : 0;
-#pragma unroll
-    for (int m = 1; m < GL; m <<= 1) bad |= __shfl_xor(bad, m, 64);
-    const bool invalid = bad != 0;
-    for (int p = 0; p < passes; ++p) {
-        float mx = 0.0f;
-#pragma unroll
-        for (int v = 0; v < NV; ++v) mx = fmaxf(mx, fabsf(r[v]));
-#pragma unroll
-        for (int m = 1; m < GL; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-        const float scale = __fdiv_rn(mx, 127.0f);
-        const float inverse = mx > 0.0f ? __fdiv_rn(127.0f, mx) : 0.0f;
-        std::uint32_t word[NV / 4];
-#pragma unroll
-        for (int i = 0; i < NV / 4; ++i) word[i] = 0u;
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            int code = 0;
-            if (!invalid) {
-                const float scaled = rintf(__fmul_rn(r[v], inverse));
-                code = static_cast<int>(fminf(fmaxf(scaled, -127.0f), 127.0f));
-            }
-            word[v / 4] |= static_cast<std::uint32_t>(code & 0xff) << (8 * (v % 4));
-            r[v] = __fmaf_rn(-static_cast<float>(code), scale, r[v]);
-        }
-        std::int8_t* dst = codes_out + p * code_pass_stride;
-        if constexpr (NV == 4) {
-            *reinterpret_cast<std::uint32_t*>(dst) = word[0];
-        } else {
-            static_assert(NV == 8, "4 or 8 values per lane");
-            *reinterpret_cast<uint2*>(dst) = make_uint2(word[0], word[1]);
-        }
-        if (leader) scale_out[p * scale_pass_stride] = invalid ? __builtin_nanf("") : scale;
-    }
-}
 
 // Plain quantizer: 4 lanes per group, 8 consecutive values per lane.
 __global__ __launch_bounds__(256) void a8_quantize(const __half* __restrict__ x, std::int8_t* codes,

@@ -19,22 +19,67 @@
 // the A fragments as stored (lane 16q + m holds row m's bytes 8q .. 8q+7 of
 // groups 2c and 2c+1 of chunk c, 16 bytes), a lane's four weight-row scales
 // of a chunk are one 16-byte load from the tiled scales ([block][chunk][row]
-// [2 groups]), and its activation scales are the two of its own token
-// ([pass][token][group] fp32, as the workspace holds them). B fragments are
-// 8 bytes of the token's group codes at [pass][token][group][8q ..].
+// [2 groups]), and its activation scales are the two of its own token. B
+// fragments are 8 bytes of the token's group codes at [group][8q ..].
+//
+// Two kernels share that arithmetic:
+// * a8_tiled_decode reads a filled A8 workspace ([pass][token][group][32]
+//   codes, then fp32 scales [pass][token][group]) from global memory;
+// * a8_tiled_fused (up to 16 tokens, k % 8 == 0, its activations within 64 KB
+//   of LDS) quantizes the fp16 activations itself: each workgroup issues its
+//   first two weight batches, quantizes every token's groups into LDS with the
+//   quantizer's arithmetic (workgroup 0 also writes them to the workspace, so
+//   the workspace ends as the quantizer leaves it), and its waves read their B
+//   fragments from LDS. One launch replaces the quantizer's and the
+//   projection's; the group sums and their order are those of a8_tiled_decode
+//   at the same shape, so the two give the same bytes.
 //
 // Launch: W waves over RB row blocks per workgroup, the chunks split evenly
 // over the waves, two batches of one chunk in flight per wave (the loads are
 // unconditional and the loop's entry and back edge leave the same requests
 // outstanding, so each multiply waits only for its own batch); the W partial
 // tiles are summed through LDS in wave order, so results are deterministic.
-#include "common.hpp"
+#include "a8_group.hpp"
+
+#include <algorithm>
+#include <type_traits>
 
 namespace vt {
 namespace {
 
 typedef int int4v __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+
+// Runs a wave's `batches` multiplies with NBUF batches in flight: buf[j]
+// holds batch j on entry, and batch i + NBUF is requested into batch i's
+// buffer as soon as batch i is multiplied. The steady loop requests
+// unconditionally (every wait then covers only the batch about to be
+// multiplied) and multiplies with the second-group check off
+// (consume(batch, std::false_type)); the tail, the last NBUF .. 2 * NBUF - 1
+// batches, which hold the wave's last chunk, checks (std::true_type).
+template <int NBUF, class Batch, class Fetch, class Consume>
+__device__ __forceinline__ void run_pipeline(int batches, Batch (&buf)[NBUF], Fetch& fetch, Consume& consume) {
+    int i = 0;
+    for (; i + 2 * NBUF - 1 < batches; i += NBUF) {
+#pragma unroll
+        for (int j = 0; j < NBUF; ++j) {
+            consume(buf[j], std::false_type{});
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(i + NBUF + j, buf[j]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // Here batches - i < 2 * NBUF: at most batches i + NBUF .. i + 2 * NBUF - 2
+    // remain to be requested.
+#pragma unroll
+    for (int j = 0; j < NBUF; ++j) {
+        if (i + j < batches) consume(buf[j], std::true_type{});
+        if (j < NBUF - 1 && i + NBUF + j < batches) fetch(i + NBUF + j, buf[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < NBUF - 1; ++j)
+        if (i + NBUF + j < batches) consume(buf[j], std::true_type{});
+}
 
 template <int RB, int NB, int P>
 struct A8Batch {
@@ -45,7 +90,7 @@ struct A8Batch {
     bool pair;                // group 2c + 1 exists (false only in the last chunk of an odd group count)
 };
 
-template <int W, int RB, int NB, int P>
+template <int W, int RB, int NB, int P, int NBUF>
 __global__ __launch_bounds__(W * 64) void a8_tiled_decode(const std::int8_t* __restrict__ acodes,
                                                           const float* __restrict__ ascales,
                                                           const uint4* __restrict__ codes,
@@ -117,7 +162,10 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_decode(const std::int8_t* __r
         for (int tb = 0; tb < NB; ++tb) y[b][tb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
     const int4v zero = {0, 0, 0, 0};
 
-    auto consume = [&](const A8Batch<RB, NB, P>& t) {
+    // Only a wave's last chunk can lack its second group, and it is one of the
+    // loop's tail multiplies: the loop body takes the group unconditionally.
+    auto consume = [&](const A8Batch<RB, NB, P>& t, auto last) {
+        const bool second = !decltype(last)::value || t.pair;
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             const long wa = static_cast<long>(static_cast<unsigned long>(t.w[b].x) | (static_cast<unsigned long>(t.w[b].y) << 32));
@@ -141,7 +189,7 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_decode(const std::int8_t* __r
                     const float wsa = half_lo(pair[e]), wsb = half_hi(pair[e]);
                     if constexpr (P == 1) {
                         y[b][tb][e] = fmaf(static_cast<float>(da[0][e]), wsa * t.as[0][tb][0], y[b][tb][e]);
-                        if (t.pair)
+                        if (second)
                             y[b][tb][e] = fmaf(static_cast<float>(db[0][e]), wsb * t.as[0][tb][1], y[b][tb][e]);
                     } else {
                         const float ta = fmaf(static_cast<float>(da[1][e]), t.as[1][tb][0],
@@ -149,7 +197,7 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_decode(const std::int8_t* __r
                         const float tbv = fmaf(static_cast<float>(db[1][e]), t.as[1][tb][1],
                                                static_cast<float>(db[0][e]) * t.as[0][tb][1]);
                         y[b][tb][e] = fmaf(ta, wsa, y[b][tb][e]);
-                        if (t.pair) y[b][tb][e] = fmaf(tbv, wsb, y[b][tb][e]);
+                        if (second) y[b][tb][e] = fmaf(tbv, wsb, y[b][tb][e]);
                     }
                 }
             }
@@ -157,24 +205,10 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_decode(const std::int8_t* __r
     };
 
     if (batches > 0) {
-        A8Batch<RB, NB, P> ta, tb2;
-        fetch(0, ta);
-        fetch(1, tb2);
-        int i = 0;
-        for (; i + 3 < batches; i += 2) {
-            consume(ta);
-            __builtin_amdgcn_sched_barrier(0);
-            fetch(i + 2, ta);
-            __builtin_amdgcn_sched_barrier(0);
-            consume(tb2);
-            __builtin_amdgcn_sched_barrier(0);
-            fetch(i + 3, tb2);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        consume(ta);
-        if (i + 2 < batches) fetch(i + 2, ta);
-        if (i + 1 < batches) consume(tb2);
-        if (i + 2 < batches) consume(ta);
+        A8Batch<RB, NB, P> buf[NBUF];
+#pragma unroll
+        for (int j = 0; j < NBUF; ++j) fetch(j, buf[j]);
+        run_pipeline<NBUF>(batches, buf, fetch, consume);
     }
 #pragma unroll
     for (int b = 0; b < RB; ++b)
@@ -198,33 +232,283 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_decode(const std::int8_t* __r
     }
 }
 
-template <int W, int RB, int NB, int P>
-void launch_a8_tiled(const std::int8_t* acodes, const float* ascales, const uint4* codes, const uint4* scales,
-                     __half* out, int tokens, int n, int groups, int chunks, int blocks, hipStream_t stream) {
-    a8_tiled_decode<W, RB, NB, P><<<(blocks + RB - 1) / RB, W * 64, 0, stream>>>(acodes, ascales, codes, scales, out,
-                                                                                 tokens, n, groups, chunks, blocks);
+// Bytes of LDS rows in a8_tiled_fused: a (pass, token) code row holds the
+// groups' 32 codes plus 32 bytes of padding (rows of consecutive tokens start
+// on different banks); a scale row holds an even number of floats, two more
+// than the groups rounded up to even (the pair of a chunk is one 8-byte read).
+__host__ __device__ constexpr int a8_code_row(int groups) { return 32 * groups + 32; }
+__host__ __device__ constexpr int a8_scale_row(int groups) { return 2 * ((groups + 1) / 2) + 2; }
+// Quantizer tasks (4 per group and token) per thread of a8_tiled_fused: the
+// workgroup quantizes all activations in one round of loads.
+constexpr int kA8FusedTasks = 3;
+
+template <int RB, int P>
+struct FusedBatch {
+    uint4 w[RB];   // 16 weight code bytes per block (groups 2c and 2c + 1)
+    uint4 ws[RB];  // four rows' scale pairs (fp16)
+    uint2 xa[P];   // the lane's 8 activation code bytes of group 2c (from LDS)
+    uint2 xb[P];   // ... of group 2c + 1
+    float2 as[P];  // the token's activation scales of the two groups (from LDS)
+    int ch;        // the chunk
+};
+
+template <int W, int RB, int P, int NBUF>
+__global__ __launch_bounds__(W * 64) void a8_tiled_fused(const __half* x, std::int8_t* __restrict__ wcodes,
+                                                         float* __restrict__ wscales, const uint4* __restrict__ codes,
+                                                         const uint4* __restrict__ scales, __half* __restrict__ out,
+                                                         int tokens, int n, int k, int groups, int chunks, int blocks) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, r = lane & 15;
+    const int block0 = blockIdx.x * RB;
+    const int used = (groups + 1) / 2;
+    const int per = (used + W - 1) / W;
+    const int c0 = min(wave * per, used), c1 = min(c0 + per, used);
+    const int batches = c1 - c0;
+    const int rs = a8_code_row(groups), ss = a8_scale_row(groups);
+    std::int8_t* lcodes = reinterpret_cast<std::int8_t*>(lds);
+    float* lscales = reinterpret_cast<float*>(lds + static_cast<std::size_t>(P) * tokens * rs);
+
+    const uint4* wsrc[RB];
+    const uint4* ssrc[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+        const std::int64_t blk = min(block0 + b, blocks - 1);  // clamped blocks are never stored
+        wsrc[b] = codes + blk * chunks * 64 + lane;
+        ssrc[b] = scales + blk * chunks * 4 + q;
+    }
+    // B fragments of this lane's token (absent tokens read the last token's
+    // row and feed only outputs that are never stored).
+    const int tr = min(r, tokens - 1);
+    const std::int8_t* xrow[P];
+    const float* srow[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        xrow[p] = lcodes + (p * tokens + tr) * rs + 8 * q;
+        srow[p] = lscales + (p * tokens + tr) * ss;
+    }
+    // Chunk i of the wave, clamped to the wave's last chunk (a wave without
+    // chunks reads chunk used - 1 and multiplies nothing): weights from
+    // global memory, activations from LDS. In the last chunk of an odd group
+    // count the second group is not the workspace's: its LDS bytes are not
+    // written and its term is skipped.
+    auto fetch_weights = [&](int i, FusedBatch<RB, P>& t) {
+        t.ch = min(c0 + i, c1 - 1);
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            t.w[b] = stream_load(wsrc[b] + static_cast<std::int64_t>(t.ch) * 64);
+            t.ws[b] = stream_load(ssrc[b] + static_cast<std::int64_t>(t.ch) * 4);
+        }
+    };
+    auto fetch_activations = [&](FusedBatch<RB, P>& t) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            t.xa[p] = *reinterpret_cast<const uint2*>(xrow[p] + 64 * t.ch);
+            t.xb[p] = *reinterpret_cast<const uint2*>(xrow[p] + 64 * t.ch + 32);
+            t.as[p] = *reinterpret_cast<const float2*>(srow[p] + 2 * t.ch);
+        }
+    };
+    // Quantize every token's groups into LDS: 4 lanes per group, 8 columns
+    // each (k % 8 == 0, so a lane's columns are all inside the row or all past
+    // it), at most kA8FusedTasks tasks per thread (the host admits only such
+    // launches). Their loads are unconditional (clamped addresses, masked
+    // values) and go out before the first NBUF weight batches, so those are in
+    // flight while the activations are quantized (and, counted in order, the
+    // activation loads are not held behind them).
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    const int tasks = tokens * groups * 4;
+    FusedBatch<RB, P> buf[NBUF];
+    {
+        uint4 u[kA8FusedTasks];
+#pragma unroll
+        for (int j = 0; j < kA8FusedTasks; ++j) {
+            const int task = min(static_cast<int>(threadIdx.x) + j * W * 64, tasks - 1);
+            const int gi = task >> 2, t = gi / groups, col = 32 * (gi - t * groups) + 8 * (task & 3);
+            u[j] = *reinterpret_cast<const uint4*>(x + static_cast<std::int64_t>(t) * k + min(col, k - 8));
+        }
+        __asm__ __volatile__("" ::: "memory");  // keeps these loads here, ahead of the weights'
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NBUF; ++j) fetch_weights(j, buf[j]);
+#pragma unroll
+        for (int j = 0; j < kA8FusedTasks; ++j) {
+            const int task = threadIdx.x + j * W * 64;
+            if (task >= tasks) break;  // the 4 lanes of a group stop together
+            const int sub = task & 3, gi = task >> 2;
+            const int t = gi / groups, g = gi - t * groups;
+            const bool inside = 32 * g + 8 * sub < k;
+            float v[8] = {half_lo(u[j].x), half_hi(u[j].x), half_lo(u[j].y), half_hi(u[j].y),
+                          half_lo(u[j].z), half_hi(u[j].z), half_lo(u[j].w), half_hi(u[j].w)};
+            bool bad = false;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[e] = inside ? v[e] : 0.0f;
+                bad |= !isfinite(v[e]);
+            }
+            const bool invalid = group_invalid<4>(bad);
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                std::uint32_t word[2];
+                const float sc = quantize_pass<8, 4>(v, invalid, word);
+                const uint2 pair = make_uint2(word[0], word[1]);
+                *reinterpret_cast<uint2*>(lcodes + (p * tokens + t) * rs + 32 * g + 8 * sub) = pair;
+                if (sub == 0) lscales[(p * tokens + t) * ss + g] = sc;
+                if (blockIdx.x == 0) {
+                    *reinterpret_cast<uint2*>(wcodes + (p * count + gi) * 32 + 8 * sub) = pair;
+                    if (sub == 0) wscales[p * count + gi] = sc;
+                }
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NBUF; ++j) fetch_activations(buf[j]);
+
+    float4v y[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) y[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    const int4v zero = {0, 0, 0, 0};
+
+    // Only a wave's last chunk can lack its second group, and it is one of the
+    // loop's tail multiplies: the loop body takes the group unconditionally.
+    auto consume = [&](const FusedBatch<RB, P>& t, auto last) {
+        const bool second = !decltype(last)::value || 2 * t.ch + 1 < groups;
+        long xa[P], xb[P];
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            xa[p] = static_cast<long>(static_cast<unsigned long>(t.xa[p].x) | (static_cast<unsigned long>(t.xa[p].y) << 32));
+            xb[p] = static_cast<long>(static_cast<unsigned long>(t.xb[p].x) | (static_cast<unsigned long>(t.xb[p].y) << 32));
+        }
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            const long wa = static_cast<long>(static_cast<unsigned long>(t.w[b].x) | (static_cast<unsigned long>(t.w[b].y) << 32));
+            const long wb = static_cast<long>(static_cast<unsigned long>(t.w[b].z) | (static_cast<unsigned long>(t.w[b].w) << 32));
+            const std::uint32_t wpair[4] = {t.ws[b].x, t.ws[b].y, t.ws[b].z, t.ws[b].w};
+            int4v da[P], db[P];
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                da[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa[p], zero, 0, 0, 0);
+                db[p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wb, xb[p], zero, 0, 0, 0);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float wsa = half_lo(wpair[e]), wsb = half_hi(wpair[e]);
+                if constexpr (P == 1) {
+                    y[b][e] = fmaf(static_cast<float>(da[0][e]), wsa * t.as[0].x, y[b][e]);
+                    if (second) y[b][e] = fmaf(static_cast<float>(db[0][e]), wsb * t.as[0].y, y[b][e]);
+                } else {
+                    const float ta = fmaf(static_cast<float>(da[1][e]), t.as[1].x, static_cast<float>(da[0][e]) * t.as[0].x);
+                    const float tbv = fmaf(static_cast<float>(db[1][e]), t.as[1].y, static_cast<float>(db[0][e]) * t.as[0].y);
+                    y[b][e] = fmaf(ta, wsa, y[b][e]);
+                    if (second) y[b][e] = fmaf(tbv, wsb, y[b][e]);
+                }
+            }
+        }
+    };
+    auto fetch = [&](int i, FusedBatch<RB, P>& t) {
+        fetch_weights(i, t);
+        fetch_activations(t);
+    };
+
+    if (batches > 0) run_pipeline<NBUF>(batches, buf, fetch, consume);
+    __syncthreads();  // every wave is done with the activations: LDS now holds the partial tiles
+    float4v* partial = reinterpret_cast<float4v*>(lds);
+#pragma unroll
+    for (int b = 0; b < RB; ++b) partial[(wave * RB + b) * 64 + lane] = y[b];
+    __syncthreads();
+    for (int b = wave; b < RB; b += W) {
+        float4v sum = partial[b * 64 + lane];
+        for (int w = 1; w < W; ++w) {
+            const float4v v = partial[(w * RB + b) * 64 + lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum[e] += v[e];
+        }
+        const int blk = block0 + b;
+        if (blk >= blocks || r >= tokens) continue;
+        __half* o = out + static_cast<std::int64_t>(r) * n + 16 * blk + 4 * q;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (16 * blk + 4 * q + e < n) o[e] = from_f32<__half>(sum[e]);
+    }
 }
 
-// Shapes (unsplit K). One token block: 16 waves over two row blocks while that
-// grid has at most 256 workgroups (one per CU), else 8 waves over three. Two
-// token blocks: 8 waves over two row blocks (the other shapes spill).
+// Workgroup shape of both kernels (unsplit K): W waves over RB row blocks,
+// NBUF batches in flight per wave. Two token blocks take 8 waves over two row
+// blocks (the other shapes spill); one token block takes 16 waves over one
+// row block up to 256 blocks, over two up to 511 (grids of at most 256
+// workgroups, one per CU), else 8 waves over three.
+struct A8Shape {
+    int waves, rb, nbuf;
+};
+
+A8Shape a8_shape(int token_blocks, int blocks) {
+    if (token_blocks == 2) return {8, 2, 2};
+    return blocks <= 256 ? A8Shape{16, 1, 2} : blocks <= 511 ? A8Shape{16, 2, 2} : A8Shape{8, 3, 2};
+}
+
+template <int W, int RB, int NBUF>
+struct ShapeTag {
+    static constexpr int waves = W, rb = RB, nbuf = NBUF;
+};
+
+// Calls f(ShapeTag) for the compiled shape equal to sh.
+template <class... Tags, class F>
+void visit_shape(const A8Shape& sh, F&& f) {
+    const bool found = ((sh.waves == Tags::waves && sh.rb == Tags::rb && sh.nbuf == Tags::nbuf ? (f(Tags{}), true)
+                                                                                            : false) ||
+                        ...);
+    require(found, "internal: A8 decode shape not compiled");
+}
+
+template <class F>
+void visit_one_block_shape(const A8Shape& sh, F&& f) {
+    visit_shape<ShapeTag<16, 1, 2>, ShapeTag<16, 2, 2>, ShapeTag<8, 3, 2>>(sh, f);
+}
+
 template <int NB, int P>
 void dispatch_a8_tiled(const std::int8_t* acodes, const float* ascales, const uint4* codes, const uint4* scales,
                        __half* out, int tokens, int n, int groups, int chunks, int blocks, hipStream_t stream) {
-    if constexpr (NB == 2)
-        launch_a8_tiled<8, 2, NB, P>(acodes, ascales, codes, scales, out, tokens, n, groups, chunks, blocks, stream);
-    else if ((blocks + 1) / 2 <= 256)
-        launch_a8_tiled<16, 2, NB, P>(acodes, ascales, codes, scales, out, tokens, n, groups, chunks, blocks, stream);
-    else
-        launch_a8_tiled<8, 3, NB, P>(acodes, ascales, codes, scales, out, tokens, n, groups, chunks, blocks, stream);
+    auto launch = [&](auto tag) {
+        using T = decltype(tag);
+        a8_tiled_decode<T::waves, T::rb, NB, P, T::nbuf><<<(blocks + T::rb - 1) / T::rb, T::waves * 64, 0, stream>>>(
+            acodes, ascales, codes, scales, out, tokens, n, groups, chunks, blocks);
+    };
+    const A8Shape sh = a8_shape(NB, blocks);
+    if constexpr (NB == 2) visit_shape<ShapeTag<8, 2, 2>>(sh, launch);
+    else visit_one_block_shape(sh, launch);
 }
+
+std::size_t a8_fused_lds(int tokens, int groups, int passes, const A8Shape& sh) {
+    const std::size_t act = static_cast<std::size_t>(passes) * tokens *
+                            (a8_code_row(groups) + 4 * static_cast<std::size_t>(a8_scale_row(groups)));
+    return std::max(act, static_cast<std::size_t>(sh.waves) * sh.rb * 64 * sizeof(float4v));
+}
+
+template <int P>
+void dispatch_a8_fused(const __half* x, std::int8_t* wcodes, float* wscales, const uint4* codes, const uint4* scales,
+                       __half* out, int tokens, int n, int k, int groups, int chunks, int blocks, std::size_t lds,
+                       hipStream_t stream) {
+    auto launch = [&](auto tag) {
+        using T = decltype(tag);
+        a8_tiled_fused<T::waves, T::rb, P, T::nbuf><<<(blocks + T::rb - 1) / T::rb, T::waves * 64, lds, stream>>>(
+            x, wcodes, wscales, codes, scales, out, tokens, n, k, groups, chunks, blocks);
+    };
+    visit_one_block_shape(a8_shape(1, blocks), launch);
+}
+
+constexpr std::size_t kA8FusedLdsMax = 64 * 1024;  // the default dynamic LDS limit of a launch
 
 }  // namespace
 
 std::uint64_t a8_bytes(int tokens, int k, int passes);
+void a8_quantize_launch(const void* x, void* workspace, std::uint64_t available, int tokens, int k, int passes,
+                        hipStream_t stream);
 
-void a8_tiled_launch(const void* workspace, std::uint64_t available, const void* codes, const void* scales, void* out,
-                     int tokens, int n, int k, int padded, int passes, hipStream_t stream) {
+namespace {
+
+void validate_a8_tiled(const void* workspace, std::uint64_t available, const void* codes, const void* scales,
+                       const void* out, int tokens, int n, int k, int padded, int passes) {
     require(workspace && codes && scales && out, "null A8 operand");
     require(tokens > 0 && tokens <= 32, "the matrix-core A8 decode kernel takes 1..32 tokens");
     require(n > 0 && k > 0 && padded == padded_k(k), "invalid A8 projection geometry");
@@ -233,6 +517,13 @@ void a8_tiled_launch(const void* workspace, std::uint64_t available, const void*
     require(available >= a8_bytes(tokens, k, passes), "invalid A8 workspace size");
     require(aligned(workspace, 16) && aligned(codes, 16) && aligned(scales, 16) && aligned(out, 2),
             "misaligned A8 operand (workspace and tiled planes need 16 bytes)");
+}
+
+}  // namespace
+
+void a8_tiled_launch(const void* workspace, std::uint64_t available, const void* codes, const void* scales, void* out,
+                     int tokens, int n, int k, int padded, int passes, hipStream_t stream) {
+    validate_a8_tiled(workspace, available, codes, scales, out, tokens, n, k, padded, passes);
     const int groups = (k + 31) / 32;
     const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
     const auto* acodes = static_cast<const std::int8_t*>(workspace);
@@ -250,6 +541,33 @@ void a8_tiled_launch(const void* workspace, std::uint64_t available, const void*
     }
 }
 
+void a8_tiled_linear_launch(const void* x, void* workspace, std::uint64_t available, const void* codes,
+                            const void* scales, void* out, int tokens, int n, int k, int padded, int passes,
+                            hipStream_t stream) {
+    validate_a8_tiled(workspace, available, codes, scales, out, tokens, n, k, padded, passes);
+    require(x != nullptr && aligned(x, 2), "invalid A8 input");
+    const int groups = (k + 31) / 32, chunks = padded / 64, blocks = (n + 15) / 16;
+    // The fused kernel: one token block, whole 16-byte activation pieces, its
+    // LDS within the default limit and every quantizer task in its one round.
+    const A8Shape sh = a8_shape(1, blocks);
+    const std::size_t lds = a8_fused_lds(tokens, groups, passes, sh);
+    if (tokens > 16 || k % 8 != 0 || !aligned(x, 16) || lds > kA8FusedLdsMax ||
+        4L * tokens * groups > static_cast<long>(kA8FusedTasks) * sh.waves * 64) {
+        a8_quantize_launch(x, workspace, available, tokens, k, passes, stream);
+        a8_tiled_launch(workspace, available, codes, scales, out, tokens, n, k, padded, passes, stream);
+        return;
+    }
+    const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
+    auto* wcodes = static_cast<std::int8_t*>(workspace);
+    auto* wscales = reinterpret_cast<float*>(wcodes + count * 32 * passes);
+    const auto* xp = static_cast<const __half*>(x);
+    const auto* cp = static_cast<const uint4*>(codes);
+    const auto* sp = static_cast<const uint4*>(scales);
+    auto* op = static_cast<__half*>(out);
+    if (passes == 1) dispatch_a8_fused<1>(xp, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks, blocks, lds, stream);
+    else dispatch_a8_fused<2>(xp, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks, blocks, lds, stream);
+}
+
 }  // namespace vt
 
 // Extension: the W8A8 projection of venturi_q8_dp4a_run at 1..32 tokens on
@@ -264,5 +582,18 @@ extern "C" __attribute__((visibility("default"))) int venturi_q8_a8_tiled_run(co
     return vt::guarded([&] {
         vt::a8_tiled_launch(workspace, available, codes, scales, out, tokens, n, k, padded, passes,
                             static_cast<hipStream_t>(stream));
+    });
+}
+
+// Extension: venturi_q8_dp4a_quantize followed by venturi_q8_a8_tiled_run, in
+// one launch where the activations fit the fused kernel (the workspace ends
+// holding the quantized activations either way, and the outputs are the same
+// bytes as the two calls').
+extern "C" __attribute__((visibility("default"))) int venturi_q8_a8_tiled_linear_run(
+    const void* x, void* workspace, std::uint64_t available, const void* codes, const void* scales, void* out,
+    int tokens, int n, int k, int padded, int passes, void* stream) {
+    return vt::guarded([&] {
+        vt::a8_tiled_linear_launch(x, workspace, available, codes, scales, out, tokens, n, k, padded, passes,
+                                   static_cast<hipStream_t>(stream));
     });
 }

@@ -13,7 +13,9 @@ fp16 activations into a caller-owned workspace (``workspace_bytes`` bytes,
   (one accumulator per output), equal to the reference up to fp32
   association: up to 32 tokens the int8 decode kernel over the resident's
   tiled planes (``venturi_q8_a8_tiled_run``, the layout of the A16 decode
-  route, built once per resident), above that the prefill GEMM's large tiles;
+  route, built once per resident; ``run`` quantizes and projects in one
+  launch through ``venturi_q8_a8_tiled_linear_run`` where the activations
+  fit), above that the prefill GEMM's large tiles;
 * ``auto``: ``mfma`` up to 32 tokens and from 64 (decode and prefill),
   ``exact`` between (the SIMT kernel streams the weights there, and the
   prefill GEMM's 256-token tiles would mostly hold padding).
@@ -99,8 +101,19 @@ class PreparedQ8DP4A:
         disjoint(workspace, (x,) + r.storage_tensors)
         if workspace.data_ptr() % 16:
             raise ValueError("A8 workspace requires 16-byte alignment")
-        self.quantize(x, workspace=workspace)
-        return self.project(out=out, workspace=workspace)
+        if self.kernel != "tiled":
+            self.quantize(x, workspace=workspace)
+            return self.project(out=out, workspace=workspace)
+        codes, scales = r.tiled_planes()
+        with torch.cuda.device(r.device):
+            r.backend._check(
+                self._native.venturi_q8_a8_tiled_linear_run(
+                    x.data_ptr(), workspace.data_ptr(), self.workspace_bytes, codes.data_ptr(), scales.data_ptr(),
+                    out.data_ptr(), self.tokens, r.vocab_size, r.hidden_size, r.padded_k, self.passes,
+                    stream_of(r.device),
+                )
+            )
+        return out
 
 
 def prepare_q8_dp4a(resident, *, tokens, residual_compensation, route="auto"):
