@@ -103,8 +103,13 @@ def test_q4_plan_auto_route_is_dense(backend, device):
     x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(3)).half()
     xd = x.to(device)
     out = torch.empty(tokens, n, dtype=torch.float16, device=device)
-    with pytest.raises(TypeError):  # a dense plan needs its workspace, as the reference's dense plans do
-        plan.run(xd, out=out)
+    # Without a workspace (the reference's run(x, out=)) the plan runs the
+    # fused matrix-core GEMM: the bytes of the mfma route.
+    plain = torch.empty_like(out)
+    plan.run(xd, out=plain)
+    fused = torch.empty_like(out)
+    resident.prepare(tokens=tokens, route="mfma").run(xd, out=fused)
+    assert torch.equal(plain.view(torch.int16), fused.view(torch.int16))
     ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
     plan.run(xd, out=out, workspace=ws)
     got = out.cpu().float().numpy()
@@ -112,9 +117,7 @@ def test_q4_plan_auto_route_is_dense(backend, device):
     ref = (xf.astype(np.float32) @ wd.astype(np.float32).T).astype(np.float16).astype(np.float64)
     diff = np.abs(got - ref)
     assert (diff <= np.maximum(2e-3, ulp16(ref))).all()
-    # The fused matrix-core route on the same plan is the same contract.
-    fused = torch.empty_like(out)
-    resident.prepare(tokens=tokens, route="mfma").run(xd, out=fused)
+    # The fused matrix-core route on the same weights is the same contract.
     _bound_check(fused.cpu().float().numpy(), x, packed, high, scales, k, 4)
 
 
@@ -335,8 +338,14 @@ def test_q8_plan_auto_route_is_dense(backend, device):
     assert plan.route == "venturi-q8-dense" and plan.workspace_bytes > 0
     x = torch.randn(Q8_DENSE_TOKENS, k, generator=torch.Generator().manual_seed(6)).half()
     out = torch.empty(Q8_DENSE_TOKENS, n, dtype=torch.float16, device=device)
-    with pytest.raises(TypeError):
-        plan.run(x.to(device), out=out)
+    # Without a workspace (the reference's run(x, out=)) the plan runs the
+    # fused matrix-core prefill kernel: the bytes of the mfma route.
+    plain = torch.empty_like(out)
+    plan.run(x.to(device), out=plain)
+    fused = torch.empty_like(out)
+    resident.prepare(tokens=Q8_DENSE_TOKENS, route="mfma").run(x.to(device), out=fused)
+    assert torch.equal(plain.view(torch.int16), fused.view(torch.int16))
+    _q8_check(plain.cpu().float().numpy(), x, codes.numpy(), scales.numpy(), k)
     ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
     plan.run(x.to(device), out=out, workspace=ws)
     _q8_check(out.cpu().float().numpy(), x, codes.numpy(), scales.numpy(), k)

@@ -23,7 +23,9 @@ from .weights import Q4RowSplitWeight, decode_k64_fp16, rtn_k64
 #   fused   the research order of q4_fused.cuh:10-89 (FP32 weights), fp16;
 #   dense   the reference's ChunkedDense path (qwen_runtime.cuh:348-364): rows
 #           decoded to fp16(q*scale) in the caller's workspace, then hipBLASLt
-#           (fp32 accumulation), fp16, k % 8 == 0 and n % 8 == 0.
+#           (fp32 accumulation), fp16, k % 8 == 0 and n % 8 == 0; run(x, out=)
+#           without a workspace, as the reference calls a plan, runs the mfma
+#           GEMM instead (no workspace, the same contract bound).
 # auto: for fp16 activations dense from DENSE_TOKENS tokens (where the library
 # GEMM outruns the fused matrix-core kernel despite decoding the weights:
 # config-2 shapes at 1024 tokens 0.95-1.44x, at 2048 1.36-1.62x), else mfma;
@@ -216,7 +218,12 @@ class Q4LinearPlan:
         admit(x, (self.tokens, r.in_features), r.dtype, r.device, "x")
         admit(out, (self.tokens, r.out_features), r.dtype, r.device, "out")
         disjoint(out, (x,) + self.storage_tensors)
-        if self.kernel == "dense":
+        kernel = self.kernel
+        if kernel == "dense" and workspace is None:
+            # The reference's run(x, out=) passes no workspace: the fused
+            # matrix-core GEMM, which needs none, serves the call.
+            kernel = "mfma"
+        if kernel == "dense":
             admit(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
             if workspace.data_ptr() % 256 or x.data_ptr() % 16 or out.data_ptr() % 16:
                 raise ValueError("the dense Q4 route needs a 256-byte aligned workspace and 16-byte aligned x and out")
@@ -224,12 +231,12 @@ class Q4LinearPlan:
         w, lib, stream = r.weight, r.backend._native, stream_of(r.device)
         args = (x.data_ptr(), w.codes.data_ptr(), w.scales.data_ptr(), out.data_ptr())
         with torch.cuda.device(r.device):
-            if self.kernel == "dense":
+            if kernel == "dense":
                 status = lib.venturi_row_dense_run(
                     *args[:2], None, *args[2:], self.tokens, w.out_features, w.in_features, w.padded_k, 4,
                     DTYPE_CODES[r.dtype], workspace.data_ptr(), self.workspace_bytes, stream
                 )
-            elif self.kernel == "mfma" and self.tokens < DECODE_TILED_TOKENS:
+            elif kernel == "mfma" and self.tokens < DECODE_TILED_TOKENS:
                 tc, ts = r.tiled
                 slots = self.slots
                 status = lib.venturi_q4_tiled_run(
@@ -237,7 +244,7 @@ class Q4LinearPlan:
                     w.in_features, w.padded_k, DTYPE_CODES[r.dtype], None if slots is None else slots.data_ptr(),
                     0 if slots is None else slots.numel(), stream
                 )
-            elif self.kernel == "mfma":
+            elif kernel == "mfma":
                 status = lib.venturi_q4_gemm_run(
                     *args, self.tokens, w.out_features, w.in_features, w.padded_k, DTYPE_CODES[r.dtype], stream
                 )

@@ -20,7 +20,11 @@ Kernel families, chosen once per plan (``prepare(tokens=, route=)``):
   multiplied by hipBLASLt over the doubled K (every product exact, fp32
   sums: equal to the canonical order up to fp32 association); FP16, K and N
   multiples of 8, row-major planes, every scale below 516; the plan takes a
-  caller-owned workspace of ``workspace_bytes``;
+  caller-owned workspace of ``workspace_bytes`` (the two-term fp16 shadow of
+  a chunk of up to 8192 rows, 4 bytes per weight, plus hipBLASLt's 32 MiB:
+  210-533 MB at the config-2 shapes);
+  ``run(x, out=)`` without one, as the reference calls a plan, runs the
+  ``mfma`` prefill kernel instead (no workspace, the same tolerance);
 * ``auto``: ``dense`` from DENSE_TOKENS tokens where its conditions hold,
   else ``mfma`` where its conditions hold (FP16 activations, K % 8 == 0),
   else ``exact``.
@@ -345,7 +349,12 @@ class Q8OutputHead:
         admit(out, (self.tokens, self.out_features), r.dtype, r.device, "out")
         disjoint(out, (x,) + self.storage_tensors)
         lib = r.backend._native
-        if self.kernel == "dense":
+        kernel = self.kernel
+        if kernel == "dense" and workspace is None:
+            # The reference's run(x, out=) passes no workspace: the fused
+            # matrix-core prefill kernel, which needs none, serves the call.
+            kernel = "prefill"
+        if kernel == "dense":
             admit(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
             if workspace.data_ptr() % 256 or x.data_ptr() % 16 or out.data_ptr() % 16:
                 raise ValueError("the dense Q8 route needs a 256-byte aligned workspace and 16-byte aligned x and out")
@@ -357,11 +366,11 @@ class Q8OutputHead:
                     r.hidden_size, r.padded_k, DTYPE_CODES[r.dtype], workspace.data_ptr(), self.workspace_bytes,
                     stream_of(r.device)))
             return out
-        if self.kernel in ("exact", "prefill"):
-            entry = lib.venturi_q8_head_run if self.kernel == "exact" else lib.venturi_q8_prefill_run
+        if kernel in ("exact", "prefill"):
+            entry = lib.venturi_q8_head_run if kernel == "exact" else lib.venturi_q8_prefill_run
             planes, tail = r.row_major_planes(), ()
         else:
-            entry = lib.venturi_q8_tiled_swiglu_run if self.kernel == "swiglu" else lib.venturi_q8_tiled_run
+            entry = lib.venturi_q8_tiled_swiglu_run if kernel == "swiglu" else lib.venturi_q8_tiled_run
             planes = self.tiles
             tail = (0, 0) if self.slots is None else (self.slots.data_ptr(), self.slots.numel())
         with torch.cuda.device(r.device):
