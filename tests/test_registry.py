@@ -1,5 +1,6 @@
 """Codec registry geometry and byte accounting (quantization/layout.py, codecs.py)."""
 
+import numpy as np
 import pytest
 import torch
 
@@ -124,3 +125,40 @@ def test_linear_contracts_on_gfx950(monkeypatch):
     assert set(described) == {"q4_g64_fp16", "q8_g32_fp16"}
     fused = describe_linear_contracts(_weights("q4_g64_fp16"), "fp16", "fused")
     assert fused["q4_g64_fp16"]["weight_decode"] == "fp32-scaled-integer-products"
+
+
+@pytest.mark.parametrize("fmt,bits", [("q8_g32_fp16", 8), ("q4_g64_fp16", 4), ("q5_g64_fp16", 5), ("q6_g64_fp16", 6)])
+@pytest.mark.parametrize("code_dtype", [torch.uint8, torch.int8])
+def test_dequantize_matches_a_per_element_decode(fmt, bits, code_dtype):
+    # Random planes against a scalar decode written per column from the layout;
+    # the code plane's dtype (int8 or uint8 bytes) must not change the result.
+    if bits == 8 and code_dtype == torch.uint8:
+        pytest.skip("Q8 codes are int8")
+    rng = np.random.default_rng(bits * 7 + (code_dtype == torch.int8))
+    rows, cols = 3, 200
+    padded = 256
+    group = 32 if bits == 8 else 64
+    scales = torch.from_numpy(rng.uniform(0, 0.05, (rows, padded // group)).astype(np.float16))
+    if bits == 8:
+        codes = torch.from_numpy(rng.integers(-127, 128, (rows, padded)).astype(np.int8))
+        high = None
+    else:
+        codes = torch.from_numpy(rng.integers(0, 256, (rows, padded // 2)).astype(np.uint8)).view(code_dtype)
+        hb = bits - 4
+        high = torch.from_numpy(rng.integers(0, 256, (rows, padded * hb // 8)).astype(np.uint8)) if hb else None
+    got = dequantize_planes(codes, scales, high, (rows, cols), fmt).float().numpy()
+    body = codes.view(torch.uint8).numpy() if bits < 8 else codes.numpy()
+    for r in range(rows):
+        for c in range(cols):
+            if bits == 8:
+                q = int(body[r, c])
+            else:
+                q = (int(body[r, c // 2]) >> (4 * (c % 2))) & 15
+                if bits > 4:
+                    hb = bits - 4
+                    word = int(high.numpy()[r, (c * hb) // 8])
+                    q |= ((word >> ((c * hb) % 8)) & ((1 << hb) - 1)) << 4
+                if q >= 1 << (bits - 1):
+                    q -= 1 << bits
+            expected = np.float16(np.float32(q) * np.float32(scales[r, c // group].item()))
+            assert got[r, c] == np.float32(expected), (r, c)

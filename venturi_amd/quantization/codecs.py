@@ -93,36 +93,44 @@ def codec_for(fmt: str) -> Codec:
 
 
 def dequantize_planes(codes, scales, high, shape, fmt):
-    """CPU reference decode of stored planes to fp16 (codecs.py:144-177).
+    """CPU decode of stored planes to fp16 (the reference's is codecs.py:105-139).
 
-    Rejects non-finite or negative scales and, for Q8, the forbidden code -128.
+    Written from the plane layout: a row's padded columns (k rounded up to 128)
+    carry one code each; Q8 stores them as int8 (-128 is forbidden), the 4-bit
+    body of Q4/Q5/Q6 packs column 2j in the low nibble of byte j and 2j + 1 in
+    the high nibble, and Q5/Q6 keep the upper bits of column c at bit offset
+    c * (bits - 4) of the row's high plane (least significant bit first). The
+    code is the two's complement of its bits; the weight is code * scale of
+    the column's group. Rejects non-finite or negative scales.
     """
     codec = codec_for(fmt)
-    n, k = shape
     if not codec.quantized:
         raise ValueError("Expected a quantized codec")
-    groups = (-(-k // 128) * 128) // codec.group
-    plane = codes.numpy().reshape(n, groups, 32)
-    scale = scales.numpy().reshape(n, groups).astype(np.float32)
+    rows, cols = shape
+    padded = -(-cols // 128) * 128
+    scale = scales.numpy().astype(np.float32).reshape(rows, padded // codec.group)
     if not np.isfinite(scale).all() or (scale < 0).any():
         raise ValueError("Invalid stored scale")
+    code = _column_codes(codec, codes.numpy().reshape(rows, -1), high, rows, padded)
+    weight = code.astype(np.float32) * np.repeat(scale, codec.group, axis=1)
+    return torch.from_numpy(np.ascontiguousarray(weight[:, :cols])).to(torch.float16)
+
+
+def _column_codes(codec, plane, high, rows, padded):
+    """Signed integer code of every padded column, [rows, padded] int32."""
     if codec.bits == 8:
         if (plane == -128).any():
             raise ValueError("Forbidden Q8 code")
-        signed = plane.astype(np.float32)
-    else:
-        lanes = np.empty((n, groups, 64), dtype=np.int32)
-        lanes[:, :, 0::2] = plane & 15
-        lanes[:, :, 1::2] = plane >> 4
-        if codec.high_plane:
-            extra = codec.bits - 4
-            if high is None:
-                raise ValueError("Missing high-bit plane")
-            hi = high.numpy().reshape(n, groups, 8 * extra)
-            for lane in range(64):
-                bits = (hi[:, :, lane * extra // 8] >> (lane * extra % 8)) & ((1 << extra) - 1)
-                lanes[:, :, lane] |= bits.astype(np.int32) << 4
-        half_range = 1 << (codec.bits - 1)
-        signed = np.where(lanes >= half_range, lanes - (1 << codec.bits), lanes).astype(np.float32)
-    values = (signed * scale[:, :, None]).reshape(n, -1)[:, :k]
-    return torch.from_numpy(np.ascontiguousarray(values)).to(torch.float16)
+        return plane.astype(np.int32)
+    body = plane.view(np.uint8)
+    code = np.empty((rows, padded), dtype=np.int32)
+    code[:, 0::2] = body & 0x0F
+    code[:, 1::2] = body >> 4
+    if codec.high_plane:
+        if high is None:
+            raise ValueError("Missing high-bit plane")
+        extra = codec.bits - 4
+        bits = np.unpackbits(high.numpy().view(np.uint8).reshape(rows, -1), axis=1, bitorder="little")
+        upper = bits[:, : padded * extra].reshape(rows, padded, extra).astype(np.int32) @ (1 << np.arange(extra))
+        code |= upper << 4
+    return code - ((code >> (codec.bits - 1)) << codec.bits)
