@@ -22,17 +22,24 @@
 // [2 groups]), and its activation scales are the two of its own token. B
 // fragments are 8 bytes of the token's group codes at [group][8q ..].
 //
-// Two kernels share that arithmetic:
+// Three forms share that arithmetic:
 // * a8_tiled_decode reads a filled A8 workspace ([pass][token][group][32]
-//   codes, then fp32 scales [pass][token][group]) from global memory;
-// * a8_tiled_fused (up to 16 tokens, k % 8 == 0, its activations within 64 KB
-//   of LDS) quantizes the fp16 activations itself: each workgroup issues its
-//   first two weight batches, quantizes every token's groups into LDS with the
-//   quantizer's arithmetic (workgroup 0 also writes them to the workspace, so
-//   the workspace ends as the quantizer leaves it), and its waves read their B
-//   fragments from LDS. One launch replaces the quantizer's and the
-//   projection's; the group sums and their order are those of a8_tiled_decode
-//   at the same shape, so the two give the same bytes.
+//   codes, then fp32 scales [pass][token][group]) from global memory, each
+//   lane its own B fragments (up to 32 tokens);
+// * a8_tiled_lds<STAGE = true> copies a filled workspace into LDS once per
+//   workgroup (up to 16 tokens where the copy fits one round of loads and the
+//   LDS keeps the shape's workgroups resident), and its waves read their B
+//   fragments from LDS: the per-lane 8- and 4-byte fragment loads of the
+//   first form, repeated by every workgroup, become one coalesced copy;
+// * a8_tiled_lds<STAGE = false> (a8_tiled_fused; up to 16 tokens, k % 8 == 0,
+//   its activations within 64 KB of LDS) quantizes the fp16 activations
+//   itself: each workgroup issues its first two weight batches, quantizes
+//   every token's groups into LDS with the quantizer's arithmetic (workgroup 0
+//   also writes them to the workspace, so the workspace ends as the quantizer
+//   leaves it), and reads its B fragments from LDS. One launch replaces the
+//   quantizer's and the projection's.
+// The group sums and their order depend only on the workgroup shape, which
+// all three take from one table: at one shape they give the same bytes.
 //
 // Launch: W waves over RB row blocks per workgroup, the chunks split evenly
 // over the waves, two batches of one chunk in flight per wave (the loads are
@@ -241,6 +248,9 @@ __host__ __device__ constexpr int a8_scale_row(int groups) { return 2 * ((groups
 // Quantizer tasks (4 per group and token) per thread of a8_tiled_fused: the
 // workgroup quantizes all activations in one round of loads.
 constexpr int kA8FusedTasks = 3;
+// Workspace units (16 bytes of codes) and scales per thread of the staging
+// form: every admitted launch copies its activations in one round of loads.
+constexpr int kA8StageUnits = 10, kA8StageScales = 8;
 
 template <int RB, int P>
 struct FusedBatch {
@@ -252,11 +262,15 @@ struct FusedBatch {
     int ch;        // the chunk
 };
 
-template <int W, int RB, int P, int NBUF>
-__global__ __launch_bounds__(W * 64) void a8_tiled_fused(const __half* x, std::int8_t* __restrict__ wcodes,
-                                                         float* __restrict__ wscales, const uint4* __restrict__ codes,
-                                                         const uint4* __restrict__ scales, __half* __restrict__ out,
-                                                         int tokens, int n, int k, int groups, int chunks, int blocks) {
+// STAGE = false: a8_tiled_fused, the activations quantized from x (and
+// written to the workspace by workgroup 0). STAGE = true: the activations
+// copied from a filled workspace (acodes, ascales) into the same LDS rows.
+template <int W, int RB, int P, int NBUF, bool STAGE>
+__global__ __launch_bounds__(W * 64) void a8_tiled_lds(const __half* x, const std::int8_t* __restrict__ acodes,
+                                                       const float* __restrict__ ascales, std::int8_t* __restrict__ wcodes,
+                                                       float* __restrict__ wscales, const uint4* __restrict__ codes,
+                                                       const uint4* __restrict__ scales, __half* __restrict__ out,
+                                                       int tokens, int n, int k, int groups, int chunks, int blocks) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -319,7 +333,40 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_fused(const __half* x, std::i
     const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
     const int tasks = tokens * groups * 4;
     FusedBatch<RB, P> buf[NBUF];
-    {
+    if constexpr (STAGE) {
+        // Copy: the codes as 16-byte units of the (pass, token) rows, the
+        // scales one by one; at most kA8StageUnits / kA8StageScales per thread
+        // (the host admits only such launches), all loads before the weights'.
+        const int units = P * tokens * groups * 2, nscales = P * tokens * groups;
+        const uint4* src = reinterpret_cast<const uint4*>(acodes);
+        uint4 u[kA8StageUnits];
+        float sv[kA8StageScales];
+#pragma unroll
+        for (int j = 0; j < kA8StageUnits; ++j) u[j] = src[min(static_cast<int>(threadIdx.x) + j * W * 64, units - 1)];
+#pragma unroll
+        for (int j = 0; j < kA8StageScales; ++j)
+            sv[j] = ascales[min(static_cast<int>(threadIdx.x) + j * W * 64, nscales - 1)];
+        __asm__ __volatile__("" ::: "memory");  // keeps these loads here, ahead of the weights'
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NBUF; ++j) fetch_weights(j, buf[j]);
+#pragma unroll
+        for (int j = 0; j < kA8StageUnits; ++j) {
+            const int i = threadIdx.x + j * W * 64;
+            if (i < units) {
+                const int row = i / (2 * groups);
+                *reinterpret_cast<uint4*>(lcodes + row * rs + (i - row * 2 * groups) * 16) = u[j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kA8StageScales; ++j) {
+            const int i = threadIdx.x + j * W * 64;
+            if (i < nscales) {
+                const int row = i / groups;
+                lscales[row * ss + (i - row * groups)] = sv[j];
+            }
+        }
+    } else {
         uint4 u[kA8FusedTasks];
 #pragma unroll
         for (int j = 0; j < kA8FusedTasks; ++j) {
@@ -485,19 +532,26 @@ std::size_t a8_fused_lds(int tokens, int groups, int passes, const A8Shape& sh) 
     return std::max(act, static_cast<std::size_t>(sh.waves) * sh.rb * 64 * sizeof(float4v));
 }
 
-template <int P>
-void dispatch_a8_fused(const __half* x, std::int8_t* wcodes, float* wscales, const uint4* codes, const uint4* scales,
-                       __half* out, int tokens, int n, int k, int groups, int chunks, int blocks, std::size_t lds,
-                       hipStream_t stream) {
+template <int P, bool STAGE>
+void dispatch_a8_lds(const __half* x, const std::int8_t* acodes, const float* ascales, std::int8_t* wcodes,
+                     float* wscales, const uint4* codes, const uint4* scales, __half* out, int tokens, int n, int k,
+                     int groups, int chunks, int blocks, std::size_t lds, hipStream_t stream) {
     auto launch = [&](auto tag) {
         using T = decltype(tag);
-        a8_tiled_fused<T::waves, T::rb, P, T::nbuf><<<(blocks + T::rb - 1) / T::rb, T::waves * 64, lds, stream>>>(
-            x, wcodes, wscales, codes, scales, out, tokens, n, k, groups, chunks, blocks);
+        auto* kernel = a8_tiled_lds<T::waves, T::rb, P, T::nbuf, STAGE>;
+        if (lds > 64 * 1024) {
+            static const hipError_t raised = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            check(raised);
+        }
+        kernel<<<(blocks + T::rb - 1) / T::rb, T::waves * 64, lds, stream>>>(
+            x, acodes, ascales, wcodes, wscales, codes, scales, out, tokens, n, k, groups, chunks, blocks);
     };
     visit_one_block_shape(a8_shape(1, blocks), launch);
 }
 
-constexpr std::size_t kA8FusedLdsMax = 64 * 1024;  // the default dynamic LDS limit of a launch
+constexpr std::size_t kA8FusedLdsMax = 64 * 1024;   // the default dynamic LDS limit of a launch
+constexpr std::size_t kA8StageLdsMax = 160 * 1024;  // gfx950 LDS per workgroup
 
 }  // namespace
 
@@ -532,6 +586,22 @@ void a8_tiled_launch(const void* workspace, std::uint64_t available, const void*
     const auto* sp = static_cast<const uint4*>(scales);
     auto* op = static_cast<__half*>(out);
     const int chunks = padded / 64, blocks = (n + 15) / 16;
+    // The staging form (activations copied into LDS once per workgroup): one
+    // token block, one round of copy loads per thread, and LDS within what
+    // keeps the shape's workgroups resident (two per CU for 8-wave shapes).
+    const A8Shape sh = a8_shape(1, blocks);
+    const std::size_t lds = a8_fused_lds(tokens, groups, passes, sh);
+    const long threads = sh.waves * 64L;
+    if (tokens <= 16 && lds <= (sh.waves == 16 ? kA8StageLdsMax : kA8StageLdsMax / 2) &&
+        2L * passes * tokens * groups <= kA8StageUnits * threads && 1L * passes * tokens * groups <= kA8StageScales * threads) {
+        if (passes == 1)
+            dispatch_a8_lds<1, true>(nullptr, acodes, ascales, nullptr, nullptr, cp, sp, op, tokens, n, k, groups, chunks,
+                                     blocks, lds, stream);
+        else
+            dispatch_a8_lds<2, true>(nullptr, acodes, ascales, nullptr, nullptr, cp, sp, op, tokens, n, k, groups, chunks,
+                                     blocks, lds, stream);
+        return;
+    }
     if (tokens <= 16) {
         if (passes == 1) dispatch_a8_tiled<1, 1>(acodes, ascales, cp, sp, op, tokens, n, groups, chunks, blocks, stream);
         else dispatch_a8_tiled<1, 2>(acodes, ascales, cp, sp, op, tokens, n, groups, chunks, blocks, stream);
@@ -564,8 +634,12 @@ void a8_tiled_linear_launch(const void* x, void* workspace, std::uint64_t availa
     const auto* cp = static_cast<const uint4*>(codes);
     const auto* sp = static_cast<const uint4*>(scales);
     auto* op = static_cast<__half*>(out);
-    if (passes == 1) dispatch_a8_fused<1>(xp, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks, blocks, lds, stream);
-    else dispatch_a8_fused<2>(xp, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks, blocks, lds, stream);
+    if (passes == 1)
+        dispatch_a8_lds<1, false>(xp, nullptr, nullptr, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks, blocks,
+                                  lds, stream);
+    else
+        dispatch_a8_lds<2, false>(xp, nullptr, nullptr, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks, blocks,
+                                  lds, stream);
 }
 
 }  // namespace vt
