@@ -533,9 +533,10 @@ std::size_t a8_fused_lds(int tokens, int groups, int passes, const A8Shape& sh) 
 }
 
 template <int P, bool STAGE>
-void dispatch_a8_lds(const __half* x, const std::int8_t* acodes, const float* ascales, std::int8_t* wcodes,
-                     float* wscales, const uint4* codes, const uint4* scales, __half* out, int tokens, int n, int k,
-                     int groups, int chunks, int blocks, std::size_t lds, hipStream_t stream) {
+void dispatch_a8_lds(const A8Shape& sh, const __half* x, const std::int8_t* acodes, const float* ascales,
+                     std::int8_t* wcodes, float* wscales, const uint4* codes, const uint4* scales, __half* out,
+                     int tokens, int n, int k, int groups, int chunks, int blocks, std::size_t lds,
+                     hipStream_t stream) {
     auto launch = [&](auto tag) {
         using T = decltype(tag);
         auto* kernel = a8_tiled_lds<T::waves, T::rb, P, T::nbuf, STAGE>;
@@ -547,7 +548,10 @@ void dispatch_a8_lds(const __half* x, const std::int8_t* acodes, const float* as
         kernel<<<(blocks + T::rb - 1) / T::rb, T::waves * 64, lds, stream>>>(
             x, acodes, ascales, wcodes, wscales, codes, scales, out, tokens, n, k, groups, chunks, blocks);
     };
-    visit_one_block_shape(a8_shape(1, blocks), launch);
+    if constexpr (STAGE)
+        visit_shape<ShapeTag<16, 1, 2>, ShapeTag<16, 2, 2>, ShapeTag<8, 3, 2>, ShapeTag<16, 3, 2>>(sh, launch);
+    else
+        visit_one_block_shape(sh, launch);
 }
 
 constexpr std::size_t kA8FusedLdsMax = 64 * 1024;   // the default dynamic LDS limit of a launch
@@ -589,17 +593,23 @@ void a8_tiled_launch(const void* workspace, std::uint64_t available, const void*
     // The staging form (activations copied into LDS once per workgroup): one
     // token block, one round of copy loads per thread, and LDS within what
     // keeps the shape's workgroups resident (two per CU for 8-wave shapes).
-    const A8Shape sh = a8_shape(1, blocks);
-    const std::size_t lds = a8_fused_lds(tokens, groups, passes, sh);
+    // A staged copy too large for two 8-wave workgroups per CU takes one of 16
+    // waves over the same three row blocks (the same waves per CU).
+    A8Shape sh = a8_shape(1, blocks);
+    std::size_t lds = a8_fused_lds(tokens, groups, passes, sh);
+    if (sh.waves == 8 && lds > kA8StageLdsMax / 2) {
+        sh = A8Shape{16, sh.rb, sh.nbuf};
+        lds = a8_fused_lds(tokens, groups, passes, sh);
+    }
     const long threads = sh.waves * 64L;
     if (tokens <= 16 && lds <= (sh.waves == 16 ? kA8StageLdsMax : kA8StageLdsMax / 2) &&
         2L * passes * tokens * groups <= kA8StageUnits * threads && 1L * passes * tokens * groups <= kA8StageScales * threads) {
         if (passes == 1)
-            dispatch_a8_lds<1, true>(nullptr, acodes, ascales, nullptr, nullptr, cp, sp, op, tokens, n, k, groups, chunks,
-                                     blocks, lds, stream);
+            dispatch_a8_lds<1, true>(sh, nullptr, acodes, ascales, nullptr, nullptr, cp, sp, op, tokens, n, k, groups,
+                                     chunks, blocks, lds, stream);
         else
-            dispatch_a8_lds<2, true>(nullptr, acodes, ascales, nullptr, nullptr, cp, sp, op, tokens, n, k, groups, chunks,
-                                     blocks, lds, stream);
+            dispatch_a8_lds<2, true>(sh, nullptr, acodes, ascales, nullptr, nullptr, cp, sp, op, tokens, n, k, groups,
+                                     chunks, blocks, lds, stream);
         return;
     }
     if (tokens <= 16) {
@@ -635,11 +645,11 @@ void a8_tiled_linear_launch(const void* x, void* workspace, std::uint64_t availa
     const auto* sp = static_cast<const uint4*>(scales);
     auto* op = static_cast<__half*>(out);
     if (passes == 1)
-        dispatch_a8_lds<1, false>(xp, nullptr, nullptr, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks, blocks,
-                                  lds, stream);
+        dispatch_a8_lds<1, false>(sh, xp, nullptr, nullptr, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks,
+                                  blocks, lds, stream);
     else
-        dispatch_a8_lds<2, false>(xp, nullptr, nullptr, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks, blocks,
-                                  lds, stream);
+        dispatch_a8_lds<2, false>(sh, xp, nullptr, nullptr, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks,
+                                  blocks, lds, stream);
 }
 
 }  // namespace vt
