@@ -72,9 +72,14 @@ int venturi_q8_a8_gemm_run(const void* workspace, uint64_t available, const int8
  * venturi_q8_tiled_run reads (codes [block][chunk][lane][16 B], scales
  * [block][chunk][row][2]); the scaled group terms summed in natural order, so
  * outputs match the reference to fp32 association. Same workspace as
- * venturi_q8_dp4a_run; workspace and planes 16-byte aligned. */
+ * venturi_q8_dp4a_run; workspace and planes 16-byte aligned. Shapes whose
+ * launch splits K over two workgroups take `slots`: at least
+ * venturi_q8_a8_tiled_workspace_bytes bytes, 8-byte aligned, armed once with
+ * venturi_q8_tiled_workspace_init and left idle by every run (calls sharing
+ * one slot buffer run on one stream); NULL / 0 for the other shapes. */
 int venturi_q8_a8_tiled_run(const void* workspace, uint64_t available, const void* codes, const void* scales,
-                            void* out, int tokens, int n, int k, int padded, int passes, void* stream);
+                            void* out, int tokens, int n, int k, int padded, int passes, void* slots,
+                            uint64_t slot_bytes, void* stream);
 
 /* Extension (no counterpart in the reference): venturi_q8_dp4a_quantize
  * (q8_dp4a.cuh:15-45) of fp16 x [tokens][k] into the workspace followed by
@@ -82,10 +87,15 @@ int venturi_q8_a8_tiled_run(const void* workspace, uint64_t available, const voi
  * 16-byte aligned and the quantized activations fit 64 KB of LDS (each
  * workgroup quantizes them itself), else as the two launches. Either way the
  * workspace ends holding the quantizer's bytes and out the bytes of the two
- * calls. */
+ * calls. Slots as for venturi_q8_a8_tiled_run. */
 int venturi_q8_a8_tiled_linear_run(const void* x, void* workspace, uint64_t available, const void* codes,
                                    const void* scales, void* out, int tokens, int n, int k, int padded, int passes,
-                                   void* stream);
+                                   void* slots, uint64_t slot_bytes, void* stream);
+
+/* Extension (no counterpart in the reference): bytes of the exchange slots the
+ * two A8 entry points above need at this shape; 0 when its launch does not
+ * split K, and 0 with a message for invalid geometry. */
+uint64_t venturi_q8_a8_tiled_workspace_bytes(int tokens, int n, int k, int passes);
 
 /* One matrix of a fused projection: resident Q8 planes, its fp16 output
  * [tokens][stride] (rows n, stride >= n). 32 bytes, as ops_api.h:8-9. */

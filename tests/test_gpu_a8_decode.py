@@ -166,13 +166,28 @@ def test_tiled_a8_rejections(backend, device):
     planes = torch.empty(4096, dtype=torch.uint8, device=device)
     out = torch.empty(64, dtype=torch.float16, device=device)
     args = (ws.data_ptr(), ws.numel(), planes.data_ptr(), planes.data_ptr(), out.data_ptr())
-    assert lib.venturi_q8_a8_tiled_run(*args, 33, 1, 32, 128, 1, s) == -1
+    no_slots = (None, 0, s)
+    assert lib.venturi_q8_a8_tiled_run(*args, 33, 1, 32, 128, 1, *no_slots) == -1
     assert "1..32 tokens" in lib.error()
-    assert lib.venturi_q8_a8_tiled_run(*args, 1, 16, 64, 64, 1, s) == -1
+    assert lib.venturi_q8_a8_tiled_run(*args, 1, 16, 64, 64, 1, *no_slots) == -1
     assert "geometry" in lib.error()
-    assert lib.venturi_q8_a8_tiled_run(*args, 1, 16, 64, 128, 3, s) == -1
-    assert lib.venturi_q8_a8_tiled_run(ws.data_ptr() + 4, ws.numel() - 4, *args[2:], 1, 16, 64, 128, 1, s) == -1
+    assert lib.venturi_q8_a8_tiled_run(*args, 1, 16, 64, 128, 3, *no_slots) == -1
+    assert lib.venturi_q8_a8_tiled_run(ws.data_ptr() + 4, ws.numel() - 4, *args[2:], 1, 16, 64, 128, 1, *no_slots) == -1
     assert "misaligned" in lib.error()
-    assert lib.venturi_q8_a8_tiled_run(ws.data_ptr(), 8, *args[2:], 1, 16, 64, 128, 1, s) == -1
+    assert lib.venturi_q8_a8_tiled_run(ws.data_ptr(), 8, *args[2:], 1, 16, 64, 128, 1, *no_slots) == -1
     assert "workspace" in lib.error()
+    # A shape whose launch splits K refuses to run without its slots.
+    n, k, tokens = 5120, 17408, 8
+    assert lib.venturi_q8_a8_tiled_workspace_bytes(tokens, n, k, 2) == tokens * (n // 16) * 64
+    need = int(lib.venturi_q8_a8_tiled_workspace_bytes(tokens, n, k, 2))
+    big_ws = torch.empty(int(lib.venturi_q8_dp4a_bytes(tokens, k, 2)), dtype=torch.uint8, device=device)
+    big_planes = torch.empty(n * k + 64, dtype=torch.uint8, device=device)
+    big_out = torch.empty(tokens, n, dtype=torch.float16, device=device)
+    assert lib.venturi_q8_a8_tiled_run(big_ws.data_ptr(), big_ws.numel(), big_planes.data_ptr(), big_planes.data_ptr(),
+                                       big_out.data_ptr(), tokens, n, k, k, 2, None, 0, s) == -1
+    assert "slot buffer" in lib.error()
+    slots = torch.empty(need, dtype=torch.uint8, device=device)
+    assert lib.venturi_q8_a8_tiled_run(big_ws.data_ptr(), big_ws.numel(), big_planes.data_ptr(), big_planes.data_ptr(),
+                                       big_out.data_ptr(), tokens, n, k, k, 2, slots.data_ptr(), need - 8, s) == -1
+    assert "slot buffer" in lib.error()
     torch.cuda.synchronize(device)

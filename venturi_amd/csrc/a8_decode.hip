@@ -252,6 +252,49 @@ constexpr int kA8FusedTasks = 3;
 // form: every admitted launch copies its activations in one round of loads.
 constexpr int kA8StageUnits = 10, kA8StageScales = 8;
 
+// The idle pattern of an exchange slot: both fp32 halves a signalling NaN,
+// which no arithmetic result takes (the pattern venturi_q8_tiled_workspace_init
+// writes).
+constexpr unsigned long long kA8SlotIdle = 0x7f8000017f800001ull;
+
+// Stores lane (q, r)'s outputs: rows 16 blk + 4q .. +3 of token r. KS == 2:
+// the tile is one of two K halves; the lane exchanges its row pairs (4q, 4q+1)
+// and (4q+2, 4q+3) with two 64-bit slots of (r, blk, q): the first half to
+// arrive finds the idle pattern and leaves its pair, the second adds the
+// other pair (a sum of two fp32 terms, the same whichever arrives first),
+// re-arms the slot and stores. Only the slot is shared: no fence, no waiting.
+template <int KS>
+__device__ __forceinline__ void a8_finish(__half* __restrict__ out, unsigned long long* __restrict__ slots,
+                                          const float4v& sum, int blk, int q, int r, int tokens, int n, int blocks) {
+    if (r >= tokens) return;
+    __half* o = out + static_cast<std::int64_t>(r) * n + 16 * blk + 4 * q;
+    const int row0 = 16 * blk + 4 * q;
+    if constexpr (KS == 1) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (row0 + e < n) o[e] = from_f32<__half>(sum[e]);
+    } else {
+        static_assert(KS == 2, "K is split in two at most");
+        unsigned long long* slot = slots + ((static_cast<std::int64_t>(r) * blocks + blk) * 4 + q) * 2;
+        unsigned long long old[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const unsigned long long packed = (static_cast<unsigned long long>(__float_as_uint(sum[2 * h + 1])) << 32) |
+                                              __float_as_uint(sum[2 * h]);
+            old[h] = __hip_atomic_exchange(slot + h, packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (old[h] == kA8SlotIdle) continue;
+            __hip_atomic_store(slot + h, kA8SlotIdle, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float lo = sum[2 * h] + __uint_as_float(static_cast<std::uint32_t>(old[h]));
+            const float hi = sum[2 * h + 1] + __uint_as_float(static_cast<std::uint32_t>(old[h] >> 32));
+            if (row0 + 2 * h < n) o[2 * h] = from_f32<__half>(lo);
+            if (row0 + 2 * h + 1 < n) o[2 * h + 1] = from_f32<__half>(hi);
+        }
+    }
+}
+
 template <int RB, int P>
 struct FusedBatch {
     uint4 w[RB];   // 16 weight code bytes per block (groups 2c and 2c + 1)
@@ -265,22 +308,31 @@ struct FusedBatch {
 // STAGE = false: a8_tiled_fused, the activations quantized from x (and
 // written to the workspace by workgroup 0). STAGE = true: the activations
 // copied from a filled workspace (acodes, ascales) into the same LDS rows.
-template <int W, int RB, int P, int NBUF, bool STAGE>
+// KS == 2 (staged form only): workgroups 2g and 2g + 1 take the first and
+// second half of row-block group g's chunks; LDS holds only the half's groups
+// and the two partial tiles meet through the slots (a8_finish).
+template <int W, int RB, int P, int NBUF, bool STAGE, int KS>
 __global__ __launch_bounds__(W * 64) void a8_tiled_lds(const __half* x, const std::int8_t* __restrict__ acodes,
                                                        const float* __restrict__ ascales, std::int8_t* __restrict__ wcodes,
                                                        float* __restrict__ wscales, const uint4* __restrict__ codes,
                                                        const uint4* __restrict__ scales, __half* __restrict__ out,
-                                                       int tokens, int n, int k, int groups, int chunks, int blocks) {
+                                                       unsigned long long* __restrict__ slots, int tokens, int n, int k,
+                                                       int groups, int chunks, int blocks) {
+    static_assert(KS == 1 || (KS == 2 && STAGE), "only the staged form splits K");
     extern __shared__ __align__(16) unsigned char lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r = lane & 15;
-    const int block0 = blockIdx.x * RB;
+    const int block0 = static_cast<int>(blockIdx.x / KS) * RB;
     const int used = (groups + 1) / 2;
-    const int per = (used + W - 1) / W;
-    const int c0 = min(wave * per, used), c1 = min(c0 + per, used);
+    const int kper = (used + KS - 1) / KS;
+    const int k0 = KS == 1 ? 0 : min(static_cast<int>(blockIdx.x % KS) * kper, used);
+    const int k1 = min(k0 + kper, used);  // the workgroup's chunks [k0, k1), k0 < k1 (the host splits only long K)
+    const int per = (k1 - k0 + W - 1) / W;
+    const int c0 = min(k0 + wave * per, k1), c1 = min(c0 + per, k1);
     const int batches = c1 - c0;
-    const int rs = a8_code_row(groups), ss = a8_scale_row(groups);
+    const int lg = KS == 1 ? groups : 2 * kper;  // groups an LDS row holds
+    const int rs = a8_code_row(lg), ss = a8_scale_row(lg);
     std::int8_t* lcodes = reinterpret_cast<std::int8_t*>(lds);
     float* lscales = reinterpret_cast<float*>(lds + static_cast<std::size_t>(P) * tokens * rs);
 
@@ -316,11 +368,12 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_lds(const __half* x, const st
         }
     };
     auto fetch_activations = [&](FusedBatch<RB, P>& t) {
+        const int lc = t.ch - k0;  // the chunk within the workgroup's LDS rows
 #pragma unroll
         for (int p = 0; p < P; ++p) {
-            t.xa[p] = *reinterpret_cast<const uint2*>(xrow[p] + 64 * t.ch);
-            t.xb[p] = *reinterpret_cast<const uint2*>(xrow[p] + 64 * t.ch + 32);
-            t.as[p] = *reinterpret_cast<const float2*>(srow[p] + 2 * t.ch);
+            t.xa[p] = *reinterpret_cast<const uint2*>(xrow[p] + 64 * lc);
+            t.xb[p] = *reinterpret_cast<const uint2*>(xrow[p] + 64 * lc + 32);
+            t.as[p] = *reinterpret_cast<const float2*>(srow[p] + 2 * lc);
         }
     };
     // Quantize every token's groups into LDS: 4 lanes per group, 8 columns
@@ -337,15 +390,24 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_lds(const __half* x, const st
         // Copy: the codes as 16-byte units of the (pass, token) rows, the
         // scales one by one; at most kA8StageUnits / kA8StageScales per thread
         // (the host admits only such launches), all loads before the weights'.
-        const int units = P * tokens * groups * 2, nscales = P * tokens * groups;
+        // The workgroup's groups [2 k0, g1) of every (pass, token) row.
+        const int g1 = min(2 * k1, groups), gv = g1 - 2 * k0;
+        const int units = P * tokens * gv * 2, nscales = P * tokens * gv;
         const uint4* src = reinterpret_cast<const uint4*>(acodes);
         uint4 u[kA8StageUnits];
         float sv[kA8StageScales];
 #pragma unroll
-        for (int j = 0; j < kA8StageUnits; ++j) u[j] = src[min(static_cast<int>(threadIdx.x) + j * W * 64, units - 1)];
+        for (int j = 0; j < kA8StageUnits; ++j) {
+            const int i = min(static_cast<int>(threadIdx.x) + j * W * 64, units - 1);
+            const int row = i / (2 * gv);
+            u[j] = src[(row * groups + 2 * k0) * 2 + (i - row * 2 * gv)];
+        }
 #pragma unroll
-        for (int j = 0; j < kA8StageScales; ++j)
-            sv[j] = ascales[min(static_cast<int>(threadIdx.x) + j * W * 64, nscales - 1)];
+        for (int j = 0; j < kA8StageScales; ++j) {
+            const int i = min(static_cast<int>(threadIdx.x) + j * W * 64, nscales - 1);
+            const int row = i / gv;
+            sv[j] = ascales[row * groups + 2 * k0 + (i - row * gv)];
+        }
         __asm__ __volatile__("" ::: "memory");  // keeps these loads here, ahead of the weights'
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -354,16 +416,16 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_lds(const __half* x, const st
         for (int j = 0; j < kA8StageUnits; ++j) {
             const int i = threadIdx.x + j * W * 64;
             if (i < units) {
-                const int row = i / (2 * groups);
-                *reinterpret_cast<uint4*>(lcodes + row * rs + (i - row * 2 * groups) * 16) = u[j];
+                const int row = i / (2 * gv);
+                *reinterpret_cast<uint4*>(lcodes + row * rs + (i - row * 2 * gv) * 16) = u[j];
             }
         }
 #pragma unroll
         for (int j = 0; j < kA8StageScales; ++j) {
             const int i = threadIdx.x + j * W * 64;
             if (i < nscales) {
-                const int row = i / groups;
-                lscales[row * ss + (i - row * groups)] = sv[j];
+                const int row = i / gv;
+                lscales[row * ss + (i - row * gv)] = sv[j];
             }
         }
     } else {
@@ -472,11 +534,7 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_lds(const __half* x, const st
             for (int e = 0; e < 4; ++e) sum[e] += v[e];
         }
         const int blk = block0 + b;
-        if (blk >= blocks || r >= tokens) continue;
-        __half* o = out + static_cast<std::int64_t>(r) * n + 16 * blk + 4 * q;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (16 * blk + 4 * q + e < n) o[e] = from_f32<__half>(sum[e]);
+        if (blk < blocks) a8_finish<KS>(out, slots, sum, blk, q, r, tokens, n, blocks);
     }
 }
 
@@ -487,6 +545,7 @@ __global__ __launch_bounds__(W * 64) void a8_tiled_lds(const __half* x, const st
 // workgroups, one per CU), else 8 waves over three.
 struct A8Shape {
     int waves, rb, nbuf;
+    int ks = 1;  // workgroups splitting K (2: the staged form's halves, exchanging through slots)
 };
 
 A8Shape a8_shape(int token_blocks, int blocks) {
@@ -494,16 +553,17 @@ A8Shape a8_shape(int token_blocks, int blocks) {
     return blocks <= 256 ? A8Shape{16, 1, 2} : blocks <= 511 ? A8Shape{16, 2, 2} : A8Shape{8, 3, 2};
 }
 
-template <int W, int RB, int NBUF>
+template <int W, int RB, int NBUF, int KS = 1>
 struct ShapeTag {
-    static constexpr int waves = W, rb = RB, nbuf = NBUF;
+    static constexpr int waves = W, rb = RB, nbuf = NBUF, ks = KS;
 };
 
 // Calls f(ShapeTag) for the compiled shape equal to sh.
 template <class... Tags, class F>
 void visit_shape(const A8Shape& sh, F&& f) {
-    const bool found = ((sh.waves == Tags::waves && sh.rb == Tags::rb && sh.nbuf == Tags::nbuf ? (f(Tags{}), true)
-                                                                                            : false) ||
+    const bool found = ((sh.waves == Tags::waves && sh.rb == Tags::rb && sh.nbuf == Tags::nbuf && sh.ks == Tags::ks
+                             ? (f(Tags{}), true)
+                             : false) ||
                         ...);
     require(found, "internal: A8 decode shape not compiled");
 }
@@ -526,30 +586,34 @@ void dispatch_a8_tiled(const std::int8_t* acodes, const float* ascales, const ui
     else visit_one_block_shape(sh, launch);
 }
 
-std::size_t a8_fused_lds(int tokens, int groups, int passes, const A8Shape& sh) {
+// LDS bytes of a8_tiled_lds: the activation rows of the workgroup's groups
+// (all of them, or a K half's), later reused for the partial tiles.
+std::size_t a8_lds_bytes(int tokens, int groups, int passes, const A8Shape& sh) {
+    const int lg = sh.ks == 1 ? groups : 2 * (((groups + 1) / 2 + 1) / 2);
     const std::size_t act = static_cast<std::size_t>(passes) * tokens *
-                            (a8_code_row(groups) + 4 * static_cast<std::size_t>(a8_scale_row(groups)));
+                            (a8_code_row(lg) + 4 * static_cast<std::size_t>(a8_scale_row(lg)));
     return std::max(act, static_cast<std::size_t>(sh.waves) * sh.rb * 64 * sizeof(float4v));
 }
 
 template <int P, bool STAGE>
 void dispatch_a8_lds(const A8Shape& sh, const __half* x, const std::int8_t* acodes, const float* ascales,
                      std::int8_t* wcodes, float* wscales, const uint4* codes, const uint4* scales, __half* out,
-                     int tokens, int n, int k, int groups, int chunks, int blocks, std::size_t lds,
-                     hipStream_t stream) {
+                     unsigned long long* slots, int tokens, int n, int k, int groups, int chunks, int blocks,
+                     std::size_t lds, hipStream_t stream) {
     auto launch = [&](auto tag) {
         using T = decltype(tag);
-        auto* kernel = a8_tiled_lds<T::waves, T::rb, P, T::nbuf, STAGE>;
+        auto* kernel = a8_tiled_lds<T::waves, T::rb, P, T::nbuf, STAGE, T::ks>;
         if (lds > 64 * 1024) {
             static const hipError_t raised = hipFuncSetAttribute(
                 reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             check(raised);
         }
-        kernel<<<(blocks + T::rb - 1) / T::rb, T::waves * 64, lds, stream>>>(
-            x, acodes, ascales, wcodes, wscales, codes, scales, out, tokens, n, k, groups, chunks, blocks);
+        kernel<<<(blocks + T::rb - 1) / T::rb * T::ks, T::waves * 64, lds, stream>>>(
+            x, acodes, ascales, wcodes, wscales, codes, scales, out, slots, tokens, n, k, groups, chunks, blocks);
     };
     if constexpr (STAGE)
-        visit_shape<ShapeTag<16, 1, 2>, ShapeTag<16, 2, 2>, ShapeTag<8, 3, 2>, ShapeTag<16, 3, 2>>(sh, launch);
+        visit_shape<ShapeTag<16, 1, 2>, ShapeTag<16, 2, 2>, ShapeTag<8, 3, 2>, ShapeTag<16, 3, 2>,
+                    ShapeTag<16, 3, 2, 2>>(sh, launch);
     else
         visit_one_block_shape(sh, launch);
 }
@@ -577,10 +641,52 @@ void validate_a8_tiled(const void* workspace, std::uint64_t available, const voi
             "misaligned A8 operand (workspace and tiled planes need 16 bytes)");
 }
 
+// How a filled workspace is projected: the staged form (activations copied
+// into LDS once per workgroup) where one token block, one round of copy loads
+// per thread and the LDS fit (LDS that would not let two 8-wave workgroups
+// share a CU goes to one 16-wave workgroup over the same row blocks; LDS past
+// one workgroup's share of the CU splits K over two workgroups of 16 waves and
+// three row blocks, which exchange their halves through slots, where that grid
+// runs in at most two rounds of one workgroup per CU), else the register form.
+struct A8TiledPlan {
+    bool staged;
+    A8Shape shape;
+    std::size_t lds;
+};
+
+A8TiledPlan a8_tiled_plan(int tokens, int n, int k, int passes) {
+    const int groups = (k + 31) / 32, blocks = (n + 15) / 16;
+    A8Shape sh = a8_shape(tokens <= 16 ? 1 : 2, blocks);
+    if (tokens > 16) return {false, sh, 0};
+    std::size_t lds = a8_lds_bytes(tokens, groups, passes, sh);
+    if (sh.waves == 8 && lds > kA8StageLdsMax / 2) {
+        sh = A8Shape{16, sh.rb, sh.nbuf};
+        lds = a8_lds_bytes(tokens, groups, passes, sh);
+    }
+    if (lds > kA8StageLdsMax && (groups + 1) / 2 >= 2 * 16 && (blocks + 2) / 3 * 2 <= 512) {
+        sh = A8Shape{16, 3, 2, 2};
+        lds = a8_lds_bytes(tokens, groups, passes, sh);
+    }
+    const long threads = sh.waves * 64L;
+    const long rows_groups = 1L * passes * tokens * (sh.ks == 1 ? groups : 2 * (((groups + 1) / 2 + 1) / 2));
+    const bool fits = lds <= (sh.waves == 16 ? kA8StageLdsMax : kA8StageLdsMax / 2) &&
+                      2 * rows_groups <= kA8StageUnits * threads && rows_groups <= kA8StageScales * threads;
+    if (fits) return {true, sh, lds};
+    return {false, a8_shape(1, blocks), 0};
+}
+
 }  // namespace
 
+std::uint64_t a8_tiled_slot_bytes(int tokens, int n, int k, int passes) {
+    require(tokens > 0 && tokens <= 32 && n > 0 && k > 0 && (passes == 1 || passes == 2),
+            "invalid A8 projection geometry");
+    const A8TiledPlan plan = a8_tiled_plan(tokens, n, k, passes);
+    return plan.staged && plan.shape.ks == 2 ? static_cast<std::uint64_t>(tokens) * ((n + 15) / 16) * 64 : 0;
+}
+
 void a8_tiled_launch(const void* workspace, std::uint64_t available, const void* codes, const void* scales, void* out,
-                     int tokens, int n, int k, int padded, int passes, hipStream_t stream) {
+                     int tokens, int n, int k, int padded, int passes, void* slots, std::uint64_t slot_bytes,
+                     hipStream_t stream) {
     validate_a8_tiled(workspace, available, codes, scales, out, tokens, n, k, padded, passes);
     const int groups = (k + 31) / 32;
     const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
@@ -590,26 +696,18 @@ void a8_tiled_launch(const void* workspace, std::uint64_t available, const void*
     const auto* sp = static_cast<const uint4*>(scales);
     auto* op = static_cast<__half*>(out);
     const int chunks = padded / 64, blocks = (n + 15) / 16;
-    // The staging form (activations copied into LDS once per workgroup): one
-    // token block, one round of copy loads per thread, and LDS within what
-    // keeps the shape's workgroups resident (two per CU for 8-wave shapes).
-    // A staged copy too large for two 8-wave workgroups per CU takes one of 16
-    // waves over the same three row blocks (the same waves per CU).
-    A8Shape sh = a8_shape(1, blocks);
-    std::size_t lds = a8_fused_lds(tokens, groups, passes, sh);
-    if (sh.waves == 8 && lds > kA8StageLdsMax / 2) {
-        sh = A8Shape{16, sh.rb, sh.nbuf};
-        lds = a8_fused_lds(tokens, groups, passes, sh);
-    }
-    const long threads = sh.waves * 64L;
-    if (tokens <= 16 && lds <= (sh.waves == 16 ? kA8StageLdsMax : kA8StageLdsMax / 2) &&
-        2L * passes * tokens * groups <= kA8StageUnits * threads && 1L * passes * tokens * groups <= kA8StageScales * threads) {
+    const A8TiledPlan plan = a8_tiled_plan(tokens, n, k, passes);
+    if (plan.staged) {
+        auto* sl = static_cast<unsigned long long*>(slots);
+        if (plan.shape.ks == 2)
+            require(sl && aligned(sl, 8) && slot_bytes >= a8_tiled_slot_bytes(tokens, n, k, passes),
+                    "this A8 projection splits K: pass its slot buffer (venturi_q8_a8_tiled_workspace_bytes)");
         if (passes == 1)
-            dispatch_a8_lds<1, true>(sh, nullptr, acodes, ascales, nullptr, nullptr, cp, sp, op, tokens, n, k, groups,
-                                     chunks, blocks, lds, stream);
+            dispatch_a8_lds<1, true>(plan.shape, nullptr, acodes, ascales, nullptr, nullptr, cp, sp, op, sl, tokens, n,
+                                     k, groups, chunks, blocks, plan.lds, stream);
         else
-            dispatch_a8_lds<2, true>(sh, nullptr, acodes, ascales, nullptr, nullptr, cp, sp, op, tokens, n, k, groups,
-                                     chunks, blocks, lds, stream);
+            dispatch_a8_lds<2, true>(plan.shape, nullptr, acodes, ascales, nullptr, nullptr, cp, sp, op, sl, tokens, n,
+                                     k, groups, chunks, blocks, plan.lds, stream);
         return;
     }
     if (tokens <= 16) {
@@ -623,18 +721,19 @@ void a8_tiled_launch(const void* workspace, std::uint64_t available, const void*
 
 void a8_tiled_linear_launch(const void* x, void* workspace, std::uint64_t available, const void* codes,
                             const void* scales, void* out, int tokens, int n, int k, int padded, int passes,
-                            hipStream_t stream) {
+                            void* slots, std::uint64_t slot_bytes, hipStream_t stream) {
     validate_a8_tiled(workspace, available, codes, scales, out, tokens, n, k, padded, passes);
     require(x != nullptr && aligned(x, 2), "invalid A8 input");
     const int groups = (k + 31) / 32, chunks = padded / 64, blocks = (n + 15) / 16;
     // The fused kernel: one token block, whole 16-byte activation pieces, its
     // LDS within the default limit and every quantizer task in its one round.
     const A8Shape sh = a8_shape(1, blocks);
-    const std::size_t lds = a8_fused_lds(tokens, groups, passes, sh);
+    const std::size_t lds = a8_lds_bytes(tokens, groups, passes, sh);
     if (tokens > 16 || k % 8 != 0 || !aligned(x, 16) || lds > kA8FusedLdsMax ||
         4L * tokens * groups > static_cast<long>(kA8FusedTasks) * sh.waves * 64) {
         a8_quantize_launch(x, workspace, available, tokens, k, passes, stream);
-        a8_tiled_launch(workspace, available, codes, scales, out, tokens, n, k, padded, passes, stream);
+        a8_tiled_launch(workspace, available, codes, scales, out, tokens, n, k, padded, passes, slots, slot_bytes,
+                        stream);
         return;
     }
     const std::int64_t count = static_cast<std::int64_t>(tokens) * groups;
@@ -645,11 +744,11 @@ void a8_tiled_linear_launch(const void* x, void* workspace, std::uint64_t availa
     const auto* sp = static_cast<const uint4*>(scales);
     auto* op = static_cast<__half*>(out);
     if (passes == 1)
-        dispatch_a8_lds<1, false>(sh, xp, nullptr, nullptr, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks,
-                                  blocks, lds, stream);
+        dispatch_a8_lds<1, false>(sh, xp, nullptr, nullptr, wcodes, wscales, cp, sp, op, nullptr, tokens, n, k, groups,
+                                  chunks, blocks, lds, stream);
     else
-        dispatch_a8_lds<2, false>(sh, xp, nullptr, nullptr, wcodes, wscales, cp, sp, op, tokens, n, k, groups, chunks,
-                                  blocks, lds, stream);
+        dispatch_a8_lds<2, false>(sh, xp, nullptr, nullptr, wcodes, wscales, cp, sp, op, nullptr, tokens, n, k, groups,
+                                  chunks, blocks, lds, stream);
 }
 
 }  // namespace vt
@@ -658,13 +757,14 @@ void a8_tiled_linear_launch(const void* x, void* workspace, std::uint64_t availa
 // int8 matrix cores over the tiled Q8 planes (the layout of
 // venturi_q8_tiled_run); same A8 workspace; outputs equal the reference's up
 // to fp32 association (exact int32 group dots, groups summed in natural order).
-extern "C" __attribute__((visibility("default"))) int venturi_q8_a8_tiled_run(const void* workspace,
-                                                                             std::uint64_t available,
-                                                                             const void* codes, const void* scales,
-                                                                             void* out, int tokens, int n, int k,
-                                                                             int padded, int passes, void* stream) {
+// Shapes whose launch splits K take an exchange-slot buffer of
+// venturi_q8_a8_tiled_workspace_bytes bytes, armed once with
+// venturi_q8_tiled_workspace_init and left idle by every run.
+extern "C" __attribute__((visibility("default"))) int venturi_q8_a8_tiled_run(
+    const void* workspace, std::uint64_t available, const void* codes, const void* scales, void* out, int tokens,
+    int n, int k, int padded, int passes, void* slots, std::uint64_t slot_bytes, void* stream) {
     return vt::guarded([&] {
-        vt::a8_tiled_launch(workspace, available, codes, scales, out, tokens, n, k, padded, passes,
+        vt::a8_tiled_launch(workspace, available, codes, scales, out, tokens, n, k, padded, passes, slots, slot_bytes,
                             static_cast<hipStream_t>(stream));
     });
 }
@@ -675,9 +775,19 @@ extern "C" __attribute__((visibility("default"))) int venturi_q8_a8_tiled_run(co
 // bytes as the two calls').
 extern "C" __attribute__((visibility("default"))) int venturi_q8_a8_tiled_linear_run(
     const void* x, void* workspace, std::uint64_t available, const void* codes, const void* scales, void* out,
-    int tokens, int n, int k, int padded, int passes, void* stream) {
+    int tokens, int n, int k, int padded, int passes, void* slots, std::uint64_t slot_bytes, void* stream) {
     return vt::guarded([&] {
-        vt::a8_tiled_linear_launch(x, workspace, available, codes, scales, out, tokens, n, k, padded, passes,
-                                   static_cast<hipStream_t>(stream));
+        vt::a8_tiled_linear_launch(x, workspace, available, codes, scales, out, tokens, n, k, padded, passes, slots,
+                                   slot_bytes, static_cast<hipStream_t>(stream));
     });
+}
+
+// Extension: bytes of the exchange slots the two entry points above need for
+// this shape (0 when its launch does not split K; 0 with a message on invalid
+// geometry).
+extern "C" __attribute__((visibility("default"))) std::uint64_t venturi_q8_a8_tiled_workspace_bytes(int tokens, int n,
+                                                                                                   int k, int passes) {
+    std::uint64_t bytes = 0;
+    if (!vt::host_guarded([&] { bytes = vt::a8_tiled_slot_bytes(tokens, n, k, passes); })) return 0;
+    return bytes;
 }

@@ -31,8 +31,9 @@ SIGNATURES = {
     "venturi_q8_dp4a_quantize": ([_P, _P, _U64] + [_I] * 3 + [_P], _I),
     "venturi_q8_dp4a_run": ([_P, _U64] + [_P] * 3 + [_I] * 5 + [_P], _I),
     "venturi_q8_a8_gemm_run": ([_P, _U64] + [_P] * 3 + [_I] * 5 + [_P], _I),
-    "venturi_q8_a8_tiled_run": ([_P, _U64] + [_P] * 3 + [_I] * 5 + [_P], _I),
-    "venturi_q8_a8_tiled_linear_run": ([_P, _P, _U64] + [_P] * 3 + [_I] * 5 + [_P], _I),
+    "venturi_q8_a8_tiled_run": ([_P, _U64] + [_P] * 3 + [_I] * 5 + [_P, _U64, _P], _I),
+    "venturi_q8_a8_tiled_linear_run": ([_P, _P, _U64] + [_P] * 3 + [_I] * 5 + [_P, _U64, _P], _I),
+    "venturi_q8_a8_tiled_workspace_bytes": ([_I] * 4, _U64),
     "venturi_q8_fused_run": ([_P, _U64, _P] + [_I] * 5 + [_P], _I),
     "venturi_swiglu_q8_quantize": ([_P] * 3 + [_U64] + [_I] * 3 + [_P, _P], _I),
     "venturi_rms_run": ([_P] * 3 + [_I] * 3 + [_F, _P], _I),

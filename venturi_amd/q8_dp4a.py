@@ -42,6 +42,7 @@ class PreparedQ8DP4A:
     workspace_bytes: int
     _native: object
     kernel: str = "exact"
+    slots: object = None  # exchange slots of a tiled launch that splits K (plan-owned, left idle by every run)
 
     @property
     def precision_profile(self):
@@ -73,12 +74,14 @@ class PreparedQ8DP4A:
         r = self.resident
         admit(out, (self.tokens, r.vocab_size), torch.float16, r.device, "out")
         admit(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
-        disjoint(out, (workspace,) + r.storage_tensors)
+        disjoint(out, (workspace,) + r.storage_tensors + self._slot_tensors)
         if workspace.data_ptr() % 16:
             raise ValueError("A8 workspace requires 16-byte alignment")
+        tail = ()
         if self.kernel == "tiled":
             entry = self._native.venturi_q8_a8_tiled_run
             codes, scales = r.tiled_planes()
+            tail = self._slot_args()
         else:
             entry = self._native.venturi_q8_dp4a_run if self.kernel == "exact" else self._native.venturi_q8_a8_gemm_run
             codes, scales = r.row_major_planes()
@@ -86,19 +89,26 @@ class PreparedQ8DP4A:
             r.backend._check(
                 entry(
                     workspace.data_ptr(), self.workspace_bytes, codes.data_ptr(), scales.data_ptr(),
-                    out.data_ptr(), self.tokens, r.vocab_size, r.hidden_size, r.padded_k, self.passes,
+                    out.data_ptr(), self.tokens, r.vocab_size, r.hidden_size, r.padded_k, self.passes, *tail,
                     stream_of(r.device),
                 )
             )
         return out
+
+    @property
+    def _slot_tensors(self):
+        return () if self.slots is None else (self.slots,)
+
+    def _slot_args(self):
+        return (None, 0) if self.slots is None else (self.slots.data_ptr(), self.slots.numel())
 
     def run(self, x, *, out, workspace):
         r = self.resident
         admit(x, (self.tokens, r.hidden_size), torch.float16, r.device, "x")
         admit(out, (self.tokens, r.vocab_size), torch.float16, r.device, "out")
         admit(workspace, (self.workspace_bytes,), torch.uint8, r.device, "workspace")
-        disjoint(out, (x, workspace) + r.storage_tensors)
-        disjoint(workspace, (x,) + r.storage_tensors)
+        disjoint(out, (x, workspace) + r.storage_tensors + self._slot_tensors)
+        disjoint(workspace, (x,) + r.storage_tensors + self._slot_tensors)
         if workspace.data_ptr() % 16:
             raise ValueError("A8 workspace requires 16-byte alignment")
         if self.kernel != "tiled":
@@ -110,7 +120,7 @@ class PreparedQ8DP4A:
                 self._native.venturi_q8_a8_tiled_linear_run(
                     x.data_ptr(), workspace.data_ptr(), self.workspace_bytes, codes.data_ptr(), scales.data_ptr(),
                     out.data_ptr(), self.tokens, r.vocab_size, r.hidden_size, r.padded_k, self.passes,
-                    stream_of(r.device),
+                    *self._slot_args(), stream_of(r.device),
                 )
             )
         return out
@@ -147,4 +157,23 @@ def prepare_q8_dp4a(resident, *, tokens, residual_compensation, route="auto"):
     if route == "mfma" and tokens <= A8_TILED_MAX_TOKENS:
         kernel = "tiled"
         resident.tiled_planes()  # built once per resident, outside any capture
+        slots = _a8_slots(resident, tokens, passes)
+        return PreparedQ8DP4A(resident, tokens, passes, size, native, kernel, slots)
     return PreparedQ8DP4A(resident, tokens, passes, size, native, kernel)
+
+
+def _a8_slots(resident, tokens, passes):
+    """The plan's exchange slots when its tiled launch splits K (None when it does not).
+
+    Every run leaves them idle again, so runs of one plan must be ordered (one
+    stream at a time); concurrent streams prepare a plan each."""
+    lib = resident.backend._native
+    nbytes = lib.venturi_q8_a8_tiled_workspace_bytes(tokens, resident.vocab_size, resident.hidden_size, passes)
+    if nbytes == 0:
+        resident.backend._check(-1 if lib.venturi_blocks_error() else 0)
+        return None
+    with torch.cuda.device(resident.device):
+        slots = torch.empty(nbytes, dtype=torch.uint8, device=resident.device)
+        resident.backend._check(lib.venturi_q8_tiled_workspace_init(slots.data_ptr(), nbytes, stream_of(resident.device)))
+        torch.cuda.current_stream(resident.device).synchronize()
+    return slots
