@@ -586,7 +586,7 @@ def a8_decode(backend, device, steps, warmup, copy_mb, tokens_list=(1, 8)):
         "route": route,
         "GB/s": round(total / wall / 1e9, 1),
         "roofline": {"bound": "hbm", "kernel": "a8 quantize + " + (
-                         "int8 matrix-core W8A8 decode projection (a8_tiled_decode)" if route == "venturi-q8-a8-mfma"
+                         "int8 matrix-core W8A8 decode projection (a8_tiled_lds / a8_tiled_decode)" if route == "venturi-q8-a8-mfma"
                          else "reference-order W8A8 projection"),
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4)},
