@@ -51,7 +51,7 @@ def test_config1_decode_bitexact(backend, device):
 
 
 @pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
-@pytest.mark.parametrize("tokens", [1, 4, 8, 16])
+@pytest.mark.parametrize("tokens", [1, 4, 8, 16, 32])
 def test_config2_shapes_sampled_rows(backend, device, n, k, tokens):
     # Full-size launch; the oracle checks a seeded sample of 256 rows.
     print(f"case q8-config2 n={n} k={k} tokens={tokens}", flush=True)
@@ -67,6 +67,26 @@ def test_config2_shapes_sampled_rows(backend, device, n, k, tokens):
     rows = np.sort(np.random.default_rng(n).choice(n, 256, replace=False))
     expected = oracle.q8_linear(bits(x), codes[rows], scales[rows], k)
     np.testing.assert_array_equal(bits(out)[:, rows], expected)
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 3, 17])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_exact_wide_rows(backend, device, tokens, dtype):
+    # k = 45 000: the whole activation tile of one or two tokens exceeds LDS,
+    # so every token count runs the slab form (K walked in staged slabs), with
+    # a ragged last chunk and row count.
+    n, k = 37, 45000
+    print(f"case q8-exact-wide n={n} k={k} tokens={tokens} dtype={dtype}", flush=True)
+    codes, scales = random_q8(n, k, 77 + tokens)
+    weight = Q8RowSplitWeight(codes, scales, k)
+    x = torch.randn(tokens, k, generator=torch.Generator().manual_seed(5 + tokens)).to(dtype)
+    resident = backend.upload_linear(weight, dtype=dtype, device=device)
+    guard, out = guarded_out(tokens, n, dtype, device)
+    resident.prepare(tokens=tokens, route="exact").run(x.to(device), out=out)
+    g = guard.cpu()
+    assert g[0] == 47 and g[-1] == 47
+    expected = oracle.q8_linear(bits(x), codes.numpy(), scales.numpy(), k, dtype=0 if dtype == torch.float16 else 1)
+    np.testing.assert_array_equal(bits(out), expected)
 
 
 def test_impulse_last_column_and_nonfinite(backend, device):

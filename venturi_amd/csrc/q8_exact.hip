@@ -11,12 +11,13 @@
 // gfx950 mapping: one 64-lane wave owns all 256 virtual threads of a row;
 // lane L holds j = 4L..4L+3, so one chunk of 256 columns is a single dword
 // per lane (256 contiguous bytes per wave) and every virtual thread's FMA
-// chain stays in one lane in increasing column order. The activations of
-// the workgroup's token tile are staged once in LDS (zero past k): streamed
-// weights would otherwise evict them from the vector L1 and every chunk
-// would re-read them from L2, which halves the achievable HBM rate. The
-// code*scale product is exact in fp32 (8-bit by 11-bit significands), so
-// its evaluation order is immaterial.
+// chain stays in one lane in increasing column order. The activations are
+// staged in LDS (zero past k): streamed weights would otherwise evict them
+// from the vector L1 and every chunk would re-read them from L2, which halves
+// the achievable HBM rate. One and two tokens stage the whole token tile once
+// per persistent workgroup; from three tokens, where the FMAs bind, the slab
+// form stages K in slabs. The code*scale product is exact in fp32 (8-bit by
+// 11-bit significands), so its evaluation order is immaterial.
 #include "common.hpp"
 
 #include <algorithm>
@@ -254,6 +255,222 @@ __global__ __launch_bounds__(kThreads) void q8_exact(const T* __restrict__ x,
     }
 }
 
+// Multi-token form. A workgroup of W waves owns W*RR rows and a tile of TT
+// tokens and walks K in slabs of S chunks: the tile's activations for one
+// slab are staged in LDS as fp32 (two buffers, one barrier per slab) while
+// every wave streams its RR rows' code words and scales for the next slab
+// into registers. Each weight value code*scale is formed once and multiplied
+// into TT tokens; each staged activation is read once per RR rows. The
+// products are plain fp32 FMAs on fp32 operands: on MI355X v_fma_mix_f32 (an
+// FMA taking an fp16 operand) issues at 0.6 of v_fma_f32's rate, so the
+// activations are converted once when staged and the scales once per chunk.
+// A virtual thread's FMA chain still advances one chunk at a time in
+// increasing column order inside one lane, so the association is the
+// canonical one, and the LDS footprint (2*TT*S KiB) does not grow with K.
+template <int TT, int RR, int S, int W>
+struct SlabGeom {
+    static constexpr int kThreads = W * 64;
+    static constexpr int kUnits = TT * S * 64;          // 4-column activation units per slab
+    static constexpr int kPer = kUnits / kThreads;      // units staged per thread
+    static_assert(kUnits % kThreads == 0, "whole activation units per thread");
+};
+
+template <int S, int RR>
+struct SlabWeights {
+    std::uint32_t cw[S][RR];
+    unsigned short sb[S][RR];
+};
+
+template <class T, int TT, int RR, int S, int W, bool VEC, bool SHIFT>
+__global__ __launch_bounds__(W * 64) void q8_exact_slab(const T* __restrict__ x,
+                                                       const std::int8_t* __restrict__ codes,
+                                                       const __half* __restrict__ scales,
+                                                       T* __restrict__ out, int tokens, int n, int k,
+                                                       int padded, int shift) {
+    using G = SlabGeom<TT, RR, S, W>;
+    __shared__ float4 xs[2][G::kUnits];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.y * TT;
+    const int chunks = (k + 255) >> 8;
+    const int slabs = (chunks + S - 1) / S;
+    const int groups = padded >> 5;
+    const int last_word = (padded >> 2) - 1;
+    // Persistent workgroups: workgroup b owns row groups b, b + gridDim.x, ...
+    // (W*RR rows each) and walks the flat sequence of its (row group, slab)
+    // items, so the pipeline runs on across row groups.
+    const int rgroups = (n + W * RR - 1) / (W * RR);
+    const int total = ((rgroups - 1 - static_cast<int>(blockIdx.x)) / static_cast<int>(gridDim.x) + 1) * slabs;
+
+    // Activation staging: unit i of a slab is token i / (S*64), columns
+    // 4 * (i % (S*64)) .. +3 of the slab. Loads use clamped addresses and the
+    // units past k or past `tokens` are zeroed when stored, so no load is
+    // predicated (a predicated load would make the compiler wait for it at
+    // once).
+    uint2 xr[G::kPer];
+    auto xload = [&](int slab) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < G::kPer; ++u) {
+            const int i = tid + u * G::kThreads;
+            const int t = min(t0 + i / (S * 64), tokens - 1);
+            const int col = slab * S * 256 + 4 * (i % (S * 64));
+            const T* src = x + static_cast<std::int64_t>(t) * k;
+            if constexpr (VEC) {
+                xr[u] = *reinterpret_cast<const uint2*>(src + min(col, k - 4));
+            } else {
+                const unsigned short* p = reinterpret_cast<const unsigned short*>(src);
+                unsigned short h[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) h[v] = p[min(col + v, k - 1)];
+                xr[u].x = h[0] | (static_cast<std::uint32_t>(h[1]) << 16);
+                xr[u].y = h[2] | (static_cast<std::uint32_t>(h[3]) << 16);
+            }
+        }
+    };
+    auto xstore = [&](int slab, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < G::kPer; ++u) {
+            const int i = tid + u * G::kThreads;
+            const bool live_token = t0 + i / (S * 64) < tokens;
+            const int col = slab * S * 256 + 4 * (i % (S * 64));
+            uint2 w = xr[u];
+            if constexpr (VEC) {
+                if (!live_token || col >= k) w = make_uint2(0u, 0u);
+            } else {
+                const std::uint32_t m0 = live_token && col < k ? 0xffffu : 0u;
+                const std::uint32_t m1 = live_token && col + 1 < k ? 0xffff0000u : 0u;
+                const std::uint32_t m2 = live_token && col + 2 < k ? 0xffffu : 0u;
+                const std::uint32_t m3 = live_token && col + 3 < k ? 0xffff0000u : 0u;
+                w.x &= m0 | m1;
+                w.y &= m2 | m3;
+            }
+            if constexpr (std::is_same<T, __half>::value)
+                xs[buf][i] = make_float4(half_lo(w.x), half_hi(w.x), half_lo(w.y), half_hi(w.y));
+            else
+                xs[buf][i] = make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+        }
+    };
+    // The RR rows' code words and scales of one slab of row group rg; indices
+    // are clamped into the row (columns past k meet zero activations) and
+    // rows past n are read again as row n-1 and never stored.
+    auto wload = [&](int rg, int slab, SlabWeights<S, RR>& w) __attribute__((always_inline)) {
+        const int row0 = (rg * W + wave) * RR;
+#pragma unroll
+        for (int r = 0; r < RR; ++r) {
+            const std::int64_t row = min(row0 + r, n - 1);
+            const std::uint32_t* wp = reinterpret_cast<const std::uint32_t*>(codes + row * padded);
+            const unsigned short* sp = reinterpret_cast<const unsigned short*>(scales + row * groups);
+#pragma unroll
+            for (int u = 0; u < S; ++u) {
+                const int c = slab * S + u;
+                const int word = min(c * 64 + lane, last_word);
+                if constexpr (SHIFT)
+                    w.cw[u][r] = __builtin_amdgcn_alignbyte(stream_load(wp + word + 1), stream_load(wp + word), shift);
+                else
+                    w.cw[u][r] = stream_load(wp + word);
+                w.sb[u][r] = stream_load(sp + min(c * 8 + (lane >> 3), groups - 1));
+            }
+        }
+    };
+
+    float acc[TT][RR][4];
+    auto reset = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int r = 0; r < RR; ++r)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[t][r][v] = 0.0f;
+    };
+    // The first `live` chunks of the slab in `buf` (all S but in a row's
+    // last slab).
+    auto consume = [&](int buf, const SlabWeights<S, RR>& w, int live) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            if (u >= live) break;
+            float s[RR];
+#pragma unroll
+            for (int r = 0; r < RR; ++r) {
+                s[r] = __half2float(__ushort_as_half(w.sb[u][r]));
+                asm volatile("" : "+v"(s[r]));  // keep the conversion out of the FMAs (no v_fma_mix_f32)
+            }
+            float wv[RR][4];
+            word_weights<RR>(w.cw[u], s, wv);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const float4 x4 = xs[buf][t * S * 64 + u * 64 + lane];
+                const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+                for (int r = 0; r < RR; ++r)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[t][r][v] = fmaf(xv[v], wv[r][v], acc[t][r][v]);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // one chunk at a time (bounds the registers of hoisted reads)
+        }
+    };
+    // End of a row group: the canonical reduction of every output, stored
+    // by lane 0.
+    auto finish = [&](int rg) __attribute__((always_inline)) {
+        const int row0 = (rg * W + wave) * RR;
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int r = 0; r < RR; ++r) {
+                const float y = canonical_sum(acc[t][r][0], acc[t][r][1], acc[t][r][2], acc[t][r][3]);
+                if (lane == 0 && t0 + t < tokens && row0 + r < n)
+                    out[static_cast<std::int64_t>(t0 + t) * n + row0 + r] = from_f32<T>(y);
+            }
+        reset();
+    };
+
+    // Two register sets of weights (ping-pong) and two LDS buffers: while
+    // item i is multiplied, item i+1's activations and weights are in
+    // flight (past the last item, the last item is fetched again and never
+    // used); the activations are stored into the other buffer after the
+    // multiply, then one barrier. The scheduling barriers keep the next
+    // item's loads ahead of the multiply (the scheduler would otherwise sink
+    // them to their use and expose their latency). (c_rg, c_slab) is the
+    // item being multiplied, (p_rg, p_slab) the one after it.
+    const int live_last = chunks - (slabs - 1) * S;
+    int c_rg = blockIdx.x, c_slab = 0;
+    int p_rg = blockIdx.x, p_slab = 0;
+    auto advance = [&](int& rg, int& slab) __attribute__((always_inline)) {
+        if (++slab == slabs) {
+            slab = 0;
+            rg += gridDim.x;
+        }
+    };
+    // One item: prefetch, multiply, finish a row group, stage, barrier.
+    auto step = [&](int i, int buf, const SlabWeights<S, RR>& cur, SlabWeights<S, RR>& nxt) __attribute__((always_inline)) {
+        const bool more = i + 1 < total;
+        const int f_rg = more ? p_rg : c_rg, f_slab = more ? p_slab : c_slab;
+        xload(f_slab);
+        wload(f_rg, f_slab, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        const bool end = c_slab == slabs - 1;
+        consume(buf, cur, end ? live_last : S);
+        if (end) finish(c_rg);
+        xstore(f_slab, buf ^ 1);
+        __syncthreads();
+        advance(c_rg, c_slab);
+        advance(p_rg, p_slab);
+    };
+
+    SlabWeights<S, RR> wa, wb;
+    reset();
+    xload(0);
+    wload(c_rg, 0, wa);
+    xstore(0, 0);
+    __syncthreads();
+    advance(p_rg, p_slab);
+    for (int i = 0; i < total; i += 2) {
+        step(i, 0, wa, wb);
+        if (i + 1 >= total) break;
+        step(i + 1, 1, wb, wa);
+    }
+}
+
 // LDS bytes for TT tokens at width k with tiles of U chunks.
 inline std::size_t exact_lds_bytes(int tt, int u, int k) {
     const int chunks = (k + 255) >> 8;
@@ -309,20 +526,59 @@ void launch_tile(const void* x, const std::int8_t* codes, const __half* scales, 
     }
 }
 
+template <class T, int TT, int RR, int S, int W>
+void launch_slab(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n, int k,
+                 int padded, hipStream_t stream) {
+    // Persistent grid: as many workgroups per token tile as stay resident
+    // together (occupancy x CUs, shared by the token tiles), at most one per
+    // row group.
+    constexpr int kT = W * 64;
+    static const int capacity = [] {
+        int device = 0, cus = 0, per = 0;
+        check(hipGetDevice(&device));
+        check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+        check(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per, reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, true, false>), kT, 0));
+        return std::max(1, cus * per);
+    }();
+    const int rgroups = (n + W * RR - 1) / (W * RR);
+    const int tiles = (tokens + TT - 1) / TT;
+    require(tiles <= 65535, "token tiles exceed the launch grid");
+    const dim3 grid(std::max(1, std::min(rgroups, capacity / tiles)), tiles);
+    const bool vec = (k % 4 == 0) && aligned(x, 8);
+    const int shift = static_cast<int>(reinterpret_cast<std::uintptr_t>(codes) & 3);
+    const T* xp = static_cast<const T*>(x);
+    T* op = static_cast<T*>(out);
+    const std::int8_t* base = codes - shift;  // 4-byte aligned
+    if (shift == 0) {
+        if (vec) q8_exact_slab<T, TT, RR, S, W, true, false><<<grid, kT, 0, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
+        else q8_exact_slab<T, TT, RR, S, W, false, false><<<grid, kT, 0, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
+    } else {
+        if (vec) q8_exact_slab<T, TT, RR, S, W, true, true><<<grid, kT, 0, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
+        else q8_exact_slab<T, TT, RR, S, W, false, true><<<grid, kT, 0, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
+    }
+}
+
 template <class T>
 void launch_exact(const void* x, const std::int8_t* codes, const __half* scales, void* out,
                   int tokens, int n, int k, int padded, hipStream_t stream) {
-    // Token tiles share one weight stream. From 8 tokens, 8-token tiles of one
-    // row each where their activations fit in LDS (k up to 10240): half the
-    // weight streams of 4-token tiles and 1.25 instead of 1.5 instructions per
-    // FMA (config-2 QKV / o_proj / gate+up at 8-16 tokens 17-34% faster);
-    // 4-token tiles of two rows otherwise.
-    if (tokens == 1) launch_tile<T, 1, 1, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else if (tokens == 2 || exact_lds_bytes(4, 4, k) > kMaxLds)
+    // One and two tokens: the whole activation tile staged once per
+    // persistent workgroup (the weight stream binds). From three tokens the
+    // FMAs bind and the slab form runs them as plain fp32 FMAs: tiles of 4
+    // tokens x 2 rows per wave, 8 x 2, 16 x 1, and 8 x 4 beyond 16 tokens
+    // (config-2 step on MI355X, QKV / o_proj / gate+up / down: 4 tokens
+    // 22.6 / 23.5 / 70.6 / 58.5 -> 15.7 / 16.5 / 55.2 / 36.9 us; 8 tokens
+    // 32.2 / 29.6 / 111.4 / 111.8 -> 21.3 / 23.3 / 85.0 / 53.5; 16 tokens
+    // 64.0 / 60.0 / 203.3 / 222.1 -> 45.4 / 41.9 / 184.2 / 103.6; same bytes).
+    // The slab form also serves widths whose whole tile exceeds LDS.
+    if (tokens == 1 && exact_lds_bytes(1, 4, k) <= kMaxLds)
+        launch_tile<T, 1, 1, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else if (tokens <= 2 && exact_lds_bytes(2, 4, k) <= kMaxLds)
         launch_tile<T, 2, 1, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else if (tokens >= 8 && exact_lds_bytes(8, 4, k) <= kMaxLds)
-        launch_tile<T, 8, 1, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else launch_tile<T, 4, 2, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else if (tokens <= 4) launch_slab<T, 4, 2, 4, 8>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else if (tokens <= 8) launch_slab<T, 8, 2, 2, 8>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else if (tokens <= 16) launch_slab<T, 16, 1, 2, 8>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else launch_slab<T, 8, 4, 2, 8>(x, codes, scales, out, tokens, n, k, padded, stream);
 }
 
 // One thread per 8 columns of a token's row (one scale covers them: 8 divides
