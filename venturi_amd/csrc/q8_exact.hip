@@ -267,12 +267,16 @@ __global__ __launch_bounds__(kThreads) void q8_exact(const T* __restrict__ x,
 // A virtual thread's FMA chain still advances one chunk at a time in
 // increasing column order inside one lane, so the association is the
 // canonical one, and the LDS footprint (2*TT*S KiB) does not grow with K.
-template <int TT, int RR, int S, int W>
+template <int TT, int RR, int S, int W, int B>
 struct SlabGeom {
     static constexpr int kThreads = W * 64;
     static constexpr int kUnits = TT * S * 64;          // 4-column activation units per slab
     static constexpr int kPer = kUnits / kThreads;      // units staged per thread
+    static constexpr int kRed = B * 256;                // floats of one wave's reduction scratch
+    static constexpr std::size_t kLds = 2 * kUnits * sizeof(float4) + W * kRed * sizeof(float);
     static_assert(kUnits % kThreads == 0, "whole activation units per thread");
+    static_assert(B == 0 || B == 4 || B == 8, "outputs reduced together (0: one at a time in registers)");
+    static_assert(B == 0 || (TT * RR) % B == 0, "whole batches of outputs");
 };
 
 template <int S, int RR>
@@ -281,17 +285,20 @@ struct SlabWeights {
     unsigned short sb[S][RR];
 };
 
-template <class T, int TT, int RR, int S, int W, bool VEC, bool SHIFT>
+template <class T, int TT, int RR, int S, int W, int B, bool VEC, bool SHIFT>
 __global__ __launch_bounds__(W * 64) void q8_exact_slab(const T* __restrict__ x,
                                                        const std::int8_t* __restrict__ codes,
                                                        const __half* __restrict__ scales,
                                                        T* __restrict__ out, int tokens, int n, int k,
                                                        int padded, int shift) {
-    using G = SlabGeom<TT, RR, S, W>;
-    __shared__ float4 xs[2][G::kUnits];
+    using G = SlabGeom<TT, RR, S, W, B>;
+    // Dynamic LDS: two activation slabs, then one reduction scratch per wave.
+    extern __shared__ float4 slab_lds[];
+    auto* xs = reinterpret_cast<float4(*)[G::kUnits]>(slab_lds);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float* red = reinterpret_cast<float*>(slab_lds + 2 * G::kUnits) + wave * G::kRed;
     const int t0 = blockIdx.y * TT;
     const int chunks = (k + 255) >> 8;
     const int slabs = (chunks + S - 1) / S;
@@ -409,18 +416,67 @@ __global__ __launch_bounds__(W * 64) void q8_exact_slab(const T* __restrict__ x,
             __builtin_amdgcn_sched_barrier(0);  // one chunk at a time (bounds the registers of hoisted reads)
         }
     };
-    // End of a row group: the canonical reduction of every output, stored
-    // by lane 0.
+    // End of a row group: the canonical reduction of the wave's TT*RR
+    // outputs, B at a time through the wave's own LDS scratch (no barrier:
+    // one wave's LDS operations complete in order). Output o's 256 partials
+    // are stored in virtual-thread order, reference warp w (lanes 8w..8w+7)
+    // in floats o*256 + 32w .. +31 with its eight 16-byte segments rotated
+    // by w (segment s of warp w at slot (s + w) % 8, so eight lanes reading
+    // the same segment of eight warps hit distinct banks), and lane
+    // (q, w) = (lane / 8, lane % 8) reads reference warp w of output q and
+    // runs that warp's shfl_down 16/8/4/2/1
+    // tree in registers (the same additions in the same order as
+    // canonical_sum: j + 16, + 8, + 4 across lanes there, + 2, + 1 within
+    // the lane); the eight warp sums of an output, in lanes 8q..8q+7, then
+    // take the two exact zero additions and the +4 / +2 / +1 steps as DPP
+    // row shifts inside their 16-lane row. About 7-12 instructions per
+    // output instead of canonical_sum's 32. With B = 4 the upper half of the
+    // wave repeats the lower half's work and stores nothing; B = 0 runs
+    // canonical_sum per output and needs no scratch (shapes whose LDS then
+    // keeps two workgroups per CU).
     auto finish = [&](int rg) __attribute__((always_inline)) {
         const int row0 = (rg * W + wave) * RR;
+        if constexpr (B == 0) {
 #pragma unroll
-        for (int t = 0; t < TT; ++t)
+            for (int t = 0; t < TT; ++t)
 #pragma unroll
-            for (int r = 0; r < RR; ++r) {
-                const float y = canonical_sum(acc[t][r][0], acc[t][r][1], acc[t][r][2], acc[t][r][3]);
-                if (lane == 0 && t0 + t < tokens && row0 + r < n)
-                    out[static_cast<std::int64_t>(t0 + t) * n + row0 + r] = from_f32<T>(y);
+                for (int r = 0; r < RR; ++r) {
+                    const float y = canonical_sum(acc[t][r][0], acc[t][r][1], acc[t][r][2], acc[t][r][3]);
+                    if (lane == 0 && t0 + t < tokens && row0 + r < n)
+                        out[static_cast<std::int64_t>(t0 + t) * n + row0 + r] = from_f32<T>(y);
+                }
+            reset();
+            return;
+        }
+        constexpr int kB = B == 0 ? 1 : B;
+        const int q = (lane >> 3) % kB, w = lane & 7;
+#pragma unroll
+        for (int b = 0; b < (TT * RR) / kB; ++b) {
+#pragma unroll
+            for (int i = 0; i < kB; ++i) {
+                const int o = b * kB + i, t = o / RR, r = o % RR;
+                *reinterpret_cast<float4*>(red + i * 256 + (lane >> 3) * 32 + (((lane & 7) + (lane >> 3)) & 7) * 4) =
+                    make_float4(acc[t][r][0], acc[t][r][1], acc[t][r][2], acc[t][r][3]);
             }
+            const float* src = red + q * 256 + w * 32;
+            float v[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 f = *reinterpret_cast<const float4*>(src + ((i + w) & 7) * 4);
+                v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+            }
+#pragma unroll
+            for (int h = 16; h >= 1; h >>= 1)
+#pragma unroll
+                for (int j = 0; j < h; ++j) v[j] = v[j] + v[j + h];
+            float y = (v[0] + 0.0f) + 0.0f;
+            y += row_shl<4>(y);
+            y += row_shl<2>(y);
+            y += row_shl<1>(y);
+            const int o = b * kB + q, t = o / RR, r = o % RR;
+            if (w == 0 && (lane >> 3) < kB && t0 + t < tokens && row0 + r < n)
+                out[static_cast<std::int64_t>(t0 + t) * n + row0 + r] = from_f32<T>(y);
+        }
         reset();
     };
 
@@ -526,19 +582,28 @@ void launch_tile(const void* x, const std::int8_t* codes, const __half* scales, 
     }
 }
 
-template <class T, int TT, int RR, int S, int W>
+template <class T, int TT, int RR, int S, int W, int B>
 void launch_slab(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n, int k,
                  int padded, hipStream_t stream) {
     // Persistent grid: as many workgroups per token tile as stay resident
     // together (occupancy x CUs, shared by the token tiles), at most one per
     // row group.
+    using G = SlabGeom<TT, RR, S, W, B>;
     constexpr int kT = W * 64;
-    static const int capacity = [] {
+    const void* kernels[4] = {
+        reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, true, false>),
+        reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, false, false>),
+        reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, true, true>),
+        reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, false, true>),
+    };
+    static const int capacity = [&kernels] {
+        if (G::kLds > 64 * 1024)
+            for (const void* f : kernels)
+                check(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(G::kLds)));
         int device = 0, cus = 0, per = 0;
         check(hipGetDevice(&device));
         check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
-        check(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per, reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, true, false>), kT, 0));
+        check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernels[0], kT, G::kLds));
         return std::max(1, cus * per);
     }();
     const int rgroups = (n + W * RR - 1) / (W * RR);
@@ -551,11 +616,11 @@ void launch_slab(const void* x, const std::int8_t* codes, const __half* scales, 
     T* op = static_cast<T*>(out);
     const std::int8_t* base = codes - shift;  // 4-byte aligned
     if (shift == 0) {
-        if (vec) q8_exact_slab<T, TT, RR, S, W, true, false><<<grid, kT, 0, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
-        else q8_exact_slab<T, TT, RR, S, W, false, false><<<grid, kT, 0, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
+        if (vec) q8_exact_slab<T, TT, RR, S, W, B, true, false><<<grid, kT, G::kLds, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
+        else q8_exact_slab<T, TT, RR, S, W, B, false, false><<<grid, kT, G::kLds, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
     } else {
-        if (vec) q8_exact_slab<T, TT, RR, S, W, true, true><<<grid, kT, 0, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
-        else q8_exact_slab<T, TT, RR, S, W, false, true><<<grid, kT, 0, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
+        if (vec) q8_exact_slab<T, TT, RR, S, W, B, true, true><<<grid, kT, G::kLds, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
+        else q8_exact_slab<T, TT, RR, S, W, B, false, true><<<grid, kT, G::kLds, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
     }
 }
 
@@ -565,20 +630,20 @@ void launch_exact(const void* x, const std::int8_t* codes, const __half* scales,
     // One and two tokens: the whole activation tile staged once per
     // persistent workgroup (the weight stream binds). From three tokens the
     // FMAs bind and the slab form runs them as plain fp32 FMAs: tiles of 4
-    // tokens x 2 rows per wave, 8 x 2, 16 x 1, and 8 x 4 beyond 16 tokens
-    // (config-2 step on MI355X, QKV / o_proj / gate+up / down: 4 tokens
-    // 22.6 / 23.5 / 70.6 / 58.5 -> 15.7 / 16.5 / 55.2 / 36.9 us; 8 tokens
-    // 32.2 / 29.6 / 111.4 / 111.8 -> 21.3 / 23.3 / 85.0 / 53.5; 16 tokens
-    // 64.0 / 60.0 / 203.3 / 222.1 -> 45.4 / 41.9 / 184.2 / 103.6; same bytes).
-    // The slab form also serves widths whose whole tile exceeds LDS.
+    // tokens x 2 rows per wave, 8 x 2, and 8 x 4 (slabs of 4 chunks, batched
+    // reductions) beyond 8 tokens (config-2 step on MI355X, QKV / o_proj /
+    // gate+up / down: 4 tokens 22.6 / 23.5 / 70.6 / 58.5 -> 15.7 / 16.5 /
+    // 55.2 / 36.9 us; 8 tokens 32.2 / 29.6 / 111.4 / 111.8 -> 21.3 / 23.3 /
+    // 85.0 / 53.5; 16 tokens 64.0 / 60.0 / 203.3 / 222.1 -> 39.1 / 43.5 /
+    // 160.0 / 107.8; same bytes). The slab form also serves widths whose
+    // whole tile exceeds LDS.
     if (tokens == 1 && exact_lds_bytes(1, 4, k) <= kMaxLds)
         launch_tile<T, 1, 1, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
     else if (tokens <= 2 && exact_lds_bytes(2, 4, k) <= kMaxLds)
         launch_tile<T, 2, 1, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else if (tokens <= 4) launch_slab<T, 4, 2, 4, 8>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else if (tokens <= 8) launch_slab<T, 8, 2, 2, 8>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else if (tokens <= 16) launch_slab<T, 16, 1, 2, 8>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else launch_slab<T, 8, 4, 2, 8>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else if (tokens <= 4) launch_slab<T, 4, 2, 4, 8, 0>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else if (tokens <= 8) launch_slab<T, 8, 2, 2, 8, 0>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else launch_slab<T, 8, 4, 4, 8, 8>(x, codes, scales, out, tokens, n, k, padded, stream);
 }
 
 // One thread per 8 columns of a token's row (one scale covers them: 8 divides
