@@ -160,6 +160,17 @@ def test_row_prefill_large_grids(backend, device, nbits, shape, tokens):
     _row_gemm_contract(backend, device, nbits, n, k, tokens)
 
 
+@pytest.mark.parametrize("nbits", [4, 5, 6])
+@pytest.mark.parametrize("shape,tokens", [((5120, 136), 2085), ((6144, 264), 2048), ((7168, 72), 300)])
+def test_row_prefill_wide_tiles(backend, device, nbits, shape, tokens):
+    # From 256 tokens the prefill takes 256-token tiles of 160, 192 or 224
+    # rows, picked per row count (these three pick each width on a 256-CU
+    # part); ragged token, row and group tails.
+    n, k = shape
+    print(f"case row-prefill-wide bits={nbits} n={n} k={k} tokens={tokens}", flush=True)
+    _row_gemm_contract(backend, device, nbits, n, k, tokens)
+
+
 def _row_gemm_contract(backend, device, nbits, n, k, tokens):
     packed, high, scales = _planes(n, k, nbits, 77 * nbits + n + tokens)
     padded = packed.shape[1] * 2

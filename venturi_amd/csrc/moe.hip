@@ -733,37 +733,44 @@ std::uint64_t align256(std::uint64_t v) { return (v + 255) / 256 * 256; }
 // once per workgroup into fp16) in two LDS buffers. Rows are eight 16-byte
 // units XOR-swizzled by (row >> 1) & 7, so 16 consecutive rows' fragment reads
 // cover all 64 banks once. Global loads run PF groups ahead in registers.
-template <int WM, int WN, int TI, int TJ>
+template <int WM, int WN, int TI, int TJ, int GS>
 struct RowPrefillGeom {
     static constexpr int kThreads = WM * WN * 64;
     static constexpr int kTM = WM * TI * 16;
     static constexpr int kTN = WN * TJ * 16;
-    static constexpr int kAUnits = kTM * 8;  // 16-byte activation loads per group (64 halves a row)
-    static constexpr int kBUnits = kTN * 2;  // 16-byte code loads per group (32 code bytes a row)
+    static constexpr int kU = 8 * GS;             // 16-byte units of a staged row (64 halves a group)
+    static constexpr int kAUnits = kTM * kU;      // 16-byte activation loads per stage
+    static constexpr int kBUnits = kTN * 2 * GS;  // 16-byte code loads per stage (32 code bytes a row a group)
     static constexpr int kAPer = (kAUnits + kThreads - 1) / kThreads;
     static constexpr int kBPer = (kBUnits + kThreads - 1) / kThreads;
+    static constexpr std::size_t kLds = 2 * static_cast<std::size_t>(kTM + kTN) * kU * 16;
     static_assert(kAUnits % kThreads == 0, "whole activation loads per thread");
-    static_assert(kBUnits % kThreads == 0 || kBUnits < kThreads, "whole code loads per thread");
+    static_assert(kLds <= 160 * 1024, "prefill tiles exceed LDS");
 };
 
 __device__ __forceinline__ int swizzle8(int row) { return (row >> 1) & 7; }
 
-template <int HB, int WM, int WN, int TI, int TJ, int PF>
+// GS groups (64 columns each) per stage, one barrier per stage; a staged row
+// holds the stage's groups one after another, each group's eight units
+// swizzled as above.
+template <int HB, int WM, int WN, int TI, int TJ, int PF, int GS>
 __global__ __launch_bounds__(WM * WN * 64) void row_prefill(const __half* __restrict__ x,
                                                            const std::uint8_t* __restrict__ codes,
                                                            const std::uint8_t* __restrict__ high,
                                                            const __half* __restrict__ scales, __half* __restrict__ out,
                                                            int tokens, int n, int k, int padded) {
-    using G = RowPrefillGeom<WM, WN, TI, TJ>;
-    constexpr int TM = G::kTM, TN = G::kTN, T = G::kThreads;
+    using G = RowPrefillGeom<WM, WN, TI, TJ, GS>;
+    constexpr int TM = G::kTM, TN = G::kTN, T = G::kThreads, U = G::kU;
     struct Stage {
         uint4 a[G::kAPer];
         uint4 b[G::kBPer];
         std::uint32_t h[G::kBPer][HB ? HB : 1];
         unsigned short s[G::kBPer];
     };
-    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][TM * 8];
-    __shared__ __attribute__((aligned(16))) uint4 b_lds[2][TN * 8];
+    // Dynamic LDS: two activation buffers [TM * U], then two weight buffers [TN * U].
+    extern __shared__ uint4 rp_lds[];
+    auto* a_lds = reinterpret_cast<uint4(*)[TM * U]>(rp_lds);
+    auto* b_lds = reinterpret_cast<uint4(*)[TN * U]>(rp_lds + 2 * TM * U);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -772,30 +779,39 @@ __global__ __launch_bounds__(WM * WN * 64) void row_prefill(const __half* __rest
     const int q = lane >> 4, r = lane & 15;
     const int t0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
     const int groups = padded / 64;
+    const int stages = (groups + GS - 1) / GS;
 
-    // Activation unit i = tid + u*T: token i / 8, columns 8 * (i % 8) of the group.
+    // Activation unit i = tid + u*T: token i / U, group (i / 8) % GS of the
+    // stage, columns 8 * (i % 8) of that group.
     const __half* a_src[G::kAPer];
     bool a_row_ok[G::kAPer];
 #pragma unroll
     for (int u = 0; u < G::kAPer; ++u) {
-        const int tok = (tid + u * T) / 8;
+        const int tok = (tid + u * T) / U;
         a_row_ok[u] = t0 + tok < tokens;
-        a_src[u] = x + static_cast<std::int64_t>(min(t0 + tok, tokens - 1)) * k + 8 * ((tid + u * T) & 7);
+        a_src[u] = x + static_cast<std::int64_t>(min(t0 + tok, tokens - 1)) * k;
     }
-    // Code unit i: row i / 2, code bytes 16 * (i % 2) of the group (columns 32 * (i % 2) ..).
+    // Code unit i: row i / (2 GS), group (i / 2) % GS of the stage, code bytes
+    // 16 * (i % 2) of that group (columns 32 * (i % 2) ..).
     std::int64_t b_row[G::kBPer];
 #pragma unroll
-    for (int u = 0; u < G::kBPer; ++u) b_row[u] = min(n0 + min((tid + u * T) / 2, TN - 1), n - 1);
+    for (int u = 0; u < G::kBPer; ++u) b_row[u] = min(n0 + min((tid + u * T) / (2 * GS), TN - 1), n - 1);
 
-    auto load = [&](int g, Stage& st) __attribute__((always_inline)) {
+    // Groups past the last one (groups % GS != 0) are read clamped to the last
+    // group; their activations are stored as zeros.
+    auto load = [&](int sg, Stage& st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < G::kAPer; ++u)
-            st.a[u] = *reinterpret_cast<const uint4*>(a_src[u] - 8 * ((tid + u * T) & 7) +
-                                                       min(64 * g + 8 * ((tid + u * T) & 7), k - 8));
+        for (int u = 0; u < G::kAPer; ++u) {
+            const int i = tid + u * T;
+            const int g = sg * GS + (i / 8) % GS;
+            st.a[u] = *reinterpret_cast<const uint4*>(a_src[u] + min(64 * g + 8 * (i & 7), k - 8));
+        }
 #pragma unroll
         for (int u = 0; u < G::kBPer; ++u) {
-            if (G::kBUnits < T && tid >= G::kBUnits) break;
-            const int half = (tid + u * T) & 1;
+            const int i = tid + u * T;
+            if (G::kBUnits % T != 0 && i >= G::kBUnits) break;
+            const int half = i & 1;
+            const int g = min(sg * GS + (i / 2) % GS, groups - 1);
             st.b[u] = *reinterpret_cast<const uint4*>(codes + b_row[u] * (padded / 2) + 32 * g + 16 * half);
             st.s[u] = __half_as_ushort(scales[b_row[u] * groups + g]);
             if constexpr (HB > 0) {
@@ -806,19 +822,19 @@ __global__ __launch_bounds__(WM * WN * 64) void row_prefill(const __half* __rest
             }
         }
     };
-    auto store = [&](const Stage& st, int g, int buf) __attribute__((always_inline)) {
+    auto store = [&](const Stage& st, int sg, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < G::kAPer; ++u) {
             const int i = tid + u * T;
-            const int tok = i / 8, unit = i & 7;
-            const bool ok = a_row_ok[u] && 64 * g + 8 * unit < k;  // k % 8 == 0: a unit is all in or all out
-            a_lds[buf][tok * 8 + (unit ^ swizzle8(tok))] = ok ? interleave8(st.a[u]) : make_uint4(0u, 0u, 0u, 0u);
+            const int tok = i / U, gg = (i / 8) % GS, unit = i & 7;
+            const bool ok = a_row_ok[u] && 64 * (sg * GS + gg) + 8 * unit < k;  // k % 8 == 0: a unit is all in or all out
+            a_lds[buf][tok * U + gg * 8 + (unit ^ swizzle8(tok))] = ok ? interleave8(st.a[u]) : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
         for (int u = 0; u < G::kBPer; ++u) {
             const int i = tid + u * T;
-            if (G::kBUnits < T && i >= G::kBUnits) break;
-            const int row = i / 2, half = i & 1;
+            if (G::kBUnits % T != 0 && i >= G::kBUnits) break;
+            const int row = i / (2 * GS), gg = (i / 2) % GS, half = i & 1;
             const half2v s2 = __builtin_bit_cast(half2v, static_cast<std::uint32_t>(st.s[u]) * 0x10001u);
             const std::uint32_t words[4] = {st.b[u].x, st.b[u].y, st.b[u].z, st.b[u].w};
 #pragma unroll
@@ -831,7 +847,7 @@ __global__ __launch_bounds__(WM * WN * 64) void row_prefill(const __half* __rest
                     const std::uint32_t hbits = (st.h[u][(HB * w) >> 2] >> (8 * ((HB * w) & 3))) & ((1u << (8 * HB)) - 1u);
                     v = dequant8_high<HB>(words[w], hbits, s2);
                 }
-                b_lds[buf][row * 8 + ((4 * half + w) ^ swizzle8(row))] = __builtin_bit_cast(uint4, v);
+                b_lds[buf][row * U + gg * 8 + ((4 * half + w) ^ swizzle8(row))] = __builtin_bit_cast(uint4, v);
             }
         }
     };
@@ -843,17 +859,19 @@ __global__ __launch_bounds__(WM * WN * 64) void row_prefill(const __half* __rest
         for (int j = 0; j < TJ; ++j) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
+        for (int gg = 0; gg < GS; ++gg)
+#pragma unroll
         for (int sl = 0; sl < 2; ++sl) {  // two 32-column slices of the group
             half8 fb[TJ];
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
                 const int row = wn * TJ * 16 + j * 16 + r;
-                fb[j] = __builtin_bit_cast(half8, b_lds[buf][row * 8 + ((4 * sl + q) ^ swizzle8(row))]);
+                fb[j] = __builtin_bit_cast(half8, b_lds[buf][row * U + gg * 8 + ((4 * sl + q) ^ swizzle8(row))]);
             }
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
                 const int tok = wm * TI * 16 + i * 16 + r;
-                const half8 fa = __builtin_bit_cast(half8, a_lds[buf][tok * 8 + ((4 * sl + q) ^ swizzle8(tok))]);
+                const half8 fa = __builtin_bit_cast(half8, a_lds[buf][tok * U + gg * 8 + ((4 * sl + q) ^ swizzle8(tok))]);
 #pragma unroll
                 for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa, fb[j], acc[i][j], 0, 0, 0);
             }
@@ -862,19 +880,19 @@ __global__ __launch_bounds__(WM * WN * 64) void row_prefill(const __half* __rest
 
     Stage st[PF];
 #pragma unroll
-    for (int s = 0; s < PF; ++s) load(min(s, groups - 1), st[s]);
+    for (int s = 0; s < PF; ++s) load(min(s, stages - 1), st[s]);
     store(st[0], 0, 0);
-    if (PF < groups) load(PF, st[0]);
+    if (PF < stages) load(PF, st[0]);
     __syncthreads();
-    for (int g0 = 0; g0 < groups; g0 += PF) {
+    for (int g0 = 0; g0 < stages; g0 += PF) {
 #pragma unroll
         for (int s = 0; s < PF; ++s) {
             const int g = g0 + s;
-            if (g >= groups) break;
+            if (g >= stages) break;
             compute(g & 1);
-            if (g + 1 < groups) {
+            if (g + 1 < stages) {
                 store(st[(s + 1) % PF], g + 1, (g + 1) & 1);
-                if (g + 1 + PF < groups) load(g + 1 + PF, st[(s + 1) % PF]);
+                if (g + 1 + PF < stages) load(g + 1 + PF, st[(s + 1) % PF]);
             }
             __syncthreads();
         }
@@ -893,14 +911,20 @@ __global__ __launch_bounds__(WM * WN * 64) void row_prefill(const __half* __rest
         }
 }
 
-template <int HB, int WM, int WN, int TI, int TJ, int PF>
+template <int HB, int WM, int WN, int TI, int TJ, int PF, int GS = 1>
 void launch_row_prefill(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
                         __half* out, int tokens, int n, int k, int padded, hipStream_t stream) {
-    using G = RowPrefillGeom<WM, WN, TI, TJ>;
+    using G = RowPrefillGeom<WM, WN, TI, TJ, GS>;
     const dim3 grid((n + G::kTN - 1) / G::kTN, (tokens + G::kTM - 1) / G::kTM);
     require(grid.y <= 65535, "token tiles exceed the launch grid");
-    row_prefill<HB, WM, WN, TI, TJ, PF><<<grid, G::kThreads, 0, stream>>>(x, codes, high, scales, out, tokens, n, k,
-                                                                         padded);
+    if constexpr (G::kLds > 64 * 1024) {
+        static const hipError_t raised = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(row_prefill<HB, WM, WN, TI, TJ, PF, GS>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(G::kLds));
+        check(raised);
+    }
+    row_prefill<HB, WM, WN, TI, TJ, PF, GS><<<grid, G::kThreads, G::kLds, stream>>>(x, codes, high, scales, out,
+                                                                                   tokens, n, k, padded);
 }
 
 // ---------------------------------------------------------------------------
@@ -1249,6 +1273,44 @@ void row_decode_dispatch(const __half* x, const std::uint8_t* codes, const std::
 // GEMM reads each weight once per 16 or 32 tokens).
 constexpr int kRowPrefillMinTokens = 32;
 
+// Prefill tiles. Below 256 tokens: 128 tokens x 128 rows (8 waves of 32 x 64).
+// From 256 tokens: 256 tokens x 32*TJ rows, 8 waves of 64 x 16*TJ (one
+// workgroup per CU by LDS), TJ in {5, 6, 7} picked for the fewest tile rounds
+// over the CUs weighted by the wider tiles' higher rate (fewer LDS bytes per
+// MFMA): at M = 2048 on MI355X, 5120 rows take TJ = 5 (256 tiles, one round),
+// 7168 and 34816 rows TJ = 7 (config-2 W4A16 at M = 2048: QKV / o_proj /
+// gate+up / down 214 / 196 / 908 / 532 -> 155-162 / 144-151 / 729-774 /
+// 386-409 us against 128 x 128 tiles; same bytes).
+template <int HB>
+void row_prefill_dispatch(const __half* x, const std::uint8_t* codes, const std::uint8_t* high, const __half* scales,
+                          __half* out, int tokens, int n, int k, int padded, hipStream_t stream) {
+    if (tokens < 256) {
+        launch_row_prefill<HB, 4, 2, 2, 4, 2>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+        return;
+    }
+    static const int cus = [] {
+        int device = 0, count = 0;
+        check(hipGetDevice(&device));
+        check(hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device));
+        return std::max(1, count);
+    }();
+    const std::int64_t token_tiles = (tokens + 255) / 256;
+    int best = 5;
+    double best_cost = 0.0;
+    for (int tj = 5; tj <= 7; ++tj) {
+        const std::int64_t tiles = token_tiles * ((n + 32 * tj - 1) / (32 * tj));
+        const double rate = tj == 5 ? 1.0 : tj == 6 ? 1.1 : 1.2;  // work per unit time, measured
+        const double cost = static_cast<double>((tiles + cus - 1) / cus) * tj / rate;
+        if (tj == 5 || cost < best_cost) {
+            best = tj;
+            best_cost = cost;
+        }
+    }
+    if (best == 5) launch_row_prefill<HB, 4, 2, 4, 5, 2>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+    else if (best == 6) launch_row_prefill<HB, 4, 2, 4, 6, 2>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+    else launch_row_prefill<HB, 4, 2, 4, 7, 1>(x, codes, high, scales, out, tokens, n, k, padded, stream);
+}
+
 void row_gemm_launch(const void* x, const void* codes, const void* high, const void* scales, void* out, int tokens,
                      int n, int k, int padded, int bits, int dtype, hipStream_t stream) {
     require(bits == 4 || bits == 5 || bits == 6, "row codecs are 4, 5 or 6 bits");
@@ -1265,10 +1327,9 @@ void row_gemm_launch(const void* x, const void* codes, const void* high, const v
     const auto* sp = static_cast<const __half*>(scales);
     auto* op = static_cast<__half*>(out);
     if (tokens >= kRowPrefillMinTokens) {
-        // Prefill: 128-token tiles that read each weight once per tile.
-        if (bits == 4) launch_row_prefill<0, 4, 2, 2, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
-        else if (bits == 5) launch_row_prefill<1, 4, 2, 2, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
-        else launch_row_prefill<2, 4, 2, 2, 4, 2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
+        if (bits == 4) row_prefill_dispatch<0>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
+        else if (bits == 5) row_prefill_dispatch<1>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
+        else row_prefill_dispatch<2>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
         return;
     }
     if (bits == 4) row_decode_dispatch<0>(xp, cp, hp, sp, op, tokens, n, k, padded, stream);
