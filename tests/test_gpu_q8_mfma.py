@@ -57,7 +57,7 @@ def test_mfma_tolerances_tails_and_guards(backend, device, shape, tokens):
 @pytest.mark.parametrize("tokens", [33, 64, 100, 256, 300])
 def test_prefill_gemm_tolerances_tails_and_guards(backend, device, shape, tokens):
     # venturi_q8_prefill_run: the same contract as the decode kernels (exact
-    # group dots on matrix cores, fp32 group scaling), 256 x 128 tiles.
+    # group dots on matrix cores, fp32 group scaling), at small ragged shapes.
     n, k = shape
     print(f"case q8-prefill n={n} k={k} tokens={tokens}", flush=True)
     codes, scales = random_q8(n, k, 901 + n + tokens)
@@ -74,8 +74,10 @@ def test_prefill_gemm_tolerances_tails_and_guards(backend, device, shape, tokens
     print(f"flips={flips} of {tokens * n}", flush=True)
 
 
-@pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 17408)])
+@pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 17408), (34816, 5120)])
 def test_prefill_config2_m2048_sampled_rows(backend, device, n, k):
+    # The three row counts take the three tilings (128 x 224, 128 x 160 and
+    # 256 x 128 tiles on a 256-CU part).
     gen = torch.Generator(device=device).manual_seed(n + k + 1)
     w = torch.randn(n, k, generator=gen, device=device) * 0.02
     packed = backend.quantize_q8(w)

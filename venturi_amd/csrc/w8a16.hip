@@ -19,6 +19,8 @@
 // tile leaves through LDS as 16-byte row units.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace vt {
 namespace {
 
@@ -363,18 +365,41 @@ void q8_prefill_launch(const void* x, const std::int8_t* codes, const __half* sc
     require(dtype == kF16, "the Q8 prefill GEMM takes FP16 activations");
     require(k % 8 == 0 && aligned(x, 16), "the Q8 prefill GEMM needs k % 8 == 0 and 16-byte aligned x");
     require(aligned(codes, 16) && aligned(scales, 2) && aligned(out, 2), "misaligned Q8 operand");
-    // 256 x 128 tiles, one group per stage, unless that grid leaves CUs with
-    // uneven shares (fewer than 384 workgroups: n = 5120 at 2048 tokens gives
-    // 320); then 128 x 128 tiles with two groups per stage (o_proj and down at
-    // M = 2048: 383 -> 436 and 401 -> 467 TFLOP/s; same bits either way, the
-    // groups being summed in natural order).
+    // Three tilings, each one workgroup of 8 waves per CU: 256 x 128 (waves of
+    // 64 x 64), 128 x 160 (32 x 80) and 128 x 224 (32 x 112). The launch takes
+    // the one with the least time over whole tile rounds on the CUs, from
+    // their measured rates per unit of work (1 : 0.76 : 0.89): at M = 2048,
+    // 7168 rows take 128 x 224 (512 tiles, two rounds), 5120 rows 128 x 160
+    // (512 tiles), 34816 rows 256 x 128 (config-2 W8A16 QKV / o_proj / gate+up
+    // / down 303 / 306 / 1225 / 818 -> 297 / 256 / 1225 / 685 us; same bits
+    // in every tiling, the groups being summed in natural order).
     const auto* xp = static_cast<const __half*>(x);
     auto* op = static_cast<__half*>(out);
-    const long big_grid = static_cast<long>((n + 127) / 128) * ((tokens + 255) / 256);
-    if (big_grid < 384)
-        launch_prefill<2, 4, 4, 2, 2, 2>(xp, codes, scales, op, tokens, n, k, padded, stream);
-    else
-        launch_prefill<4, 2, 4, 4, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
+    static const int cus = [] {
+        int device = 0, count = 0;
+        check(hipGetDevice(&device));
+        check(hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device));
+        return std::max(1, count);
+    }();
+    struct Tiling {
+        int tm, tn;
+        double rate;
+    };
+    constexpr Tiling kTilings[3] = {{256, 128, 1.0}, {128, 160, 0.76}, {128, 224, 0.89}};
+    int best = 0;
+    double best_cost = 0.0;
+    for (int i = 0; i < 3; ++i) {
+        const Tiling& t = kTilings[i];
+        const std::int64_t tiles = static_cast<std::int64_t>((tokens + t.tm - 1) / t.tm) * ((n + t.tn - 1) / t.tn);
+        const double cost = static_cast<double>((tiles + cus - 1) / cus) * t.tm * t.tn / t.rate;
+        if (i == 0 || cost < best_cost) {
+            best = i;
+            best_cost = cost;
+        }
+    }
+    if (best == 0) launch_prefill<4, 2, 4, 4, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
+    else if (best == 1) launch_prefill<4, 2, 2, 5, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
+    else launch_prefill<4, 2, 2, 7, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
 }
 
 }  // namespace vt
