@@ -322,10 +322,20 @@ void a8_fast_launch(const void* workspace, const std::int8_t* codes, const __hal
     const auto* acodes = static_cast<const std::int8_t*>(workspace);
     const auto* ascales = reinterpret_cast<const float*>(acodes + count * 32 * passes);
     auto* y = static_cast<__half*>(out);
-    if (passes == 1)
-        launch_fast<1, 4, 2, 4, 4>(acodes, ascales, codes, scales, y, tokens, n, padded, groups, stream);
-    else
+    if (passes == 2) {
         launch_fast<2, 4, 2, 2, 4>(acodes, ascales, codes, scales, y, tokens, n, padded, groups, stream);
+        return;
+    }
+    // One pass: 256 x 128, 128 x 160 or 128 x 224 tiles (waves of 64 x 64,
+    // 32 x 80, 32 x 112), whichever leaves the fewest tile rounds on the CUs
+    // at the measured rates (config 3 at M = 2048 on MI355X: QKV / o_proj /
+    // gate+up / down 457 / 435 / 1781 / 1162 -> 408 / 389 / 1781 / 1038 us;
+    // same bits in every tiling, the groups being summed in natural order).
+    constexpr GemmTiling kTilings[3] = {{256, 128, 1.0}, {128, 160, 0.76}, {128, 224, 0.89}};
+    const int best = pick_tiling(tokens, n, kTilings);
+    if (best == 0) launch_fast<1, 4, 2, 4, 4>(acodes, ascales, codes, scales, y, tokens, n, padded, groups, stream);
+    else if (best == 1) launch_fast<1, 4, 2, 2, 5>(acodes, ascales, codes, scales, y, tokens, n, padded, groups, stream);
+    else launch_fast<1, 4, 2, 2, 7>(acodes, ascales, codes, scales, y, tokens, n, padded, groups, stream);
 }
 
 }  // namespace vt

@@ -188,4 +188,41 @@ __device__ __forceinline__ float warp32_sum(float v) {
     return v;
 }
 
+// GEMM tile shapes of the prefill kernels: each candidate is one workgroup of
+// 8 waves per CU; pick_tiling returns the one with the least time over whole
+// tile rounds on the device's CUs, from the candidates' measured rates per
+// unit of work (a tile round costs tm * tn / rate).
+struct GemmTiling {
+    int tm, tn;
+    double rate;
+};
+
+inline int device_cus() {
+    static const int cus = [] {
+        int device = 0, count = 0;
+        check(hipGetDevice(&device));
+        check(hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device));
+        return count > 0 ? count : 1;
+    }();
+    return cus;
+}
+
+template <int N>
+inline int pick_tiling(int tokens, int n, const GemmTiling (&tilings)[N]) {
+    const int cus = device_cus();
+    int best = 0;
+    double best_cost = 0.0;
+    for (int i = 0; i < N; ++i) {
+        const GemmTiling& t = tilings[i];
+        const std::int64_t tiles =
+            static_cast<std::int64_t>((tokens + t.tm - 1) / t.tm) * ((n + t.tn - 1) / t.tn);
+        const double cost = static_cast<double>((tiles + cus - 1) / cus) * t.tm * t.tn / t.rate;
+        if (i == 0 || cost < best_cost) {
+            best = i;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
 }  // namespace vt

@@ -1288,12 +1288,7 @@ void row_prefill_dispatch(const __half* x, const std::uint8_t* codes, const std:
         launch_row_prefill<HB, 4, 2, 2, 4, 2>(x, codes, high, scales, out, tokens, n, k, padded, stream);
         return;
     }
-    static const int cus = [] {
-        int device = 0, count = 0;
-        check(hipGetDevice(&device));
-        check(hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device));
-        return std::max(1, count);
-    }();
+    const int cus = device_cus();
     const std::int64_t token_tiles = (tokens + 255) / 256;
     int best = 5;
     double best_cost = 0.0;

@@ -375,28 +375,8 @@ void q8_prefill_launch(const void* x, const std::int8_t* codes, const __half* sc
     // in every tiling, the groups being summed in natural order).
     const auto* xp = static_cast<const __half*>(x);
     auto* op = static_cast<__half*>(out);
-    static const int cus = [] {
-        int device = 0, count = 0;
-        check(hipGetDevice(&device));
-        check(hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device));
-        return std::max(1, count);
-    }();
-    struct Tiling {
-        int tm, tn;
-        double rate;
-    };
-    constexpr Tiling kTilings[3] = {{256, 128, 1.0}, {128, 160, 0.76}, {128, 224, 0.89}};
-    int best = 0;
-    double best_cost = 0.0;
-    for (int i = 0; i < 3; ++i) {
-        const Tiling& t = kTilings[i];
-        const std::int64_t tiles = static_cast<std::int64_t>((tokens + t.tm - 1) / t.tm) * ((n + t.tn - 1) / t.tn);
-        const double cost = static_cast<double>((tiles + cus - 1) / cus) * t.tm * t.tn / t.rate;
-        if (i == 0 || cost < best_cost) {
-            best = i;
-            best_cost = cost;
-        }
-    }
+    constexpr GemmTiling kTilings[3] = {{256, 128, 1.0}, {128, 160, 0.76}, {128, 224, 0.89}};
+    const int best = pick_tiling(tokens, n, kTilings);
     if (best == 0) launch_prefill<4, 2, 4, 4, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
     else if (best == 1) launch_prefill<4, 2, 2, 5, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
     else launch_prefill<4, 2, 2, 7, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
