@@ -615,14 +615,17 @@ def prefill_a16(backend, device, steps, warmup):
     W8A16 against the canonical-order route (venturi_q8_head_run); W4A16
     against the reference's own W4A16 path on this GPU (fp16(q*s) weights
     decoded by venturi_row_dequant_rows, then torch's fp16 linear with fp32
-    accumulation, as the reference's dequant-then-F.linear path does).
+    accumulation, as the reference's dequant-then-F.linear path does). `parity`
+    is the hand-written kernel's output; the library route's agreement is
+    `library_route.parity` (for W4A16 that compares hipBLASLt with torch's
+    linear, itself hipBLASLt on this GPU).
     """
     m = 2048
     gen = torch.Generator(device=device).manual_seed(11)
     stream = torch.cuda.current_stream(device)
     sections = {}
     for codec, quantize in (("w8a16", backend.quantize_q8), ("w4a16", backend.quantize_q4)):
-        stages, total_flops, total_s, fused_s, route, parity = {}, 0, 0.0, 0.0, None, {}
+        stages, total_flops, total_s, fused_s, route, parity, lib_parity = {}, 0, 0.0, 0.0, None, {}, {}
         for name, n, k in PROJECTIONS:
             packed = quantize(torch.randn(n, k, generator=gen, device=device) * 0.02)
             resident = backend.upload_linear(packed, dtype=torch.float16, device=device)
@@ -634,10 +637,11 @@ def prefill_a16(backend, device, steps, warmup):
             ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device) if plan.workspace_bytes else None
             kw = {} if ws is None else {"workspace": ws}
             t = event_time(lambda: plan.run(x, out=out, **kw), steps, warmup, stream)
-            fused_us = None
+            fused_us, fused_out = None, None
             if route in ("venturi-q4-dense", "venturi-q8-dense"):  # the fused kernel on the same weights, for comparison
                 fused = resident.prepare(tokens=m, route="mfma")
-                fused_us = round(event_time(lambda: fused.run(x, out=out), steps, warmup, stream) * 1e6, 1)
+                fused_out = torch.empty_like(out)
+                fused_us = round(event_time(lambda: fused.run(x, out=fused_out), steps, warmup, stream) * 1e6, 1)
                 plan.run(x, out=out, **kw)
             if codec == "w8a16":
                 ref = torch.empty_like(out)
@@ -648,7 +652,11 @@ def prefill_a16(backend, device, steps, warmup):
                 ref = torch.nn.functional.linear(x, dense)
                 del dense
             torch.cuda.synchronize(device)
-            parity[name] = compact(agreement(out, ref))
+            # `parity` is the hand-written kernel's (the roofline's); the library
+            # route's own agreement is kept beside it.
+            parity[name] = compact(agreement(out if fused_out is None else fused_out, ref))
+            if fused_out is not None:
+                lib_parity[name] = compact(agreement(out, ref))
             flops = 2 * m * n * k
             total_flops += flops
             total_s += t
@@ -657,7 +665,7 @@ def prefill_a16(backend, device, steps, warmup):
             if fused_us is not None:
                 stages[name]["fused_mfma_us"] = fused_us
             fused_s += t if fused_us is None else fused_us / 1e6
-            del resident, plan, x, out, ref, ws
+            del resident, plan, x, out, ref, ws, fused_out
         tf = total_flops / total_s / 1e12
         fused_tf = total_flops / fused_s / 1e12
         kernel = "q8_prefill" if codec == "w8a16" else "row_prefill"
@@ -671,9 +679,11 @@ def prefill_a16(backend, device, steps, warmup):
                                         "frac": round(fused_tf / FP16_PEAK_TFLOPS, 4)},
                            **({"library_route": {"kernel": library, "note": "the auto route at 2048 tokens (vendor "
                                                  "GEMM over a decoded shadow), for comparison",
-                                                 "TFLOP/s": round(tf, 1), "frac": round(tf / FP16_PEAK_TFLOPS, 4)}}
+                                                 "TFLOP/s": round(tf, 1), "frac": round(tf / FP16_PEAK_TFLOPS, 4),
+                                                 "parity": compact(merge_agreement(lib_parity.values()))}}
                               if library else {}),
-                           "parity": {"against": "canonical-order route" if codec == "w8a16" else
+                           "parity": {"kernel": kernel,
+                                      "against": "canonical-order route" if codec == "w8a16" else
                                       "decoded fp16 weights + torch fp16 linear (the reference's W4A16 path)",
                                       "summary": compact(merge_agreement(parity.values())),
                                       "per_projection": parity},
