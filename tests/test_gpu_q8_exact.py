@@ -183,7 +183,7 @@ def test_device_pack_near_ties(backend, device, dtype, trim):
 
 
 @pytest.mark.parametrize("offset", [1, 2, 3, 4, 5, 8, 17])
-@pytest.mark.parametrize("shape,tokens", [((7, 65), 1), ((33, 300), 3), ((70, 1024), 5), ((5, 5120), 1)])
+@pytest.mark.parametrize("shape,tokens", [((7, 65), 1), ((33, 300), 3), ((70, 1024), 5), ((5, 5120), 1), ((40, 2056), 17)])
 def test_head_run_accepts_unaligned_codes(backend, device, offset, shape, tokens):
     # venturi_q8_head_run takes any code pointer, as the reference's does
     # (blocks.cu:935-948): a plane that starts `offset` bytes into a buffer (a

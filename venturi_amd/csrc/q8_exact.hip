@@ -582,7 +582,11 @@ void launch_tile(const void* x, const std::int8_t* codes, const __half* scales, 
     }
 }
 
-template <class T, int TT, int RR, int S, int W, int B>
+// GENERAL: whether the shape is also built for code planes that start off a
+// 4-byte boundary and for activations read element-wise (k % 4 != 0 or x not
+// 8-byte aligned); the 8 x 4 tiles spill in those forms, so such calls take
+// the 8 x 2 tiles.
+template <class T, int TT, int RR, int S, int W, int B, bool GENERAL = true>
 void launch_slab(const void* x, const std::int8_t* codes, const __half* scales, void* out, int tokens, int n, int k,
                  int padded, hipStream_t stream) {
     // Persistent grid: as many workgroups per token tile as stay resident
@@ -592,14 +596,14 @@ void launch_slab(const void* x, const std::int8_t* codes, const __half* scales, 
     constexpr int kT = W * 64;
     const void* kernels[4] = {
         reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, true, false>),
-        reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, false, false>),
-        reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, true, true>),
-        reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, false, true>),
+        GENERAL ? reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, !GENERAL, false>) : nullptr,
+        GENERAL ? reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, true, GENERAL>) : nullptr,
+        GENERAL ? reinterpret_cast<const void*>(q8_exact_slab<T, TT, RR, S, W, B, !GENERAL, GENERAL>) : nullptr,
     };
     static const int capacity = [&kernels] {
         if (G::kLds > 64 * 1024)
             for (const void* f : kernels)
-                check(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(G::kLds)));
+                if (f) check(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(G::kLds)));
         int device = 0, cus = 0, per = 0;
         check(hipGetDevice(&device));
         check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
@@ -615,12 +619,14 @@ void launch_slab(const void* x, const std::int8_t* codes, const __half* scales, 
     const T* xp = static_cast<const T*>(x);
     T* op = static_cast<T*>(out);
     const std::int8_t* base = codes - shift;  // 4-byte aligned
-    if (shift == 0) {
-        if (vec) q8_exact_slab<T, TT, RR, S, W, B, true, false><<<grid, kT, G::kLds, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
-        else q8_exact_slab<T, TT, RR, S, W, B, false, false><<<grid, kT, G::kLds, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
-    } else {
-        if (vec) q8_exact_slab<T, TT, RR, S, W, B, true, true><<<grid, kT, G::kLds, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
+    if (shift == 0 && vec) {
+        q8_exact_slab<T, TT, RR, S, W, B, true, false><<<grid, kT, G::kLds, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
+    } else if constexpr (GENERAL) {
+        if (shift == 0) q8_exact_slab<T, TT, RR, S, W, B, false, false><<<grid, kT, G::kLds, stream>>>(xp, codes, scales, op, tokens, n, k, padded, 0);
+        else if (vec) q8_exact_slab<T, TT, RR, S, W, B, true, true><<<grid, kT, G::kLds, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
         else q8_exact_slab<T, TT, RR, S, W, B, false, true><<<grid, kT, G::kLds, stream>>>(xp, base, scales, op, tokens, n, k, padded, shift);
+    } else {
+        throw Invalid("this exact-route shape is built for 4-byte aligned codes and vector activation loads only");
     }
 }
 
@@ -642,8 +648,9 @@ void launch_exact(const void* x, const std::int8_t* codes, const __half* scales,
     else if (tokens <= 2 && exact_lds_bytes(2, 4, k) <= kMaxLds)
         launch_tile<T, 2, 1, 4>(x, codes, scales, out, tokens, n, k, padded, stream);
     else if (tokens <= 4) launch_slab<T, 4, 2, 4, 8, 0>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else if (tokens <= 8) launch_slab<T, 8, 2, 2, 8, 0>(x, codes, scales, out, tokens, n, k, padded, stream);
-    else launch_slab<T, 8, 4, 4, 8, 8>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else if (tokens <= 8 || (reinterpret_cast<std::uintptr_t>(codes) & 3) != 0 || k % 4 != 0 || !aligned(x, 8))
+        launch_slab<T, 8, 2, 2, 8, 0>(x, codes, scales, out, tokens, n, k, padded, stream);
+    else launch_slab<T, 8, 4, 4, 8, 8, false>(x, codes, scales, out, tokens, n, k, padded, stream);
 }
 
 // One thread per 8 columns of a token's row (one scale covers them: 8 divides
