@@ -365,21 +365,24 @@ void q8_prefill_launch(const void* x, const std::int8_t* codes, const __half* sc
     require(dtype == kF16, "the Q8 prefill GEMM takes FP16 activations");
     require(k % 8 == 0 && aligned(x, 16), "the Q8 prefill GEMM needs k % 8 == 0 and 16-byte aligned x");
     require(aligned(codes, 16) && aligned(scales, 2) && aligned(out, 2), "misaligned Q8 operand");
-    // Three tilings, each one workgroup of 8 waves per CU: 256 x 128 (waves of
-    // 64 x 64), 128 x 160 (32 x 80) and 128 x 224 (32 x 112). The launch takes
-    // the one with the least time over whole tile rounds on the CUs, from
-    // their measured rates per unit of work (1 : 0.76 : 0.89): at M = 2048,
+    // Four tilings of 8 waves: 256 x 128 (waves of 64 x 64), 128 x 160
+    // (32 x 80), 128 x 224 (32 x 112), each one workgroup per CU, and
+    // 128 x 128 with two groups per stage (the small grids' tiling). The
+    // launch takes the one with the least time over whole tile rounds on the
+    // CUs, from their measured rates per unit of work (1 : 0.76 : 0.89 :
+    // 0.80): small grids take 128 x 128 as before; at M = 2048,
     // 7168 rows take 128 x 224 (512 tiles, two rounds), 5120 rows 128 x 160
     // (512 tiles), 34816 rows 256 x 128 (config-2 W8A16 QKV / o_proj / gate+up
     // / down 303 / 306 / 1225 / 818 -> 297 / 256 / 1225 / 685 us; same bits
     // in every tiling, the groups being summed in natural order).
     const auto* xp = static_cast<const __half*>(x);
     auto* op = static_cast<__half*>(out);
-    constexpr GemmTiling kTilings[3] = {{256, 128, 1.0}, {128, 160, 0.76}, {128, 224, 0.89}};
+    constexpr GemmTiling kTilings[4] = {{256, 128, 1.0}, {128, 160, 0.76}, {128, 224, 0.89}, {128, 128, 0.80}};
     const int best = pick_tiling(tokens, n, kTilings);
     if (best == 0) launch_prefill<4, 2, 4, 4, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
     else if (best == 1) launch_prefill<4, 2, 2, 5, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
-    else launch_prefill<4, 2, 2, 7, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
+    else if (best == 2) launch_prefill<4, 2, 2, 7, 2, 1>(xp, codes, scales, op, tokens, n, k, padded, stream);
+    else launch_prefill<2, 4, 4, 2, 2, 2>(xp, codes, scales, op, tokens, n, k, padded, stream);
 }
 
 }  // namespace vt
