@@ -629,8 +629,9 @@ struct TiledShape {
 
 TiledShape tiled_shape(int tokens, int blocks) {
     // One token: up to 256 row blocks take one block per workgroup (every wave
-    // issuing four chunks per batch), which fills the chip where two blocks per
-    // workgroup would leave half of it idle (config 1: 7.3 -> 6.2 us).
+    // issuing four chunks per batch, two where a wave has at most four),
+    // which fills the chip where two blocks per workgroup would leave half of
+    // it idle (config 1: 7.3 -> 6.2 us; two-chunk batches 6.3 -> 5.5 us).
     if (tokens == 1) return blocks <= 256 ? TiledShape{true, 1, 1} : blocks < 1024 ? TiledShape{true, 2, 1} : TiledShape{true, 3, 1};
     const TiledShape candidates[] = {{false, 2, 1}, {false, 3, 1}, {false, 3, 2}, {false, 4, 2}};
     TiledShape best{false, 3, 1};
@@ -677,7 +678,9 @@ template <bool SWIGLU>
 void tiled_dispatch(const __half* xp, const uint4* cp, const std::uint32_t* sp, __half* op, unsigned long long* slots,
                     int tokens, int n, int k, int chunks, int blocks, hipStream_t stream) {
     const TiledShape sh = tiled_shape(tokens, blocks);
-    if (sh.lds && sh.rb == 1)
+    if (sh.lds && sh.rb == 1 && chunks <= 64)  // at most four chunks a wave: two batches of two (config 1: 6.3 -> 5.5 us)
+        launch_tiled_lds<16, 1, 2, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+    else if (sh.lds && sh.rb == 1)
         launch_tiled_lds<16, 1, 4, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else if (sh.lds && sh.rb == 2)
         launch_tiled_lds<16, 2, 1, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
