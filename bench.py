@@ -15,6 +15,11 @@ are then replayed back to back, each between one pair of HIP events on the
 launch stream, for the per-launch durations (every graph's output is checked
 against an eager launch).
 
+The line is compact by default: per-launch records are arrays over the token
+counts `M` for each projection (`us`, and `GB/s` for the headline launches and
+the exact route), agreement records keep their summary (and a max-ulp array per
+launch); `--full` prints every record as its own object.
+
 Printed JSON (one line): `value` is the whole-job algorithmic throughput in
 GB/s (weights N*Kp*(1+2/32) + activations M*K*2 + outputs M*N*2, per launch)
 over the timed region's wall clock; `roofline` is the dominant kernel's
@@ -38,6 +43,7 @@ sections of the same line carry their own roofline objects: `config1`
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -86,6 +92,8 @@ def parse():
     p.add_argument("--only", default=None,
                    help="comma-separated sections to run (config2,config1,head,q4,q56,codecs,a8dec,a8,a16,moe,model); "
                    "without config2 no headline metric is printed (for counter runs)")
+    p.add_argument("--full", action="store_true",
+                   help="print per-launch and per-projection records as one object each (the default line is compact)")
     p.add_argument("--eager", action="store_true",
                    help="time config-2 launches issued from Python instead of HIP-graph replays (for counter runs)")
     return p.parse_args()
@@ -129,6 +137,87 @@ def merge_agreement(items):
 
 def compact(stats):
     return {k: (float(f"{v:.4g}") if isinstance(v, float) else v) for k, v in stats.items()}
+
+
+_LAUNCH_KEY = re.compile(r"^(?P<proj>[a-z_]+?)_m(?P<m>\d+)(?P<suffix>_p\d+)?$")
+
+
+def launch_table(detail):
+    """Per-launch records keyed '<projection>_m<M>[_p<passes>]' as one array per field and projection.
+
+    {'qkv_m1': {'us': 9.5, 'GB/s': 4120}, 'qkv_m4': ...} becomes
+    {'M': [1, 4, ...], 'us': {'qkv': [9.5, ...]}, 'GB/s': {...}}; a string or
+    boolean field that is the same in every record is kept once. Records of
+    another shape are returned unchanged.
+    """
+    ms, numeric, uniform = [], {}, {}
+    for key, rec in detail.items():
+        hit = _LAUNCH_KEY.match(key)
+        if hit is None or not isinstance(rec, dict):
+            return detail
+        m, name = int(hit["m"]), hit["proj"] + (hit["suffix"] or "")
+        if m not in ms:
+            ms.append(m)
+        for field, v in rec.items():
+            if isinstance(v, bool) or isinstance(v, str):
+                uniform.setdefault(field, set()).add(v)
+            elif isinstance(v, (int, float)):
+                numeric.setdefault(field, {}).setdefault(name, {})[m] = v
+    out = {"M": ms}
+    for field, per in numeric.items():
+        out[field] = {name: [vals.get(m) for m in ms] for name, vals in per.items()}
+    for field, values in uniform.items():
+        out[field] = values.pop() if len(values) == 1 else sorted(values, key=str)
+    return out
+
+
+# Sections of the printed line in order: the contract's fields first, then the
+# sections least often read, so that a reader holding only the end of a long
+# line still has the headline's per-launch table, parity and exact route.
+_LINE_ORDER = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+               "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline", "timing", "all_kernels_GBps",
+               "graph_equals_eager", "codecs", "q56_decode", "config1", "model_decode", "moe_w4a16", "prefill_a16",
+               "prefill_a8", "a8_decode", "q4_decode", "vocab_head", "exact_route", "parity", "per_launch")
+
+
+def shorten(result):
+    """The printed line in compact form, so that the whole line stays a few KB.
+
+    Per-launch records become arrays over M (`launch_table`); per-launch
+    agreement records keep their max-ulp column (the section's summary holds
+    the rest); per-projection agreement records are left to the summary;
+    GB/s columns are kept for the headline's launches and the exact route and
+    left out elsewhere (the section's own GB/s and roofline stay); stage
+    fractions of peak are left out (their TFLOP/s / TOPS stay).
+    """
+    keep_rate = ("exact_route",)  # besides the headline's own per_launch
+
+    def walk(node, path):
+        if not isinstance(node, dict):
+            return node
+        out = {}
+        for key, value in node.items():
+            if key == "per_projection":
+                continue
+            if key.startswith("frac_") and key.endswith("_peak") and "stages" in path:
+                continue
+            if key == "per_launch" and isinstance(value, dict):
+                sample = next(iter(value.values()), None)
+                if isinstance(sample, dict) and "max_ulp" in sample:
+                    table = launch_table({k: {"max_ulp": v["max_ulp"]} for k, v in value.items()})
+                else:
+                    table = launch_table({k: walk(v, path + (key,)) for k, v in value.items()})
+                    if path and path[0] not in keep_rate and isinstance(table.get("GB/s"), dict) and "us" in table:
+                        table.pop("GB/s")
+                out[key] = table
+            else:
+                out[key] = walk(value, path + (key,))
+        return out
+
+    short = walk(result, ())
+    ordered = {k: short[k] for k in _LINE_ORDER if k in short}
+    ordered.update({k: v for k, v in short.items() if k not in ordered})
+    return ordered
 
 
 def event_time(fn, reps, warmup, stream):
@@ -1184,7 +1273,7 @@ def main():
     if cpu_copies is not None:
         log("CPU baseline (reference CPU path)")
         result["cpu_baseline"] = cpu_baseline(cpu_copies, args.cpu_seconds)
-    print(json.dumps(result), flush=True)
+    print(json.dumps(result if args.full else shorten(result)), flush=True)
 
 
 if __name__ == "__main__":
