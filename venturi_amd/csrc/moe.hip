@@ -308,15 +308,25 @@ __device__ int2 route_expert(const Q4Tiled& p, int expert, bool writer, unsigned
 
 // Grouped expert GEMM over the tiled planes with a fraction of an expert per
 // workgroup: W = 8 waves, wave v owns RB consecutive 16-row blocks (global
-// block b = tile * 8 + w of the tiled layout), so a workgroup covers 8 * RB
-// blocks and stages every activation chunk once in LDS for all of them. With
-// 128 experts and 4 parts per expert the grid is 512 workgroups, two per CU,
-// all resident at once. Weights are double-buffered in registers by half
-// chunk (1 KB per block): the loads of the next half are issued as soon as a
-// half has been multiplied, so each wave keeps RB KB in flight. Each
-// activation fragment is read from LDS once per step and multiplied by all RB
-// blocks. Passes of up to 16 * NBMAX tokens.
-template <int EPI, int W, int RB, int NBMAX, bool ROUTE>
+// block b = tile * 8 + w of the tiled layout), so a row tile (part) is 8 * RB
+// blocks, whose activation chunks are staged once in LDS for all of them.
+// Weights are double-buffered in registers by half chunk (1 KB per block):
+// the loads of the next half are issued as soon as a half has been
+// multiplied, so each wave keeps RB KB in flight. Each activation fragment is
+// read from LDS once per step and multiplied by all RB blocks. Passes of up
+// to 16 * NBMAX tokens.
+//
+// A workgroup carries TT consecutive row tiles of one expert. Under the last
+// chunk of a tile the first chunk of the next (its weights and activations,
+// into the same registers) is already in flight, so only the epilogue sits
+// between two tiles, and the routing and the first chunk's latency (about
+// 3-8 us per workgroup on MI355X at 128 experts x 512 tokens) are paid once.
+// Down takes TT = 2: 128 experts x 8 tiles become 512 workgroups, two per
+// CU, in one round instead of two (42 -> 35 us). Gate/up keeps TT = 1 (768
+// workgroups filling the CUs as slots free): with TT = 2 its 384 workgroups
+// leave half the CUs with two and half with one, and the CUs with two set the
+// time. TT = 1 compiles to the single-tile loop.
+template <int EPI, int W, int RB, int NBMAX, bool ROUTE, int TT>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void q4_grouped(Q4Tiled p, int parts,
                                                                                                 int blocks) {
     __shared__ __attribute__((aligned(16))) _Float16 xl[2][16 * NBMAX * kXStride];
@@ -325,21 +335,24 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
     constexpr int kPass = 16 * NBMAX;
 
     const int linear = blockIdx.x;
-    int expert, part;
-    if (p.experts % 8 == 0) {  // an expert's parts share one XCD (round-robin dispatch) and its L2
+    const int wgs = (parts + TT - 1) / TT;  // workgroups per expert
+    int expert, wg;
+    if (p.experts % 8 == 0) {  // an expert's workgroups share one XCD (round-robin dispatch) and its L2
         const int xcd = linear % 8, idx = linear / 8;
-        expert = 8 * (idx / parts) + xcd;
-        part = idx % parts;
+        expert = 8 * (idx / wgs) + xcd;
+        wg = idx % wgs;
     } else {
-        expert = linear / parts;
-        part = linear % parts;
+        expert = linear / wgs;
+        wg = linear % wgs;
     }
+    const int first_part = wg * TT;
+    const int tiles = min(TT, parts - first_part);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int seg_begin, seg_end;
     if constexpr (ROUTE) {
-        const int2 range = route_expert<W>(p, expert, part == 0, plist, rsum, tid, lane, wave);
+        const int2 range = route_expert<W>(p, expert, wg == 0, plist, rsum, tid, lane, wave);
         seg_begin = range.x;
         seg_end = range.y;
     } else {
@@ -349,14 +362,15 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
     if (seg_begin >= seg_end) return;
     const int q = lane >> 4, m = lane & 15;
     constexpr int T = W * 64;
-    const int b0 = (part * W + wave) * RB;  // this wave's first row block
-    // Per-block unit offsets (wave-uniform); clamped blocks are never stored.
-    std::int64_t unit[RB];
+    // Unit offset of block r of tile t for this wave (wave-uniform); clamped
+    // blocks are never stored.
+    auto unit = [&](int t, int r) {
+        const int b = min(((first_part + t) * W + wave) * RB + r, blocks - 1);
+        return static_cast<std::int64_t>(b >> 3) * p.chunks * 8 + (b & 7);
+    };
+    std::int64_t unit0[RB];  // a single-tile workgroup's, computed once
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-        const int b = min(b0 + r, blocks - 1);
-        unit[r] = static_cast<std::int64_t>(b >> 3) * p.chunks * 8 + (b & 7);
-    }
+    for (int r = 0; r < RB; ++r) unit0[r] = unit(0, r);
     const uint4* wbase = p.codes + expert * p.code_stride + lane;
     const __half* sbase = p.scales + expert * p.scale_stride + lane;
 
@@ -384,11 +398,11 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
             struct XStage {
                 uint4 v[XL];
             };
-            // Half h of chunk c for every block: 16 code bytes and the group scale.
-            auto load_half = [&](int c, int h, Half& st) {
+            // Half h of chunk c of tile t for every block: 16 code bytes and the group scale.
+            auto load_half = [&](int t, int c, int h, Half& st) {
 #pragma unroll
                 for (int r = 0; r < RB; ++r) {
-                    const std::int64_t u = unit[r] + static_cast<std::int64_t>(c) * 8;
+                    const std::int64_t u = (TT == 1 ? unit0[r] : unit(t, r)) + static_cast<std::int64_t>(c) * 8;
                     st.w[r] = stream_load(wbase + u * 128 + 64 * h);
                     if (h == 0) st.s[r] = stream_load(reinterpret_cast<const unsigned short*>(sbase + u * 64));
                 }
@@ -415,10 +429,6 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
             };
 
             float4v acc[RB][NB];
-#pragma unroll
-            for (int r = 0; r < RB; ++r)
-#pragma unroll
-                for (int b = 0; b < NB; ++b) acc[r][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
             // Multiplies half h of the current chunk (code words 4h .. 4h + 3 of
             // every block, activation columns 64q + 32h ..) from LDS buffer buf.
@@ -443,81 +453,126 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
             };
 
             Half h0, h1;
-            load_half(0, 0, h0);
-            load_half(0, 1, h1);
+            load_half(0, 0, 0, h0);
+            load_half(0, 0, 1, h1);
             XStage xs;
             load_x(0, xs);
             store_x(0, xs, xl[0]);
             __syncthreads();
-            for (int c = 0; c < p.chunks; ++c) {
-                const int next = min(c + 1, p.chunks - 1);  // the last chunk re-reads itself (unused)
-                load_x(next, xs);
-                const _Float16* buf = xl[c & 1];
+            for (int ti = 0; ti < tiles; ++ti) {
 #pragma unroll
-                for (int r = 0; r < RB; ++r) scale[r] = h0.s[r];
-                compute_half(h0, 0, buf);
-                load_half(next, 0, h0);
-                compute_half(h1, 1, buf);
-                load_half(next, 1, h1);
-                store_x(c + 1, xs, xl[(c + 1) & 1]);
-                __syncthreads();
-            }
+                for (int r = 0; r < RB; ++r)
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) acc[r][b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+                const bool more = ti + 1 < tiles;  // the next tile's first chunk follows this tile's last
+                if constexpr (TT == 1) {
+                    for (int c = 0; c < p.chunks; ++c) {
+                        const int next = min(c + 1, p.chunks - 1);  // the last chunk re-reads itself (unused)
+                        load_x(next, xs);
+                        const _Float16* buf = xl[c & 1];
+#pragma unroll
+                        for (int r = 0; r < RB; ++r) scale[r] = h0.s[r];
+                        compute_half(h0, 0, buf);
+                        load_half(0, next, 0, h0);
+                        compute_half(h1, 1, buf);
+                        load_half(0, next, 1, h1);
+                        store_x(c + 1, xs, xl[(c + 1) & 1]);
+                        __syncthreads();
+                    }
+                } else {
+                    for (int c = 0; c < p.chunks; ++c) {
+                        const bool last = c + 1 == p.chunks;
+                        // Next (tile, chunk): the following chunk, the next tile's first, or
+                        // past the last tile's last chunk a re-read of it (unused).
+                        const int nt = last && more ? ti + 1 : ti;
+                        const int nc = last ? (more ? 0 : c) : c + 1;
+                        load_x(nc, xs);
+                        const _Float16* buf = xl[c & 1];
+#pragma unroll
+                        for (int r = 0; r < RB; ++r) scale[r] = h0.s[r];
+                        compute_half(h0, 0, buf);
+                        load_half(nt, nc, 0, h0);
+                        compute_half(h1, 1, buf);
+                        load_half(nt, nc, 1, h1);
+                        if (!(last && more)) store_x(c + 1, xs, xl[(c + 1) & 1]);  // the next tile's chunk 0 waits for the epilogue
+                        __syncthreads();
+                    }
+                }
 
-            // Epilogue through LDS: the staging buffers are free after the last
-            // chunk's barrier. The pass's output tile (tokens x the workgroup's
-            // 16 W RB rows, or its 8 W RB SwiGLU columns) is written there from
-            // the D layout (lane holds row slot m of block b for tokens
-            // 16j + 4q + i), then every token row leaves as 16-byte stores: 2-byte
-            // stores straight from the D layout leave 32-byte pieces of lines
-            // that other workgroups also write (about 12 us of a 50 us launch at
-            // 128 experts x 512 tokens x top-8). Row stride: 8 halves past the
-            // tile width, so the four token quads of a store land on distinct
-            // banks.
-            constexpr int kOutCols = EPI == kSwiGLU ? W * RB * 8 : W * RB * 16;
-            constexpr int kOutStride = kOutCols + 8;
-            static_assert(16 * NBMAX * kOutStride <= 2 * 16 * NBMAX * kXStride, "the output tile fits the staging buffers");
-            static_assert(W * RB % 8 == 0, "a workgroup covers whole SwiGLU column tiles");
-            __half* tile = reinterpret_cast<__half*>(&xl[0][0]);
-            const int first = part * W * RB;  // the workgroup's first row block
+                // Epilogue through LDS: the staging buffers are free after the last
+                // chunk's barrier. The pass's output tile (tokens x the workgroup's
+                // 16 W RB rows, or its 8 W RB SwiGLU columns) is written there from
+                // the D layout (lane holds row slot m of block b for tokens
+                // 16j + 4q + i), then every token row leaves as 16-byte stores: 2-byte
+                // stores straight from the D layout leave 32-byte pieces of lines
+                // that other workgroups also write (about 12 us of a 50 us launch at
+                // 128 experts x 512 tokens x top-8). Row stride: 8 halves past the
+                // tile width, so the four token quads of a store land on distinct
+                // banks.
+                constexpr int kOutCols = EPI == kSwiGLU ? W * RB * 8 : W * RB * 16;
+                constexpr int kOutStride = kOutCols + 8;
+                static_assert(16 * NBMAX * kOutStride <= 2 * 16 * NBMAX * kXStride, "the output tile fits the staging buffers");
+                static_assert(W * RB % 8 == 0, "a workgroup covers whole SwiGLU column tiles");
+                __half* tile = reinterpret_cast<__half*>(&xl[0][0]);
+                const int first = (first_part + ti) * W * RB;  // the tile's first row block
 #pragma unroll
-            for (int r = 0; r < RB; ++r) {
-                const int slot_blk = b0 + r - first;
+                for (int r = 0; r < RB; ++r) {
+                    const int slot_blk = wave * RB + r;
 #pragma unroll
-                for (int b = 0; b < NB; ++b) {
+                    for (int b = 0; b < NB; ++b) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int t = 16 * b + 4 * q + i;
-                        const float v = acc[r][b][i];
-                        if (EPI == kSwiGLU) {
-                            const float other = __shfl_xor(v, 8, 64);  // lane m^8 holds the paired up/gate row
-                            if (m < 8) {
-                                const float g = __half2float(from_f32<__half>(v));
-                                const float u = __half2float(from_f32<__half>(other));
-                                const float a = __half2float(from_f32<__half>(silu(g)));
-                                tile[t * kOutStride + 8 * slot_blk + m] = from_f32<__half>(__fmul_rn(a, u));
+                        for (int i = 0; i < 4; ++i) {
+                            const int t = 16 * b + 4 * q + i;
+                            const float v = acc[r][b][i];
+                            if (EPI == kSwiGLU) {
+                                const float other = __shfl_xor(v, 8, 64);  // lane m^8 holds the paired up/gate row
+                                if (m < 8) {
+                                    const float g = __half2float(from_f32<__half>(v));
+                                    const float u = __half2float(from_f32<__half>(other));
+                                    const float a = __half2float(from_f32<__half>(silu(g)));
+                                    tile[t * kOutStride + 8 * slot_blk + m] = from_f32<__half>(__fmul_rn(a, u));
+                                }
+                            } else {
+                                tile[t * kOutStride + 16 * slot_blk + m] = from_f32<__half>(v);  // scaled when stored
                             }
-                        } else {
-                            float y = __half2float(from_f32<__half>(v));
-                            if (EPI == kScore) y = __fmul_rn(y, __half2float(p.score[pass + min(t, live - 1)]));
-                            tile[t * kOutStride + 16 * slot_blk + m] = from_f32<__half>(y);
                         }
                     }
                 }
-            }
-            __syncthreads();
-            // Rows t < live; columns of blocks past the last one, or past the
-            // matrix, are not stored (SwiGLU columns of block blk start at
-            // (blk >> 3) * 64 + 8 * (blk & 7); W * RB is a multiple of 8). The
-            // column limit is a multiple of 8 (hidden and intermediate sizes
-            // are), so a 16-byte unit is stored whole or not at all.
-            const int col0 = EPI == kSwiGLU ? (first >> 3) * (kRows / 2) : 16 * first;
-            const int limit = EPI == kSwiGLU ? p.half_rows : p.n;
-            constexpr int kUnits = kOutCols / 8;
-            for (int u = tid; u < live * kUnits; u += T) {
-                const int t = u / kUnits, c = 8 * (u % kUnits);
-                if (col0 + c < limit)
-                    *reinterpret_cast<uint4*>(p.out + static_cast<std::int64_t>(pass + t) * p.out_stride + col0 + c) =
-                        *reinterpret_cast<const uint4*>(tile + t * kOutStride + c);
+                __syncthreads();
+                // Rows t < live; columns of blocks past the last one, or past the
+                // matrix, are not stored (SwiGLU columns of block blk start at
+                // (blk >> 3) * 64 + 8 * (blk & 7); W * RB is a multiple of 8). The
+                // column limit is a multiple of 8 (hidden and intermediate sizes
+                // are), so a 16-byte unit is stored whole or not at all.
+                const int col0 = EPI == kSwiGLU ? (first >> 3) * (kRows / 2) : 16 * first;
+                const int limit = EPI == kSwiGLU ? p.half_rows : p.n;
+                constexpr int kUnits = kOutCols / 8;
+                for (int u = tid; u < live * kUnits; u += T) {
+                    const int row = u / kUnits, c = 8 * (u % kUnits);
+                    if (col0 + c < limit) {
+                        uint4 w = *reinterpret_cast<const uint4*>(tile + row * kOutStride + c);
+                        // fp16(fp16(y) * score), the product in fp32: applied here, one score per
+                        // stored row unit, rather than per D-layout value, where the next tile's
+                        // chunk is live in registers (twelve score loads per lane there spilled).
+                        if constexpr (EPI == kScore) {
+                            const float sc = __half2float(p.score[pass + row]);
+                            std::uint32_t* h = reinterpret_cast<std::uint32_t*>(&w);
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                const __half lo = from_f32<__half>(__fmul_rn(half_lo(h[j]), sc));
+                                const __half hi = from_f32<__half>(__fmul_rn(half_hi(h[j]), sc));
+                                h[j] = static_cast<std::uint32_t>(__half_as_ushort(lo)) |
+                                       (static_cast<std::uint32_t>(__half_as_ushort(hi)) << 16);
+                            }
+                        }
+                        *reinterpret_cast<uint4*>(p.out + static_cast<std::int64_t>(pass + row) * p.out_stride + col0 + c) = w;
+                    }
+                }
+                if (more) {  // the staging buffers again hold activations: the next tile's first chunk
+                    __syncthreads();
+                    store_x(0, xs, xl[0]);
+                    __syncthreads();
+                }
             }
         };
         switch ((live + 15) >> 4) {
@@ -713,11 +768,12 @@ void combine_dispatch(int top_k, const std::int64_t* ids, const int* pair_slot, 
     }
 }
 
-template <int EPI, int W, int RB, int NBMAX, bool ROUTE = false>
+template <int EPI, int W, int RB, int NBMAX, bool ROUTE, int TT>
 void launch_q4_grouped(const Q4Tiled& p, hipStream_t stream) {
     const int blocks = p.row_tiles * 8;
     const int parts = (blocks + W * RB - 1) / (W * RB);
-    q4_grouped<EPI, W, RB, NBMAX, ROUTE><<<dim3(p.experts * parts), W * 64, 0, stream>>>(p, parts, blocks);
+    const int wgs = (parts + TT - 1) / TT;
+    q4_grouped<EPI, W, RB, NBMAX, ROUTE, TT><<<dim3(p.experts * wgs), W * 64, 0, stream>>>(p, parts, blocks);
 }
 
 std::uint64_t align256(std::uint64_t v) { return (v + 255) / 256 * 256; }
@@ -1395,8 +1451,8 @@ void moe_q4_launch_cfg(const void* x, const std::int64_t* ids, const void* score
     gu.slot_score = slot_score;
     gu.pairs = pairs;
     gu.top_k = top_k;
-    if (route_inside) launch_q4_grouped<kSwiGLU, GW, GRB, NBMAX, true>(gu, stream);
-    else launch_q4_grouped<kSwiGLU, GW, GRB, NBMAX>(gu, stream);
+    if (route_inside) launch_q4_grouped<kSwiGLU, GW, GRB, NBMAX, true, 1>(gu, stream);
+    else launch_q4_grouped<kSwiGLU, GW, GRB, NBMAX, false, 1>(gu, stream);
 
     Q4Tiled dn{};
     dn.x = h;
@@ -1414,7 +1470,7 @@ void moe_q4_launch_cfg(const void* x, const std::int64_t* ids, const void* score
     dn.x_stride = inter;
     dn.out_stride = hidden;
     dn.experts = experts;
-    launch_q4_grouped<kScore, DW, DRB, NBMAX>(dn, stream);
+    launch_q4_grouped<kScore, DW, DRB, NBMAX, false, 2>(dn, stream);
 
     combine_dispatch(top_k, ids, pair_slot, v, static_cast<__half*>(out), tokens, hidden, stream);
 }
