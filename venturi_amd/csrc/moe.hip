@@ -325,7 +325,8 @@ __device__ int2 route_expert(const Q4Tiled& p, int expert, bool writer, unsigned
 // CU, in one round instead of two (42 -> 35 us). Gate/up keeps TT = 1 (768
 // workgroups filling the CUs as slots free): with TT = 2 its 384 workgroups
 // leave half the CUs with two and half with one, and the CUs with two set the
-// time. TT = 1 compiles to the single-tile loop.
+// time; 512 workgroups of which a share carry two tiles measured no faster
+// than one tile each (67.5 vs 67.3 us). TT = 1 compiles to the single-tile loop.
 template <int EPI, int W, int RB, int NBMAX, bool ROUTE, int TT>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void q4_grouped(Q4Tiled p, int parts,
                                                                                                 int blocks) {
@@ -352,7 +353,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int seg_begin, seg_end;
     if constexpr (ROUTE) {
-        const int2 range = route_expert<W>(p, expert, wg == 0, plist, rsum, tid, lane, wave);
+        const int2 range = route_expert<W>(p, expert, first_part == 0, plist, rsum, tid, lane, wave);
         seg_begin = range.x;
         seg_end = range.y;
     } else {
