@@ -147,6 +147,10 @@ def run_and_check(backend, device, geometry, tokens, seed, duplicates=False):
         (MoEGeometry(512, 8, 2, 200), 1),
         (MoEGeometry(384, 24, 8, 256), 300),
         (MoEGeometry(128, 8, 2, 1032), 40),  # down K of five 256-column chunks, the last one ragged
+        # Down's workgroups carry two 256-row tiles of one expert: three tiles leave the
+        # last workgroup one (with experts not a multiple of 8, and with three passes).
+        (MoEGeometry(640, 10, 3, 96), 70),
+        (MoEGeometry(768, 4, 4, 64), 100),
     ],
 )
 def test_moe_stages(backend, device, geometry, tokens):
