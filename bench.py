@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Q8 quantized-linear decode benchmark on one MI355X (gfx950).
 
-Workload: the Qwen-27B-class Q8 decode projection set at
+Workload (config 2): the Qwen-27B-class Q8 decode projection set at
 hidden 5120 -- fused QKV [7168 x 5120], o_proj [5120 x 6144], gate+up
 [34816 x 5120], down [5120 x 17408] -- with weights N(0, 0.02) packed to
 q8_g32_fp16 on the device and fp16 N(0, 1) activations, run at token counts
@@ -32,7 +32,7 @@ than 2e-3 off, rel-L2); `exact_route` times that canonical route on the same
 job; `cpu_baseline` times the reference's CPU path (torch FP32 GEMM over
 materialised weights) on a bounded sample of the same workload. Further
 sections of the same line carry their own roofline objects: `config1`
-(4096 x 4096 at one token, rotated copies), `vocab_head`
+(config 1, 4096 x 4096 at one token, rotated copies), `vocab_head`
 (the 248 320 x 5120 Q8 head held once in the tiled layout), `q4_decode`
 (the metric's Q4 leg), `q56_decode`, `codecs`, `a8_decode` (the A8 path at
 1 and 8 tokens, one and two passes), `prefill_a8` (config 3),
@@ -498,7 +498,7 @@ def cpu_baseline(copies, seconds):
 
 
 def config1(backend, device, steps, warmup, copy_mb):
-    """one q8_g32_fp16 [4096 x 4096] projection at one token.
+    """Config 1: one q8_g32_fp16 [4096 x 4096] projection at one token.
 
     Weights N(0, 0.02) (copy 0 from seed 0), x fp16 N(0, 1) from seed 1. The
     17.8 MB matrix fits the 256 MB Infinity Cache, so each graph rotates
@@ -533,7 +533,7 @@ def config1(backend, device, steps, warmup, copy_mb):
 
 
 def prefill_a8(backend, device, steps, warmup, cpu_seconds):
-    """RMSNorm + 1-pass A8 at hidden 5120, int8 GEMMs at the config-2 shapes, M = 2048.
+    """Config 3: RMSNorm + 1-pass A8 at hidden 5120, int8 GEMMs at the config-2 shapes, M = 2048.
 
     x fp16 [2048, 5120] ~ N(0, 1) with 51 seeded channels (1%) scaled by 20;
     gamma ~ N(1, 0.1); eps 1e-6. QKV and gate+up consume the fused RMS+A8
@@ -986,7 +986,7 @@ def moe_reference(x, ids, scores, dense_gu, dense_dn):
 
 
 def moe_w4a16(backend, device, steps, warmup, cpu_seconds):
-    """routed-expert Q4 W4A16 MoE, 128 experts, H 2048, I 768, 512 tokens top-8.
+    """Config 4: routed-expert Q4 W4A16 MoE, 128 experts, H 2048, I 768, 512 tokens top-8.
 
     Expert weights N(0, 0.02) packed on the device with quantize_q4_rtn
     arithmetic; x fp16 N(0, 1); per token 8 distinct ids from a seeded
@@ -1134,7 +1134,7 @@ def vocab_head(backend, device, steps, warmup, tokens_list=(1, 4, 16)):
 
 
 def model_decode(backend, device, steps, warmup, batches=(1, 8, 32)):
-    """64 decoder layers x the config-2 projections, all resident (256 Q8 matrices).
+    """Config 5: 64 decoder layers x the config-2 projections, all resident (256 Q8 matrices).
 
     One step chains, per layer: h -> QKV; a seeded fp16 [B, 6144] -> o_proj;
     h -> gate+up fused with SiLU*up (the native runtime's SwiGLU arithmetic

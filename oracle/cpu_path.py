@@ -1,6 +1,6 @@
 """The reference's CPU execution path, restated for the bench's cpu_baseline leg.
 
-TEST/BASELINE INFRASTRUCTURE ONLY (never imported by venturi_amd).
+TEST AND CPU-BASELINE-LEG INFRASTRUCTURE ONLY (never imported by venturi_amd).
 
 Restates TorchBackend.upload_linear + _TorchQuantizedLinear.run
 (ops/blocks.py:891-931, 1020-1063): Q8/Q4 weights are materialised once as

@@ -147,7 +147,7 @@ def test_matrix_core_projection_bytes(backend, device, passes, tokens, shape):
 
 @pytest.mark.parametrize("n,k", [(7168, 5120), (5120, 6144), (34816, 5120), (5120, 17408)])
 def test_config3_prefill_sampled(backend, device, n, k):
-    # BASELINE config 3 shapes at 2048 tokens; the oracle checks a seeded sample
+    # Config-3 shapes at 2048 tokens; the oracle checks a seeded sample
     # of 64 tokens x 128 rows (every output's order is independent of the others).
     tokens = 2048
     gen = torch.Generator(device=device).manual_seed(n ^ k)

@@ -34,7 +34,7 @@ def test_exact_bytes_tails_and_guards(backend, device, dtype, shape, tokens):
 
 
 def test_config1_decode_bitexact(backend, device):
-    # W ~ N(0, 0.02) [4096, 4096] seed 0, x ~ N(0, 1) [1, 4096].
+    # Config 1: W ~ N(0, 0.02) [4096, 4096] seed 0, x ~ N(0, 1) [1, 4096].
     w = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(0)) * 0.02
     weight = Q8RowSplitWeight.from_dense(w.half())
     x = torch.randn(1, 4096, generator=torch.Generator().manual_seed(1)).half()
