@@ -202,3 +202,34 @@ def test_moe_invalid_ids_give_nan_rows(backend, device):
     assert np.array_equal(bits(sub_out), bits(rows[valid]))
     with pytest.raises(ValueError, match="real expert ids"):
         routed_experts(x.to(device), ids.to(device), scores.to(device), bank)
+
+
+@pytest.mark.parametrize("geometry,tokens", [(MoEGeometry(512, 16, 4, 256), 64), (MoEGeometry(64, 16, 8, 32), 1100)])
+def test_moe_graph_replays(backend, device, geometry, tokens):
+    """One plan.run captured in a HIP graph: each replay, on new inputs copied into the captured
+    buffers with eager work and synchronisations between, equals an eager run bit for bit
+    (in-launch routing at 256 pairs; the separate routing launch at 8800 pairs)."""
+    print(f"case moe graph E={geometry.num_experts} H={geometry.hidden_size} T={tokens}", flush=True)
+    bank, _, _ = build(backend, device, geometry, 5)
+    plan = bank.prepare(tokens=tokens)
+    x, ids, scores = (t.to(device) for t in routing(tokens, geometry, 6))
+    out = torch.empty((tokens, geometry.hidden_size), dtype=torch.float16, device=device)
+    workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)
+    plan.run(x, ids, scores, out=out, workspace=workspace)  # warm-up outside capture
+    torch.cuda.synchronize(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run(x, ids, scores, out=out, workspace=workspace)
+    eager = torch.empty_like(out)
+    eager_ws = torch.empty_like(workspace)
+    for replay in range(3):
+        nx, nids, nscores = routing(tokens, geometry, 100 + replay)
+        x.copy_(nx.to(device))
+        ids.copy_(nids.to(device))
+        scores.copy_(nscores.to(device))
+        out.fill_(7)
+        plan.run(x, ids, scores, out=eager, workspace=eager_ws)  # eager work between replays
+        torch.cuda.synchronize(device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        assert np.array_equal(bits(out), bits(eager)), replay
