@@ -11,30 +11,37 @@ from venturi_amd.q4 import decode_q4_fp16, quantize_q4_rtn
 
 @pytest.mark.parametrize("k", [1, 31, 32, 65, 128, 129])
 def test_q8_nearest_even_stored_scale_and_padding(k):
-    # Reference test_q8_weights.py:82-116: scalar per-element oracle.
-    source = torch.randn(11, k, generator=torch.Generator().manual_seed(38), dtype=torch.bfloat16) * 0.01
-    source[0].zero_()
-    saved = source.clone()
-    a = Q8RowSplitWeight.from_dense(source, rows_per_chunk=3)
-    b = Q8RowSplitWeight.from_dense(source, rows_per_chunk=11)
-    assert torch.equal(a.codes, b.codes) and torch.equal(a.scales, b.scales)
-    assert torch.equal(source, saved)
-    assert a.format == "q8_g32_fp16" and a.group_size == 32
-    assert a.nbytes == a.codes.numel() + 2 * a.scales.numel()
-    assert not bool((a.codes == -128).any())
-    assert torch.count_nonzero(a.codes[:, k:]) == 0
-    assert torch.count_nonzero(a.scales[0]) == 0
-    for row in range(11):
-        for begin in range(0, k, 32):
-            group = source[row, begin : begin + 32].float()
-            stored = torch.tensor(float(group.abs().max()) / 127, dtype=torch.float16).item()
-            for col, value in enumerate(group.tolist(), begin):
-                code = 0 if stored == 0 else max(-127, min(127, round(value / stored)))
-                assert a.codes[row, col].item() == code
-    exact = a.dequantize_reference()
-    error = (source.double() - exact).abs()
-    scale = a.scales.double().repeat_interleave(32, -1)[:, :k]
-    assert bool((error <= scale * 0.501 + 1e-12).all())
+    """The reference's known-answer input for the Q8 packer (tests/test_q8_weights.py:18-52:
+    11 bf16 rows of N(0, 1) * 0.01 from seed 38, row 0 all zero, row chunks of 3 and of 11),
+    checked against the format's definition computed here in float32 / float16 with numpy:
+    s = fp16(max|x| / 127) per 32-column group of the zero-padded row, q = rint(x / s) clamped
+    to [-127, 127], or 0 where s == 0."""
+    src = torch.randn(11, k, generator=torch.Generator().manual_seed(38), dtype=torch.bfloat16) * 0.01
+    src[0].zero_()
+    before = src.clone()
+    chunked = {c: Q8RowSplitWeight.from_dense(src, rows_per_chunk=c) for c in (3, 11)}
+    assert torch.equal(src, before), "the packer must not modify its source"
+    w = chunked[3]
+    assert torch.equal(chunked[11].codes, w.codes) and torch.equal(chunked[11].scales, w.scales)
+    assert (w.format, w.group_size) == ("q8_g32_fp16", 32)
+    assert w.nbytes == w.codes.numel() + 2 * w.scales.numel()
+
+    padded = w.codes.shape[1]
+    rows = np.zeros((11, padded), dtype=np.float32)
+    rows[:, :k] = src.float().numpy()
+    groups = rows.reshape(11, padded // 32, 32)
+    s16 = (np.abs(groups).max(axis=2) / np.float32(127)).astype(np.float16)
+    s32 = s16.astype(np.float32)[:, :, None]
+    safe = np.where(s32 > 0, s32, np.float32(1))
+    q = np.where(s32 > 0, np.clip(np.rint(groups / safe), -127, 127), 0).astype(np.int8)
+    assert np.array_equal(w.scales.numpy().view(np.uint16), s16.view(np.uint16))
+    assert np.array_equal(w.codes.numpy(), q.reshape(11, padded))
+    assert int(w.codes.numpy().min()) > -128 and not w.scales[0].any()  # no -128 code; a zero row keeps zero scales
+    assert not w.codes[:, k:].any()  # padding columns hold zero codes
+    # Reconstruction lies within half a quantization step (plus rounding slack).
+    step = np.repeat(s16.astype(np.float64), 32, axis=1)[:, :k]
+    err = np.abs(src.double().numpy() - w.dequantize_reference().numpy())
+    assert (err <= 0.501 * step + 1e-12).all()
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32, torch.float64])
@@ -80,22 +87,21 @@ def test_q8_descriptor_guards(bad):
 
 @pytest.mark.parametrize("k", [1, 63, 64, 65, 127, 128, 129, 4097])
 def test_q4_pack_signed_codes_and_tail(k):
-    # Reference test_q4_weights.py:10-26 scalar storage oracle.
+    """The reference's storage case (tests/test_q4_weights.py:10-26: codes cycling through all 16
+    signed values, group scales (i % 7 + 1) / 8) unpacked here from the layout's definition: column
+    2j in the low nibble of byte j, two's complement, rows padded to a multiple of 128 columns."""
     values = (torch.arange(3 * k).reshape(3, k) % 16 - 8).to(torch.int8)
     scales = (torch.arange(3 * ((k + 63) // 64)).reshape(3, -1) % 7 + 1).to(torch.float16) / 8
     weight = Q4RowSplitWeight.from_codes(values, scales)
-    expected = torch.empty((3, k), dtype=torch.float64)
-    for row in range(3):
-        for col in range(k):
-            byte = int(weight.codes[row, col // 2])
-            nibble = (byte // (16 if col % 2 else 1)) % 16
-            integer = nibble if nibble <= 7 else nibble - 16
-            assert integer == int(values[row, col])
-            expected[row, col] = integer * float(scales[row, col // 64])
-    torch.testing.assert_close(weight.dequantize_reference(), expected, rtol=0, atol=0)
-    assert weight.codes.shape == (3, ((k + 127) // 128) * 64)
+    assert tuple(weight.codes.shape) == (3, ((k + 127) // 128) * 64)
+    raw = weight.codes.numpy()
+    nibbles = np.stack((raw & 15, raw >> 4), axis=2).reshape(3, -1)[:, :k].astype(np.int16)
+    signed = np.where(nibbles > 7, nibbles - 16, nibbles)
+    assert np.array_equal(signed, values.numpy())
+    expected = signed * np.repeat(scales.numpy().astype(np.float64), 64, axis=1)[:, :k]
+    assert np.array_equal(weight.dequantize_reference().numpy(), expected)
     packed, plane = oracle.q4_pack_codes(values.numpy(), scales.numpy())
-    assert np.array_equal(weight.codes.numpy(), packed) and np.array_equal(weight.scales.numpy(), plane)
+    assert np.array_equal(raw, packed) and np.array_equal(weight.scales.numpy(), plane)
 
 
 def test_q4_known_bytes_and_group_scales():
@@ -109,15 +115,19 @@ def test_q4_known_bytes_and_group_scales():
 
 
 def test_q4_payload_alignment_and_shared_views():
-    # Reference test_q4_weights.py:47-60.
-    payload = torch.zeros(260, dtype=torch.uint8)
-    payload[0] = 0xF8
-    payload[256:].view(torch.float16).copy_(torch.tensor([0.5, 2], dtype=torch.float16))
+    """One row of 65 columns as a payload (the reference's case, tests/test_q4_weights.py:47-60):
+    64 code bytes (65 columns padded to 128) then zeros up to byte 256, then the fp16 scales; the
+    descriptor views the payload in place, and any other byte count is refused."""
+    codes_plane = np.zeros(256, dtype=np.uint8)
+    codes_plane[0] = 0xF8  # column 0: -8, column 1: -1
+    scale_plane = np.array([0.5, 2.0], dtype=np.float16).view(np.uint8)
+    payload = torch.from_numpy(np.concatenate((codes_plane, scale_plane)))
     weight = Q4RowSplitWeight.from_payload(payload, out_features=1, in_features=65)
-    assert weight.codes.data_ptr() == payload.data_ptr()
-    assert weight.scales.data_ptr() == payload.data_ptr() + 256
-    assert weight.dequantize_reference()[0, :2].tolist() == [-4, -0.5]
-    for wrong in [payload[:-1], torch.cat((payload, torch.zeros(1, dtype=torch.uint8)))]:
+    base = payload.data_ptr()
+    assert (weight.codes.data_ptr() - base, weight.scales.data_ptr() - base) == (0, 256)
+    assert weight.dequantize_reference()[0, :2].tolist() == [-4.0, -0.5]
+    for size in (payload.numel() - 1, payload.numel() + 1):
+        wrong = torch.zeros(size, dtype=torch.uint8)
         with pytest.raises(ValueError, match="byte count"):
             Q4RowSplitWeight.from_payload(wrong, out_features=1, in_features=65)
 
