@@ -54,31 +54,41 @@ def test_hip_capabilities_match_format_and_layout_exactly():
                      weight_layout="row_split_k128_v1")
 
 
-def test_capability_definitions_are_copied_and_validated():
+def test_operator_support_snapshots_its_sets():
+    """A capability record keeps what it was given at construction: later changes to the caller's
+    device and dtype sets do not reach it (reference contract, tests/test_backend_contract.py)."""
     devices, dtypes = {"cpu"}, {torch.float32}
     op = OperatorSupport("linear", devices, dtypes, "dense")
-    devices.add("mps")
-    dtypes.add(torch.float64)
     caps = BackendCapabilities("third-party", [op])
+    devices |= {"mps"}
+    dtypes |= {torch.float64}
+    assert (op.device_types, op.dtypes) == (frozenset({"cpu"}), frozenset({torch.float32}))
     assert caps.operators == (op,)
-    assert op.device_types == frozenset({"cpu"}) and op.dtypes == frozenset({torch.float32})
     assert caps.supports("linear", dtype=torch.float32, device="cpu")
     assert not caps.supports("linear", dtype=torch.float32, device="mps")
-    with pytest.raises(ValueError, match="requires an explicit format"):
-        OperatorSupport("linear", {"cpu"}, {torch.float32}, weight_layout="unknown")
-    with pytest.raises(TypeError, match="torch.dtype"):
-        OperatorSupport("linear", {"cpu"}, {"float32"})
-    with pytest.raises(ValueError, match="operation, devices and dtypes"):
-        OperatorSupport("", {"cpu"}, {torch.float32})
-    with pytest.raises(ValueError, match="nonempty strings"):
-        OperatorSupport("linear", {""}, {torch.float32})
-    with pytest.raises(ValueError, match="nonempty strings"):
-        OperatorSupport("linear", {"cpu"}, {torch.float32}, "")
-    with pytest.raises(TypeError, match="must be bool"):
-        OperatorSupport("linear", {"cpu"}, {torch.float32}, materializes_weights=1)
-    with pytest.raises(ValueError, match="typed operators"):
-        BackendCapabilities("x", ["linear"])
-    with pytest.raises(TypeError, match="must be bool"):
-        BackendCapabilities("x", [op], reference=1)
+    assert not caps.supports("linear", dtype=torch.float64, device="cpu")
+
+
+@pytest.mark.parametrize(
+    "build,error,text",
+    [
+        (lambda: OperatorSupport("linear", {"cpu"}, {torch.float32}, weight_layout="unknown"), ValueError,
+         "requires an explicit format"),
+        (lambda: OperatorSupport("linear", {"cpu"}, {"float32"}), TypeError, "torch.dtype"),
+        (lambda: OperatorSupport("", {"cpu"}, {torch.float32}), ValueError, "operation, devices and dtypes"),
+        (lambda: OperatorSupport("linear", {""}, {torch.float32}), ValueError, "nonempty strings"),
+        (lambda: OperatorSupport("linear", {"cpu"}, {torch.float32}, ""), ValueError, "nonempty strings"),
+        (lambda: OperatorSupport("linear", {"cpu"}, {torch.float32}, materializes_weights=1), TypeError, "must be bool"),
+        (lambda: BackendCapabilities("x", ["linear"]), ValueError, "typed operators"),
+        (lambda: BackendCapabilities("x", [OperatorSupport("linear", {"cpu"}, {torch.float32})], reference=1),
+         TypeError, "must be bool"),
+    ],
+)
+def test_capability_records_reject_malformed_definitions(build, error, text):
+    with pytest.raises(error, match=text):
+        build()
+
+
+def test_backend_protocol_is_abstract():
     with pytest.raises(TypeError):
         Backend()

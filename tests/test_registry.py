@@ -45,21 +45,23 @@ def test_byte_counts_at_baseline_shapes():
 
 @pytest.mark.parametrize("fmt,bits", [("q4_g64_fp16", 4), ("q5_g64_fp16", 5), ("q6_g64_fp16", 6)])
 def test_all_signed_codes_and_high_bit_positions(fmt, bits):
-    # Known-answer pattern of the reference (test_codec_loading.py:88-113).
-    values = [(i % (1 << bits)) - (1 << (bits - 1)) for i in range(128)]
-    codes = torch.zeros((1, 64), dtype=torch.uint8)
-    high = torch.zeros((1, 16 * (bits - 4)), dtype=torch.uint8) if bits > 4 else None
-    for group in range(2):
-        for lane in range(64):
-            unsigned = values[group * 64 + lane] % (1 << bits)
-            codes[0, group * 32 + lane // 2] |= (unsigned & 15) << (4 * (lane % 2))
-            if high is not None:
-                hb = bits - 4
-                high[0, group * 8 * hb + lane * hb // 8] |= (unsigned >> 4) << (lane * hb % 8)
+    """Every signed code of the width, in column order over two 64-column groups (the reference's
+    known-answer pattern, tests/test_codec_loading.py:88-113), written into planes built here from
+    the layout: low nibbles two per byte, column 2j first; the bits above them as one
+    little-endian bit stream of `bits - 4` bits per column; then decoded over 117 columns."""
+    values = np.array([(i % (1 << bits)) - (1 << (bits - 1)) for i in range(128)], dtype=np.int64)
+    unsigned = values & ((1 << bits) - 1)
+    low = (unsigned & 15).reshape(-1, 2)
+    codes = torch.from_numpy((low[:, 0] | (low[:, 1] << 4)).astype(np.uint8)[None, :])
+    high = None
+    if bits > 4:
+        hb = bits - 4
+        stream = ((unsigned[:, None] >> (4 + np.arange(hb))) & 1).reshape(-1)  # bit b of column c at c * hb + b
+        high = torch.from_numpy(np.packbits(stream.astype(np.uint8), bitorder="little")[None, :])
     scales = torch.tensor([[0.125, 0.25]], dtype=torch.float16)
     actual = dequantize_planes(codes, scales, high, (1, 117), fmt)
-    expected = torch.tensor([[v * (0.125 if i < 64 else 0.25) for i, v in enumerate(values[:117])]], dtype=torch.float16)
-    assert torch.equal(actual, expected)
+    group_scale = np.where(np.arange(117) < 64, 0.125, 0.25)
+    assert np.array_equal(actual.numpy().astype(np.float64), (values[:117] * group_scale)[None, :])
 
 
 def test_dequantize_rejects_invalid_planes():
