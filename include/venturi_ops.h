@@ -158,8 +158,10 @@ int venturi_q8_prefill_run(const void* x, const int8_t* codes, const void* scale
 
 /* Extension: workspace of the tiled projections below for (tokens, n, swiglu):
  * the exchange slots of launches that split K over two workgroups, or 0 when
- * the launch for this shape does not split. 0 with a message on invalid
- * arguments (tokens outside 1..32, n <= 0, odd n with swiglu). */
+ * no launch for (tokens, n) splits. The size does not depend on K: at one
+ * token, 4097-6144 rows reserve slots that only rows of more than 8064
+ * columns use. 0 with a message on invalid arguments (tokens outside 1..32,
+ * n <= 0, odd n with swiglu). */
 size_t venturi_q8_tiled_workspace_bytes(int tokens, int n, int swiglu);
 
 /* Extension: puts a workspace of the tiled projections in its idle state (every

@@ -66,7 +66,14 @@ def test_tiled_split_workspace_sizes(lib):
     def slots(tokens, blocks):
         return tokens * blocks * 64
 
-    assert lib.venturi_q8_tiled_workspace_bytes(1, 5120, 0) == 0  # one token: unsplit
+    # One token: 257-384 blocks reserve slots for long rows (107 x 2 workgroups
+    # where K has at least 128 chunks); fewer or more blocks stay unsplit.
+    assert lib.venturi_q8_tiled_workspace_bytes(1, 5120, 0) == slots(1, 320)
+    assert lib.venturi_q8_tiled_workspace_bytes(1, 4096, 0) == 0  # 256 blocks: one per workgroup
+    assert lib.venturi_q8_tiled_workspace_bytes(1, 4097, 0) == slots(1, 257)
+    assert lib.venturi_q8_tiled_workspace_bytes(1, 6144, 0) == slots(1, 384)
+    assert lib.venturi_q8_tiled_workspace_bytes(1, 6160, 0) == 0  # 385 blocks: 129 x 2 would pass 256
+    assert lib.venturi_q8_tiled_workspace_bytes(1, 7168, 0) == 0
     assert lib.venturi_q8_tiled_workspace_bytes(4, 5120, 0) == slots(4, 320)  # 107 x 2 workgroups
     assert lib.venturi_q8_tiled_workspace_bytes(4, 7168, 0) == 0  # 224 unsplit workgroups
     assert lib.venturi_q8_tiled_workspace_bytes(32, 7168, 0) == slots(32, 448)  # 112 x 2 above 16 tokens

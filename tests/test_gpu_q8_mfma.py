@@ -133,13 +133,14 @@ def test_mfma_route_admission(backend, device):
     assert bf.prepare(tokens=8).route == "venturi-q8-exact"
 
 
-@pytest.mark.parametrize("shape", [(16, 64), (34, 136), (200, 1000), (16400, 136), (18, 16392)])
+@pytest.mark.parametrize("shape", [(16, 64), (34, 136), (200, 1000), (16400, 136), (18, 16392), (5000, 8200)])
 @pytest.mark.parametrize("tokens", [1, 3, 4, 8, 13, 16, 32])
 def test_fused_swiglu_equals_projection_then_silu_mul(backend, device, shape, tokens):
     # The fused epilogue must give the bytes of the mfma projection followed by
     # venturi_silu_mul_run (every row's dot is computed by the same MFMA sequence
     # in both tilings). Shapes cover an odd intermediate size (17), >= 1024 paired
-    # blocks and K >= 16384 (the staged-activation kernels).
+    # blocks, K >= 16384 (the staged-activation kernels) and 313 blocks of 130
+    # chunks (K split over two workgroups, at one token too).
     n, k = shape
     print(f"case q8-swiglu n={n} k={k} tokens={tokens}", flush=True)
     codes, scales = random_q8(n, k, 311 + n + tokens)
@@ -175,7 +176,8 @@ def test_fused_swiglu_admission(backend, device):
 SLOT_IDLE = 0x7F8000017F800001
 
 
-@pytest.mark.parametrize("n,k,tokens", [(5120, 6144, 4), (7168, 5120, 32), (200, 1000, 13), (16, 64, 2), (100, 200, 24)])
+@pytest.mark.parametrize("n,k,tokens", [(5120, 6144, 4), (7168, 5120, 32), (200, 1000, 13), (16, 64, 2), (100, 200, 24),
+                                          (5120, 17408, 1), (4200, 8192, 1), (4100, 8200, 1)])
 def test_split_k_deterministic_idle_slots_and_graph_replays(backend, device, n, k, tokens):
     # Shapes whose launch splits K over two workgroups that exchange halves
     # through the plan's slots. Two runs give the same bytes, every slot is idle
@@ -196,7 +198,7 @@ def test_split_k_deterministic_idle_slots_and_graph_replays(backend, device, n, 
     torch.cuda.synchronize(device)
     assert torch.equal(first.view(torch.int16), second.view(torch.int16))
     assert bool((slots.view(torch.int64) == SLOT_IDLE).all())
-    if n * k <= 200 * 1000:
+    if n * k <= 40_000_000:
         check(first, x, codes.numpy(), scales.numpy(), k)
     replayed = torch.full_like(first, 3.0)
     graph = torch.cuda.CUDAGraph()

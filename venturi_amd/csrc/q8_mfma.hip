@@ -616,7 +616,10 @@ void launch_tiled(const __half* x, const uint4* codes, const std::uint32_t* scal
 // chunks per batch) up to 256 blocks, over two row blocks below 1024 blocks,
 // else 8 waves over three (one chunk per batch: with two, the two batches in
 // flight hold 12 KB per wave and gate+up at one token measured 32.0 against
-// 29.9 us). More tokens: register fragments, 8
+// 29.9 us). Long rows (at least 128 chunks) of 257-384 blocks split K instead:
+// 8 waves over three blocks and half the chunks, the halves exchanged through
+// slots, so 2 * ceil(blocks / 3) workgroups (down, 320 blocks x 272 chunks:
+// 214 instead of 160; 19.9 -> 18.7 us). More tokens: register fragments, 8
 // waves, one batch of chunks in flight behind the current one, and the
 // (row blocks, K halves) shape of the candidates below whose grid is largest
 // without passing 256 workgroups; ties go to the unsplit shape up to 16 tokens
@@ -627,12 +630,21 @@ struct TiledShape {
     int rb, ks;
 };
 
-TiledShape tiled_shape(int tokens, int blocks) {
+// Chunk count that admits every split (slot buffers are sized with it, as
+// the workspace query does not take K).
+constexpr int kAnyChunks = 1 << 30;
+
+TiledShape tiled_shape(int tokens, int blocks, int chunks) {
     // One token: up to 256 row blocks take one block per workgroup (every wave
     // issuing four chunks per batch, two where a wave has at most four),
     // which fills the chip where two blocks per workgroup would leave half of
     // it idle (config 1: 7.3 -> 6.2 us; two-chunk batches 6.3 -> 5.5 us).
-    if (tokens == 1) return blocks <= 256 ? TiledShape{true, 1, 1} : blocks < 1024 ? TiledShape{true, 2, 1} : TiledShape{true, 3, 1};
+    if (tokens == 1) {
+        if (blocks <= 256) return TiledShape{true, 1, 1};
+        if (blocks < 1024)
+            return (blocks + 2) / 3 * 2 <= 256 && chunks >= 128 ? TiledShape{true, 3, 2} : TiledShape{true, 2, 1};
+        return TiledShape{true, 3, 1};
+    }
     const TiledShape candidates[] = {{false, 2, 1}, {false, 3, 1}, {false, 3, 2}, {false, 4, 2}};
     TiledShape best{false, 3, 1};
     long best_grid = 0;
@@ -649,7 +661,7 @@ TiledShape tiled_shape(int tokens, int blocks) {
 }
 
 std::size_t tiled_slot_bytes(int tokens, int blocks) {
-    return tiled_shape(tokens, blocks).ks > 1 ? static_cast<std::size_t>(tokens) * blocks * 8 * sizeof(unsigned long long)
+    return tiled_shape(tokens, blocks, kAnyChunks).ks > 1 ? static_cast<std::size_t>(tokens) * blocks * 8 * sizeof(unsigned long long)
                                              : 0;
 }
 
@@ -677,13 +689,15 @@ void launch_tiled_shape(const TiledShape& sh, const __half* xp, const uint4* cp,
 template <bool SWIGLU>
 void tiled_dispatch(const __half* xp, const uint4* cp, const std::uint32_t* sp, __half* op, unsigned long long* slots,
                     int tokens, int n, int k, int chunks, int blocks, hipStream_t stream) {
-    const TiledShape sh = tiled_shape(tokens, blocks);
+    const TiledShape sh = tiled_shape(tokens, blocks, chunks);
     if (sh.lds && sh.rb == 1 && chunks <= 64)  // at most four chunks a wave: two batches of two (config 1: 6.3 -> 5.5 us)
         launch_tiled_lds<16, 1, 2, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else if (sh.lds && sh.rb == 1)
         launch_tiled_lds<16, 1, 4, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else if (sh.lds && sh.rb == 2)
         launch_tiled_lds<16, 2, 1, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
+    else if (sh.lds && sh.ks == 2)
+        launch_tiled_lds<8, 3, 1, 1, 2, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else if (sh.lds)
         launch_tiled_lds<8, 3, 1, 1, 1, SWIGLU>(xp, cp, sp, op, slots, tokens, n, k, chunks, blocks, stream);
     else if (tokens <= 16)
