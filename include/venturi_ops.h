@@ -291,8 +291,11 @@ int venturi_q4_tiled_run(const void* x, const void* codes, const void* scales, v
 
 /* Extension: venturi_q4_tiled_run for 4-, 5- and 6-bit row codecs: bits 4 reads
  * the copy described above; bits 5/6 read q5.tile_row_codec's copy (codes tiled
- * as for Q4 but with the row-major nibbles, high plane [ceil(n/16)][padded/128]
- * [64 lanes][4*(bits-4) bytes], scales as for Q4; high 4-byte aligned). Same
+ * as for Q4 with the nibbles unbiased; high plane [ceil(n/16)][padded/128][64
+ * lanes][bits-4 32-bit registers], each column's upper bits with the sign bit
+ * flipped, the pair (c+2m, c+2m+1) of the lane's word j at bits (bits-4)*jj +
+ * (0, 8, 4, 12)[m] and 16 above in register j / (4/(bits-4)), jj = j mod
+ * 4/(bits-4); scales as for Q4; high 4-byte aligned). Same
  * slot buffer rule; unsplit shapes give the bits of venturi_row_gemm_run on the
  * row-major planes. No counterpart in the reference; for callers that decode
  * q5/q6 rows from a resident tiled copy. */

@@ -27,7 +27,6 @@ import pytest
 import torch
 
 from venturi_amd.q4 import tile_q4
-from venturi_amd.q5 import tile_row_codec
 
 
 @pytest.mark.parametrize("n,row_bytes", [(1, 64), (16, 128), (37, 192), (130, 1024)])
@@ -66,32 +65,3 @@ def test_biased_nibble_values():
     # columns: c0 = 0, c1 = 7, c2 = -8, c3 = -1, c4..c7 = 0 -> nibbles [c0, c2, c4, c6, c1, c3, c5, c7] + 8
     # = [8, 0, 8, 8, 15, 7, 8, 8], two per byte, low nibble first
     assert list(word) == [0x08, 0x88, 0x7F, 0x88]
-
-
-@pytest.mark.parametrize("bits", [5, 6])
-@pytest.mark.parametrize("n,row_bytes", [(1, 64), (37, 192)])
-def test_tile_row_codec_layout(bits, n, row_bytes):
-    # Q5/Q6 copy: codes as the row-major bytes (no re-packing); high-plane lane
-    # (r, q) of chunk c = the row's 4 * hb stream bytes at 16 * hb * c + 4 * hb * q.
-    hb = bits - 4
-    rng = np.random.default_rng(7 * n + bits)
-    codes = rng.integers(0, 256, size=(n, row_bytes), dtype=np.uint8)
-    high = rng.integers(0, 256, size=(n, row_bytes * hb // 4), dtype=np.uint8)
-    scales = rng.random((n, row_bytes // 32)).astype(np.float16)
-    tc, th, ts = tile_row_codec(torch.from_numpy(codes), torch.from_numpy(high), torch.from_numpy(scales), bits)
-    blocks, chunks = (n + 15) // 16, row_bytes // 64
-    tc, th, ts = tc.numpy(), th.numpy(), ts.numpy()
-    for b in range(blocks):
-        for c in range(chunks):
-            for q in range(4):
-                for r in range(16):
-                    row = 16 * b + r
-                    if row < n:
-                        assert np.array_equal(tc[b, c, q, r], codes[row, 64 * c + 16 * q: 64 * c + 16 * q + 16])
-                        lo = 16 * hb * c + 4 * hb * q
-                        assert np.array_equal(th[b, c, q, r], high[row, lo: lo + 4 * hb])
-                    else:
-                        assert not tc[b, c, q, r].any() and not th[b, c, q, r].any()
-            for r in range(16):
-                if 16 * b + r < n:
-                    assert np.array_equal(ts[b, c, r], scales[16 * b + r, 2 * c: 2 * c + 2])

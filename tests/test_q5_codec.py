@@ -221,3 +221,50 @@ def test_q5_linear_fp64_bound():
     mag = np.abs(x.double().numpy()) @ np.abs(wd.astype(np.float64)).T
     ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(exact), 2.0**-14))) - 10)
     assert (np.abs(y - exact) <= 0.5 * ulp + k * 2.0**-24 * mag).all()
+
+
+@pytest.mark.parametrize("bits", [5, 6])
+@pytest.mark.parametrize("n", [1, 37])
+def test_tiled_copy_layout(bits, n):
+    # q5.tile_row_codec's decode copy read back by its documented layout, one
+    # weight at a time: nibble j of a word is column c + 2j, nibble 4 + j column
+    # c + 2j + 1; the pair (c + 2m, c + 2m + 1) of word jj of high register i
+    # sits at bits hb * jj + (0, 8, 4, 12)[m] and 16 above, biased by
+    # 2^(bits - 1). Every code of the range, rows past n zero.
+    from venturi_amd.q5 import tile_row_codec
+
+    hb = bits - 4
+    k, padded = 264, 384
+    rng = np.random.default_rng(bits + n)
+    codes = rng.integers(-(1 << (bits - 1)), 1 << (bits - 1), size=(n, padded))
+    codes[0, :64] = np.arange(-(1 << (bits - 1)), 1 << (bits - 1)).repeat(64 >> (bits - 1))[:64]
+    codes[:, k:] = 0
+    scales = (rng.random((n, padded // 64)) * 0.02).astype(np.float16)
+    packed, high, sc = oracle.pack_row_codec(codes, scales, bits)
+    tc, th, ts = tile_row_codec(torch.from_numpy(packed), torch.from_numpy(high), torch.from_numpy(sc), bits)
+    tc, th, ts = tc.numpy(), th.numpy(), ts.numpy()
+    blocks, chunks = (n + 15) // 16, padded // 128
+    assert tc.shape == (blocks, chunks, 4, 16, 16) and th.shape == (blocks, chunks, 4, 16, 4 * hb)
+    regs = th.reshape(blocks, chunks, 4, 16, hb, 4).astype(np.uint32)
+    regs = regs[..., 0] | (regs[..., 1] << 8) | (regs[..., 2] << 16) | (regs[..., 3] << 24)
+    per = 4 // hb
+    got = np.zeros((blocks * 16, padded), np.int64)
+    for blk in range(blocks):
+        for c in range(chunks):
+            for q in range(4):
+                for r in range(16):
+                    word_bytes = tc[blk, c, q, r]
+                    for j in range(4):
+                        word = int.from_bytes(bytes(word_bytes[4 * j:4 * j + 4]), "little")
+                        reg = int(regs[blk, c, q, r, j // per])
+                        base = hb * (j % per)
+                        for m in range(4):
+                            for side in range(2):  # column c + 2m + side
+                                nibble = (word >> (4 * (m + 4 * side))) & 15
+                                field = (reg >> (base + (0, 8, 4, 12)[m] + 16 * side)) & ((1 << hb) - 1)
+                                col = 128 * c + 32 * q + 8 * j + 2 * m + side
+                                got[16 * blk + r, col] = (nibble | (field << 4)) - (1 << (bits - 1))
+    assert np.array_equal(got[:n], codes)
+    # Rows past n hold all-zero bytes (code -2^(bits-1) with scale 0: never stored).
+    assert not tc[-1, :, :, (n - 1) % 16 + 1:].any() and not th[-1, :, :, (n - 1) % 16 + 1:].any()
+    assert np.array_equal(ts.transpose(0, 2, 1, 3).reshape(blocks * 16, chunks * 2)[:n], sc)

@@ -170,6 +170,57 @@ __device__ __forceinline__ half8 dequant8_high(std::uint32_t word, std::uint32_t
     return w;
 }
 
+// Eight Q5 (HB = 1) / Q6 (HB = 2) columns c .. c+7 of the tiled copy: `u` is
+// the word's nibbles in dequant8_biased's order (unbiased), `reg` the high
+// register holding this word as its word jj. A pair's upper fields sit at
+// bits o + (0, 8, 4, 12)[m] and 16 above (o = HB * jj), biased so that nibble
+// and fields form u = q + 2^(3 + HB); each pair's two fields go to bit 4 of
+// its fp16 halves (1024 + u) or to bit 8 (1024 + 16 u, the x16 form), one
+// shift serving the pairs at +4 and +8. q = 1024 + u - 1024 - 2^(3+HB) and
+// (1024 + 16 u) / 16 - 64 - 2^(3+HB) are exact; fp16(q * s) is the one rounding.
+struct HighMasks {
+    std::uint32_t four, eight;  // the fields' positions: bit 4 / bit 8 of each half
+};
+
+template <int HB>
+__device__ __forceinline__ HighMasks high_masks() {
+    constexpr std::uint32_t f = (1u << HB) - 1u;
+    HighMasks m{(f << 4) * 0x10001u, (f << 8) * 0x10001u};
+    asm volatile("" : "+v"(m.four), "+v"(m.eight));  // kept in VGPRs for v_and_or_b32
+    return m;
+}
+
+template <int HB>
+__device__ __forceinline__ half8 dequant8_biased_high(std::uint32_t u, std::uint32_t reg, int jj, half2v s2,
+                                                      const BiasedMasks& m, const HighMasks& hm) {
+    const std::uint32_t v = u >> 8;
+    const int o = HB * jj;
+    const std::uint32_t at4 = reg << (4 - o);  // pair (c, c+1): offset o
+    const std::uint32_t mid = reg >> o;        // pairs (c+4, c+5) at o + 4 and (c+2, c+3) at o + 8
+    const std::uint32_t at12 = reg >> (4 + o); // pair (c+6, c+7): offset o + 12
+    // The nibble terms are opaque to the combiner, which would otherwise fold
+    // the two mask-and-ors of a pair into two ands and a three-input or.
+    std::uint32_t na = (u & m.lo) | m.one, nb = (u & m.hi) | m.one, nc = (v & m.lo) | m.one, nd = (v & m.hi) | m.one;
+    asm("" : "+v"(na), "+v"(nb), "+v"(nc), "+v"(nd));
+    const half2v a = __builtin_bit_cast(half2v, (at4 & hm.four) | na);
+    const half2v b = __builtin_bit_cast(half2v, (mid & hm.eight) | nb);
+    const half2v c = __builtin_bit_cast(half2v, (mid & hm.four) | nc);
+    const half2v d = __builtin_bit_cast(half2v, (at12 & hm.eight) | nd);
+    constexpr float bias = 1 << (3 + HB);
+    const half2v lo_bias = {static_cast<_Float16>(-1024.0f - bias), static_cast<_Float16>(-1024.0f - bias)};
+    const half2v sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+    const half2v hi_bias = {static_cast<_Float16>(-64.0f - bias), static_cast<_Float16>(-64.0f - bias)};
+    const half2v q[4] = {a + lo_bias, b * sixteenth + hi_bias, c + lo_bias, d * sixteenth + hi_bias};  // exact
+    half8 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v x = q[i] * s2;  // one fp16 rounding of q * s
+        w[2 * i] = x[0];
+        w[2 * i + 1] = x[1];
+    }
+    return w;
+}
+
 // Eight consecutive activations x0..x7 -> x0, x2, x4, x6, x1, x3, x5, x7.
 __device__ __forceinline__ uint4 interleave8(uint4 v) {
     uint4 r;
@@ -1006,11 +1057,13 @@ void launch_row_prefill(const __half* x, const std::uint8_t* codes, const std::u
 // 64-byte (scales) wave access. The copy stores each word's nibbles pre-biased
 // (q + 8) and reordered (nibble j holds column 2j, nibble 4 + j column 2j + 1)
 // so that dequant8_biased yields the eight columns in natural order: the
-// activation fragments need no interleave (Q5/Q6 copies keep the row-major
-// nibbles and tile the high plane [row block][chunk][lane][4 * HB bytes], the
-// bits lane (r, q) reads from the row-major plane). Every product and sum is the same
-// as in the row-major path (the MFMA's k slots hold the same column pairs), so
-// both layouts give the same bits.
+// activation fragments need no interleave. Q5/Q6 copies order the nibbles the
+// same way (unbiased) and tile the high plane [row block][chunk][lane][HB
+// registers] with each column's upper bits biased (sign flipped) and placed so
+// that dequant8_biased_high reads a column pair's fields with one shift and
+// one mask-and-or (the layout is q5.tile_row_codec's). Every product and sum
+// is the same as in the row-major path (the MFMA's k slots hold the same
+// column pairs), so both layouts give the same bits.
 template <int HB, int RB, int NB, int STEPS>
 struct RowDecodeBatch {
     uint4 w[STEPS][RB];
@@ -1065,6 +1118,7 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
     for (int tb = 0; tb < NB; ++tb)
         xr[tb] = x + static_cast<std::int64_t>(min(16 * tb + r, tokens - 1)) * k + 32 * q;
     const BiasedMasks masks = biased_masks();
+    const HighMasks hmasks = TILED && HB > 0 ? high_masks<HB ? HB : 1>() : HighMasks{0u, 0u};
     using Batch = RowDecodeBatch<HB, RB, NB, STEPS>;
     const int batches = (c1 - c0 + STEPS - 1) / STEPS;
     // Batch i holds chunks c0 + i * STEPS + s; chunks past c1 are clamped to c1 - 1
@@ -1122,7 +1176,7 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
         for (int tb = 0; tb < NB; ++tb)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                fa[tb][j] = __builtin_bit_cast(half8, TILED && HB == 0 ? t.x[st][tb][j] : interleave8(t.x[st][tb][j]));
+                fa[tb][j] = __builtin_bit_cast(half8, TILED ? t.x[st][tb][j] : interleave8(t.x[st][tb][j]));
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
             // Columns 32q .. 32q+31 of the chunk lie in its group q / 2.
@@ -1134,6 +1188,9 @@ __global__ __launch_bounds__(W * 64) void row_decode_gemm(const __half* __restri
                 half8 wf;
                 if constexpr (TILED && HB == 0) {
                     wf = dequant8_biased(words[j], s2, masks);
+                } else if constexpr (TILED) {
+                    wf = dequant8_biased_high<HB>(words[j], t.h[st][b][(HB * j) >> 2], j % (4 / HB), s2, masks,
+                                                  hmasks);
                 } else if constexpr (HB == 0) {
                     wf = dequant8(words[j], s2);
                 } else {

@@ -27,26 +27,53 @@ def quantize_q5_rtn(weight, *, max_elements=16 * 2**20):
     return Q5RowSplitWeight.from_codes(codes, scales)
 
 
+# Bit offsets of the four column pairs of an 8-column word inside its 16-bit
+# half of a high-plane register: pairs (c, c+1), (c+2, c+3), (c+4, c+5),
+# (c+6, c+7) of word jj of the register sit at hb * jj plus these.
+_PAIR_OFFSETS = (0, 8, 4, 12)
+
+
 def tile_row_codec(codes, high, scales, bits):
     """Tiled decode copy of q5_g64 / q6_g64 planes (read by ``venturi_row_tiled_run``).
 
     Codes [row block][chunk][lane l = 16q + r][16 bytes] as for Q4 (row r of the
-    16-row block, code bytes 16q .. 16q+15 of the 128-column chunk) but with the
-    row-major nibbles; high plane [row block][chunk][lane][4 * hb bytes] (the
-    lane's 32 columns' upper hb = bits - 4 bits, LSB-first as in the row-major
-    stream); scales [row block][chunk][r][2]. Rows past n are zero.
+    16-row block, columns 128c + 32q .. +32 of the chunk, four 4-byte words of
+    8 columns) with the low nibbles as stored (no bias) in Q4's tiled order:
+    nibble j of a word holds column c + 2j, nibble 4 + j column c + 2j + 1.
+    High plane [row block][chunk][lane][hb 4-byte registers] (hb = bits - 4):
+    each column's upper hb bits biased (the sign bit flipped, so nibble and
+    upper bits form the code plus 2^(bits - 1)); register i holds words
+    jj = 0 .. 4/hb - 1 of the lane (word 4i/hb + jj), the pair (c + 2m,
+    c + 2m + 1) of word jj at bits hb * jj + (0, 8, 4, 12)[m] and 16 above.
+    Scales [row block][chunk][r][2]. Rows past n are zero.
     """
     if bits not in (5, 6):
         raise ValueError("tile_row_codec takes 5- or 6-bit planes")
     hb = bits - 4
     n, row_bytes = codes.shape
+    padded = 2 * row_bytes
     chunks = row_bytes // 64
     blocks = (n + 15) // 16
-    c = torch.zeros((blocks * 16, row_bytes), dtype=torch.uint8, device=codes.device)
-    h = torch.zeros((blocks * 16, chunks * 16 * hb), dtype=torch.uint8, device=codes.device)
-    s = torch.zeros((blocks * 16, chunks * 2), dtype=torch.float16, device=codes.device)
-    c[:n] = codes
-    h[:n] = high
+    device = codes.device
+    nib = torch.stack((codes & 15, codes >> 4), -1).reshape(n, padded // 8, 8)
+    nib = nib[:, :, [0, 2, 4, 6, 1, 3, 5, 7]].reshape(n, row_bytes, 2)
+    packed = nib[..., 0] | (nib[..., 1] << 4)
+    # Upper bits per column from the LSB-first stream, then biased.
+    stream = (high.unsqueeze(-1) >> torch.arange(8, dtype=torch.uint8, device=device)) & 1
+    stream = stream.reshape(n, padded, hb).to(torch.int64)
+    upper = sum(stream[..., b] << b for b in range(hb)) ^ (1 << (hb - 1))
+    upper = upper.view(n, chunks, 4, 4, 8)  # [row][chunk][q][word][column]
+    per = 4 // hb  # words per register
+    words = torch.arange(4, device=device)
+    offset = (hb * (words % per))[:, None] + torch.tensor(_PAIR_OFFSETS, device=device)[None, :]  # [word][pair]
+    fields = (upper[..., 0::2] << offset) | (upper[..., 1::2] << (offset + 16))
+    regs = fields.sum(-1).view(n, chunks, 4, hb, per).sum(-1)  # disjoint bits: sums are ors
+    regs = (regs - ((regs >> 31) << 32)).to(torch.int32)  # the same 32 bits as int32
+    c = torch.zeros((blocks * 16, row_bytes), dtype=torch.uint8, device=device)
+    h = torch.zeros((blocks * 16, chunks * 16 * hb), dtype=torch.uint8, device=device)
+    s = torch.zeros((blocks * 16, chunks * 2), dtype=torch.float16, device=device)
+    c[:n] = packed
+    h[:n] = regs.reshape(n, chunks * 4 * hb).view(torch.uint8)
     s[:n] = scales
     tc = c.view(blocks, 16, chunks, 4, 16).permute(0, 2, 3, 1, 4).contiguous()
     th = h.view(blocks, 16, chunks, 4, 4 * hb).permute(0, 2, 3, 1, 4).contiguous()
