@@ -176,7 +176,7 @@ def launch_table(detail):
 # line still has the headline's per-launch table, parity and exact route.
 _LINE_ORDER = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
                "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline", "timing", "all_kernels_GBps",
-               "graph_equals_eager", "codecs", "q56_decode", "config1", "model_decode", "moe_w4a16", "prefill_a16",
+               "graph_equals_eager", "codecs", "config1", "q56_decode", "model_decode", "moe_w4a16", "prefill_a16",
                "prefill_a8", "a8_decode", "q4_decode", "vocab_head", "exact_route", "parity", "per_launch")
 
 
@@ -188,18 +188,31 @@ def shorten(result):
     the rest); per-projection agreement records are left to the summary;
     GB/s columns are kept for the headline's launches and the exact route and
     left out elsewhere (the section's own GB/s and roofline stay); stage
-    fractions of peak are left out (their TFLOP/s / TOPS stay).
+    fractions of peak are left out (their TFLOP/s / TOPS stay), and so are the
+    prefill stages' TFLOP/s (the times stay), the library route's note and
+    agreement record, the Q5/Q6 per-launch tables (their GB/s and roofline
+    stay) and the section baselines' sample text (`--full` prints them all).
     """
     keep_rate = ("exact_route",)  # besides the headline's own per_launch
+
+    def dropped(key, path):
+        if key == "per_projection":
+            return True
+        if "stages" in path and (key.startswith("frac_") and key.endswith("_peak")
+                                 or path[0] == "prefill_a16" and key == "TFLOP/s"):
+            return True
+        if path[-1:] == ("library_route",) and key in ("note", "parity"):
+            return True
+        if path[:1] == ("q56_decode",) and key == "per_launch":
+            return True
+        return path[1:] == ("cpu_baseline",) and key == "sample"
 
     def walk(node, path):
         if not isinstance(node, dict):
             return node
         out = {}
         for key, value in node.items():
-            if key == "per_projection":
-                continue
-            if key.startswith("frac_") and key.endswith("_peak") and "stages" in path:
+            if dropped(key, path):
                 continue
             if key == "per_launch" and isinstance(value, dict):
                 sample = next(iter(value.values()), None)

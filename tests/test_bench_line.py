@@ -33,7 +33,13 @@ def _result():
         "a8_decode": {"GB/s": 3900.0, "per_launch": a8},
         "vocab_head": {"per_launch": {"m1": {"us": 205.0}, "m1_exact_route": {"us": 255.0}}},
         "prefill_a8": {"parity": {"summary": _agreement(54), "per_projection": {"qkv": _agreement(15)}},
-                       "stages": {"qkv": {"us": 475.2, "TOPS": 316.3, "frac_int8_peak": 0.06}}},
+                       "stages": {"qkv": {"us": 475.2, "TOPS": 316.3, "frac_int8_peak": 0.06}},
+                       "cpu_baseline": {"value": 1.0, "unit": "TOP/s", "cores": 16, "kind": "oracle", "sample": "s"}},
+        "prefill_a16": {"w4a16": {"TFLOP/s": 1100.0, "library_route": {"kernel": "k", "TFLOP/s": 1100.0, "note": "n",
+                                                                       "parity": _agreement(43)},
+                                  "stages": {"qkv": {"us": 123.0, "TFLOP/s": 1200.0, "fused_mfma_us": 150.0}}}},
+        "q56_decode": {"q5": {"GB/s": 3100.0, "roofline": {"frac": 0.39},
+                              "per_launch": {f"qkv_m{m}": {"us": 9.0, "GB/s": 2000.0} for m in (1, 4)}}},
         "cpu_baseline": {"value": 12.0},
     }
 
@@ -71,4 +77,12 @@ def test_shorten_keeps_sections_and_orders_them():
     assert short["parity"]["per_launch"]["max_ulp"]["down"] == [3.0, 3.0, 3.0, 3.0]
     assert "per_projection" not in short["prefill_a8"]["parity"]
     assert short["prefill_a8"]["stages"]["qkv"] == {"us": 475.2, "TOPS": 316.3}
+    # Prefill stages keep their times, the library route its rate, Q5/Q6 their section rates;
+    # section baselines drop the sample text (the headline's keeps it).
+    w4 = short["prefill_a16"]["w4a16"]
+    assert w4["stages"]["qkv"] == {"us": 123.0, "fused_mfma_us": 150.0}
+    assert w4["library_route"] == {"kernel": "k", "TFLOP/s": 1100.0}
+    assert short["q56_decode"]["q5"] == {"GB/s": 3100.0, "roofline": {"frac": 0.39}}
+    assert "sample" not in short["prefill_a8"]["cpu_baseline"] and short["prefill_a8"]["cpu_baseline"]["value"] == 1.0
+    assert short["cpu_baseline"] == full["cpu_baseline"]
     json.dumps(short)  # still one JSON object
