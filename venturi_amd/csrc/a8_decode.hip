@@ -647,7 +647,9 @@ void validate_a8_tiled(const void* workspace, std::uint64_t available, const voi
 // share a CU goes to one 16-wave workgroup over the same row blocks; LDS past
 // one workgroup's share of the CU splits K over two workgroups of 16 waves and
 // three row blocks, which exchange their halves through slots, where that grid
-// runs in at most two rounds of one workgroup per CU), else the register form.
+// runs in at most two rounds of one workgroup per CU, or where rows of at
+// least 128 chunks in 257-384 blocks would leave CUs idle), else the register
+// form.
 struct A8TiledPlan {
     bool staged;
     A8Shape shape;
@@ -664,6 +666,11 @@ A8TiledPlan a8_tiled_plan(int tokens, int n, int k, int passes) {
         lds = a8_lds_bytes(tokens, groups, passes, sh);
     }
     if (lds > kA8StageLdsMax && (groups + 1) / 2 >= 2 * 16 && (blocks + 2) / 3 * 2 <= 512) {
+        sh = A8Shape{16, 3, 2, 2};
+        lds = a8_lds_bytes(tokens, groups, passes, sh);
+    } else if (blocks > 256 && (blocks + 2) / 3 * 2 <= 256 && (groups + 1) / 2 >= 128) {
+        // Long rows of 257-384 blocks split K as well: 2 * ceil(blocks / 3)
+        // workgroups instead of ceil(blocks / 2) (down at 8 tokens: 214, not 160).
         sh = A8Shape{16, 3, 2, 2};
         lds = a8_lds_bytes(tokens, groups, passes, sh);
     }
